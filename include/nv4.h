@@ -1,0 +1,111 @@
+/*
+ * nv4.h -- C ABI of the MI355X (gfx950) quantized-linear library libnv4.so.
+ *
+ * Plain pointers and sizes only.  bf16/fp16 buffers are passed as void*;
+ * `stream` is a hipStream_t (NULL = the null stream) passed as void* so this
+ * header needs no HIP headers.  The caller owns every buffer; no entry point
+ * allocates, frees or synchronises.  Launches are asynchronous on `stream`
+ * and may be captured into a HIP graph.  Inputs are never modified and
+ * nothing outside the output ranges is written.
+ *
+ * Return value: NV4_OK (0); a negative NV4_E* code when the arguments are
+ * rejected (nothing is launched); or a positive hipError_t from the launch.
+ * Nothing aborts or prints.
+ *
+ * Entry points replace, one for one, the kernels behind the reference's
+ * Python operators (paths relative to the reference repository):
+ *   nv4_rht_quant_pack  <- nanovllm/kernels/rht_a4_tilelang.py:150 rht_quant_pack
+ *                          (kernel :37-136)
+ *   nv4_w4a4_gemm       <- nanovllm/kernels/w4a4_grouped_kernel.py:104 w4a4_grouped_gemm
+ *                          and :32 compile_grouped_gemm(..., output_fp32, weight_grouped)
+ *   nv4_w4a16_gemm      <- nanovllm/layers/linear_w4a16.py:11 tl_dequant_matmul_w4a16
+ *                          (called from W4A16Linear.forward :128-148)
+ */
+#ifndef NV4_H
+#define NV4_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define NV4_OK 0
+#define NV4_E_NULL (-1)      /* a required pointer is NULL */
+#define NV4_E_SHAPE (-2)     /* M/N/K outside what the contract allows */
+#define NV4_E_ALIGN (-3)     /* a pointer is not aligned as documented */
+#define NV4_E_LAYOUT (-4)    /* unknown rotation layout */
+#define NV4_E_DTYPE (-5)     /* unknown dtype code */
+#define NV4_E_GROUP (-6)     /* unsupported quantization group size */
+
+/* Rotation layouts for nv4_rht_quant_pack. */
+#define NV4_LAYOUT_REFERENCE 0 /* "row_DH_paley12_kron_sylvester_v1": full-width
+                                  Sylvester H4096, or H12 (Paley) x H1024 for K=12288 */
+#define NV4_LAYOUT_BLOCK128 1  /* Hadamard-128 on every aligned 128-block, x RN(1/sqrt 128)
+                                  (no reference counterpart) */
+
+/* dtype codes */
+#define NV4_BF16 0
+#define NV4_FP16 1
+#define NV4_FP32 2
+
+/*
+ * Fused randomized Hadamard transform + group-128 INT4 quantization + packing.
+ * Replaces rht_quant_pack (nanovllm/kernels/rht_a4_tilelang.py:150-163).
+ *   x      bf16 [M,K] row-major, 16-byte aligned
+ *   signs  int8 [K], values +/-1, 16-byte aligned
+ *   packed int8 [M,K/2] out: two's-complement nibbles, even k in the low nibble
+ *   scale  bf16 [M,K/128] out: BF16(max|r|*0.9/7) rounded before the codes
+ *          (1.0 for an all-zero group, at least 2^-126)
+ * layout NV4_LAYOUT_REFERENCE requires K in {4096, 12288};
+ * NV4_LAYOUT_BLOCK128 accepts any K that is a positive multiple of 128 up to 65536.
+ * M >= 1.
+ */
+int nv4_rht_quant_pack(const void* x, const int8_t* signs, int8_t* packed, void* scale,
+                       int64_t M, int64_t K, int layout, void* stream);
+
+/*
+ * Grouped W4A4 GEMM: C[M,N] = sum over 128-groups g (in order) of
+ * fmaf(float(dot_g), sa[m,g]*sw[n,g], total), rounded to bf16 at the end.
+ * Replaces w4a4_grouped_gemm / compile_grouped_gemm
+ * (nanovllm/kernels/w4a4_grouped_kernel.py:32,104-129).
+ *   a   int8 [M,K/2] packed activation codes (16-byte aligned)
+ *   w   int8 [N,K/2] packed weight codes (16-byte aligned)
+ *   sa  bf16 [M,K/128]
+ *   sw  bf16 [N,K/128] when sw_grouped != 0 (production), else bf16 [N]
+ *       (per-channel: total = sum fmaf(float(dot_g), sa[m,g], total); C = bf16(total*sw[n]))
+ *   out bf16 [M,N], or fp32 [M,N] (the value before the final rounding) when out_fp32 != 0
+ * M >= 1, N >= 1 with N % 8 == 0, K >= 128 with K % 128 == 0.
+ */
+int nv4_w4a4_gemm(const int8_t* a, const int8_t* w, const void* sa, const void* sw,
+                  int sw_grouped, void* out, int out_fp32,
+                  int64_t M, int64_t N, int64_t K, void* stream);
+
+/*
+ * W4A16 GEMM with GPTQ weights (zero-point convention w = (q - z - 1) * s).
+ * Replaces tl_dequant_matmul_w4a16 (nanovllm/layers/linear_w4a16.py:11-59).
+ *   x        [M,K] activations, x_dtype NV4_BF16 (reference) or NV4_FP16
+ *   qweight  int32 [K/8,N]: nibble k%8 (bits 4*(k%8)) of row k/8 holds q[k,n]
+ *   qzeros   int32 [K/group,N/8]: nibble n%8 of [g, n/8] holds z[g,n]
+ *   scales   fp16 [K/group,N]
+ *   out      [M,N] out, out_dtype NV4_BF16 (reference) or NV4_FP16
+ * Dequantization: bf16 activations use deq = bf16(bf16(q-z-1) * bf16(s)) as the
+ * reference does; fp16 activations use deq = fp16((q-z-1) * s).  Products are
+ * accumulated in fp32 over the whole K (deterministic; no split-K atomics).
+ * group == 128; K % 128 == 0; N % 8 == 0; M >= 1.  x and out 16-byte aligned.
+ */
+int nv4_w4a16_gemm(const void* x, int x_dtype, const int32_t* qweight, const int32_t* qzeros,
+                   const void* scales, void* out, int out_dtype,
+                   int64_t M, int64_t N, int64_t K, int group, void* stream);
+
+/* Library version string. */
+const char* nv4_version(void);
+
+/* Human-readable text for an NV4_E* code (or "hip error" for positive codes). */
+const char* nv4_strerror(int code);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* NV4_H */

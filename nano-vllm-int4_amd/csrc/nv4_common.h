@@ -1,0 +1,53 @@
+// Shared device helpers for the nv4 HIP kernels (gfx950 / CDNA4, wave64).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/nv4.h"
+
+namespace nv4 {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v16i __attribute__((ext_vector_type(16)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+typedef float v16f __attribute__((ext_vector_type(16)));
+typedef short v8s __attribute__((ext_vector_type(8)));
+typedef _Float16 v8h __attribute__((ext_vector_type(8)));
+typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
+
+constexpr int kWave = 64;
+
+constexpr int ilog2c(int v) { return v <= 1 ? 0 : 1 + ilog2c(v / 2); }
+
+__device__ __forceinline__ float bf16_to_f32(uint32_t h) { return __uint_as_float(h << 16); }
+
+// fp32 -> bf16 bits, round to nearest even (NaN kept as a quiet NaN).
+__device__ __forceinline__ uint32_t f32_to_bf16_rne(float f) {
+    uint32_t u = __float_as_uint(f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return (u >> 16) | 0x40u;
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return u >> 16;
+}
+
+// Two packed signed nibbles per byte, even k in the low nibble.  Returns the
+// nibbles as int8 lanes scaled by 16 (the nibble in the high half of each
+// byte): lo16 = low nibbles of the 4 bytes, hi16 = high nibbles.  Both
+// operands of a product scaled this way give 256 * the true integer dot.
+__device__ __forceinline__ uint32_t nib_lo16(uint32_t w) { return (w << 4) & 0xF0F0F0F0u; }
+__device__ __forceinline__ uint32_t nib_hi16(uint32_t w) { return w & 0xF0F0F0F0u; }
+
+// 8 packed bytes (16 nibbles) -> one 16-lane int8 MFMA operand, scaled by 16.
+// Nibble order inside the operand: lo(b0..b3), hi(b0..b3), lo(b4..b7), hi(b4..b7).
+// A and B operands built by the same function pair element for element, so
+// the product sums exactly the same 16 k values on both sides.
+__device__ __forceinline__ v4i unpack8_x16(uint32_t d0, uint32_t d1) {
+    v4i r;
+    r[0] = (int)nib_lo16(d0);
+    r[1] = (int)nib_hi16(d0);
+    r[2] = (int)nib_lo16(d1);
+    r[3] = (int)nib_hi16(d1);
+    return r;
+}
+
+}  // namespace nv4

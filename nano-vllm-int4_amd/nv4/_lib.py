@@ -1,0 +1,84 @@
+"""ctypes binding of libnv4.so, the gfx950 HIP library behind every nv4 operator.
+
+There is no fallback: if the library is missing or fails to load, every
+operator raises.  Build it with ``make -C nano-vllm-int4_amd`` (or
+``__graft_entry__.build()``).
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+from pathlib import Path
+
+_HERE = Path(__file__).resolve().parent
+LIB_PATH = Path(os.environ.get("NV4_LIB", _HERE / "libnv4.so"))
+
+NV4_OK = 0
+NV4_E_NULL = -1
+NV4_E_SHAPE = -2
+NV4_E_ALIGN = -3
+NV4_E_LAYOUT = -4
+NV4_E_DTYPE = -5
+NV4_E_GROUP = -6
+
+LAYOUT_REFERENCE = 0
+LAYOUT_BLOCK128 = 1
+BF16, FP16, FP32 = 0, 1, 2
+
+# Every symbol declared in include/nv4.h, with its ctypes signature.
+_P, _I, _I64 = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64
+SIGNATURES = {
+    "nv4_rht_quant_pack": ([_P, _P, _P, _P, _I64, _I64, _I, _P], _I),
+    "nv4_w4a4_gemm": ([_P, _P, _P, _P, _I, _P, _I, _I64, _I64, _I64, _P], _I),
+    "nv4_w4a16_gemm": ([_P, _I, _P, _P, _P, _P, _I, _I64, _I64, _I64, _I, _P], _I),
+    "nv4_version": ([], ctypes.c_char_p),
+    "nv4_strerror": ([_I], ctypes.c_char_p),
+}
+
+_lib = None
+_lock = threading.Lock()
+
+
+class NV4LibraryError(RuntimeError):
+    """libnv4.so is missing or does not load."""
+
+
+def load():
+    """Load libnv4.so once; raise NV4LibraryError when it is not there."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is None:
+            if not LIB_PATH.exists():
+                raise NV4LibraryError(
+                    f"{LIB_PATH} is missing: build the HIP library first "
+                    "(make -C nano-vllm-int4_amd, or __graft_entry__.build())")
+            try:
+                lib = ctypes.CDLL(str(LIB_PATH))
+            except OSError as exc:  # pragma: no cover - depends on the host
+                raise NV4LibraryError(f"cannot load {LIB_PATH}: {exc}") from exc
+            for name, (args, res) in SIGNATURES.items():
+                fn = getattr(lib, name)
+                fn.argtypes = args
+                fn.restype = res
+            _lib = lib
+    return _lib
+
+
+def strerror(code: int) -> str:
+    return load().nv4_strerror(int(code)).decode()
+
+
+def check(code: int, op: str) -> None:
+    """Map an ABI return code to the exception the reference raises for it."""
+    if code == NV4_OK:
+        return
+    if code < 0:
+        raise ValueError(f"{op}: {strerror(code)} (nv4 code {code})")
+    raise RuntimeError(f"{op}: HIP launch failed with hipError_t {code}")
+
+
+def version() -> str:
+    return load().nv4_version().decode()

@@ -1,0 +1,52 @@
+"""W4A16 GEMM with GPTQ-packed INT4 weights (MI355X).
+
+Replaces the TileLang kernel ``tl_dequant_matmul_w4a16`` of the reference
+(nanovllm/layers/linear_w4a16.py:11-59).  Same packed formats: qweight int32
+[K/8, N] (nibble k%8 of row k/8), qzeros int32 [K/128, N/8] (nibble n%8),
+fp16 scales [K/128, N]; same zero convention w = (q - z - 1) * s and, for bf16
+activations, the same bf16 rounding of the dequantized weight.  Unlike the
+reference (split-K 8 with bf16 atomics onto a zeroed output) the HIP kernel
+sums all of K in fp32 and writes each output once, so results do not depend
+on scheduling.  FP16 activations are accepted as well (output fp16).
+"""
+from __future__ import annotations
+
+import ctypes
+
+import torch
+
+from .. import _lib
+
+_DT = {torch.bfloat16: _lib.BF16, torch.float16: _lib.FP16}
+
+
+def dequant_matmul_w4a16(x, qweight, qzeros, scales, group_size=128, out=None):
+    """x [M,K] bf16/fp16 -> out [M,N] in x's dtype."""
+    if x.ndim != 2 or x.dtype not in _DT:
+        raise ValueError("Expected BF16 or FP16 activations [M,K]")
+    M, K = x.shape
+    if qweight.dtype != torch.int32 or qzeros.dtype != torch.int32 or scales.dtype != torch.float16:
+        raise TypeError("Expected int32 qweight/qzeros and fp16 scales")
+    if qweight.ndim != 2 or qweight.shape[0] * 8 != K:
+        raise ValueError("qweight must be [K/8, N]")
+    N = qweight.shape[1]
+    if group_size != 128 or K % 128 or N % 8 or M < 1:
+        raise ValueError("Require group_size 128, K divisible by 128, N divisible by 8, M > 0")
+    if tuple(qzeros.shape) != (K // 128, N // 8) or tuple(scales.shape) != (K // 128, N):
+        raise ValueError("Require qzeros [K/128, N/8] and scales [K/128, N]")
+    if out is None:
+        out = torch.empty((M, N), device=x.device, dtype=x.dtype)
+    if tuple(out.shape) != (M, N) or out.dtype not in _DT:
+        raise ValueError("Output must be BF16 or FP16 [M,N]")
+    tensors = (x, qweight, qzeros, scales, out)
+    if any(not t.is_cuda or not t.is_contiguous() or t.device != x.device for t in tensors):
+        raise ValueError("All tensors must be contiguous on one CUDA device")
+    lib = _lib.load()
+    stream = torch.cuda.current_stream(x.device).cuda_stream
+    with torch.cuda.device(x.device):
+        rc = lib.nv4_w4a16_gemm(ctypes.c_void_p(x.data_ptr()), _DT[x.dtype],
+                                ctypes.c_void_p(qweight.data_ptr()), ctypes.c_void_p(qzeros.data_ptr()),
+                                ctypes.c_void_p(scales.data_ptr()), ctypes.c_void_p(out.data_ptr()),
+                                _DT[out.dtype], M, N, K, group_size, ctypes.c_void_p(stream))
+    _lib.check(rc, "dequant_matmul_w4a16")
+    return out

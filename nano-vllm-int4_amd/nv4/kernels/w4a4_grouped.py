@@ -1,0 +1,115 @@
+"""Grouped W4A4 INT4 GEMM (MI355X): G=128 activations, G=128 or per-channel weights.
+
+Drop-in for ``nanovllm.kernels.w4a4_grouped_kernel`` (reference file
+nanovllm/kernels/w4a4_grouped_kernel.py): ``w4a4_grouped_gemm`` keeps the
+signature, validation order and exceptions of :104-129, ``compile_grouped_gemm``
+keeps :32 (including the fp32-output diagnostic and the 1-D weight-scale
+form), ``GroupedConfig``/``best_grouped_config`` keep :21-28/:94-101.
+
+Each output element is, for g in order, ``total = fmaf(float(dot_g),
+sa[m,g]*sw[n,g], total)`` with exact int32 group dots, rounded to bf16 at the
+end (or ``total = fmaf(float(dot_g), sa[m,g], total)``; ``bf16(total*sw[n])``
+for 1-D weight scales).  The HIP kernels (``nv4_w4a4_gemm``) take M at run time:
+nothing is compiled per shape, and there is no split-K and no atomics.
+"""
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass
+from functools import lru_cache
+
+import torch
+
+from .. import _lib
+
+GROUP_SIZE = 128
+
+
+@dataclass(frozen=True)
+class GroupedConfig:
+    """Launch hint kept for API compatibility (w4a4_grouped_kernel.py:21-28).
+    The HIP kernels choose their own tiles from M; any valid config gives the
+    same bits."""
+    bm: int = 32
+    bn: int = 64
+    stages: int = 2
+    threads: int = 128
+    cache_scales: bool = False
+    cache_weight_scales: bool = False
+
+
+def _validate_config(cfg: GroupedConfig) -> None:
+    if min(cfg.bm, cfg.bn, cfg.threads) < 1 or cfg.stages < 0 or cfg.threads % 32:
+        raise ValueError("Require positive dimensions, K divisible by 128, N divisible by 8, and whole warps")
+
+
+def _launch(a_packed, w_packed, a_scale, w_scale, out, output_fp32, weight_grouped):
+    M, N, K = a_packed.shape[0], w_packed.shape[0], a_packed.shape[1] * 2
+    lib = _lib.load()
+    stream = torch.cuda.current_stream(a_packed.device).cuda_stream
+    with torch.cuda.device(a_packed.device):
+        rc = lib.nv4_w4a4_gemm(ctypes.c_void_p(a_packed.data_ptr()), ctypes.c_void_p(w_packed.data_ptr()),
+                               ctypes.c_void_p(a_scale.data_ptr()), ctypes.c_void_p(w_scale.data_ptr()),
+                               1 if weight_grouped else 0, ctypes.c_void_p(out.data_ptr()),
+                               1 if output_fp32 else 0, M, N, K, ctypes.c_void_p(stream))
+    _lib.check(rc, "w4a4_grouped_gemm")
+
+
+@lru_cache(None)
+def compile_grouped_gemm(M, N, K, cfg=GroupedConfig(), output_fp32=False, weight_grouped=False):
+    """Return ``kernel(A, W, Sa, Sw, C)`` for exact (M, N, K), as the reference does
+    (its kernel is JIT-specialised on M; this one only checks the shapes)."""
+    if min(M, N, K) < 1 or K % GROUP_SIZE or N % 8:
+        raise ValueError("Require positive dimensions, K divisible by 128, N divisible by 8, and whole warps")
+    _validate_config(cfg)
+    out_dtype = torch.float32 if output_fp32 else torch.bfloat16
+    sw_shape = (N, K // GROUP_SIZE) if weight_grouped else (N,)
+
+    def kernel(a_packed, w_packed, a_scale, w_scale, out):
+        if (tuple(a_packed.shape) != (M, K // 2) or tuple(w_packed.shape) != (N, K // 2)
+                or tuple(a_scale.shape) != (M, K // GROUP_SIZE) or tuple(w_scale.shape) != sw_shape
+                or tuple(out.shape) != (M, N) or out.dtype != out_dtype):
+            raise ValueError("Arguments do not match the compiled (M, N, K) kernel")
+        tensors = (a_packed, w_packed, a_scale, w_scale, out)
+        if any(not t.is_cuda or not t.is_contiguous() or t.device != a_packed.device for t in tensors):
+            raise ValueError("All inputs must be contiguous CUDA tensors on one device")
+        _launch(a_packed, w_packed, a_scale, w_scale, out, output_fp32, weight_grouped)
+    return kernel
+
+
+@lru_cache(None)
+def best_grouped_config(M, N, K, weight_grouped=False):
+    """Reference dispatch-table lookup (w4a4_grouped_kernel.py:94-101); the HIP
+    kernels do not use it, so it returns the reference defaults."""
+    return GroupedConfig() if M <= 32 else GroupedConfig(64, 128, 2, 128)
+
+
+def w4a4_grouped_gemm(a_packed, w_packed, a_scale, w_scale, out=None, config=None):
+    """Packed INT4; BF16 Sa[M,K/128], Sw[N] or Sw[N,K/128], output[M,N]."""
+    if a_packed.ndim != 2 or w_packed.ndim != 2 or a_packed.shape[1] != w_packed.shape[1]:
+        raise ValueError("Packed inputs must have compatible [M,K/2] and [N,K/2] shapes")
+    M, K = a_packed.shape[0], a_packed.shape[1] * 2
+    N = w_packed.shape[0]
+    if a_packed.dtype != torch.int8 or w_packed.dtype != torch.int8:
+        raise TypeError("Packed inputs must use int8 storage")
+    if K % GROUP_SIZE or N % 8 or min(M, N, K) < 1:
+        raise ValueError("Require positive dimensions, K divisible by 128, N divisible by 8")
+    weight_grouped = w_scale.ndim == 2
+    expected_w_scale = (N, K // GROUP_SIZE) if weight_grouped else (N,)
+    if tuple(a_scale.shape) != (M, K // GROUP_SIZE) or tuple(w_scale.shape) != expected_w_scale:
+        raise ValueError("Require Sa[M,K/128] and Sw[N] or Sw[N,K/128]")
+    if a_scale.dtype != torch.bfloat16 or w_scale.dtype != torch.bfloat16:
+        raise TypeError("Both scale tensors must be BF16")
+    tensors = (a_packed, w_packed, a_scale, w_scale)
+    if any(not value.is_cuda or not value.is_contiguous() or value.device != a_packed.device
+           for value in tensors):
+        raise ValueError("All inputs must be contiguous CUDA tensors on one device")
+    if out is None:
+        out = torch.empty((M, N), device=a_packed.device, dtype=torch.bfloat16)
+    if (tuple(out.shape) != (M, N) or out.dtype != torch.bfloat16 or out.device != a_packed.device
+            or not out.is_contiguous()):
+        raise ValueError("Output must be contiguous BF16 [M,N] on the input device")
+    if config is not None:
+        _validate_config(config)
+    _launch(a_packed, w_packed, a_scale, w_scale, out, False, weight_grouped)
+    return out

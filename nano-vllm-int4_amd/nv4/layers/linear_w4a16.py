@@ -1,0 +1,34 @@
+"""GPTQ W4A16 linear (MI355X).
+
+Drop-in for ``nanovllm.layers.linear_w4a16.W4A16Linear`` (reference
+nanovllm/layers/linear_w4a16.py:98-148): same constructor, the same
+parameters (``qweight`` int32 [in/8, out], ``qzeros`` int32 [in/128, out/8],
+``scales`` fp16 [in/128, out], all ``requires_grad=False``), same forward
+shape handling.  The GEMM is the HIP kernel ``nv4_w4a16_gemm``.
+"""
+import torch
+from torch import nn
+
+from ..kernels.w4a16 import dequant_matmul_w4a16
+
+
+class W4A16Linear(nn.Module):
+
+    def __init__(self, in_features, out_features, group_size=128):
+        super().__init__()
+        assert group_size == 128
+        self.in_features = in_features
+        self.out_features = out_features
+        self.group_size = group_size
+        self.qweight = nn.Parameter(torch.empty(in_features // 8, out_features, dtype=torch.int32),
+                                    requires_grad=False)
+        self.qzeros = nn.Parameter(torch.empty(in_features // group_size, out_features // 8, dtype=torch.int32),
+                                   requires_grad=False)
+        self.scales = nn.Parameter(torch.empty(in_features // group_size, out_features, dtype=torch.float16),
+                                   requires_grad=False)
+
+    def forward(self, x):
+        shape = x.shape
+        x = x.reshape(-1, self.in_features).contiguous()
+        out = dequant_matmul_w4a16(x, self.qweight, self.qzeros, self.scales, self.group_size)
+        return out.reshape(*shape[:-1], self.out_features)

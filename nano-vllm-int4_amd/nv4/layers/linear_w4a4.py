@@ -1,0 +1,41 @@
+"""Single-GPU RHT-aware W4A4 linear, W128/A128, clipping 0.9 (MI355X).
+
+Drop-in for ``nanovllm.layers.linear_w4a4.W4A4Linear`` (reference
+nanovllm/layers/linear_w4a4.py:15-36): same constructor checks, the same
+buffers (``packed_weight`` int8 [out, in/2], ``weight_scale`` bf16
+[out, in/128], ``signs`` int8 [in]) so state dicts and the checkpoint loader
+carry over, and the same forward: RHT + quantize + pack the activations
+(K1), then the grouped INT4 GEMM (K2), both HIP kernels on the current stream.
+Temporary buffers come from torch's caching allocator, so the forward can be
+captured in a HIP graph.
+"""
+import torch
+from torch import nn
+import torch.distributed as dist
+
+from ..kernels.rht_a4 import rht_quant_pack
+from ..kernels.w4a4_grouped import w4a4_grouped_gemm
+
+
+class W4A4Linear(nn.Module):
+    def __init__(self, input_size: int, output_size: int, bias: bool = False):
+        super().__init__()
+        if dist.is_available() and dist.is_initialized() and dist.get_world_size() != 1:
+            raise ValueError("W4A4Linear supports one GPU only")
+        if bias or input_size not in (4096, 12288) or output_size % 8:
+            raise ValueError("W4A4 requires bias-free Qwen3-8B projection shapes")
+        self.in_features, self.out_features = input_size, output_size
+        self.register_buffer("packed_weight", torch.empty(output_size, input_size // 2, dtype=torch.int8))
+        self.register_buffer("weight_scale", torch.empty(output_size, input_size // 128, dtype=torch.bfloat16))
+        self.register_buffer("signs", torch.empty(input_size, dtype=torch.int8))
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        if x.shape[-1] != self.in_features or x.dtype != torch.bfloat16:
+            raise ValueError("W4A4Linear requires BF16 activations with the configured input width")
+        flat = x.reshape(-1, self.in_features).contiguous()
+        m, k = flat.shape
+        packed = torch.empty((m, k // 2), dtype=torch.int8, device=x.device)
+        scale = torch.empty((m, k // 128), dtype=torch.bfloat16, device=x.device)
+        rht_quant_pack(flat, self.signs, out_packed=packed, out_scale=scale)
+        out = w4a4_grouped_gemm(packed, self.packed_weight, scale, self.weight_scale)
+        return out.reshape(*x.shape[:-1], self.out_features)

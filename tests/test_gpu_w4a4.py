@@ -1,0 +1,158 @@
+"""GPU parity of K2 (grouped W4A4 INT4 GEMM) against the oracle.
+
+Restates benchmarks/verify_w4a4_aw_grouped.py and verify_w4a4_grouped.py:
+the reference shapes (17,96,512), (33,136,4096), (32,128,12288) with codes
+in [-8,7], a zero row in each operand, zeroed scale stripes, BF16 and fp32
+outputs bit-exact against the per-group FMA reference, 64-element canaries,
+three repeated calls, and the constant-scale reductions to the per-channel
+API.  Adds an M sweep across the kernel boundaries (skinny M <= 64, tiled
+above; tails in M and N) and the four Qwen3-8B projections at M = 32 (every
+element) and M = 4096 (a row sample, like the reference's pipeline audit,
+benchmarks/bench_rht_a4.py:184-190).  Bar: bit-exact.
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from conftest import bf16_bits, bits_to_bf16
+from nv4 import compile_grouped_gemm, rht_quant_pack, w4a4_grouped_gemm
+from nv4 import workloads as W
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda:0"
+
+
+def gemm_inputs(M, N, K, seed):
+    rng = np.random.default_rng(seed)
+    qa = rng.integers(-8, 8, (M, K)).astype(np.int8)
+    qw = rng.integers(-8, 8, (N, K)).astype(np.int8)
+    qa[0] = 0
+    qw[0] = 0
+    sa = oracle.f32_to_bf16((rng.random((M, K // 128)) * 2).astype(np.float32))
+    sw = oracle.f32_to_bf16((rng.random((N, K // 128)) * .03).astype(np.float32))
+    if M > 1:
+        sa[1, ::2] = 0
+    if N > 1:
+        sw[1, 1::2] = 0
+    return oracle.pack_int4(qa), oracle.pack_int4(qw), sa, sw
+
+
+def to_dev(ap, wp, sa, sw):
+    return (torch.from_numpy(ap).to(DEV), torch.from_numpy(wp).to(DEV),
+            bits_to_bf16(sa).to(DEV), bits_to_bf16(sw).to(DEV))
+
+
+def describe_mismatch(got, ref):
+    bad = np.argwhere(got != ref)
+    rows = np.unique(bad[:, 0])[:10].tolist()
+    cols = np.unique(bad[:, 1])[:10].tolist()
+    return f"{len(bad)} of {got.size} differ; rows {rows}; cols {cols}"
+
+
+def assert_bits_equal(got, ref, what):
+    if not np.array_equal(got, ref):
+        raise AssertionError(f"{what}: " + describe_mismatch(got, ref))
+
+
+def run_case(M, N, K, seed, grouped=True):
+    print(f"[k2] M={M} N={N} K={K} grouped={grouped}", flush=True)
+    ap, wp, sa, sw = gemm_inputs(M, N, K, seed)
+    if not grouped:
+        sw = sw[:, 0].copy()
+    exp_bf16 = oracle.w4a4_gemm(ap, wp, sa, sw)
+    exp_f32 = oracle.w4a4_gemm(ap, wp, sa, sw, out_fp32=True)
+    a, w, s_a, s_w = to_dev(ap, wp, sa, sw)
+    storage = torch.full((M * N + 128,), -1234, device=DEV, dtype=torch.bfloat16)
+    sentinel = storage[:64].clone()
+    out = storage[64:-64].view(M, N)
+    for _ in range(3):
+        out.fill_(float("nan"))
+        got = w4a4_grouped_gemm(a, w, s_a, s_w, out=out)
+        torch.cuda.synchronize()
+        assert got.data_ptr() == out.data_ptr()
+        assert_bits_equal(bf16_bits(out), exp_bf16, "bf16 output")
+        assert torch.equal(storage[:64], sentinel) and torch.equal(storage[-64:], sentinel)
+    out32 = torch.full((M, N), float("nan"), device=DEV, dtype=torch.float32)
+    compile_grouped_gemm(M, N, K, output_fp32=True, weight_grouped=grouped)(a, w, s_a, s_w, out32)
+    torch.cuda.synchronize()
+    assert_bits_equal(out32.cpu().numpy().view(np.uint32), exp_f32.view(np.uint32), "fp32 output")
+    return ap, wp, sa, sw, a, w, s_a, s_w
+
+
+@pytest.mark.parametrize("M,N,K", [(17, 96, 512), (33, 136, 4096), (32, 128, 12288)])
+def test_k2_reference_shapes(M, N, K):
+    ap, wp, sa, sw, a, w, s_a, _ = run_case(M, N, K, 20261110 + K)
+    # Constant dyadic weight scale: grouped == per-channel API (verify_w4a4_aw_grouped.py:84-90).
+    channel = torch.full((N,), .125, device=DEV, dtype=torch.bfloat16)
+    repeated = channel[:, None].expand(N, K // 128).contiguous()
+    one = w4a4_grouped_gemm(a, w, s_a, channel)
+    two = w4a4_grouped_gemm(a, w, s_a, repeated)
+    exp = oracle.w4a4_gemm(ap, wp, sa, bf16_bits(channel))
+    assert_bits_equal(bf16_bits(one), exp, "per-channel API")
+    assert_bits_equal(bf16_bits(two), exp, "grouped API with constant scale")
+    # Constant dyadic activation scale reduces to one ungrouped integer dot (verify_w4a4_grouped.py:75-79).
+    s_a.fill_(.125)
+    sw1 = torch.rand(N, generator=torch.Generator("cpu").manual_seed(K)).mul(.03).to(torch.bfloat16).to(DEV)
+    got = w4a4_grouped_gemm(a, w, s_a, sw1)
+    qa, qw = oracle.unpack_int4(ap).astype(np.int64), oracle.unpack_int4(wp).astype(np.int64)
+    full = torch.from_numpy((qa @ qw.T).astype(np.float32))
+    exp_ptpc = ((full * .125) * sw1.cpu().float()[None, :]).to(torch.bfloat16)
+    assert torch.equal(got.cpu(), exp_ptpc)
+
+
+@pytest.mark.parametrize("M,N,K", [(17, 96, 512), (33, 136, 4096), (32, 128, 12288)])
+def test_k2_per_channel_scale(M, N, K):
+    run_case(M, N, K, 20261109 + K, grouped=False)
+
+
+@pytest.mark.parametrize("M", [1, 2, 15, 16, 17, 31, 33, 47, 48, 49, 63, 64, 65, 100, 127, 128, 129, 257])
+def test_k2_m_sweep(M):
+    run_case(M, 136, 1024, 1000 + M)
+    run_case(M, 264, 256, 2000 + M, grouped=False)
+
+
+def chain_expected(case, rows=None):
+    xb = bf16_bits(case.x)
+    if rows is not None:
+        xb = xb[rows]
+    packed, scale = oracle.rht_quant_pack(xb, case.signs.numpy())
+    return packed, scale, oracle.w4a4_gemm(packed, case.w_packed.numpy(), scale, bf16_bits(case.w_scale))
+
+
+@pytest.mark.parametrize("proj", ["o", "qkv", "gate_up", "down"])
+def test_k2_chain_qwen3_shapes_m32(proj):
+    case = W.w4a4_case(proj, 32)
+    M, N, K = case.shape
+    print(f"[chain] {proj} M={M} N={N} K={K}", flush=True)
+    x, signs = case.x.to(DEV), case.signs.to(DEV)
+    wpk, wsc = case.w_packed.to(DEV), case.w_scale.to(DEV)
+    packed = torch.empty((M, K // 2), dtype=torch.int8, device=DEV)
+    scale = torch.empty((M, K // 128), dtype=torch.bfloat16, device=DEV)
+    rht_quant_pack(x, signs, out_packed=packed, out_scale=scale)
+    out = w4a4_grouped_gemm(packed, wpk, scale, wsc)
+    torch.cuda.synchronize()
+    p_ref, s_ref, o_ref = chain_expected(case)
+    assert np.array_equal(packed.cpu().numpy(), p_ref)
+    assert np.array_equal(bf16_bits(scale), s_ref)
+    assert_bits_equal(bf16_bits(out), o_ref, f"{proj} M=32 chain")
+
+
+@pytest.mark.parametrize("proj", ["o", "qkv", "gate_up", "down"])
+def test_k2_chain_qwen3_shapes_m4096_sampled(proj):
+    case = W.w4a4_case(proj, 4096)
+    M, N, K = case.shape
+    print(f"[chain] {proj} M={M} N={N} K={K} (row sample)", flush=True)
+    x, signs = case.x.to(DEV), case.signs.to(DEV)
+    wpk, wsc = case.w_packed.to(DEV), case.w_scale.to(DEV)
+    packed = torch.empty((M, K // 2), dtype=torch.int8, device=DEV)
+    scale = torch.empty((M, K // 128), dtype=torch.bfloat16, device=DEV)
+    rht_quant_pack(x, signs, out_packed=packed, out_scale=scale)
+    out = w4a4_grouped_gemm(packed, wpk, scale, wsc)
+    torch.cuda.synchronize()
+    rows = np.unique(np.concatenate([np.arange(0, 3), np.linspace(0, M - 1, 21).round().astype(int),
+                                     np.arange(M - 3, M), [127, 128, 129]]))
+    p_ref, s_ref, o_ref = chain_expected(case, rows)
+    assert np.array_equal(packed.cpu().numpy()[rows], p_ref)
+    assert np.array_equal(bf16_bits(scale)[rows], s_ref)
+    assert_bits_equal(bf16_bits(out)[rows], o_ref, f"{proj} M=4096 sampled rows")
