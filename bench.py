@@ -1,0 +1,343 @@
+#!/usr/bin/env python3
+"""Benchmark of the W4A4 quantized-linear hot path on one MI355X.
+
+A step is one decode-sized pass of the W4A4 linear chain of one Qwen3-8B
+decoder layer: for each fused projection (qkv 4096->6144, o 4096->4096,
+gate_up 4096->24576, down 12288->4096) the fused RHT + group-128 INT4
+quantization + packing kernel, then the grouped INT4 GEMM, on M = 32 rows of
+synthetic activations (the reference's operator table, benchmarks/README.md:
+121-133, times exactly this chain at M = 32 and M = 4096).
+
+Timing rules:
+* Every step is a HIP-graph replay (captured once per weight set), so the
+  numbers are GPU time, not Python launch overhead.
+* Steps rotate through ``--rotate`` distinct weight sets (~92 MB each, 6 by
+  default = 550 MB), more than the 256 MB Infinity Cache, so weights stream
+  from HBM as they would across the 36 layers of the model.
+* The dominant kernel (the grouped INT4 GEMM) is also timed on its own: a
+  graph of back-to-back launches over the rotating weight sets, replayed
+  between HIP events on the stream it runs on; its algorithmic bytes
+  (M*K/2 + M*K/64 + N*K/2 + N*K/64 + 2*M*N per launch) over that time give
+  the roofline fraction against the 8 TB/s HBM peak.
+* The CPU baseline is the repository's C oracle (the same chain), timed on
+  this host's cores on a bounded number of steps.
+
+Prints ONE JSON line.  ``--gpus`` above 1 is rejected: this path runs on one
+GPU (rows of M are independent; see the design notes for sharding).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+for _p in (str(ROOT), str(ROOT / "nano-vllm-int4_amd")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+PROJECTIONS = ("qkv", "o", "gate_up", "down")
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, published
+INT8_PEAK_TOPS = 5000.0        # MI355X dense int8 MFMA, published (no sparsity)
+# Published reference numbers (one RTX A6000), full RHT+quant+pack+GEMM chain
+# at M = 32, benchmarks/README.md:126-129, in microseconds.
+PUBLISHED_CHAIN_M32_US = {"qkv": 28.12, "o": 21.87, "gate_up": 86.85, "down": 64.65}
+PUBLISHED_GEMM_M32_US = {"qkv": 21.25, "o": 14.97, "gate_up": 79.86, "down": 46.06}
+PUBLISHED_GEMM_M4096_US = {"qkv": 861.77, "o": 505.62, "gate_up": 3293.68, "down": 1550.64}
+
+
+def k2_bytes(M, N, K):
+    return M * K // 2 + M * K // 64 + N * K // 2 + N * K // 64 + 2 * M * N
+
+
+def k1_bytes(M, K):
+    return 2 * M * K + K + M * K // 2 + M * K // 64
+
+
+def parse_args():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=600)
+    ap.add_argument("--warmup", type=int, default=60)
+    ap.add_argument("--m", type=int, default=32, help="rows per step (decode batch)")
+    ap.add_argument("--rotate", type=int, default=6, help="distinct weight sets cycled through")
+    ap.add_argument("--no-detail", action="store_true", help="skip the per-projection M=32/M=4096 table")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
+    ap.add_argument("--cpu-seconds", type=float, default=15.0, help="target CPU baseline sample length")
+    return ap.parse_args()
+
+
+# ----------------------------------------------------------------- inputs
+def make_layer_sets(torch, W, M, rotate, dev):
+    """Weight sets: set 0 is the seeded CPU workload (shared with the oracle),
+    the others are drawn on the GPU with the same recipe."""
+    acts, sets = {}, []
+    base = {}
+    for p in PROJECTIONS:
+        case = W.w4a4_case(p, M)
+        acts[p] = case.x.to(dev)
+        base[p] = (case.signs.to(dev), case.w_packed.to(dev), case.w_scale.to(dev))
+    sets.append(base)
+    g = torch.Generator(device=dev)
+    g.manual_seed(W.BASE_SEED + 1000)
+    for _ in range(1, rotate):
+        layer = {}
+        for p in PROJECTIONS:
+            N, K = W.PROJECTIONS[p]
+            sg = (torch.randint(0, 2, (K,), generator=g, device=dev, dtype=torch.int8) * 2 - 1)
+            wp = torch.randint(-128, 128, (N, K // 2), generator=g, device=dev, dtype=torch.int16).to(torch.int8)
+            sw = (0.005 + 0.015 * torch.rand(N, K // 128, generator=g, device=dev)).to(torch.bfloat16)
+            layer[p] = (sg.contiguous(), wp.contiguous(), sw.contiguous())
+        sets.append(layer)
+    return acts, sets
+
+
+# ------------------------------------------------------------- graph timing
+def graph_launch_us(torch, launches, replays):
+    """Average microseconds per launch of ``launches`` (callables that each
+    enqueue exactly one kernel on the current stream), captured back to back
+    in one HIP graph and replayed ``replays`` times between two HIP events on
+    the capturing stream.  Inside a graph consecutive kernels start as the
+    previous one ends, so this is kernel time, not host launch time."""
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for fn in launches:
+            fn()
+    torch.cuda.current_stream().wait_stream(side)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for fn in launches:
+            fn()
+    g.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(replays):
+        g.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) * 1e3 / (replays * len(launches))
+    del g
+    return us
+
+
+# ---------------------------------------------------------------- CPU leg
+def cpu_baseline(M, seconds):
+    import numpy as np
+    import torch
+
+    import oracle
+    from nv4 import workloads as W
+
+    threads = min(16, len(os.sched_getaffinity(0)))
+    torch.set_num_threads(threads)
+
+    def bits(t):
+        return t.contiguous().view(torch.int16).numpy().view(np.uint16)
+    cases = []
+    for p in PROJECTIONS:
+        c = W.w4a4_case(p, M)
+        cases.append((bits(c.x), c.signs.numpy(), c.w_packed.numpy(), bits(c.w_scale)))
+
+    def step():
+        for x, s, wp, sw in cases:
+            pk, sc = oracle.rht_quant_pack(x, s, threads=threads)
+            oracle.w4a4_gemm(pk, wp, sc, sw, threads=threads)
+    for _ in range(2):
+        step()
+    times = []
+    t_start = time.perf_counter()
+    while len(times) < 5 or (time.perf_counter() - t_start < seconds and len(times) < 200):
+        t0 = time.perf_counter()
+        step()
+        times.append(time.perf_counter() - t0)
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    med = statistics.median(times)
+    return {
+        "value": round(med * 1e6, 1), "unit": "us/step", "cores": threads, "kind": "port",
+        "sample": (f"{len(times)} steps (after 2 warm-ups) of the oracle's W4A4 chain, M={M}, "
+                   f"qkv/o/gate_up/down, median; {threads} OpenMP threads on {model}"),
+    }
+
+
+# -------------------------------------------------------------------- main
+def main():
+    args = parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: --gpus {args.gpus} is not supported: this hot path runs on one GPU "
+              "(one MI355X per box); rows of M shard across GPUs with no exchange.", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    import nv4
+    from nv4 import workloads as W
+
+    nv4._lib.load()  # raises if the HIP library is missing: there is no fallback
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    M, R = args.m, max(1, args.rotate)
+    acts, sets = make_layer_sets(torch, W, M, R, dev)
+    pk = {p: torch.empty((M, W.PROJECTIONS[p][1] // 2), dtype=torch.int8, device=dev) for p in PROJECTIONS}
+    sc = {p: torch.empty((M, W.PROJECTIONS[p][1] // 128), dtype=torch.bfloat16, device=dev) for p in PROJECTIONS}
+    out = {p: torch.empty((M, W.PROJECTIONS[p][0]), dtype=torch.bfloat16, device=dev) for p in PROJECTIONS}
+
+    def k1(l, p):
+        nv4.rht_quant_pack(acts[p], sets[l][p][0], out_packed=pk[p], out_scale=sc[p])
+
+    def k2(l, p):
+        nv4.w4a4_grouped_gemm(pk[p], sets[l][p][1], sc[p], sets[l][p][2], out=out[p])
+
+    def step(l):
+        for p in PROJECTIONS:
+            k1(l, p)
+            k2(l, p)
+
+    # Eager reference outputs of set 0, then one graph per weight set.
+    step(0)
+    torch.cuda.synchronize()
+    eager = {p: out[p].clone() for p in PROJECTIONS}
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for l in range(R):
+            step(l)
+    torch.cuda.current_stream().wait_stream(side)
+    graphs = []
+    for l in range(R):
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            step(l)
+        graphs.append(g)
+    graphs[0].replay()
+    torch.cuda.synchronize()
+    for p in PROJECTIONS:
+        if not torch.equal(out[p].view(torch.int16), eager[p].view(torch.int16)):
+            raise RuntimeError(f"graph replay of {p} differs from the eager launch")
+
+    for i in range(args.warmup):
+        graphs[i % R].replay()
+    torch.cuda.synchronize()
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    ev0.record()
+    for i in range(args.steps):
+        graphs[i % R].replay()
+    ev1.record()
+    torch.cuda.synchronize()
+    ms_per_step = ev0.elapsed_time(ev1) / args.steps
+    step_us = ms_per_step * 1e3
+
+    # Dominant kernel: the grouped INT4 GEMM, timed per projection over the
+    # rotating weight sets (equal launch counts per projection, so the mean of
+    # the per-projection averages is the kernel's average launch).
+    k2_us = {p: graph_launch_us(torch, [lambda l=l, p=p: k2(l, p) for l in range(R)], replays=40)
+             for p in PROJECTIONS}
+    avg_launch_us = statistics.mean(k2_us.values())
+    avg_bytes = statistics.mean(k2_bytes(M, *W.PROJECTIONS[p]) for p in PROJECTIONS)
+    achieved = avg_bytes / (avg_launch_us * 1e-6) / 1e9       # GB/s
+
+    line = {
+        "metric": "INT4 GEMM us & % roofline at Qwen3-8B shapes; bs32 decode tokens/s",
+        "value": round(step_us, 2),
+        "unit": "us",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": round(step_us / sum(PUBLISHED_CHAIN_M32_US.values()), 4),
+        "vs_baseline_note": ("value / the reference's published M=32 chain time summed over the four "
+                             "projections (201.49 us, RTX A6000, benchmarks/README.md:126-129)"),
+        "dtype": "int8",
+        "data": "synthetic",
+        "config": {
+            "workload": (f"W4A4 linear chain of one Qwen3-8B decoder layer at M={M}: RHT+group-128 "
+                         "INT4 quant+pack then grouped INT4 GEMM for qkv (6144x4096), o (4096x4096), "
+                         "gate_up (24576x4096), down (4096x12288); HIP-graph replays rotating "
+                         f"{R} weight sets ({R * 92} MB) past the 256 MB Infinity Cache"),
+            "M": M, "rotate": R,
+        },
+        "roofline": {
+            "kernel": "k2_skinny (grouped INT4 GEMM, M<=64)",
+            "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+            "avg_launch_us": round(avg_launch_us, 3), "algorithmic_bytes_per_launch": int(avg_bytes),
+            "per_projection_us": {p: round(v, 3) for p, v in k2_us.items()},
+            "timing": (f"HIP events around 40 replays of a graph of {R} back-to-back launches per "
+                       "projection (one per weight set)"),
+        },
+    }
+
+    if not args.no_detail:
+        line["detail"] = detail_table(torch, nv4, W, dev, R)
+    if not args.no_cpu:
+        line["cpu_baseline"] = cpu_baseline(M, args.cpu_seconds)
+        line["cpu_baseline"]["gpu_speedup"] = round(line["cpu_baseline"]["value"] / step_us, 1)
+    print(json.dumps(line), flush=True)
+
+
+def detail_table(torch, nv4, W, dev, R):
+    """Per projection at M = 32 and M = 4096: K1 and K2 microseconds (graph
+    replays of back-to-back launches, weights rotated past the Infinity
+    Cache), their
+    roofline fractions, and the BF16 hipBLASLt GEMM (torch.mm) on the same
+    shape."""
+    res = {}
+    g = torch.Generator(device=dev)
+    g.manual_seed(W.BASE_SEED + 2000)
+    for M in (32, 4096):
+        reps = 20 if M == 32 else 3
+        rot = R if M == 32 else 2
+        for p in PROJECTIONS:
+            N, K = W.PROJECTIONS[p]
+            x = torch.randn(M, K, generator=g, device=dev).to(torch.bfloat16)
+            sg = (torch.randint(0, 2, (K,), generator=g, device=dev, dtype=torch.int8) * 2 - 1)
+            wsets = []
+            for _ in range(rot):
+                wp = torch.randint(-128, 128, (N, K // 2), generator=g, device=dev,
+                                   dtype=torch.int16).to(torch.int8)
+                sw = (0.005 + 0.015 * torch.rand(N, K // 128, generator=g, device=dev)).to(torch.bfloat16)
+                wsets.append((wp, sw))
+            pkb = torch.empty((M, K // 2), dtype=torch.int8, device=dev)
+            scb = torch.empty((M, K // 128), dtype=torch.bfloat16, device=dev)
+            ob = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+            l1 = [lambda: nv4.rht_quant_pack(x, sg, out_packed=pkb, out_scale=scb)] * rot
+            l2 = [lambda w=w: nv4.w4a4_grouped_gemm(pkb, w[0], scb, w[1], out=ob) for w in wsets]
+            us1 = graph_launch_us(torch, l1, reps)
+            us2 = graph_launch_us(torch, l2, reps)
+            del wsets
+            wb = [torch.randn(N, K, generator=g, device=dev).to(torch.bfloat16) for _ in range(2)]
+            ob16 = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+            l3 = [lambda w=w: torch.mm(x, w.t(), out=ob16) for w in wb]
+            us3 = graph_launch_us(torch, l3, reps)
+            del wb
+            entry = {"k1_us": round(us1, 2), "k2_us": round(us2, 2), "chain_us": round(us1 + us2, 2),
+                     "bf16_mm_us": round(us3, 2),
+                     "k1_hbm_frac": round(k1_bytes(M, K) / (us1 * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
+            if M == 32:
+                entry["k2_hbm_frac"] = round(k2_bytes(M, N, K) / (us2 * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)
+                entry["ref_a6000_gemm_us"] = PUBLISHED_GEMM_M32_US[p]
+            else:
+                entry["k2_int8_frac"] = round(2 * M * N * K / (us2 * 1e-6) / 1e12 / INT8_PEAK_TOPS, 4)
+                entry["ref_a6000_gemm_us"] = PUBLISHED_GEMM_M4096_US[p]
+            res[f"M{M}_{p}"] = entry
+            print(f"[detail] M={M} {p}: {entry}", file=sys.stderr, flush=True)
+    return res
+
+
+if __name__ == "__main__":
+    main()

@@ -4,11 +4,16 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 #include "../../include/nv4.h"
 
 namespace nv4 {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
+// Native 16-byte vector: copies are single loads/stores (HIP's uint4 is a
+// struct whose copies become memcpy, which can pin an array in scratch).
+typedef unsigned int v4u __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
 typedef float v4f __attribute__((ext_vector_type(4)));
 typedef float v16f __attribute__((ext_vector_type(16)));
@@ -19,6 +24,16 @@ typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
 constexpr int kWave = 64;
 
 constexpr int ilog2c(int v) { return v <= 1 ? 0 : 1 + ilog2c(v / 2); }
+
+// Calls f(std::integral_constant<int, I>{}) for I = B .. E-1: indices into
+// register arrays stay compile-time constants whatever the unroller decides.
+template <int B, int E, class F>
+__device__ __forceinline__ void static_for(F&& f) {
+    if constexpr (B < E) {
+        f(std::integral_constant<int, B>{});
+        static_for<B + 1, E>(f);
+    }
+}
 
 __device__ __forceinline__ float bf16_to_f32(uint32_t h) { return __uint_as_float(h << 16); }
 

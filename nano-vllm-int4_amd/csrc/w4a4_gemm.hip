@@ -18,11 +18,12 @@
 // the same routine and fed to v_mfma_i32_*_i8 in matching lanes.
 //
 // Two kernels, no split-K, no atomics:
-//  * k2_skinny (M <= 64, decode): one workgroup per 16 output columns, all M
-//    rows.  Its four waves take every fourth K-group, compute exact int32
-//    group dots with v_mfma_i32_16x16x64_i8, and hand them to the whole
-//    workgroup through LDS, which runs the fp32 epilogue in group order.
-//    The weight stream (N*K/2 bytes) dominates, so this kernel is HBM-bound.
+//  * k2_decode (M <= 64): one workgroup per 16 (or 32) output columns and all
+//    M rows.  Its eight waves each take one K-group per sub-round, compute
+//    the exact int32 group dots with v_mfma_i32_16x16x64_i8 and hand them to
+//    the whole workgroup through LDS, which runs the fp32 epilogue in group
+//    order.  Loads run several sub-rounds ahead.  The weight stream
+//    (N*K/2 bytes) dominates, so this kernel is HBM-bound.
 //  * k2_tiled (prefill): 128x128 output tile per workgroup, 2x2 waves of
 //    64x64 (2x2 v_mfma_i32_32x32x32_i8 blocks each), per-group epilogue in
 //    registers with the activation/weight scale tiles staged in LDS.
@@ -30,8 +31,6 @@
 
 namespace nv4 {
 namespace {
-
-__device__ __forceinline__ uint16_t ld_u16(const uint16_t* p) { return *p; }
 
 template <bool OUT_F32>
 __device__ __forceinline__ void store_out(void* out, int64_t idx, float v) {
@@ -43,95 +42,225 @@ __device__ __forceinline__ void store_out(void* out, int64_t idx, float v) {
 }
 
 // ----------------------------------------------------------------------------
-// Skinny kernel.  Output tile: all M (<= 16*MB) rows x 16 columns.
-// MFMA 16x16x64 i8 layout used here (verified by the parity tests):
-//   A operand: lane l supplies row l%16, B operand: lane l supplies column l%16;
-//   the 16 bytes a lane supplies are one "k-slot" set shared by A and B.
-//   Result: lane l holds C[4*(l/16) + i][l%16], i = 0..3.
-// Each lane loads 16 packed bytes (32 k values) per group for its row/column:
-// bytes [16*(l/16), 16*(l/16)+16) of the group's 64 bytes, split over two MFMAs.
+// Decode kernel (M <= 64).  Workgroup = 8 waves, output tile = all M rows
+// (MB blocks of 16) x BN = 16*NB columns, whole K.  Groups are handed out in
+// sub-rounds of 8: in sub-round j wave w computes the exact int32 dots of
+// group 8j+w for the whole tile, the dots go through LDS, and every thread
+// then runs the in-order fp32 epilogue of those 8 groups for the outputs it
+// owns.  Loads run D sub-rounds ahead of use in a register ring; for
+// K = 4096 every byte the workgroup needs is requested before the first MFMA.
+//
+// Weights go straight from the ring into MFMA operands: lane l loads 16 bytes
+// of column l%16 (a quarter of the group's 64 bytes).  The activation slice
+// of a sub-round (all rows x 512 bytes) is shared by the eight waves, so it
+// is loaded cooperatively in whole 128-byte lines (8 lanes per line), staged
+// in LDS one sub-round ahead and read back as MFMA operands: half-line
+// per-lane loads would double the L1 misses of the activation re-reads, which
+// every workgroup of the launch makes.
+//
+// MFMA 16x16x64 i8 layout used here (checked by the parity tests):
+//   A operand: lane l supplies row l%16, B operand: lane l supplies column
+//   l%16; both take the same 16 k-slots (set l/16), so identical unpacking
+//   pairs every k.  Result: lane l holds C[4*(l/16) + i][l%16], i = 0..3.
+// LDS activation slice: row r at r*512 bytes, its 16-byte chunk c stored at
+// chunk (c & ~7) | ((c ^ r) & 7), so the 16 rows of one operand load fall in
+// distinct bank groups.
+//
+// Every global load is unconditional (indices clamped into range): a load
+// under a thread-dependent branch makes the compiler drain all outstanding
+// loads at the branch join, which would serialise the ring.
 // ----------------------------------------------------------------------------
-template <int MB, bool SW_GROUPED, bool OUT_F32>
-__global__ void __launch_bounds__(256)
-k2_skinny(const int8_t* __restrict__ a, const int8_t* __restrict__ w,
+constexpr int DEC_WAVES = 8;
+constexpr int DEC_THREADS = DEC_WAVES * 64;
+
+template <int MB, int NB, int D, bool SW_GROUPED, bool OUT_F32>
+__global__ void __launch_bounds__(DEC_THREADS)
+k2_decode(const int8_t* __restrict__ a, const int8_t* __restrict__ w,
           const uint16_t* __restrict__ sa, const uint16_t* __restrict__ sw,
           void* __restrict__ out, int M, int N, int K) {
-    const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
-    const int n0 = blockIdx.x * 16;
-    const int G = K >> 7;
-    const int64_t KB = K >> 1;  // packed bytes per row
-    // dots[buffer][group slot][m-block][lane*4 + i]
-    __shared__ int dots[2][4][MB][256];
+    constexpr int BN = 16 * NB, NBLK = MB * NB, ROWS = MB * 16;
+    constexpr int OPT = (NBLK * 256 + DEC_THREADS - 1) / DEC_THREADS;  // outputs per thread
+    constexpr int N_SA = ROWS * 8;                                      // scale entries per sub-round
+    constexpr int N_SW = SW_GROUPED ? BN * 8 : 0;
+    constexpr int SPT = (N_SA + N_SW + DEC_THREADS - 1) / DEC_THREADS;  // scale entries per thread
+    constexpr int APT = ROWS * 32 / DEC_THREADS;                        // activation chunks per thread (= MB)
+    __shared__ __align__(16) uint8_t a_l[2][ROWS * 512];
+    __shared__ int16_t dots[2][8][NBLK][256];
+    __shared__ float sal[2][8][ROWS];
+    __shared__ float swl[2][8][BN];
+    __shared__ float ssink[1];
 
-    const int rc = lane & 15;   // row (A) / column (W) within the 16-block
-    const int part = lane >> 4; // which 16-byte quarter of the group's 64 bytes
-    const int ncol = min(n0 + rc, N - 1);
-    const int8_t* __restrict__ wp = w + (int64_t)ncol * KB + part * 16;
-    const int8_t* ap[MB];
+    const int t = threadIdx.x;
+    const int lane = t & 63, wave = t >> 6;
+    const int n0 = blockIdx.x * BN;
+    const int G = K >> 7;
+    const int S = (G + 7) >> 3;  // sub-rounds
+    const int KB = K >> 1;       // packed bytes per row
+
+    const int rc = lane & 15, part = lane >> 4;
+    const int8_t* wp[NB];
 #pragma unroll
-    for (int mb = 0; mb < MB; ++mb) {
-        const int r = min(mb * 16 + rc, M - 1);
-        ap[mb] = a + (int64_t)r * KB + part * 16;
+    for (int nb = 0; nb < NB; ++nb)
+        wp[nb] = w + (int64_t)min(n0 + nb * 16 + rc, N - 1) * KB + part * 16;
+
+    // Activation staging: thread t moves chunks q = t + 512 i (row q/32,
+    // chunk q%32 of the row's 512-byte slice).
+    const int8_t* arow[APT];
+    int a_c16[APT], a_dst[APT];
+#pragma unroll
+    for (int i = 0; i < APT; ++i) {
+        const int q = t + i * DEC_THREADS;
+        const int r = q >> 5, c = q & 31;
+        arow[i] = a + (int64_t)min(r, M - 1) * KB;
+        a_c16[i] = c * 16;
+        a_dst[i] = r * 512 + (((c & ~7) | ((c ^ r) & 7)) << 4);
+    }
+    // Start of the 512-byte slice staged for sub-round j: 512 j, moved back
+    // so that it ends at the row end when the last sub-round is partial.
+    auto slice_start = [&](int j) { return max(0, min(j * 512, KB - 512)); };
+
+    // Scale staging: entry e < N_SA is sa[row = e/8][8j + e%8], then sw.
+    const uint16_t* sp[SPT];
+    float* sdst[SPT];
+    int sgl[SPT], sstride[SPT];
+#pragma unroll
+    for (int q = 0; q < SPT; ++q) {
+        const int e = t + q * DEC_THREADS;
+        sgl[q] = e & 7;
+        if (e < N_SA) {
+            const int row = e >> 3;
+            sp[q] = sa + (int64_t)min(row, M - 1) * G;
+            sdst[q] = &sal[0][sgl[q]][row];
+            sstride[q] = 8 * ROWS;
+        } else if (e < N_SA + N_SW) {
+            const int col = (e - N_SA) >> 3;
+            sp[q] = sw + (int64_t)min(n0 + col, N - 1) * G;
+            sdst[q] = &swl[0][sgl[q]][col];
+            sstride[q] = 8 * BN;
+        } else {  // nothing to stage: load a valid scale, store to the sink
+            sp[q] = sa;
+            sdst[q] = ssink;
+            sstride[q] = 0;
+        }
     }
 
-    // Epilogue ownership: entry e = threadIdx.x of every m-block.
-    const int e_lane = threadIdx.x >> 2, e_i = threadIdx.x & 3;
-    const int e_col = e_lane & 15;
-    const int e_row0 = 4 * (e_lane >> 4) + e_i;
-    const int on = n0 + e_col;
-    float total[MB];
-#pragma unroll
-    for (int mb = 0; mb < MB; ++mb) total[mb] = 0.0f;
+    v4u rw[D][NB], ra[D][APT];
+    uint16_t rs[D][SPT];
 
-    const int rounds = (G + 3) >> 2;
-    for (int rd = 0; rd < rounds; ++rd) {
-        const int g = rd * 4 + wave;
-        const int buf = rd & 1;
-        if (g < G) {
-            const uint4 wv = *reinterpret_cast<const uint4*>(wp + (int64_t)g * 64);
-            const v4i w0 = unpack8_x16(wv.x, wv.y);
-            const v4i w1 = unpack8_x16(wv.z, wv.w);
+    auto issue = [&](int j, v4u (&w_out)[NB], v4u (&a_out)[APT], uint16_t (&s_out)[SPT]) {
+        const int64_t g = min(j * 8 + wave, G - 1);
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) w_out[nb] = *reinterpret_cast<const v4u*>(wp[nb] + g * 64);
+        const int aoff = slice_start(min(j, S - 1));
+#pragma unroll
+        for (int i = 0; i < APT; ++i)
+            a_out[i] = *reinterpret_cast<const v4u*>(arow[i] + min(aoff + a_c16[i], KB - 16));
+#pragma unroll
+        for (int q = 0; q < SPT; ++q) s_out[q] = sp[q][min(j * 8 + sgl[q], G - 1)];
+    };
+    auto stage_a = [&](int j, const v4u (&a_in)[APT]) {
+#pragma unroll
+        for (int i = 0; i < APT; ++i) *reinterpret_cast<v4u*>(&a_l[j & 1][a_dst[i]]) = a_in[i];
+    };
+
+    float total[OPT];
+#pragma unroll
+    for (int oi = 0; oi < OPT; ++oi) total[oi] = 0.0f;
+
+    auto consume = [&](int j, const v4u (&w_in)[NB], const v4u (&a_next)[APT], const uint16_t (&s_in)[SPT]) {
+        const int buf = j & 1;
+        const int g = j * 8 + wave;
+        if (g < G) {  // uniform over the wave
+            // Chunk of this group inside the staged slice.
+            const int shift = j * 512 - slice_start(j);  // bytes the slice was moved back
+            const int cbase = (wave * 64 + shift) >> 4;
+            v4i w0[NB], w1[NB];
+#pragma unroll
+            for (int nb = 0; nb < NB; ++nb) {
+                w0[nb] = unpack8_x16(w_in[nb][0], w_in[nb][1]);
+                w1[nb] = unpack8_x16(w_in[nb][2], w_in[nb][3]);
+            }
 #pragma unroll
             for (int mb = 0; mb < MB; ++mb) {
-                const uint4 av = *reinterpret_cast<const uint4*>(ap[mb] + (int64_t)g * 64);
-                v4i acc = {0, 0, 0, 0};
-                acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(unpack8_x16(av.x, av.y), w0, acc, 0, 0, 0);
-                acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(unpack8_x16(av.z, av.w), w1, acc, 0, 0, 0);
-                int4 d;
-                d.x = acc[0] >> 8; d.y = acc[1] >> 8; d.z = acc[2] >> 8; d.w = acc[3] >> 8;
-                *reinterpret_cast<int4*>(&dots[buf][wave][mb][lane * 4]) = d;
+                const int r = mb * 16 + rc;
+                const int c = cbase + part;
+                const v4u av = *reinterpret_cast<const v4u*>(
+                    &a_l[buf][r * 512 + (((c & ~7) | ((c ^ r) & 7)) << 4)]);
+                const v4i a0 = unpack8_x16(av[0], av[1]);
+                const v4i a1 = unpack8_x16(av[2], av[3]);
+#pragma unroll
+                for (int nb = 0; nb < NB; ++nb) {
+                    v4i acc = {0, 0, 0, 0};
+                    acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, w0[nb], acc, 0, 0, 0);
+                    acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, w1[nb], acc, 0, 0, 0);
+                    // 256 * dot -> dot (exact); |dot| <= 8192 fits int16.
+                    const uint32_t lo = ((uint32_t)(acc[0] >> 8) & 0xffffu) | ((uint32_t)(acc[1] >> 8) << 16);
+                    const uint32_t hi = ((uint32_t)(acc[2] >> 8) & 0xffffu) | ((uint32_t)(acc[3] >> 8) << 16);
+                    *reinterpret_cast<uint2*>(&dots[buf][wave][mb * NB + nb][lane * 4]) = make_uint2(lo, hi);
+                }
             }
         }
+#pragma unroll
+        for (int q = 0; q < SPT; ++q) sdst[q][buf * sstride[q]] = bf16_to_f32(s_in[q]);
+        if (j + 1 < S) stage_a(j + 1, a_next);  // uniform
         __syncthreads();
+        const int ng = min(8, G - j * 8);  // groups in this sub-round
 #pragma unroll
-        for (int gi = 0; gi < 4; ++gi) {
-            const int gg = rd * 4 + gi;
-            if (gg < G) {
+        for (int oi = 0; oi < OPT; ++oi) {
+            const int o = t + oi * DEC_THREADS;
+            if (o < NBLK * 256) {
+                const int row = o / BN, col = o % BN;
+                const int blk = (row >> 4) * NB + (col >> 4);
+                const int e = ((((row & 15) >> 2) * 16 + (col & 15)) << 2) + (row & 3);
+                if (ng == 8) {
+                    float d[8], s[8];
 #pragma unroll
-                for (int mb = 0; mb < MB; ++mb) {
-                    const int om = mb * 16 + e_row0;
-                    const int omc = min(om, M - 1);
-                    const float d = (float)dots[buf][gi][mb][threadIdx.x];
-                    const float s_a = bf16_to_f32(ld_u16(sa + (int64_t)omc * G + gg));
-                    if constexpr (SW_GROUPED) {
-                        const float s_w = bf16_to_f32(ld_u16(sw + (int64_t)min(on, N - 1) * G + gg));
-                        const float s = s_a * s_w;
-                        total[mb] = __builtin_fmaf(d, s, total[mb]);
-                    } else {
-                        total[mb] = __builtin_fmaf(d, s_a, total[mb]);
+                    for (int gl = 0; gl < 8; ++gl) {
+                        d[gl] = (float)dots[buf][gl][blk][e];
+                        s[gl] = SW_GROUPED ? sal[buf][gl][row] * swl[buf][gl][col] : sal[buf][gl][row];
+                    }
+#pragma unroll
+                    for (int gl = 0; gl < 8; ++gl) total[oi] = __builtin_fmaf(d[gl], s[gl], total[oi]);
+                } else {
+                    for (int gl = 0; gl < ng; ++gl) {
+                        const float d = (float)dots[buf][gl][blk][e];
+                        const float s = SW_GROUPED ? sal[buf][gl][row] * swl[buf][gl][col] : sal[buf][gl][row];
+                        total[oi] = __builtin_fmaf(d, s, total[oi]);
                     }
                 }
             }
         }
+    };
+
+    static_for<0, D>([&](auto U) { issue(U, rw[U], ra[U], rs[U]); });
+    stage_a(0, ra[0]);
+    __syncthreads();
+
+    // Steady state: consume a slot, refill it D sub-rounds ahead.  The
+    // activation slice of sub-round j+1 (slot u+1) is staged during j.
+    int j0 = 0;
+    for (; j0 + D < S; j0 += D) {
+        static_for<0, D>([&](auto U) {
+            constexpr int u = U, un = (u + 1) % D;
+            consume(j0 + u, rw[u], ra[un], rs[u]);
+            issue(j0 + u + D, rw[u], ra[u], rs[u]);
+        });
     }
+    // Tail: the last (at most D) sub-rounds are already in flight.
+    static_for<0, D>([&](auto U) {
+        constexpr int u = U, un = (u + 1) % D;
+        if (j0 + u < S) consume(j0 + u, rw[u], ra[un], rs[u]);
+    });
+
 #pragma unroll
-    for (int mb = 0; mb < MB; ++mb) {
-        const int om = mb * 16 + e_row0;
-        if (om < M && on < N) {
-            float v = total[mb];
-            if constexpr (!SW_GROUPED) v = v * bf16_to_f32(ld_u16(sw + on));
-            store_out<OUT_F32>(out, (int64_t)om * N + on, v);
+    for (int oi = 0; oi < OPT; ++oi) {
+        const int o = t + oi * DEC_THREADS;
+        const int row = o / BN, col = o % BN;
+        const int n = n0 + col;
+        if (o < NBLK * 256 && row < M && n < N) {
+            float v = total[oi];
+            if constexpr (!SW_GROUPED) v = v * bf16_to_f32(sw[n]);
+            store_out<OUT_F32>(out, (int64_t)row * N + n, v);
         }
     }
 }
@@ -270,11 +399,17 @@ k2_tiled(const int8_t* __restrict__ a, const int8_t* __restrict__ w,
     }
 }
 
-template <int MB, bool SG, bool OF>
-hipError_t launch_skinny(const int8_t* a, const int8_t* w, const void* sa, const void* sw, void* out,
+template <int MB, int NB, bool SG, bool OF>
+hipError_t launch_decode(const int8_t* a, const int8_t* w, const void* sa, const void* sw, void* out,
                          int M, int N, int K, hipStream_t st) {
-    hipLaunchKernelGGL((k2_skinny<MB, SG, OF>), dim3((unsigned)((N + 15) / 16)), dim3(256), 0, st, a, w,
-                       static_cast<const uint16_t*>(sa), static_cast<const uint16_t*>(sw), out, M, N, K);
+    // Sub-rounds in flight: all of them for K <= 4096, six beyond.
+    const dim3 grid((unsigned)((N + 16 * NB - 1) / (16 * NB)));
+    const uint16_t* sap = static_cast<const uint16_t*>(sa);
+    const uint16_t* swp = static_cast<const uint16_t*>(sw);
+    if (K <= 4096)
+        hipLaunchKernelGGL((k2_decode<MB, NB, 4, SG, OF>), grid, dim3(DEC_THREADS), 0, st, a, w, sap, swp, out, M, N, K);
+    else
+        hipLaunchKernelGGL((k2_decode<MB, NB, 6, SG, OF>), grid, dim3(DEC_THREADS), 0, st, a, w, sap, swp, out, M, N, K);
     return hipGetLastError();
 }
 
@@ -292,10 +427,15 @@ hipError_t launch_tiled(const int8_t* a, const int8_t* w, const void* sa, const 
 template <bool SG, bool OF>
 hipError_t dispatch(const int8_t* a, const int8_t* w, const void* sa, const void* sw, void* out,
                     int M, int N, int K, hipStream_t st) {
-    if (M <= 16) return launch_skinny<1, SG, OF>(a, w, sa, sw, out, M, N, K, st);
-    if (M <= 32) return launch_skinny<2, SG, OF>(a, w, sa, sw, out, M, N, K, st);
-    if (M <= 48) return launch_skinny<3, SG, OF>(a, w, sa, sw, out, M, N, K, st);
-    if (M <= 64) return launch_skinny<4, SG, OF>(a, w, sa, sw, out, M, N, K, st);
+    // Wide N: 32 columns per workgroup halves the activation re-reads while
+    // still giving every CU several workgroups.
+    const bool wide = N >= 16384;
+    if (M <= 16) return wide ? launch_decode<1, 2, SG, OF>(a, w, sa, sw, out, M, N, K, st)
+                             : launch_decode<1, 1, SG, OF>(a, w, sa, sw, out, M, N, K, st);
+    if (M <= 32) return wide ? launch_decode<2, 2, SG, OF>(a, w, sa, sw, out, M, N, K, st)
+                             : launch_decode<2, 1, SG, OF>(a, w, sa, sw, out, M, N, K, st);
+    if (M <= 48) return launch_decode<3, 1, SG, OF>(a, w, sa, sw, out, M, N, K, st);
+    if (M <= 64) return launch_decode<4, 1, SG, OF>(a, w, sa, sw, out, M, N, K, st);
     return launch_tiled<SG, OF>(a, w, sa, sw, out, M, N, K, st);
 }
 

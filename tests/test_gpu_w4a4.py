@@ -112,6 +112,17 @@ def test_k2_m_sweep(M):
     run_case(M, 264, 256, 2000 + M, grouped=False)
 
 
+@pytest.mark.parametrize("M,N,K", [(1, 4104, 4096), (16, 4104, 4096), (17, 4104, 4096), (32, 4104, 4096),
+                                   (33, 4104, 4096), (48, 264, 4096), (8, 520, 12288), (16, 264, 8192)])
+def test_k2_decode_activations_in_lds(M, N, K):
+    """Shapes served by the persistent decode kernel that keeps the packed
+    activations in LDS: every M block, a column tail, more 16-column tiles
+    than compute units (a workgroup walks several tiles), K = 8192 and 12288."""
+    run_case(M, N, K, 3000 + M + K)
+    if M in (17, 48):
+        run_case(M, N, K, 4000 + M + K, grouped=False)
+
+
 def chain_expected(case, rows=None):
     xb = bf16_bits(case.x)
     if rows is not None:
