@@ -68,6 +68,9 @@ def parse_args():
     ap.add_argument("--no-detail", action="store_true", help="skip the per-projection M=32/M=4096 table")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
     ap.add_argument("--cpu-seconds", type=float, default=15.0, help="target CPU baseline sample length")
+    ap.add_argument("--pmc-pass", action="store_true",
+                    help="for rocprofv3 --pmc: eager decode GEMM launches (3 rounds over the rotating sets) "
+                         "and three plain 256 MiB device copies as the counter calibration, then exit")
     return ap.parse_args()
 
 
@@ -124,6 +127,41 @@ def graph_launch_us(torch, launches, replays):
     us = e0.elapsed_time(e1) * 1e3 / (replays * len(launches))
     del g
     return us
+
+
+# ------------------------------------------------------------ counter pass
+COPY_BYTES = 256 << 20
+
+
+def pmc_pass(torch, k1, k2, R):
+    """Kernels for a hardware-counter run: K1 + K2 of every projection and
+    weight set, three rounds, then three device-to-device copies of exactly
+    COPY_BYTES (read COPY_BYTES, write COPY_BYTES) to scale FETCH_SIZE and
+    WRITE_SIZE into bytes."""
+    for _ in range(3):
+        for l in range(R):
+            for p in PROJECTIONS:
+                k1(l, p)
+                k2(l, p)
+    src = torch.empty(COPY_BYTES, dtype=torch.uint8, device="cuda:0")
+    dst = torch.empty_like(src)
+    src.fill_(1)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(f"pmc pass done: {3 * R * len(PROJECTIONS)} K2 launches, 3 copies of {COPY_BYTES} bytes", flush=True)
+
+
+def measured_traffic():
+    """HBM bytes per decode-GEMM launch from the committed counter summary
+    (two rocprofv3 --pmc passes, FETCH_SIZE and WRITE_SIZE, scaled by the
+    copy calibration), or None when the summary is absent."""
+    path = ROOT / "profiles" / "k2_decode_m32_traffic.json"
+    try:
+        with open(path) as f:
+            return json.load(f)
+    except (OSError, ValueError):
+        return None
 
 
 # ---------------------------------------------------------------- CPU leg
@@ -206,6 +244,10 @@ def main():
             k1(l, p)
             k2(l, p)
 
+    if args.pmc_pass:
+        pmc_pass(torch, k1, k2, R)
+        return
+
     # Eager reference outputs of set 0, then one graph per weight set.
     step(0)
     torch.cuda.synchronize()
@@ -249,6 +291,7 @@ def main():
     avg_bytes = statistics.mean(k2_bytes(M, *W.PROJECTIONS[p]) for p in PROJECTIONS)
     achieved = avg_bytes / (avg_launch_us * 1e-6) / 1e9       # GB/s
 
+    traffic = measured_traffic()
     line = {
         "metric": "INT4 GEMM us & % roofline at Qwen3-8B shapes; bs32 decode tokens/s",
         "value": round(step_us, 2),
@@ -272,9 +315,11 @@ def main():
             "M": M, "rotate": R,
         },
         "roofline": {
-            "kernel": "k2_skinny (grouped INT4 GEMM, M<=64)",
+            "kernel": "k2_decode (grouped INT4 GEMM, M<=64)",
             "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": (traffic or {}).get("bytes_per_launch"),
+            "traffic_source": (traffic or {}).get("source"),
             "avg_launch_us": round(avg_launch_us, 3), "algorithmic_bytes_per_launch": int(avg_bytes),
             "per_projection_us": {p: round(v, 3) for p, v in k2_us.items()},
             "timing": (f"HIP events around 40 replays of a graph of {R} back-to-back launches per "

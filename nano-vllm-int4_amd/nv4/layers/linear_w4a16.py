@@ -12,6 +12,23 @@ from torch import nn
 from ..kernels.w4a16 import dequant_matmul_w4a16
 
 
+def tl_dequant_matmul_w4a16(A, B, C, scales, qzeros, BLOCK_M, BLOCK_N, BLOCK_K, SPLIT_K, group_size):
+    """Same call as the reference kernel (linear_w4a16.py:11-59): ``C += A @ deq(B)``.
+
+    The reference accumulates split-K partials into ``C`` with bf16 atomics and is
+    only called with a zeroed ``C`` (linear_w4a16.py:132-146); here the whole-K
+    product is computed once and added to ``C``.  The tile and split arguments
+    are accepted for compatibility and do not change the result.
+    """
+    for v in (BLOCK_M, BLOCK_N, BLOCK_K, SPLIT_K):
+        if int(v) < 1:
+            raise ValueError("tile and split sizes must be positive")
+    if C.dtype != torch.bfloat16 or tuple(C.shape) != (A.shape[0], B.shape[1]):
+        raise ValueError("C must be BF16 [M, N]")
+    C.add_(dequant_matmul_w4a16(A, B, qzeros, scales, group_size))
+    return C
+
+
 class W4A16Linear(nn.Module):
 
     def __init__(self, in_features, out_features, group_size=128):

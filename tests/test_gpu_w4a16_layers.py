@@ -80,6 +80,21 @@ def test_w4a16_linear_module():
     check_close(y.view(6, 6144), ref)
 
 
+def test_tl_dequant_matmul_w4a16_reference_call():
+    """The reference's call (linear_w4a16.py:138-146): zeroed C, tiles 16/64/32,
+    split 8; C += A @ deq(B).  A second call adds the product again."""
+    from nv4.layers import tl_dequant_matmul_w4a16
+    case = W.w4a16_case(5, N=512, K=1024, dtype=torch.bfloat16)
+    x, qw, qz, sc = (t.to(DEV) for t in (case.x, case.qweight, case.qzeros, case.scales))
+    C = torch.zeros((5, 512), device=DEV, dtype=torch.bfloat16)
+    assert tl_dequant_matmul_w4a16(x, qw, C, sc, qz, 16, 64, 32, 8, 128) is C
+    torch.cuda.synchronize()
+    direct = dequant_matmul_w4a16(x, qw, qz, sc)
+    assert torch.equal(C, direct)
+    tl_dequant_matmul_w4a16(x, qw, C, sc, qz, 16, 64, 32, 8, 128)
+    assert torch.equal(C, (direct.float() + direct.float()).to(torch.bfloat16))
+
+
 def load_w4a4(mod, case):
     with torch.no_grad():
         mod.packed_weight.copy_(case.w_packed)
