@@ -266,6 +266,158 @@ k2_decode(const int8_t* __restrict__ a, const int8_t* __restrict__ w,
 }
 
 // ----------------------------------------------------------------------------
+// Wide decode kernel (M <= 32, large N: gate_up).  Each wave owns one 16-row
+// block and 16 output columns over the whole K: it streams its weight
+// columns group by group through a register ring D groups deep and keeps its
+// running totals in registers, so the main loop has no barrier and no LDS
+// exchange.  The two row blocks of a column block are separate waves (the
+// second wave's weight loads hit the lines the first one brought into the
+// CU), which doubles the waves per SIMD that hide each other's MFMA and LDS
+// latencies.  The workgroup (CBW column blocks, one workgroup per CU for
+// gate_up) first copies into LDS the activation block, already widened to
+// MFMA int8 operands (16*q per byte), and the activation and weight scales
+// as fp32: every CU fetches and unpacks the activations once instead of once
+// per 16-column tile and group, and the main loop issues weight loads only.
+//
+// LDS activation layout: row r holds K int8 operands (K bytes) as 16-byte
+// units; unit u of a row (packed chunk c = u/2 widened: half u%2) is stored
+// at unit (u & ~7) | ((u ^ r) & 7), so the 16 rows read by one operand load
+// (same unit, rows r..r+15) fall in distinct bank groups.
+//
+// Per group g the wave does: two operand loads from LDS, 2
+// v_mfma_i32_16x16x64_i8, and for each of its 4 outputs (rows 4*(l/16)+i of
+// its block, column l%16) total = fmaf(float(dot), sa*sw, total).
+// ----------------------------------------------------------------------------
+constexpr int WIDE_A_BYTES = 128 * 1024;  // widened activation block limit (M x K bytes)
+constexpr int WIDE_SCALES = 1024;         // G * ROWS limit
+constexpr int WIDE_WSCALES = 3072;        // G * CBW * 16 limit
+
+template <int MB, int CBW, int D, bool SW_GROUPED, bool OUT_F32>
+__global__ void __launch_bounds__(CBW * MB * 64)
+k2_wide(const int8_t* __restrict__ a, const int8_t* __restrict__ w,
+        const uint16_t* __restrict__ sa, const uint16_t* __restrict__ sw,
+        void* __restrict__ out, int M, int N, int K) {
+    constexpr int T = CBW * MB * 64, ROWS = MB * 16, COLS = CBW * 16;
+    constexpr int AC = (WIDE_A_BYTES / 32 + T - 1) / T;  // packed 16-byte chunks per thread (upper bound)
+    constexpr int SC = (WIDE_SCALES + T - 1) / T;
+    constexpr int WC = SW_GROUPED ? (WIDE_WSCALES + T - 1) / T : 0;
+    __shared__ __align__(16) uint8_t a_l[WIDE_A_BYTES + 32];  // + sink
+    __shared__ __align__(16) float sa_l[WIDE_SCALES + 4];     // [g][row] + sink
+    __shared__ float sw_l[WIDE_WSCALES + 1];                  // [g][col] + sink
+
+    const int t = threadIdx.x;
+    const int lane = t & 63, wave = t >> 6;
+    const int cbl = wave / MB, mb = wave % MB;  // local column block, row block
+    const int G = K >> 7;
+    const int KB = K >> 1;
+    const int chunks_row = KB >> 4;             // packed 16-byte chunks per row
+    const int a_chunks = ROWS * chunks_row;
+    const int rc = lane & 15, part = lane >> 4;
+    const int col0 = blockIdx.x * COLS;
+    const int col = col0 + cbl * 16 + rc;
+    const int8_t* wp = w + (int64_t)min(col, N - 1) * KB + part * 16;
+
+    // ---- activation block + scales: loads first, then the weight ring.
+    v4u ra[AC];
+    uint16_t rsa[SC], rsw[WC > 0 ? WC : 1];
+#pragma unroll
+    for (int i = 0; i < AC; ++i) {
+        const int q = min(t + i * T, a_chunks - 1);
+        const int r = q / chunks_row, c = q - r * chunks_row;
+        ra[i] = *reinterpret_cast<const v4u*>(a + (int64_t)min(r, M - 1) * KB + c * 16);
+    }
+#pragma unroll
+    for (int i = 0; i < SC; ++i) {
+        const int e = min(t + i * T, G * ROWS - 1);  // e = row * G + g
+        rsa[i] = sa[(int64_t)min(e / G, M - 1) * G + e % G];
+    }
+#pragma unroll
+    for (int i = 0; i < WC; ++i) {
+        const int e = min(t + i * T, G * COLS - 1);  // e = col * G + g
+        rsw[i] = sw[(int64_t)min(col0 + e / G, N - 1) * G + e % G];
+    }
+    v4u rw[D];
+    auto issue = [&](int g, v4u& w_out) {
+        w_out = *reinterpret_cast<const v4u*>(wp + (int64_t)min(g, G - 1) * 64);
+    };
+    static_for<0, D>([&](auto U) { issue(U, rw[U]); });
+    // Widen and store: packed chunk c of row r -> units 2c, 2c+1.
+#pragma unroll
+    for (int i = 0; i < AC; ++i) {
+        const int q = t + i * T;
+        const int r = q / chunks_row, c = q - r * chunks_row;
+        const bool live = q < a_chunks;
+        const int u0 = 2 * c, u1 = 2 * c + 1;
+        const int s0 = (u0 & ~7) | ((u0 ^ r) & 7), s1 = (u1 & ~7) | ((u1 ^ r) & 7);
+        const v4i lo = unpack8_x16(ra[i][0], ra[i][1]);
+        const v4i hi = unpack8_x16(ra[i][2], ra[i][3]);
+        *reinterpret_cast<v4i*>(&a_l[live ? r * K + s0 * 16 : WIDE_A_BYTES]) = lo;
+        *reinterpret_cast<v4i*>(&a_l[live ? r * K + s1 * 16 : WIDE_A_BYTES + 16]) = hi;
+    }
+#pragma unroll
+    for (int i = 0; i < SC; ++i) {
+        const int e = t + i * T;
+        const int ec = min(e, G * ROWS - 1);
+        sa_l[e < G * ROWS ? (ec % G) * ROWS + ec / G : WIDE_SCALES] = bf16_to_f32(rsa[i]);
+    }
+#pragma unroll
+    for (int i = 0; i < WC; ++i) {
+        const int e = t + i * T;
+        const int ec = min(e, G * COLS - 1);
+        sw_l[e < G * COLS ? (ec % G) * COLS + ec / G : WIDE_WSCALES] = bf16_to_f32(rsw[i]);
+    }
+    __syncthreads();
+
+    float total[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    const int r = mb * 16 + rc;
+    const float* sap = &sa_l[mb * 16 + 4 * part];
+    const float* swq = &sw_l[cbl * 16 + rc];
+
+    auto consume = [&](int g, const v4u& w_in) {
+        const v4i w0 = unpack8_x16(w_in[0], w_in[1]);
+        const v4i w1 = unpack8_x16(w_in[2], w_in[3]);
+        const int u0 = (g * 4 + part) * 2, u1 = u0 + 1;
+        const v4i a0 = *reinterpret_cast<const v4i*>(&a_l[r * K + (((u0 & ~7) | ((u0 ^ r) & 7)) << 4)]);
+        const v4i a1 = *reinterpret_cast<const v4i*>(&a_l[r * K + (((u1 & ~7) | ((u1 ^ r) & 7)) << 4)]);
+        const v4f s_a = *reinterpret_cast<const v4f*>(sap + g * ROWS);
+        const float s_w = SW_GROUPED ? swq[g * COLS] : 1.0f;
+        v4i acc = {0, 0, 0, 0};
+        acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, w0, acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, w1, acc, 0, 0, 0);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float d = (float)(acc[i] >> 8);
+            total[i] = SW_GROUPED ? __builtin_fmaf(d, s_a[i] * s_w, total[i]) : __builtin_fmaf(d, s_a[i], total[i]);
+        }
+    };
+
+    int g0 = 0;
+    for (; g0 + D < G; g0 += D) {
+        static_for<0, D>([&](auto U) {
+            consume(g0 + U, rw[U]);
+            issue(g0 + U + D, rw[U]);
+        });
+    }
+    static_for<0, D>([&](auto U) {
+        if (g0 + U < G) consume(g0 + U, rw[U]);
+    });
+
+    if (col < N) {
+        float swn = 1.0f;
+        if constexpr (!SW_GROUPED) swn = bf16_to_f32(sw[col]);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int row = mb * 16 + 4 * part + i;
+            if (row < M) {
+                float v = total[i];
+                if constexpr (!SW_GROUPED) v = v * swn;
+                store_out<OUT_F32>(out, (int64_t)row * N + col, v);
+            }
+        }
+    }
+}
+
+// ----------------------------------------------------------------------------
 // Tiled kernel.  Workgroup tile 128 (M) x 128 (N); wave (wm, wn) owns rows
 // 64*wm.., columns 64*wn..; 2x2 blocks of 32x32.
 // MFMA 32x32x32 i8 layout: lane l supplies row (A) / column (W) l%32 and the
@@ -413,6 +565,49 @@ hipError_t launch_decode(const int8_t* a, const int8_t* w, const void* sa, const
     return hipGetLastError();
 }
 
+// Compute units of the current device (cached per device).
+int cu_count() {
+    static int cache[64];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0) dev = 0;
+    if (dev < 64 && cache[dev] > 0) return cache[dev];
+    int v = 0;
+    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v <= 0) v = 256;
+    if (dev < 64) cache[dev] = v;
+    return v;
+}
+
+// The wide kernel needs the widened activation block and the scales to fit
+// in LDS, whole 8-chunk lines per row (swizzle), and at least 4 column blocks
+// per CU.
+bool wide_fits(int M, int N, int K) {
+    const int mb = (M + 15) / 16;
+    const int per_cu = ((N + 15) / 16 + cu_count() - 1) / cu_count();
+    return M <= 32 && K % 256 == 0 && (int64_t)mb * 16 * K <= WIDE_A_BYTES &&
+           (int64_t)(K / 128) * mb * 16 <= WIDE_SCALES && per_cu >= 4 && per_cu <= 8 &&
+           (int64_t)(K / 128) * 16 * (per_cu <= 4 ? 4 : per_cu <= 6 ? 6 : 8) <= WIDE_WSCALES;
+}
+
+template <int MB, int CBW, bool SG, bool OF>
+hipError_t launch_wide_cbw(const int8_t* a, const int8_t* w, const void* sa, const void* sw, void* out,
+                           int M, int N, int K, hipStream_t st) {
+    constexpr int D = 8;  // groups in flight per wave
+    const int ncb = (N + 15) / 16;
+    hipLaunchKernelGGL((k2_wide<MB, CBW, D, SG, OF>), dim3((unsigned)((ncb + CBW - 1) / CBW)), dim3(CBW * MB * 64),
+                       0, st, a, w, static_cast<const uint16_t*>(sa), static_cast<const uint16_t*>(sw), out, M, N, K);
+    return hipGetLastError();
+}
+
+template <int MB, bool SG, bool OF>
+hipError_t launch_wide(const int8_t* a, const int8_t* w, const void* sa, const void* sw, void* out,
+                       int M, int N, int K, hipStream_t st) {
+    // Column blocks per workgroup: enough that one workgroup per CU covers N.
+    const int per_cu = ((N + 15) / 16 + cu_count() - 1) / cu_count();
+    if (per_cu <= 4) return launch_wide_cbw<MB, 4, SG, OF>(a, w, sa, sw, out, M, N, K, st);
+    if (per_cu <= 6) return launch_wide_cbw<MB, 6, SG, OF>(a, w, sa, sw, out, M, N, K, st);
+    return launch_wide_cbw<MB, 8, SG, OF>(a, w, sa, sw, out, M, N, K, st);
+}
+
 template <bool SG, bool OF>
 hipError_t launch_tiled(const int8_t* a, const int8_t* w, const void* sa, const void* sw, void* out,
                         int M, int N, int K, hipStream_t st) {
@@ -427,8 +622,13 @@ hipError_t launch_tiled(const int8_t* a, const int8_t* w, const void* sa, const 
 template <bool SG, bool OF>
 hipError_t dispatch(const int8_t* a, const int8_t* w, const void* sa, const void* sw, void* out,
                     int M, int N, int K, hipStream_t st) {
-    // Wide N: 32 columns per workgroup halves the activation re-reads while
-    // still giving every CU several workgroups.
+    // Wide N: waves own column blocks, activations fetched once per CU.
+    if (wide_fits(M, N, K)) {
+        return M <= 16 ? launch_wide<1, SG, OF>(a, w, sa, sw, out, M, N, K, st)
+                       : launch_wide<2, SG, OF>(a, w, sa, sw, out, M, N, K, st);
+    }
+    // Otherwise 32 columns per workgroup for wide N halves the activation
+    // re-reads while still giving every CU several workgroups.
     const bool wide = N >= 16384;
     if (M <= 16) return wide ? launch_decode<1, 2, SG, OF>(a, w, sa, sw, out, M, N, K, st)
                              : launch_decode<1, 1, SG, OF>(a, w, sa, sw, out, M, N, K, st);

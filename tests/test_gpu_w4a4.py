@@ -123,6 +123,16 @@ def test_k2_decode_activations_in_lds(M, N, K):
         run_case(M, N, K, 4000 + M + K, grouped=False)
 
 
+@pytest.mark.parametrize("M,N,K", [(1, 16392, 4096), (17, 16392, 4096), (32, 16392, 2048), (32, 16384, 4096)])
+def test_k2_decode_wide_n(M, N, K):
+    """Shapes served by the wide decode kernel (each wave owns 16 columns over
+    the whole K, activations resident in LDS): M blocks 1 and 2, row and
+    column tails, K = 2048 and 4096, grouped and per-channel scales."""
+    run_case(M, N, K, 5000 + M + K)
+    if M == 32:
+        run_case(M, N, K, 6000 + M + K, grouped=False)
+
+
 def chain_expected(case, rows=None):
     xb = bf16_bits(case.x)
     if rows is not None:
