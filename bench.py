@@ -3,10 +3,11 @@
 
 A step is one decode-sized pass of the W4A4 linear chain of one Qwen3-8B
 decoder layer: for each fused projection (qkv 4096->6144, o 4096->4096,
-gate_up 4096->24576, down 12288->4096) the fused RHT + group-128 INT4
-quantization + packing kernel, then the grouped INT4 GEMM, on M = 32 rows of
-synthetic activations (the reference's operator table, benchmarks/README.md:
-121-133, times exactly this chain at M = 32 and M = 4096).
+gate_up 4096->24576, down 12288->4096) the W4A4Linear forward -- RHT +
+group-128 INT4 quantization + packing of the activations, then the grouped
+INT4 GEMM -- on M = 32 rows of synthetic activations (the reference's
+operator table, benchmarks/README.md:121-133, times exactly this chain at
+M = 32 and M = 4096).
 
 Timing rules:
 * Every step is a HIP-graph replay (captured once per weight set), so the
@@ -133,30 +134,29 @@ def graph_launch_us(torch, launches, replays):
 COPY_BYTES = 256 << 20
 
 
-def pmc_pass(torch, k1, k2, R):
-    """Kernels for a hardware-counter run: K1 + K2 of every projection and
-    weight set, three rounds, then three device-to-device copies of exactly
-    COPY_BYTES (read COPY_BYTES, write COPY_BYTES) to scale FETCH_SIZE and
-    WRITE_SIZE into bytes."""
+def pmc_pass(torch, linear, R):
+    """Kernels for a hardware-counter run: the W4A4 linear (K1 + K2) of every
+    projection and weight set, three rounds, then three device-to-device
+    copies of exactly COPY_BYTES (read COPY_BYTES, write COPY_BYTES) to scale
+    FETCH_SIZE and WRITE_SIZE into bytes."""
     for _ in range(3):
         for l in range(R):
             for p in PROJECTIONS:
-                k1(l, p)
-                k2(l, p)
+                linear(l, p)
     src = torch.empty(COPY_BYTES, dtype=torch.uint8, device="cuda:0")
     dst = torch.empty_like(src)
     src.fill_(1)
     for _ in range(3):
         dst.copy_(src)
     torch.cuda.synchronize()
-    print(f"pmc pass done: {3 * R * len(PROJECTIONS)} K2 launches, 3 copies of {COPY_BYTES} bytes", flush=True)
+    print(f"pmc pass done: {3 * R * len(PROJECTIONS)} linear launches, 3 copies of {COPY_BYTES} bytes", flush=True)
 
 
 def measured_traffic():
     """HBM bytes per decode-GEMM launch from the committed counter summary
     (two rocprofv3 --pmc passes, FETCH_SIZE and WRITE_SIZE, scaled by the
     copy calibration), or None when the summary is absent."""
-    path = ROOT / "profiles" / "k2_decode_m32_traffic.json"
+    path = ROOT / "profiles" / "decode_gemm_m32_traffic.json"
     try:
         with open(path) as f:
             return json.load(f)
@@ -233,19 +233,19 @@ def main():
     sc = {p: torch.empty((M, W.PROJECTIONS[p][1] // 128), dtype=torch.bfloat16, device=dev) for p in PROJECTIONS}
     out = {p: torch.empty((M, W.PROJECTIONS[p][0]), dtype=torch.bfloat16, device=dev) for p in PROJECTIONS}
 
-    def k1(l, p):
-        nv4.rht_quant_pack(acts[p], sets[l][p][0], out_packed=pk[p], out_scale=sc[p])
+    def linear(l, p):  # W4A4Linear.forward: RHT+quant+pack, then the grouped GEMM
+        nv4.w4a4_linear(acts[p], sets[l][p][0], sets[l][p][1], sets[l][p][2],
+                        out=out[p], out_packed=pk[p], out_scale=sc[p])
 
-    def k2(l, p):
+    def gemm(l, p):  # the GEMM alone, on the codes the last linear call left in pk/sc
         nv4.w4a4_grouped_gemm(pk[p], sets[l][p][1], sc[p], sets[l][p][2], out=out[p])
 
     def step(l):
         for p in PROJECTIONS:
-            k1(l, p)
-            k2(l, p)
+            linear(l, p)
 
     if args.pmc_pass:
-        pmc_pass(torch, k1, k2, R)
+        pmc_pass(torch, linear, R)
         return
 
     # Eager reference outputs of set 0, then one graph per weight set.
@@ -282,10 +282,10 @@ def main():
     ms_per_step = ev0.elapsed_time(ev1) / args.steps
     step_us = ms_per_step * 1e3
 
-    # Dominant kernel: the grouped INT4 GEMM, timed per projection over the
-    # rotating weight sets (equal launch counts per projection, so the mean of
-    # the per-projection averages is the kernel's average launch).
-    k2_us = {p: graph_launch_us(torch, [lambda l=l, p=p: k2(l, p) for l in range(R)], replays=40)
+    # Dominant kernel: the decode GEMM, timed per projection over the rotating
+    # weight sets (equal launch counts per projection, so the mean of the
+    # per-projection averages is the kernel's average launch).
+    k2_us = {p: graph_launch_us(torch, [lambda l=l, p=p: gemm(l, p) for l in range(R)], replays=40)
              for p in PROJECTIONS}
     avg_launch_us = statistics.mean(k2_us.values())
     avg_bytes = statistics.mean(k2_bytes(M, *W.PROJECTIONS[p]) for p in PROJECTIONS)
@@ -315,7 +315,7 @@ def main():
             "M": M, "rotate": R,
         },
         "roofline": {
-            "kernel": "k2_decode (grouped INT4 GEMM, M<=64)",
+            "kernel": "decode grouped INT4 GEMM (k2_decode for qkv/o/down, k2_wide for gate_up), M=32",
             "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
             "traffic": (traffic or {}).get("bytes_per_launch"),

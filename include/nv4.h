@@ -18,6 +18,8 @@
  *                          (kernel :37-136)
  *   nv4_w4a4_gemm       <- nanovllm/kernels/w4a4_grouped_kernel.py:104 w4a4_grouped_gemm
  *                          and :32 compile_grouped_gemm(..., output_fp32, weight_grouped)
+ *   nv4_w4a4_linear     <- nanovllm/layers/linear_w4a4.py:27-35 W4A4Linear.forward
+ *                          (rht_quant_pack + w4a4_grouped_gemm)
  *   nv4_w4a16_gemm      <- nanovllm/layers/linear_w4a16.py:11 tl_dequant_matmul_w4a16
  *                          (called from W4A16Linear.forward :128-148)
  */
@@ -80,6 +82,24 @@ int nv4_rht_quant_pack(const void* x, const int8_t* signs, int8_t* packed, void*
 int nv4_w4a4_gemm(const int8_t* a, const int8_t* w, const void* sa, const void* sw,
                   int sw_grouped, void* out, int out_fp32,
                   int64_t M, int64_t N, int64_t K, void* stream);
+
+/*
+ * W4A4 linear forward: RHT + quantize + pack the activations, then the
+ * grouped INT4 GEMM -- the body of W4A4Linear.forward
+ * (nanovllm/layers/linear_w4a4.py:27-35: rht_quant_pack then
+ * w4a4_grouped_gemm), launched back to back on `stream`; identical to
+ * calling nv4_rht_quant_pack (reference layout) and nv4_w4a4_gemm (grouped
+ * scales, bf16 output) in sequence, with the same argument rules.
+ *   x        bf16 [M,K], K in {4096, 12288}
+ *   signs    int8 [K]
+ *   w, sw    packed weights int8 [N,K/2] and bf16 scales [N,K/128]
+ *   out      bf16 [M,N]
+ *   a_packed int8 [M,K/2], a_scale bf16 [M,K/128]: receive the quantized
+ *            activations (caller-owned workspace, also an output)
+ */
+int nv4_w4a4_linear(const void* x, const int8_t* signs, const int8_t* w, const void* sw,
+                    void* out, int8_t* a_packed, void* a_scale,
+                    int64_t M, int64_t N, int64_t K, void* stream);
 
 /*
  * W4A16 GEMM with GPTQ weights (zero-point convention w = (q - z - 1) * s).

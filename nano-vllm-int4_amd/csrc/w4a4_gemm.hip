@@ -642,6 +642,17 @@ hipError_t dispatch(const int8_t* a, const int8_t* w, const void* sa, const void
 }  // namespace
 }  // namespace nv4
 
+extern "C" int nv4_w4a4_linear(const void* x, const int8_t* signs, const int8_t* w, const void* sw,
+                               void* out, int8_t* a_packed, void* a_scale,
+                               int64_t M, int64_t N, int64_t K, void* stream) {
+    using namespace nv4;
+    if (!x || !signs || !w || !sw || !out || !a_packed || !a_scale) return NV4_E_NULL;
+    if (K != 4096 && K != 12288) return NV4_E_SHAPE;
+    const int rc = nv4_rht_quant_pack(x, signs, a_packed, a_scale, M, K, NV4_LAYOUT_REFERENCE, stream);
+    if (rc != NV4_OK) return rc;
+    return nv4_w4a4_gemm(a_packed, w, a_scale, sw, 1, out, 0, M, N, K, stream);
+}
+
 extern "C" int nv4_w4a4_gemm(const int8_t* a, const int8_t* w, const void* sa, const void* sw,
                              int sw_grouped, void* out, int out_fp32,
                              int64_t M, int64_t N, int64_t K, void* stream) {

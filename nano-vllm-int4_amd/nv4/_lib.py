@@ -31,6 +31,7 @@ _P, _I, _I64 = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64
 SIGNATURES = {
     "nv4_rht_quant_pack": ([_P, _P, _P, _P, _I64, _I64, _I, _P], _I),
     "nv4_w4a4_gemm": ([_P, _P, _P, _P, _I, _P, _I, _I64, _I64, _I64, _P], _I),
+    "nv4_w4a4_linear": ([_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _P], _I),
     "nv4_w4a16_gemm": ([_P, _I, _P, _P, _P, _P, _I, _I64, _I64, _I64, _I, _P], _I),
     "nv4_version": ([], ctypes.c_char_p),
     "nv4_strerror": ([_I], ctypes.c_char_p),

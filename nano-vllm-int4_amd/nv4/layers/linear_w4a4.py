@@ -5,16 +5,15 @@ nanovllm/layers/linear_w4a4.py:15-36): same constructor checks, the same
 buffers (``packed_weight`` int8 [out, in/2], ``weight_scale`` bf16
 [out, in/128], ``signs`` int8 [in]) so state dicts and the checkpoint loader
 carry over, and the same forward: RHT + quantize + pack the activations
-(K1), then the grouped INT4 GEMM (K2), both HIP kernels on the current stream.
-Temporary buffers come from torch's caching allocator, so the forward can be
-captured in a HIP graph.
+(K1), then the grouped INT4 GEMM (K2), on the current stream through one C
+ABI call (``nv4_w4a4_linear``).  Temporary buffers come from torch's caching
+allocator, so the forward can be captured in a HIP graph.
 """
 import torch
 from torch import nn
 import torch.distributed as dist
 
-from ..kernels.rht_a4 import rht_quant_pack
-from ..kernels.w4a4_grouped import w4a4_grouped_gemm
+from ..kernels.w4a4_linear import w4a4_linear
 
 
 class W4A4Linear(nn.Module):
@@ -33,9 +32,8 @@ class W4A4Linear(nn.Module):
         if x.shape[-1] != self.in_features or x.dtype != torch.bfloat16:
             raise ValueError("W4A4Linear requires BF16 activations with the configured input width")
         flat = x.reshape(-1, self.in_features).contiguous()
-        m, k = flat.shape
-        packed = torch.empty((m, k // 2), dtype=torch.int8, device=x.device)
-        scale = torch.empty((m, k // 128), dtype=torch.bfloat16, device=x.device)
-        rht_quant_pack(flat, self.signs, out_packed=packed, out_scale=scale)
-        out = w4a4_grouped_gemm(packed, self.packed_weight, scale, self.weight_scale)
+        # RHT + quantize + pack, then the grouped INT4 GEMM; packed codes and
+        # scales come from the caching allocator, so the forward can be
+        # captured in a HIP graph.
+        out = w4a4_linear(flat, self.signs, self.packed_weight, self.weight_scale)
         return out.reshape(*x.shape[:-1], self.out_features)

@@ -67,6 +67,28 @@ def silu_mul_activations(M: int, K: int, seed_g: int, seed_u: int) -> torch.Tens
     return (gf * torch.sigmoid(gf) * u.float()).to(torch.bfloat16).contiguous()
 
 
+def special_rows(m: int, k: int, seed: int = BASE_SEED) -> torch.Tensor:
+    """Seeded randn bf16 rows carrying the reference's special rows
+    (benchmarks/rht_a4_bench_common.py:104-120: a zero row, an impulse of
+    1000 at k/12 or 5, a row of ones, alternating +-1, x1e-9 and x1e4), drawn
+    from a CPU generator with the reference's seed formula."""
+    x = torch.randn(m, k, generator=_gen(seed + m * 17 + k), dtype=torch.float32).to(torch.bfloat16)
+    x[0].zero_()
+    if m > 1:
+        x[1].zero_()
+        x[1, k // 12 if k == 12288 else 5] = 1000
+    if m > 2:
+        x[2].fill_(1)
+    if m > 3:
+        x[3, ::2] = 1
+        x[3, 1::2] = -1
+    if m > 4:
+        x[4].mul_(1e-9)
+    if m > 5:
+        x[5].mul_(1e4)
+    return x.contiguous()
+
+
 def signs(K: int, seed: int) -> torch.Tensor:
     return (torch.randint(0, 2, (K,), generator=_gen(seed), dtype=torch.int8) * 2 - 1).contiguous()
 

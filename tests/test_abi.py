@@ -1,0 +1,112 @@
+"""The C ABI of libnv4.so and the host-side argument checks (CPU only).
+
+Every entry point declared in include/nv4.h is exported by the library and
+bound by nv4._lib; invalid arguments are rejected with the documented
+negative codes before anything is launched (so these calls need no GPU);
+the Python wrappers raise the reference's exceptions (ValueError/TypeError,
+nanovllm/kernels/*.py and nanovllm/layers/linear_w4a4.py) for the same
+conditions.
+"""
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+import torch
+
+from nv4 import _lib
+
+HEADER = Path(__file__).resolve().parent.parent / "include" / "nv4.h"
+P = ctypes.c_void_p
+A16 = 0x10000  # a fake, 16-byte aligned device address: never dereferenced below
+
+
+def declared():
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r"^(?:int|const char\*)\s+(nv4_\w+)\(", text, re.M)))
+
+
+def test_every_declared_symbol_is_exported_and_bound():
+    names = declared()
+    assert names, "no entry points parsed from nv4.h"
+    lib = _lib.load()
+    for n in names:
+        assert hasattr(lib, n), n
+        assert n in _lib.SIGNATURES, n
+    assert set(_lib.SIGNATURES) == set(names)
+    assert _lib.version().startswith("nv4 ")
+
+
+def test_error_text():
+    assert _lib.strerror(_lib.NV4_OK) == "ok"
+    for code in (_lib.NV4_E_NULL, _lib.NV4_E_SHAPE, _lib.NV4_E_ALIGN, _lib.NV4_E_LAYOUT, _lib.NV4_E_DTYPE,
+                 _lib.NV4_E_GROUP):
+        assert _lib.strerror(code) not in ("ok", "unknown error")
+    assert _lib.strerror(7) == "hip error"
+
+
+def test_rht_quant_pack_rejections():
+    f = _lib.load().nv4_rht_quant_pack
+    assert f(None, P(A16), P(A16), P(A16), 4, 4096, 0, None) == _lib.NV4_E_NULL
+    assert f(P(A16), P(A16), P(A16), P(A16), 0, 4096, 0, None) == _lib.NV4_E_SHAPE
+    assert f(P(A16 + 8), P(A16), P(A16), P(A16), 4, 4096, 0, None) == _lib.NV4_E_ALIGN
+    assert f(P(A16), P(A16), P(A16), P(A16), 4, 2048, 0, None) == _lib.NV4_E_SHAPE
+    assert f(P(A16), P(A16), P(A16), P(A16), 4, 100, 1, None) == _lib.NV4_E_SHAPE
+    assert f(P(A16), P(A16), P(A16), P(A16), 4, 4096, 9, None) == _lib.NV4_E_LAYOUT
+
+
+def test_w4a4_gemm_rejections():
+    f = _lib.load().nv4_w4a4_gemm
+    ok = [P(A16)] * 4
+    assert f(None, *ok[1:], 1, P(A16), 0, 4, 64, 4096, None) == _lib.NV4_E_NULL
+    assert f(*ok, 1, P(A16), 0, 4, 60, 4096, None) == _lib.NV4_E_SHAPE        # N % 8
+    assert f(*ok, 1, P(A16), 0, 4, 64, 4000, None) == _lib.NV4_E_SHAPE       # K % 128
+    assert f(*ok, 1, P(A16), 0, 0, 64, 4096, None) == _lib.NV4_E_SHAPE       # M = 0
+    assert f(P(A16 + 4), *ok[1:], 1, P(A16), 0, 4, 64, 4096, None) == _lib.NV4_E_ALIGN
+    assert f(*ok, 1, P(A16 + 2), 1, 4, 64, 4096, None) == _lib.NV4_E_ALIGN   # fp32 output
+
+
+def test_w4a16_and_linear_rejections():
+    f = _lib.load().nv4_w4a16_gemm
+    ok = [P(A16)] * 4
+    assert f(P(A16), 7, P(A16), P(A16), P(A16), P(A16), 0, 4, 64, 4096, 128, None) == _lib.NV4_E_DTYPE
+    assert f(P(A16), 0, P(A16), P(A16), P(A16), P(A16), 0, 4, 64, 4096, 64, None) == _lib.NV4_E_GROUP
+    assert f(P(A16), 0, P(A16), P(A16), P(A16), P(A16), 0, 4, 60, 4096, 128, None) == _lib.NV4_E_SHAPE
+    assert f(None, 0, *ok[:3], P(A16), 0, 4, 64, 4096, 128, None) == _lib.NV4_E_NULL
+    g = _lib.load().nv4_w4a4_linear
+    assert g(*([P(A16)] * 7), 4, 64, 2048, None) == _lib.NV4_E_SHAPE
+    assert g(None, *([P(A16)] * 6), 4, 64, 4096, None) == _lib.NV4_E_NULL
+    assert g(*([P(A16)] * 7), 0, 64, 4096, None) == _lib.NV4_E_SHAPE
+
+
+def test_python_wrappers_validate_like_the_reference():
+    from nv4 import W4A4Linear, rht_quant_pack, w4a4_grouped_gemm
+    x = torch.zeros(2, 4096, dtype=torch.bfloat16)
+    signs = torch.ones(4096, dtype=torch.int8)
+    with pytest.raises(ValueError):
+        rht_quant_pack(x.float(), signs, out_packed=torch.empty(2, 2048, dtype=torch.int8),
+                       out_scale=torch.empty(2, 32, dtype=torch.bfloat16))
+    with pytest.raises(ValueError):  # CPU tensors: the reference requires CUDA tensors
+        rht_quant_pack(x, signs, out_packed=torch.empty(2, 2048, dtype=torch.int8),
+                       out_scale=torch.empty(2, 32, dtype=torch.bfloat16))
+    a = torch.zeros(2, 2048, dtype=torch.int8)
+    w = torch.zeros(64, 2048, dtype=torch.int8)
+    sa = torch.zeros(2, 32, dtype=torch.bfloat16)
+    sw = torch.zeros(64, 32, dtype=torch.bfloat16)
+    with pytest.raises(TypeError):
+        w4a4_grouped_gemm(a.to(torch.int16), w, sa, sw)
+    with pytest.raises(TypeError):
+        w4a4_grouped_gemm(a, w, sa.float(), sw)
+    with pytest.raises(ValueError):
+        w4a4_grouped_gemm(a, torch.zeros(60, 2048, dtype=torch.int8), sa, sw[:60])
+    with pytest.raises(ValueError):
+        w4a4_grouped_gemm(a, w, sa, sw)  # CPU tensors
+    for kwargs in ({"bias": True}, {}):
+        with pytest.raises(ValueError):
+            W4A4Linear(1000 if not kwargs else 4096, 64, **kwargs)
+    with pytest.raises(ValueError):
+        W4A4Linear(4096, 60)
+    m = W4A4Linear(4096, 64)
+    assert {k: (tuple(v.shape), v.dtype) for k, v in m.state_dict().items()} == {
+        "packed_weight": ((64, 2048), torch.int8), "weight_scale": ((64, 32), torch.bfloat16),
+        "signs": ((4096,), torch.int8)}

@@ -1,0 +1,100 @@
+"""GPU parity of the W4A4 linear forward as one operator call (``nv4_w4a4_linear``).
+
+The reference's ``W4A4Linear.forward`` (nanovllm/layers/linear_w4a4.py:27-35)
+is rht_quant_pack followed by w4a4_grouped_gemm; the one-call operator must
+give the same bits as the oracle chain -- codes, scales and bf16 outputs --
+for the four Qwen3-8B projections across the decode and prefill kernels,
+repeated calls, a non-default stream and HIP-graph replay after the inputs
+change.  Bar: bit-exact.
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from conftest import bf16_bits
+from nv4 import w4a4_linear
+from nv4 import workloads as W
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda:0"
+
+
+def expected(case):
+    xb = bf16_bits(case.x)
+    packed, scale = oracle.rht_quant_pack(xb, case.signs.numpy())
+    return packed, scale, oracle.w4a4_gemm(packed, case.w_packed.numpy(), scale, bf16_bits(case.w_scale))
+
+
+def run(case, stream=None):
+    M, N, K = case.shape
+    x, signs = case.x.to(DEV), case.signs.to(DEV)
+    wp, ws = case.w_packed.to(DEV), case.w_scale.to(DEV)
+    packed = torch.full((M, K // 2), 85, dtype=torch.int8, device=DEV)
+    scale = torch.full((M, K // 128), float("nan"), dtype=torch.bfloat16, device=DEV)
+    out = torch.full((M, N), float("nan"), dtype=torch.bfloat16, device=DEV)
+    with torch.cuda.stream(stream or torch.cuda.current_stream()):
+        w4a4_linear(x, signs, wp, ws, out=out, out_packed=packed, out_scale=scale)
+    torch.cuda.synchronize()
+    return packed, scale, out
+
+
+def check(case, got, what):
+    p_ref, s_ref, o_ref = expected(case)
+    packed, scale, out = got
+    assert np.array_equal(packed.cpu().numpy(), p_ref), f"{what}: packed codes differ"
+    assert np.array_equal(bf16_bits(scale), s_ref), f"{what}: scales differ"
+    bad = np.argwhere(bf16_bits(out) != o_ref)
+    assert bad.size == 0, f"{what}: {len(bad)} outputs differ, first {bad[:5].tolist()}"
+
+
+@pytest.mark.parametrize("proj", ["o", "qkv", "gate_up", "down"])
+@pytest.mark.parametrize("M", [1, 7, 32])
+def test_linear_qwen3_shapes(proj, M):
+    print(f"[linear] {proj} M={M}", flush=True)
+    case = W.w4a4_case(proj, M)
+    check(case, run(case), f"{proj} M={M}")
+
+
+@pytest.mark.parametrize("M", [16, 17, 33, 48, 64, 65])
+def test_linear_m_blocks(M):
+    """Every decode row-block count, and M = 65 (the prefill GEMM)."""
+    for proj in ("o", "down"):
+        print(f"[linear] {proj} M={M}", flush=True)
+        case = W.w4a4_case(proj, M, seed=W.BASE_SEED + M)
+        check(case, run(case), f"{proj} M={M}")
+
+
+def test_linear_repeated_calls_and_stream():
+    case = W.w4a4_case("gate_up", 32)
+    for _ in range(3):
+        check(case, run(case), "repeat")
+    side = torch.cuda.Stream()
+    check(case, run(case, stream=side), "side stream")
+
+
+@pytest.mark.parametrize("proj", ["o", "gate_up"])
+def test_linear_graph_replay(proj):
+    """Capture once; replay after changing x, with eager work between replays."""
+    case = W.w4a4_case(proj, 32)
+    M, N, K = case.shape
+    x = case.x.to(DEV)
+    signs, wp, ws = case.signs.to(DEV), case.w_packed.to(DEV), case.w_scale.to(DEV)
+    packed = torch.empty((M, K // 2), dtype=torch.int8, device=DEV)
+    scale = torch.empty((M, K // 128), dtype=torch.bfloat16, device=DEV)
+    out = torch.empty((M, N), dtype=torch.bfloat16, device=DEV)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        w4a4_linear(x, signs, wp, ws, out=out, out_packed=packed, out_scale=scale)
+    torch.cuda.current_stream().wait_stream(side)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        w4a4_linear(x, signs, wp, ws, out=out, out_packed=packed, out_scale=scale)
+    for step, delta in enumerate((0.0, 0.125, -0.25)):
+        new_x = (case.x.float() + delta).to(torch.bfloat16)
+        x.copy_(new_x)
+        g.replay()
+        torch.cuda.synchronize()
+        shifted = W.W4A4Case(case.name, new_x, case.signs, case.w_packed, case.w_scale)
+        check(shifted, (packed, scale, out), f"{proj} replay {step}")

@@ -23,25 +23,8 @@ pytestmark = pytest.mark.gpu
 DEV = "cuda:0"
 
 
-def make_input(m, k, seed=20261108):
-    """Seeded randn bf16 rows with the reference's special rows
-    (rht_a4_bench_common.py:104-120), generated on the CPU."""
-    g = torch.Generator("cpu").manual_seed(seed + m * 17 + k)
-    x = torch.randn(m, k, generator=g, dtype=torch.float32).to(torch.bfloat16)
-    x[0].zero_()
-    if m > 1:
-        x[1].zero_()
-        x[1, k // 12 if k == 12288 else 5] = 1000
-    if m > 2:
-        x[2].fill_(1)
-    if m > 3:
-        x[3, ::2] = 1
-        x[3, 1::2] = -1
-    if m > 4:
-        x[4].mul_(1e-9)
-    if m > 5:
-        x[5].mul_(1e4)
-    return x.contiguous()
+def make_input(m, k, seed=W.BASE_SEED):
+    return W.special_rows(m, k, seed)
 
 
 def gold(x_cpu, signs_cpu, layout=oracle.LAYOUT_REFERENCE):
