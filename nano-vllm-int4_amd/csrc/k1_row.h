@@ -1,6 +1,5 @@
 // Device code of the reference-layout RHT + group-128 quantization + INT4
-// pack for one row (shared by the standalone K1 kernel and the fused decode
-// linear kernel).
+// pack (K1) for K = 4096 and K = 12288.
 //
 // Numerical contract (nanovllm/kernels/rht_a4_tilelang.py:58-135,
 // benchmarks/rht_a4_bench_common.py:19-36), reproduced bit for bit:
@@ -14,16 +13,19 @@
 //   scale = mx == 0 ? 1 : bf16_rne(max(t, 2^-126)); q = clamp(rint(a/scale), -7, 7)
 //   with IEEE division; byte = (q[2i] & 15) | (q[2i+1] & 15) << 4.
 //
-// Mapping to the hardware.  A team of T threads owns one row.  Each thread
-// keeps L = K/T fp32 values in VGPRs.  Butterfly stages run only on
-// register-index bits: the row is passed through LDS between "phases" so
-// that the next B = log2(F/T) chunk-index bits become register bits (an LDS
-// transpose), and the stages of each phase are plain VALU adds in registers.
-// The H12 stage needs all 12 chunks of one column in one thread: every phase
-// mapping keeps the chunk index in registers, so it runs in registers too.
-// Quantization reads the row back from LDS as 16 contiguous values per
-// thread, so one 128-group is 8 adjacent lanes (3 xor-shuffles for the max),
-// and each thread emits 8 packed bytes with one store.
+// Mapping to the hardware.  A 1024-point chunk is one wave: lane l loads the
+// 16 contiguous columns 16l..16l+15, so butterfly bits 0-3 are register
+// bits.  A wave-local LDS transpose (no workgroup barrier) then puts bits 4-7
+// in registers, with bits 0-3 and 8-9 on the lane index; bits 8-9 sit on
+// lane bits 0-1 and are finished with DPP quad permutes.  K = 4096 spans
+// four waves: one workgroup transpose brings bits 8-11 into registers.
+// K = 12288 needs all 12 chunks of a column for the H12 stage: one thread
+// per column reads them from LDS.  Quantization reads 16 contiguous values
+// per thread (8 adjacent lanes hold one 128-group).
+//
+// LDS layout: each 1024-column chunk is stored XOR-swizzled (swz below) so
+// that the contiguous, transposed, per-column and per-unit access patterns
+// are all free of bank conflicts on 32 or 64 banks.
 #pragma once
 
 #include "nv4_common.h"
@@ -31,36 +33,103 @@
 namespace nv4 {
 namespace {
 
-// One pad float per 16 keeps strided phase accesses bank-conflict free.
-__device__ __forceinline__ int lds_idx(int i) { return i + (i >> 4); }
+__device__ __forceinline__ int swz(int c) { return c ^ ((c >> 4) & 0x3F) ^ ((c >> 6) & 8); }
 
-__device__ __forceinline__ bool paley_positive(int s, int d) {
+// Column of chunk-local index held by lane l in register r after the
+// wave-local transpose: bits 0-3 = l >> 2, bits 4-7 = r, bits 8-9 = l & 3.
+__device__ __forceinline__ int col_t(int l, int r) { return (l >> 2) | (r << 4) | ((l & 3) << 8); }
+
+__host__ __device__ constexpr bool paley_positive(int s, int d) {
     if (s == 0 || d == 0) return true;
     const int delta = ((d - s) % 11 + 11) % 11;
     return delta == 1 || delta == 3 || delta == 4 || delta == 5 || delta == 9;
 }
 
-// Chunk-column index held by thread t in register slot r when the register
-// window starts at bit w: low thread bits below w, register bits at w..w+B-1,
-// high thread bits above.
-template <int B>
-__device__ __forceinline__ int col_of(int t, int r, int w) {
-    const int low = t & ((1 << w) - 1);
-    return low | (r << w) | ((t >> w) << (w + B));
+// DPP lane permutes (gfx9 dpp_ctrl encodings).
+constexpr int DPP_QUAD_XOR1 = 0xB1;    // quad_perm [1,0,3,2]
+constexpr int DPP_QUAD_XOR2 = 0x4E;    // quad_perm [2,3,0,1]
+constexpr int DPP_HALF_MIRROR = 0x141;  // lane i of each 8 reads lane 7-i
+
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, true));
 }
 
-// Quantize 16 contiguous values (one eighth of a 128-group, 8 adjacent lanes
-// hold the group), write 8 packed bytes and, from the group's first lane, the
-// bf16 scale.
+// Orders the LDS accesses of one wave (executed in order by the LDS unit)
+// without a workgroup barrier.
+__device__ __forceinline__ void wave_lds_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// 16 contiguous bf16 values times their int8 signs.
+__device__ __forceinline__ void load_signed16(const uint16_t* __restrict__ xp, const int8_t* __restrict__ sp,
+                                              float (&a)[16]) {
+    const v4u x0 = *reinterpret_cast<const v4u*>(xp);
+    const v4u x1 = *reinterpret_cast<const v4u*>(xp + 8);
+    const v4u sv = *reinterpret_cast<const v4u*>(sp);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        const uint32_t xw = i < 8 ? x0[(i & 7) >> 1] : x1[(i & 7) >> 1];
+        const uint32_t h = (xw >> (16 * (i & 1))) & 0xffffu;
+        const int sg = (int)(int8_t)((sv[i >> 2] >> (8 * (i & 3))) & 0xffu);
+        a[i] = bf16_to_f32(h) * (float)sg;
+    }
+}
+
+// Butterflies on register-index bits (strides 1, 2, 4, 8 in this order).
+template <int N>
+__device__ __forceinline__ void reg_butterflies(float (&a)[N]) {
+#pragma unroll
+    for (int rb = 1; rb < N; rb <<= 1)
+#pragma unroll
+        for (int r = 0; r < N; ++r)
+            if ((r & rb) == 0) {
+                const float lo = a[r], hi = a[r + rb];
+                a[r] = lo + hi;
+                a[r + rb] = lo - hi;
+            }
+}
+
+// Butterfly across lanes l and l ^ (1 << LB) (LB = 0 or 1): the lower lane
+// keeps lo + hi, the upper lo - hi; fma(v, -1, t) rounds t - v once.
+template <int LB>
+__device__ __forceinline__ void lane_butterflies(float (&a)[16], int l) {
+    const float sg = (l >> LB) & 1 ? -1.0f : 1.0f;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+        const float other = dpp<LB == 0 ? DPP_QUAD_XOR1 : DPP_QUAD_XOR2>(a[r]);
+        a[r] = __builtin_fmaf(a[r], sg, other);
+    }
+}
+
+// Max over the 8 adjacent lanes that hold one 128-group.
+__device__ __forceinline__ float group8_max(float m) {
+    m = fmaxf(m, dpp<DPP_QUAD_XOR1>(m));
+    m = fmaxf(m, dpp<DPP_QUAD_XOR2>(m));
+    return fmaxf(m, dpp<DPP_HALF_MIRROR>(m));
+}
+
+// Quantize 16 contiguous values (one eighth of a 128-group; the group's 8
+// lanes must be active together), write 8 packed bytes and, from the group's
+// first lane, the bf16 scale.
+//
+// Codes: q = clamp(rint(v / s)) with the IEEE quotient.  Fast path: p =
+// v * rcp(s) with v_rcp_f32 (<= 1 ulp), so |p - v/s| <= 1.5 * 2^-23 * |v/s|
+// < 2^-20 (|v/s| < 8 because s >= ~0.128 * max|v|).  If |p - rint(p)| <
+// 0.5 - 2^-18, then v/s, and its rounded quotient (within 2^-22), lie
+// strictly inside the same unit interval around rint(p), so rint of the IEEE
+// quotient equals rint(p).  A lane whose values fail the test (near a
+// half-integer, or s outside [2^-126, 2^100]) recomputes them with the IEEE
+// division.  Nibbles are assembled exactly in fp32: sum (q_i + 8) * 16^i over
+// four values is an integer below 2^16, and (q + 8) ^ 8 == q & 15.
 __device__ __forceinline__ void quantize16_store(const float (&v)[16], int8_t* __restrict__ dst8,
-                                                 uint16_t* __restrict__ scale_dst, bool leader,
-                                                 bool live = true) {
+                                                 uint16_t* __restrict__ scale_dst, bool leader) {
     float mx = 0.0f;
 #pragma unroll
     for (int i = 0; i < 16; ++i) mx = fmaxf(mx, fabsf(v[i]));
-    mx = fmaxf(mx, __shfl_xor(mx, 1));
-    mx = fmaxf(mx, __shfl_xor(mx, 2));
-    mx = fmaxf(mx, __shfl_xor(mx, 4));
+    mx = group8_max(mx);
     uint32_t sb;
     if (mx == 0.0f) {
         sb = 0x3F80u;  // 1.0
@@ -71,175 +140,123 @@ __device__ __forceinline__ void quantize16_store(const float (&v)[16], int8_t* _
         sb = f32_to_bf16_rne(t);
     }
     const float s = bf16_to_f32(sb);
-    uint32_t word[2] = {0u, 0u};
+    const float y = __builtin_amdgcn_rcpf(s);
+    bool exact = s <= 0x1p100f;
+    float q[16];
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
-        float q = __builtin_rintf(v[i] / s);
-        q = fminf(fmaxf(q, -7.0f), 7.0f);
-        const uint32_t nib = (uint32_t)((int)q) & 15u;
-        word[i >> 3] |= nib << (4 * (i & 7));
+        const float p = v[i] * y;
+        q[i] = __builtin_rintf(p);
+        exact = exact & (fabsf(p - q[i]) < 0x1.ffffp-2f);
     }
-    if (live) {
-        *reinterpret_cast<uint2*>(dst8) = make_uint2(word[0], word[1]);
-        if (leader) *scale_dst = (uint16_t)sb;
+    if (!exact) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) q[i] = __builtin_rintf(v[i] / s);
     }
+    uint32_t half[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        float h = __builtin_amdgcn_fmed3f(q[4 * j + 3], -7.0f, 7.0f);
+#pragma unroll
+        for (int i = 2; i >= 0; --i) h = __builtin_fmaf(h, 16.0f, __builtin_amdgcn_fmed3f(q[4 * j + i], -7.0f, 7.0f));
+        half[j] = (uint32_t)(h + 34952.0f);  // + 8 * (1 + 16 + 256 + 4096)
+    }
+    const uint32_t w0 = (half[0] | (half[1] << 16)) ^ 0x88888888u;
+    const uint32_t w1 = (half[2] | (half[3] << 16)) ^ 0x88888888u;
+    *reinterpret_cast<uint2*>(dst8) = make_uint2(w0, w1);
+    if (leader) *scale_dst = (uint16_t)sb;
 }
 
-template <int C, int F, int T>
-struct Shape {
-    static constexpr int K = C * F;
-    static constexpr int LOGF = ilog2c(F);
-    static constexpr int LC = F / T;                 // chunk columns per thread
-    static constexpr int B = ilog2c(LC);             // register bits per phase
-    static constexpr int L = C * LC;                 // values per thread
-    static constexpr int NP = (LOGF + B - 1) / B;    // butterfly phases
-    static constexpr int LDS = K + K / 16;
-    static_assert(LC >= 2 && (LC & (LC - 1)) == 0, "need >= 2 power-of-two columns per thread");
-    static_assert(T % 64 == 0 && T <= 1024, "whole waves");
-    static_assert(K % (16 * 64) == 0, "quantization units must fill whole waves");
-};
-
-__host__ __device__ constexpr int window_of(int p, int B, int LOGF) {
-    return (p * B < LOGF - B) ? p * B : LOGF - B;
+// Butterfly bits 0-9 of the 1024-point chunk whose LDS block is blk, by one
+// wave (lane l, columns 16l..16l+15 in a).  On return a holds columns
+// col_t(l, r), and blk is free for the caller.
+__device__ __forceinline__ void chunk1024_bits0_9(float (&a)[16], float* __restrict__ blk, int l) {
+    reg_butterflies(a);
+#pragma unroll
+    for (int r = 0; r < 16; ++r) blk[swz(16 * l + r)] = a[r];
+    wave_lds_sync();
+#pragma unroll
+    for (int r = 0; r < 16; ++r) a[r] = blk[swz(col_t(l, r))];
+    reg_butterflies(a);
+    lane_butterflies<0>(a, l);
+    lane_butterflies<1>(a, l);
 }
 
-// Workgroup barriers executed by k1_row<C, F, T> (2 per phase after the
-// first, 1 before quantization): waves outside the team that must keep the
-// workgroup in step call k1_row_shadow, which executes exactly these.
-template <int C, int F, int T>
-__host__ __device__ constexpr int k1_barriers() { return 2 * (Shape<C, F, T>::NP - 1) + 1; }
+// K = 12288 (12 chunks of 1024) by 1024 threads: waves 0-11 run the
+// butterflies of one chunk each, then every thread runs the H12 stage of one
+// column, and threads 0-767 quantize one 16-column unit each.
+constexpr int K12_THREADS = 1024;
+constexpr int K12_LDS = 12 * 1024;
 
-template <int C, int F, int T>
-__device__ __forceinline__ void k1_row_shadow() {
+__device__ __forceinline__ void k1_row12288(const uint16_t* __restrict__ xr, const int8_t* __restrict__ signs,
+                                            int8_t* __restrict__ prow, uint16_t* __restrict__ srow,
+                                            float* __restrict__ buf) {
+    const int t = threadIdx.x, w = t >> 6, l = t & 63;
+    if (w < 12) {
+        float a[16];
+        load_signed16(xr + w * 1024 + 16 * l, signs + w * 1024 + 16 * l, a);
+        float* blk = buf + w * 1024;
+        chunk1024_bits0_9(a, blk, l);
 #pragma unroll
-    for (int i = 0; i < k1_barriers<C, F, T>(); ++i) __syncthreads();
-}
-
-// The reference-layout transform of one row by a team of T threads (whole
-// waves; t = thread index inside the team).  C = 1, F = 4096 (K = 4096) or
-// C = 12, F = 1024 (K = 12288).  buf is the team's LDS scratch (S::LDS
-// floats).  Every thread of the workgroup must call it (it contains
-// workgroup barriers); a team with live == false computes but stores nothing.
-template <int C, int F, int T>
-__device__ __forceinline__ void k1_row(const uint16_t* __restrict__ xr, const int8_t* __restrict__ signs,
-                                       int8_t* __restrict__ prow, uint16_t* __restrict__ srow,
-                                       float* __restrict__ buf, int t, bool live) {
-    using S = Shape<C, F, T>;
-    float a[S::L];  // a[s * LC + r]
-
-    // Phase-0 mapping: column c = t*LC + r (contiguous), loaded straight from HBM.
-#pragma unroll
-    for (int s = 0; s < C; ++s) {
-        const int base = s * F + t * S::LC;
-#pragma unroll
-        for (int r0 = 0; r0 < S::LC; r0 += 8) {
-            uint4 xv;
-            uint2 sv;
-            if constexpr (S::LC >= 8) {
-                xv = *reinterpret_cast<const uint4*>(xr + base + r0);
-                sv = *reinterpret_cast<const uint2*>(signs + base + r0);
-            } else {  // LC == 4 or 2
-                const uint2 h = *reinterpret_cast<const uint2*>(xr + base + r0);
-                xv = make_uint4(h.x, h.y, 0u, 0u);
-                sv = make_uint2(*reinterpret_cast<const uint32_t*>(signs + base + r0), 0u);
-            }
-            const uint32_t xw[4] = {xv.x, xv.y, xv.z, xv.w};
-            const uint32_t sw[2] = {sv.x, sv.y};
-#pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                if (r0 + i < S::LC) {
-                    const uint32_t h = (xw[i >> 1] >> (16 * (i & 1))) & 0xffffu;
-                    const int sg = (int)(int8_t)((sw[i >> 2] >> (8 * (i & 3))) & 0xffu);
-                    a[s * S::LC + r0 + i] = bf16_to_f32(h) * (float)sg;
-                }
-            }
-        }
-    }
-
-#pragma unroll
-    for (int p = 0; p < S::NP; ++p) {
-        const int w = window_of(p, S::B, S::LOGF);
-        if (p > 0) {
-            const int wp = window_of(p - 1, S::B, S::LOGF);
-#pragma unroll
-            for (int s = 0; s < C; ++s)
-#pragma unroll
-                for (int r = 0; r < S::LC; ++r)
-                    buf[lds_idx(s * F + col_of<S::B>(t, r, wp))] = a[s * S::LC + r];
-            __syncthreads();
-#pragma unroll
-            for (int s = 0; s < C; ++s)
-#pragma unroll
-                for (int r = 0; r < S::LC; ++r)
-                    a[s * S::LC + r] = buf[lds_idx(s * F + col_of<S::B>(t, r, w))];
-            __syncthreads();
-        }
-        const int first = p * S::B;
-        const int last = (first + S::B < S::LOGF) ? first + S::B : S::LOGF;
-#pragma unroll
-        for (int bit = first; bit < last; ++bit) {
-            const int rb = 1 << (bit - w);
-#pragma unroll
-            for (int s = 0; s < C; ++s)
-#pragma unroll
-                for (int r = 0; r < S::LC; ++r) {
-                    if ((r & rb) == 0) {
-                        const float lo = a[s * S::LC + r], hi = a[s * S::LC + r + rb];
-                        a[s * S::LC + r] = lo + hi;
-                        a[s * S::LC + r + rb] = lo - hi;
-                    }
-                }
-        }
-    }
-
-    const float norm = (F == 4096) ? 0x1p-6f : (F == 1024 ? 0x1p-5f : 0.0f);
-    static_assert(F == 4096 || F == 1024, "reference chunk sizes");
-#pragma unroll
-    for (int i = 0; i < S::L; ++i) a[i] = a[i] * norm;
-
-    if constexpr (C == 12) {
-        const float inv12 = 0x1.279a74p-2f;  // RN(1/sqrt 12)
-#pragma unroll
-        for (int r = 0; r < S::LC; ++r) {
-            float out[12];
-#pragma unroll
-            for (int d = 0; d < 12; ++d) {
-                float acc = 0.0f;
-#pragma unroll
-                for (int s = 0; s < 12; ++s) {
-                    const float v = a[s * S::LC + r];
-                    acc = acc + (paley_positive(s, d) ? v : -v);
-                }
-                out[d] = acc * inv12;
-            }
-#pragma unroll
-            for (int d = 0; d < 12; ++d) a[d * S::LC + r] = out[d];
-        }
-    }
-
-    // Back to contiguous units of 16 for quantization.
-    {
-        const int wl = window_of(S::NP - 1, S::B, S::LOGF);
-#pragma unroll
-        for (int s = 0; s < C; ++s)
-#pragma unroll
-            for (int r = 0; r < S::LC; ++r)
-                buf[lds_idx(s * F + col_of<S::B>(t, r, wl))] = a[s * S::LC + r];
+        for (int r = 0; r < 16; ++r) blk[swz(col_t(l, r))] = a[r] * 0x1p-5f;
     }
     __syncthreads();
-    // K/16 units of 16 values; when T does not divide them the last pass is
-    // taken by whole waves only (units and T are multiples of 64).
-    constexpr int UNITS = S::K / 16;
+    {
+        const int c = swz(t);
+        float v[12];
 #pragma unroll
-    for (int j = 0; j < (UNITS + T - 1) / T; ++j) {
-        const int u = t + j * T;
-        if (UNITS % T == 0 || u < UNITS) {
-            float v[16];
+        for (int s = 0; s < 12; ++s) v[s] = buf[s * 1024 + c];
+        const float inv12 = 0x1.279a74p-2f;  // RN(1/sqrt 12)
 #pragma unroll
-            for (int i = 0; i < 16; ++i) v[i] = buf[lds_idx(u * 16 + i)];
-            quantize16_store(v, prow + u * 8, srow + (u >> 3), (t & 7) == 0, live);
+        for (int d = 0; d < 12; ++d) {
+            float acc = v[0];
+#pragma unroll
+            for (int s = 1; s < 12; ++s) acc = paley_positive(s, d) ? acc + v[s] : acc - v[s];
+            buf[d * 1024 + c] = acc * inv12;
         }
     }
+    __syncthreads();
+    if (w < 12) {
+        float v[16];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) v[i] = buf[w * 1024 + swz(16 * l + i)];
+        quantize16_store(v, prow + 8 * t, srow + (t >> 3), (t & 7) == 0);
+    }
+}
+
+// K = 4096 (one 4096-point chunk) by 256 threads: each wave runs bits 0-9 of
+// its 1024-column quarter, one workgroup transpose brings bits 8-11 into
+// registers (thread t: columns t | r << 8).
+constexpr int K4_LDS = 4 * 1024;
+
+__device__ __forceinline__ void k1_row4096(const uint16_t* __restrict__ xr, const int8_t* __restrict__ signs,
+                                           int8_t* __restrict__ prow, uint16_t* __restrict__ srow,
+                                           float* __restrict__ buf) {
+    const int t = threadIdx.x, w = t >> 6, l = t & 63;
+    float a[16];
+    load_signed16(xr + w * 1024 + 16 * l, signs + w * 1024 + 16 * l, a);
+    float* blk = buf + w * 1024;
+    reg_butterflies(a);
+#pragma unroll
+    for (int r = 0; r < 16; ++r) blk[swz(16 * l + r)] = a[r];
+    wave_lds_sync();
+#pragma unroll
+    for (int r = 0; r < 16; ++r) a[r] = blk[swz(col_t(l, r))];
+    reg_butterflies(a);
+#pragma unroll
+    for (int r = 0; r < 16; ++r) blk[swz(col_t(l, r))] = a[r];
+    __syncthreads();
+    // register r: bits 0-1 -> column bits 8-9, bits 2-3 -> column bits 10-11.
+#pragma unroll
+    for (int r = 0; r < 16; ++r) a[r] = buf[(r >> 2) * 1024 + swz(t | ((r & 3) << 8))];
+    reg_butterflies(a);
+#pragma unroll
+    for (int r = 0; r < 16; ++r) buf[(r >> 2) * 1024 + swz(t | ((r & 3) << 8))] = a[r] * 0x1p-6f;
+    __syncthreads();
+    float v[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) v[i] = buf[w * 1024 + swz(16 * l + i)];
+    quantize16_store(v, prow + 8 * t, srow + (t >> 3), (t & 7) == 0);
 }
 
 }  // namespace

@@ -1,22 +1,27 @@
 // K1: fused randomized Hadamard transform + group-128 INT4 quantization +
-// nibble packing, for gfx950.  The reference-layout row transform lives in
-// k1_row.h (shared with the fused decode linear kernel); this file holds the
-// standalone kernels and the C ABI entry point.
+// nibble packing, for gfx950.  The reference-layout row transforms live in
+// k1_row.h; this file holds the kernels and the C ABI entry point.
 #include "k1_row.h"
 
 namespace nv4 {
 namespace {
 
-// One workgroup of T threads per row.
-template <int C, int F, int T>
-__global__ void __launch_bounds__(T)
-k1_reference(const uint16_t* __restrict__ x, const int8_t* __restrict__ signs,
-             int8_t* __restrict__ packed, uint16_t* __restrict__ scale) {
-    using S = Shape<C, F, T>;
-    __shared__ float buf[S::LDS];
+// K = 12288: one workgroup of 1024 threads per row.
+__global__ void __launch_bounds__(K12_THREADS)
+k1_k12288(const uint16_t* __restrict__ x, const int8_t* __restrict__ signs,
+          int8_t* __restrict__ packed, uint16_t* __restrict__ scale) {
+    __shared__ float buf[K12_LDS];
     const int64_t row = blockIdx.x;
-    k1_row<C, F, T>(x + row * S::K, signs, packed + row * (S::K / 2), scale + row * (S::K / 128), buf,
-                    threadIdx.x, true);
+    k1_row12288(x + row * 12288, signs, packed + row * 6144, scale + row * 96, buf);
+}
+
+// K = 4096: one workgroup of 256 threads per row.
+__global__ void __launch_bounds__(256)
+k1_k4096(const uint16_t* __restrict__ x, const int8_t* __restrict__ signs,
+         int8_t* __restrict__ packed, uint16_t* __restrict__ scale) {
+    __shared__ float buf[K4_LDS];
+    const int64_t row = blockIdx.x;
+    k1_row4096(x + row * 4096, signs, packed + row * 2048, scale + row * 32, buf);
 }
 
 // block128 layout: every aligned 128-block gets its own 128-point Sylvester
@@ -25,11 +30,10 @@ k1_reference(const uint16_t* __restrict__ x, const int8_t* __restrict__ signs,
 __global__ void __launch_bounds__(256)
 k1_block128(const uint16_t* __restrict__ x, const int8_t* __restrict__ signs,
             int8_t* __restrict__ packed, uint16_t* __restrict__ scale, int64_t units, int K) {
-    const int64_t u = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    // Out-of-range lanes recompute unit 0 so every shuffle partner exists;
-    // their results are never stored.
-    const bool live = u < units;
-    const int64_t uu = live ? u : 0;
+    const int64_t uu = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    // units is a multiple of 8, so the 8-lane groups that exchange values
+    // below are either wholly in range or wholly out.
+    if (uu >= units) return;
     const int kcol = (int)((uu * 16) % K);
     float a[16];
     {
@@ -67,16 +71,7 @@ k1_block128(const uint16_t* __restrict__ x, const int8_t* __restrict__ signs,
     const float norm = 0x1.6a09e6p-4f;  // RN(1/sqrt 128)
 #pragma unroll
     for (int i = 0; i < 16; ++i) a[i] = a[i] * norm;
-    // Every lane runs the shuffles; only live lanes store.
-    quantize16_store(a, packed + uu * 8, scale + (uu >> 3), (lane & 7) == 0, live);
-}
-
-template <int C, int F, int T>
-hipError_t launch_reference(const void* x, const int8_t* signs, int8_t* packed, void* scale,
-                            int64_t M, hipStream_t stream) {
-    hipLaunchKernelGGL((k1_reference<C, F, T>), dim3((unsigned)M), dim3(T), 0, stream,
-                       static_cast<const uint16_t*>(x), signs, packed, static_cast<uint16_t*>(scale));
-    return hipGetLastError();
+    quantize16_store(a, packed + uu * 8, scale + (uu >> 3), (lane & 7) == 0);
 }
 
 }  // namespace
@@ -92,8 +87,16 @@ extern "C" int nv4_rht_quant_pack(const void* x, const int8_t* signs, int8_t* pa
         return NV4_E_ALIGN;
     hipStream_t st = static_cast<hipStream_t>(stream);
     if (layout == NV4_LAYOUT_REFERENCE) {
-        if (K == 4096) return (int)launch_reference<1, 4096, 256>(x, signs, packed, scale, M, st);
-        if (K == 12288) return (int)launch_reference<12, 1024, 256>(x, signs, packed, scale, M, st);
+        const auto* xp = static_cast<const uint16_t*>(x);
+        auto* sp = static_cast<uint16_t*>(scale);
+        if (K == 4096) {
+            hipLaunchKernelGGL(k1_k4096, dim3((unsigned)M), dim3(256), 0, st, xp, signs, packed, sp);
+            return (int)hipGetLastError();
+        }
+        if (K == 12288) {
+            hipLaunchKernelGGL(k1_k12288, dim3((unsigned)M), dim3(K12_THREADS), 0, st, xp, signs, packed, sp);
+            return (int)hipGetLastError();
+        }
         return NV4_E_SHAPE;
     }
     if (layout == NV4_LAYOUT_BLOCK128) {

@@ -69,7 +69,7 @@ def check_case(fn, x_cpu, signs_cpu, layout="reference", gold_pair=None):
 
 
 @pytest.mark.parametrize("k", [4096, 12288])
-@pytest.mark.parametrize("m", [1, 7, 17, 31, 32, 33, 4096, 4097])
+@pytest.mark.parametrize("m", [1, 7, 17, 31, 32, 33, 64, 65, 200, 256, 257, 4096, 4097])
 def test_k1_exact(m, k):
     check_case(rht_quant_pack, make_input(m, k), W.signs(k, 20261108 + k))
 
@@ -86,6 +86,35 @@ def test_k1_exponent_extremes(m, k):
     x[-1].zero_()
     assert torch.isfinite(x).all()
     check_case(rht_quant_pack, x, W.signs(k, 7 + k))
+
+
+def coarse_rows(m, k, seed):
+    """Rows of a few small integers: their rotated values often sit exactly
+    on half-integer multiples of the group scale (quantization ties)."""
+    rng = np.random.default_rng(seed)
+    pool = np.array([0, 0, 0, 1, -1, 2, -2, 3], np.float32)
+    vals = rng.choice(pool, size=(m, k)) if seed % 2 else rng.integers(-1, 2, (m, k)).astype(np.float32)
+    return torch.from_numpy(vals).to(torch.bfloat16)
+
+
+def exact_ties(x_cpu, signs_cpu):
+    rotated = oracle.rht_rows(bf16_bits(x_cpu), signs_cpu.numpy())
+    _, scales = oracle.quantize_rows(rotated)
+    s = np.repeat(oracle.bf16_to_f32(scales).astype(np.float64), 128, axis=1)
+    q = rotated.astype(np.float64) / s
+    return int((np.abs(q - np.floor(q) - 0.5) == 0).sum())
+
+
+@pytest.mark.parametrize("seed", [1, 2])
+@pytest.mark.parametrize("k", [4096, 12288])
+def test_k1_quantization_ties(k, seed):
+    """Values exactly halfway between two codes round to the even code (IEEE
+    quotient, rint); the kernel's reciprocal fast path must hand them to the
+    exact division."""
+    x_cpu, signs_cpu = coarse_rows(33, k, seed), W.signs(k, seed)
+    if k == 4096:
+        assert exact_ties(x_cpu, signs_cpu) >= 50, "input no longer exercises ties"
+    check_case(rht_quant_pack, x_cpu, signs_cpu)
 
 
 @pytest.mark.parametrize("k", [4096, 12288])
