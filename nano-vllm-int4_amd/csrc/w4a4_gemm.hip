@@ -17,16 +17,17 @@
 // a group is irrelevant for an exact integer sum, so A and W are unpacked by
 // the same routine and fed to v_mfma_i32_*_i8 in matching lanes.
 //
-// Two kernels, no split-K, no atomics:
+// Three kernels, no split-K, no atomics:
 //  * k2_decode (M <= 64): one workgroup per 16 (or 32) output columns and all
 //    M rows.  Its eight waves each take one K-group per sub-round, compute
 //    the exact int32 group dots with v_mfma_i32_16x16x64_i8 and hand them to
 //    the whole workgroup through LDS, which runs the fp32 epilogue in group
 //    order.  Loads run several sub-rounds ahead.  The weight stream
 //    (N*K/2 bytes) dominates, so this kernel is HBM-bound.
-//  * k2_tiled (prefill): 128x128 output tile per workgroup, 2x2 waves of
-//    64x64 (2x2 v_mfma_i32_32x32x32_i8 blocks each), per-group epilogue in
-//    registers with the activation/weight scale tiles staged in LDS.
+//  * k2_wide (M <= 32, wide N): waves own column blocks over the whole K,
+//    activations widened once per CU into LDS.
+//  * k2_prefill (M > 64, w4a4_prefill.hip): LDS-staged 128x128 tiles.
+#include "k2_launch.h"
 #include "nv4_common.h"
 
 namespace nv4 {
@@ -417,140 +418,6 @@ k2_wide(const int8_t* __restrict__ a, const int8_t* __restrict__ w,
     }
 }
 
-// ----------------------------------------------------------------------------
-// Tiled kernel.  Workgroup tile 128 (M) x 128 (N); wave (wm, wn) owns rows
-// 64*wm.., columns 64*wn..; 2x2 blocks of 32x32.
-// MFMA 32x32x32 i8 layout: lane l supplies row (A) / column (W) l%32 and the
-// k-slots of half l/32.  Result: lane l holds C[8*(i/4) + 4*(l/32) + i%4][l%32].
-// Per group each lane reads 32 packed bytes (half l/32 of the 64-byte group)
-// for each of its rows/columns; MFMA j (0..3) takes bytes 8j..8j+7 of those.
-// ----------------------------------------------------------------------------
-constexpr int TBM = 128, TBN = 128;
-
-template <bool SW_GROUPED, bool OUT_F32>
-__global__ void __launch_bounds__(256)
-k2_tiled(const int8_t* __restrict__ a, const int8_t* __restrict__ w,
-         const uint16_t* __restrict__ sa, const uint16_t* __restrict__ sw,
-         void* __restrict__ out, int M, int N, int K) {
-    extern __shared__ uint16_t smem[];  // sa tile [G][TBM], then sw tile [G][TBN]
-    const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
-    const int wm = wave >> 1, wn = wave & 1;
-    const int m0 = blockIdx.y * TBM, n0 = blockIdx.x * TBN;
-    const int G = K >> 7;
-    const int64_t KB = K >> 1;
-    uint16_t* sa_t = smem;
-    uint16_t* sw_t = smem + G * TBM;
-
-    // Stage the scale tiles (transposed to [g][row]) once.
-    for (int i = threadIdx.x; i < G * TBM; i += 256) {
-        const int r = i / G, g = i - r * G;
-        const int m = m0 + r;
-        sa_t[g * TBM + r] = m < M ? sa[(int64_t)m * G + g] : (uint16_t)0;
-    }
-    if constexpr (SW_GROUPED) {
-        for (int i = threadIdx.x; i < G * TBN; i += 256) {
-            const int c = i / G, g = i - c * G;
-            const int n = n0 + c;
-            sw_t[g * TBN + c] = n < N ? sw[(int64_t)n * G + g] : (uint16_t)0;
-        }
-    }
-    __syncthreads();
-
-    const int rc = lane & 31, half = lane >> 5;
-    const int8_t* ap[2];
-    const int8_t* wp[2];
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-        const int r = min(m0 + wm * 64 + i * 32 + rc, M - 1);
-        ap[i] = a + (int64_t)r * KB + half * 32;
-        const int c = min(n0 + wn * 64 + i * 32 + rc, N - 1);
-        wp[i] = w + (int64_t)c * KB + half * 32;
-    }
-
-    float total[2][2][16];
-#pragma unroll
-    for (int i = 0; i < 2; ++i)
-#pragma unroll
-        for (int j = 0; j < 2; ++j)
-#pragma unroll
-            for (int v = 0; v < 16; ++v) total[i][j][v] = 0.0f;
-
-    for (int g = 0; g < G; ++g) {
-        uint4 av[2][2], wv[2][2];
-#pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            av[i][0] = *reinterpret_cast<const uint4*>(ap[i] + (int64_t)g * 64);
-            av[i][1] = *reinterpret_cast<const uint4*>(ap[i] + (int64_t)g * 64 + 16);
-            wv[i][0] = *reinterpret_cast<const uint4*>(wp[i] + (int64_t)g * 64);
-            wv[i][1] = *reinterpret_cast<const uint4*>(wp[i] + (int64_t)g * 64 + 16);
-        }
-        v16i acc[2][2];
-#pragma unroll
-        for (int i = 0; i < 2; ++i)
-#pragma unroll
-            for (int j = 0; j < 2; ++j)
-#pragma unroll
-                for (int v = 0; v < 16; ++v) acc[i][j][v] = 0;
-#pragma unroll
-        for (int s = 0; s < 4; ++s) {
-            v4i ao[2], wo[2];
-#pragma unroll
-            for (int i = 0; i < 2; ++i) {
-                const uint4 q = av[i][s >> 1];
-                ao[i] = (s & 1) ? unpack8_x16(q.z, q.w) : unpack8_x16(q.x, q.y);
-                const uint4 r = wv[i][s >> 1];
-                wo[i] = (s & 1) ? unpack8_x16(r.z, r.w) : unpack8_x16(r.x, r.y);
-            }
-#pragma unroll
-            for (int i = 0; i < 2; ++i)
-#pragma unroll
-                for (int j = 0; j < 2; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(ao[i], wo[j], acc[i][j], 0, 0, 0);
-        }
-        // Epilogue for group g.
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            const int cl = wn * 64 + j * 32 + rc;  // column within the tile
-            float s_w = 0.0f;
-            if constexpr (SW_GROUPED) s_w = bf16_to_f32(sw_t[g * TBN + cl]);
-#pragma unroll
-            for (int i = 0; i < 2; ++i) {
-#pragma unroll
-                for (int v = 0; v < 16; ++v) {
-                    const int rl = wm * 64 + i * 32 + 8 * (v >> 2) + 4 * half + (v & 3);
-                    const float s_a = bf16_to_f32(sa_t[g * TBM + rl]);
-                    const float d = (float)(acc[i][j][v] >> 8);
-                    if constexpr (SW_GROUPED) {
-                        const float s = s_a * s_w;
-                        total[i][j][v] = __builtin_fmaf(d, s, total[i][j][v]);
-                    } else {
-                        total[i][j][v] = __builtin_fmaf(d, s_a, total[i][j][v]);
-                    }
-                }
-            }
-        }
-    }
-
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-        const int n = n0 + wn * 64 + j * 32 + rc;
-        float swn = 1.0f;
-        if constexpr (!SW_GROUPED) swn = bf16_to_f32(sw[min(n, N - 1)]);
-#pragma unroll
-        for (int i = 0; i < 2; ++i)
-#pragma unroll
-            for (int v = 0; v < 16; ++v) {
-                const int m = m0 + wm * 64 + i * 32 + 8 * (v >> 2) + 4 * half + (v & 3);
-                if (m < M && n < N) {
-                    float val = total[i][j][v];
-                    if constexpr (!SW_GROUPED) val = val * swn;
-                    store_out<OUT_F32>(out, (int64_t)m * N + n, val);
-                }
-            }
-    }
-}
-
 template <int MB, int NB, bool SG, bool OF>
 hipError_t launch_decode(const int8_t* a, const int8_t* w, const void* sa, const void* sw, void* out,
                          int M, int N, int K, hipStream_t st) {
@@ -609,17 +476,6 @@ hipError_t launch_wide(const int8_t* a, const int8_t* w, const void* sa, const v
 }
 
 template <bool SG, bool OF>
-hipError_t launch_tiled(const int8_t* a, const int8_t* w, const void* sa, const void* sw, void* out,
-                        int M, int N, int K, hipStream_t st) {
-    const int G = K / 128;
-    const size_t lds = (size_t)G * (TBM + TBN) * sizeof(uint16_t);
-    dim3 grid((unsigned)((N + TBN - 1) / TBN), (unsigned)((M + TBM - 1) / TBM));
-    hipLaunchKernelGGL((k2_tiled<SG, OF>), grid, dim3(256), lds, st, a, w, static_cast<const uint16_t*>(sa),
-                       static_cast<const uint16_t*>(sw), out, M, N, K);
-    return hipGetLastError();
-}
-
-template <bool SG, bool OF>
 hipError_t dispatch(const int8_t* a, const int8_t* w, const void* sa, const void* sw, void* out,
                     int M, int N, int K, hipStream_t st) {
     // Wide N: waves own column blocks, activations fetched once per CU.
@@ -636,7 +492,7 @@ hipError_t dispatch(const int8_t* a, const int8_t* w, const void* sa, const void
                              : launch_decode<2, 1, SG, OF>(a, w, sa, sw, out, M, N, K, st);
     if (M <= 48) return launch_decode<3, 1, SG, OF>(a, w, sa, sw, out, M, N, K, st);
     if (M <= 64) return launch_decode<4, 1, SG, OF>(a, w, sa, sw, out, M, N, K, st);
-    return launch_tiled<SG, OF>(a, w, sa, sw, out, M, N, K, st);
+    return k2_prefill_launch(a, w, sa, sw, SG, out, OF, M, N, K, st);
 }
 
 }  // namespace
@@ -661,13 +517,11 @@ extern "C" int nv4_w4a4_gemm(const int8_t* a, const int8_t* w, const void* sa, c
     if (M < 1 || N < 1 || K < 128 || K % 128 || N % 8) return NV4_E_SHAPE;
     if (M > 0x7fffffffLL || N > 0x7fffffffLL || K > (1LL << 20)) return NV4_E_SHAPE;
     if (M * (K / 128) > 0x7fffffffLL || N * (K / 128) > 0x7fffffffLL) return NV4_E_SHAPE;
-    if ((M + 127) / 128 > 65535) return NV4_E_SHAPE;
+    if (((M + 127) / 128) * ((N + 127) / 128) > 0x7fffffffLL) return NV4_E_SHAPE;
     if (reinterpret_cast<uintptr_t>(a) % 16 || reinterpret_cast<uintptr_t>(w) % 16 ||
         reinterpret_cast<uintptr_t>(sa) % 2 || reinterpret_cast<uintptr_t>(sw) % 2 ||
         reinterpret_cast<uintptr_t>(out) % (out_fp32 ? 4 : 2))
         return NV4_E_ALIGN;
-    // The tiled kernel stages G*(128+128) bf16 scales in LDS (<= 64 KiB).
-    if (M > 64 && (K / 128) * (TBM + TBN) * 2 > 64 * 1024) return NV4_E_SHAPE;
     hipStream_t st = static_cast<hipStream_t>(stream);
     const int m = (int)M, n = (int)N, k = (int)K;
     hipError_t e;

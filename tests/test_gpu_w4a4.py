@@ -177,3 +177,54 @@ def test_k2_chain_qwen3_shapes_m4096_sampled(proj):
     assert np.array_equal(packed.cpu().numpy()[rows], p_ref)
     assert np.array_equal(bf16_bits(scale)[rows], s_ref)
     assert_bits_equal(bf16_bits(out)[rows], o_ref, f"{proj} M=4096 sampled rows")
+
+
+def extreme_scales(rng, rows, G, frac=0.05):
+    """bf16 scale bits: ordinary values with a sprinkling of tiny normals
+    (2^-126), bf16 subnormals (2^-133), huge values (2^70) and zeros, so the
+    scale product can underflow to an fp32 subnormal or exceed 2^63."""
+    s = oracle.f32_to_bf16((rng.random((rows, G)) * 0.5 + 0.01).astype(np.float32))
+    special = np.array([0x0080, 0x0001, 0x62800000 >> 16, 0x0000, 0x0081], dtype=np.uint16)
+    pick = rng.random((rows, G)) < frac
+    s[pick] = special[rng.integers(0, len(special), pick.sum())]
+    return s
+
+
+@pytest.mark.parametrize("M,N,K,rows_special", [(200, 264, 1024, True), (257, 392, 2048, False),
+                                                 (150, 136, 12288, True)])
+def test_k2_prefill_extreme_scales(M, N, K, rows_special):
+    """Prefill tiles whose scales leave the range where the kernel folds the
+    x256 of the widened nibbles into the activation scale must take the
+    literal per-group sequence; tiles next to them keep the short form.
+    Only some rows (or some columns) carry the special values, so both forms
+    run in one launch.  Bit-exact in bf16 and fp32."""
+    print(f"[k2-extreme] M={M} N={N} K={K}", flush=True)
+    rng = np.random.default_rng(M * 7 + K)
+    ap, wp, _, _ = gemm_inputs(M, N, K, M + N + K)
+    G = K // 128
+    sa = oracle.f32_to_bf16((rng.random((M, G)) * 2 + 0.01).astype(np.float32))
+    sw = oracle.f32_to_bf16((rng.random((N, G)) * 0.03 + 0.001).astype(np.float32))
+    if rows_special:
+        sa[130:] = extreme_scales(rng, M - 130, G)
+    else:
+        sw[:128] = extreme_scales(rng, 128, G)
+    for out_fp32 in (False, True):
+        exp = oracle.w4a4_gemm(ap, wp, sa, sw, out_fp32=out_fp32)
+        a, w, s_a, s_w = to_dev(ap, wp, sa, sw)
+        if out_fp32:
+            out = torch.full((M, N), float("nan"), device=DEV, dtype=torch.float32)
+            compile_grouped_gemm(M, N, K, output_fp32=True, weight_grouped=True)(a, w, s_a, s_w, out)
+            torch.cuda.synchronize()
+            assert_bits_equal(out.cpu().numpy().view(np.uint32), exp.view(np.uint32), "fp32 output")
+        else:
+            out = w4a4_grouped_gemm(a, w, s_a, s_w)
+            torch.cuda.synchronize()
+            assert_bits_equal(bf16_bits(out), exp, "bf16 output")
+
+
+@pytest.mark.parametrize("M,N,K", [(1000, 1032, 512), (300, 520, 1024), (4096, 264, 2048)])
+def test_k2_prefill_tile_orders(M, N, K):
+    """Every output of prefill launches whose tile counts are (72, 15, 96) --
+    divisible by the 8 XCDs or not -- so every tile of both orderings is
+    written exactly once and lands where it belongs."""
+    run_case(M, N, K, 7000 + M + N)
