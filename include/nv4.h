@@ -22,6 +22,8 @@
  *                          (rht_quant_pack + w4a4_grouped_gemm)
  *   nv4_w4a16_gemm      <- nanovllm/layers/linear_w4a16.py:11 tl_dequant_matmul_w4a16
  *                          (called from W4A16Linear.forward :128-148)
+ *   nv4_paged_decode_attention <- flash_attn_with_kvcache in the decode branch of
+ *                          nanovllm/layers/attention.py:72-74 (caller of the hot path)
  */
 #ifndef NV4_H
 #define NV4_H
@@ -117,6 +119,25 @@ int nv4_w4a4_linear(const void* x, const int8_t* signs, const int8_t* w, const v
 int nv4_w4a16_gemm(const void* x, int x_dtype, const int32_t* qweight, const int32_t* qzeros,
                    const void* scales, void* out, int out_dtype,
                    int64_t M, int64_t N, int64_t K, int group, void* stream);
+
+/*
+ * Paged decode attention (one new token per sequence; GQA).
+ * Replaces flash_attn_with_kvcache(q, k_cache, v_cache, cache_seqlens, block_table,
+ * softmax_scale, causal=True) in nanovllm/layers/attention.py:72-74.
+ *   q             bf16 [B, Hq, 128]: rows q_row_stride elements apart (>= Hq*128, multiple of 8)
+ *   k/v_cache     bf16 [num_blocks, block_size, Hkv, 128]
+ *   block_tables  int32 [B, max_blocks]: the first ceil(context_lens[b]/block_size)
+ *                 entries of row b are valid block indices
+ *   context_lens  int32 [B], 1 <= context_lens[b] <= max_context
+ *   out           bf16 [B, Hq, 128] (contiguous)
+ *   workspace     fp32 scratch of at least B*Hq*S*(128+2)*4 bytes, S = ceil(max_context/256)
+ * Hq / Hkv in {1, 2, 4}; softmax(scale * q.K^T) V with fp32 arithmetic.
+ */
+int nv4_paged_decode_attention(const void* q, int64_t q_row_stride, const void* k_cache, const void* v_cache,
+                               const int32_t* block_tables, int64_t max_blocks, const int32_t* context_lens,
+                               void* out, float* workspace, int64_t workspace_bytes, int64_t B, int64_t Hq,
+                               int64_t Hkv, int64_t D, int64_t block_size, int64_t max_context, float scale,
+                               void* stream);
 
 /* Library version string. */
 const char* nv4_version(void);

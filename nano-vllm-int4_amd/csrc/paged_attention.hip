@@ -1,0 +1,263 @@
+// Paged decode attention for the Qwen3 decoder (GQA, head_dim 128, bf16 KV
+// cache), gfx950.  Replaces flash_attn_with_kvcache in the reference's
+// decode branch (nanovllm/layers/attention.py:72-74): for every sequence b
+// and query head h, o = softmax(scale * q . K^T) V over the first
+// context_lens[b] cache slots of the sequence, found through its block table.
+//
+// Decode attention reads the whole KV context of every sequence once per
+// step, so it is bound by HBM bandwidth; the kernel is laid out for streaming:
+//  * pass 1: one workgroup (4 waves) per (sequence, KV head, split of 256
+//    context tokens).  Wave w takes tokens 64w..64w+63 of the split; within a
+//    wave, lane group g (16 lanes) owns tokens 16g..16g+15 in four rounds of
+//    four, and lane j of a group owns head dims 8j..8j+7, so every K and V row
+//    of a token (256 contiguous bytes per KV head) is read as one coalesced
+//    piece.  The G query heads that share the KV head stay in registers,
+//    pre-multiplied by scale * log2(e), so the softmax runs in base 2.
+//    Scores are reduced over a group's 16 lanes with DPP, and each group
+//    keeps an online-softmax state (max m, sum l, output o) per head; the
+//    next round's loads are issued before the current round's arithmetic.
+//    The 16 group states of the workgroup are merged through LDS and written
+//    to the split workspace (or, for a single split, normalised into out).
+//  * pass 2: one workgroup per (sequence, query head) merges the splits:
+//    M = max m_s, w_s = 2^(m_s - M), o = sum w_s o_s / sum w_s l_s.
+#include "nv4_common.h"
+
+namespace nv4 {
+namespace {
+
+constexpr int PA_D = 128;        // head dim
+constexpr int PA_SPLIT = 256;    // context tokens per pass-1 workgroup
+constexpr int PA_THREADS = 256;  // 4 waves x 64 tokens
+
+constexpr int DPP_QUAD_XOR1 = 0xB1;
+constexpr int DPP_QUAD_XOR2 = 0x4E;
+constexpr int DPP_HALF_MIRROR = 0x141;
+constexpr int DPP_MIRROR = 0x140;
+
+template <int CTRL>
+__device__ __forceinline__ float pa_dpp(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, true));
+}
+
+// Sum over the 16 lanes of a DPP row (every lane gets the sum).
+__device__ __forceinline__ float row16_sum(float v) {
+    v += pa_dpp<DPP_QUAD_XOR1>(v);
+    v += pa_dpp<DPP_QUAD_XOR2>(v);
+    v += pa_dpp<DPP_HALF_MIRROR>(v);
+    v += pa_dpp<DPP_MIRROR>(v);
+    return v;
+}
+
+__device__ __forceinline__ void bf16x8_to_f32(const v4u& w, float (&f)[8]) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        f[2 * i] = __uint_as_float(w[i] << 16);
+        f[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+    }
+}
+
+template <int G>
+__global__ void __launch_bounds__(PA_THREADS)
+pa_split(const uint16_t* __restrict__ q, int64_t q_row, const uint16_t* __restrict__ kc,
+         const uint16_t* __restrict__ vc, const int32_t* __restrict__ block_tables, int max_blocks,
+         const int32_t* __restrict__ context_lens, uint16_t* __restrict__ out, float* __restrict__ part_o,
+         float* __restrict__ part_ml, int Hkv, int bs, int S, int max_ctx, float qscale) {
+    const int s = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
+    const int Hq = Hkv * G;
+    const int ctx = min(context_lens[b], max_ctx);  // never past the block table's row
+    const int start = s * PA_SPLIT;
+    if (start >= ctx) return;  // nothing of this sequence here; pass 2 skips the split
+    const int end = min(start + PA_SPLIT, ctx);
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const int g = lane >> 4, j = lane & 15;
+
+    __shared__ float sm_m[16][G], sm_l[16][G];
+    __shared__ float sm_o[16][G][PA_D];
+
+    // Query heads kvh*G .. kvh*G+G-1, dims 8j..8j+7, scaled into base 2.
+    float qv[G][8];
+#pragma unroll
+    for (int h = 0; h < G; ++h) {
+        const v4u w = *reinterpret_cast<const v4u*>(q + (int64_t)b * q_row + (int64_t)(kvh * G + h) * PA_D + 8 * j);
+        float f[8];
+        bf16x8_to_f32(w, f);
+#pragma unroll
+        for (int d = 0; d < 8; ++d) qv[h][d] = f[d] * qscale;
+    }
+    const int32_t* bt = block_tables + (int64_t)b * max_blocks;
+    const int tok0 = start + wave * 64 + g * 16;  // this group's first token
+    // Element offset of token tt's row for this KV head and lane (clamped
+    // into the sequence so every load stays in its own valid slots).
+    auto row_off = [&](int tt) {
+        const int c = min(tt, ctx - 1);
+        const int64_t slot = (int64_t)bt[c / bs] * bs + c % bs;
+        return (slot * Hkv + kvh) * PA_D + 8 * j;
+    };
+
+    float m[G], l[G], o[G][8];
+#pragma unroll
+    for (int h = 0; h < G; ++h) {
+        m[h] = -__builtin_inff();
+        l[h] = 0.0f;
+#pragma unroll
+        for (int d = 0; d < 8; ++d) o[h][d] = 0.0f;
+    }
+
+    v4u kb[2][4], vb[2][4];
+    auto issue = [&](int r, int buf) {
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int64_t off = row_off(tok0 + 4 * r + u);
+            kb[buf][u] = *reinterpret_cast<const v4u*>(kc + off);
+            vb[buf][u] = *reinterpret_cast<const v4u*>(vc + off);
+        }
+    };
+    issue(0, 0);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const int buf = r & 1;
+        if (r + 1 < 4) issue(r + 1, buf ^ 1);
+        float sc[4][G];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            float kf[8];
+            bf16x8_to_f32(kb[buf][u], kf);
+            const bool live = tok0 + 4 * r + u < end;
+#pragma unroll
+            for (int h = 0; h < G; ++h) {
+                float p = 0.0f;
+#pragma unroll
+                for (int d = 0; d < 8; ++d) p = __builtin_fmaf(qv[h][d], kf[d], p);
+                p = row16_sum(p);
+                sc[u][h] = live ? p : -__builtin_inff();
+            }
+        }
+#pragma unroll
+        for (int h = 0; h < G; ++h) {
+            float mx = fmaxf(fmaxf(sc[0][h], sc[1][h]), fmaxf(sc[2][h], sc[3][h]));
+            const float m_new = fmaxf(m[h], mx);
+            // a group whose tokens are all past the end keeps m = -inf: no update
+            const float corr = m_new == -__builtin_inff() ? 1.0f : __builtin_amdgcn_exp2f(m[h] - m_new);
+            float p[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u)
+                p[u] = m_new == -__builtin_inff() ? 0.0f : __builtin_amdgcn_exp2f(sc[u][h] - m_new);
+            l[h] = l[h] * corr + (p[0] + p[1]) + (p[2] + p[3]);
+            m[h] = m_new;
+#pragma unroll
+            for (int d = 0; d < 8; ++d) o[h][d] *= corr;
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                float vf[8];
+                bf16x8_to_f32(vb[buf][u], vf);
+#pragma unroll
+                for (int d = 0; d < 8; ++d) o[h][d] = __builtin_fmaf(p[u], vf[d], o[h][d]);
+            }
+        }
+    }
+
+    // Merge the 16 group states of the workgroup.
+    const int gs = wave * 4 + g;
+#pragma unroll
+    for (int h = 0; h < G; ++h) {
+        if (j == 0) {
+            sm_m[gs][h] = m[h];
+            sm_l[gs][h] = l[h];
+        }
+#pragma unroll
+        for (int d = 0; d < 8; ++d) sm_o[gs][h][8 * j + d] = o[h][d];
+    }
+    __syncthreads();
+    for (int e = t; e < G * PA_D; e += PA_THREADS) {
+        const int h = e / PA_D, d = e % PA_D;
+        float M = -__builtin_inff();
+#pragma unroll
+        for (int k = 0; k < 16; ++k) M = fmaxf(M, sm_m[k][h]);
+        float L = 0.0f, O = 0.0f;
+#pragma unroll
+        for (int k = 0; k < 16; ++k) {
+            const float w = sm_m[k][h] == -__builtin_inff() ? 0.0f : __builtin_amdgcn_exp2f(sm_m[k][h] - M);
+            L = __builtin_fmaf(w, sm_l[k][h], L);
+            O = __builtin_fmaf(w, sm_o[k][h][d], O);
+        }
+        const int hq = kvh * G + h;
+        if (S == 1) {
+            out[((int64_t)b * Hq + hq) * PA_D + d] = (uint16_t)f32_to_bf16_rne(O / L);
+        } else {
+            const int64_t ps = ((int64_t)b * Hq + hq) * S + s;
+            part_o[ps * PA_D + d] = O;
+            if (d == 0) {
+                part_ml[ps * 2] = M;
+                part_ml[ps * 2 + 1] = L;
+            }
+        }
+    }
+}
+
+__global__ void __launch_bounds__(PA_D)
+pa_merge(const int32_t* __restrict__ context_lens, const float* __restrict__ part_o,
+         const float* __restrict__ part_ml, uint16_t* __restrict__ out, int Hq, int S, int max_ctx) {
+    const int hq = blockIdx.x, b = blockIdx.y, d = threadIdx.x;
+    const int n = min(S, (min(context_lens[b], max_ctx) + PA_SPLIT - 1) / PA_SPLIT);
+    const int64_t base = ((int64_t)b * Hq + hq) * S;
+    float M = -__builtin_inff();
+    for (int s = 0; s < n; ++s) M = fmaxf(M, part_ml[(base + s) * 2]);
+    float L = 0.0f, O = 0.0f;
+    for (int s = 0; s < n; ++s) {
+        const float w = __builtin_amdgcn_exp2f(part_ml[(base + s) * 2] - M);
+        L = __builtin_fmaf(w, part_ml[(base + s) * 2 + 1], L);
+        O = __builtin_fmaf(w, part_o[(base + s) * PA_D + d], O);
+    }
+    out[((int64_t)b * Hq + hq) * PA_D + d] = (uint16_t)f32_to_bf16_rne(O / L);
+}
+
+template <int G>
+hipError_t pa_launch(const void* q, int64_t q_row, const void* kc, const void* vc, const int32_t* bt, int max_blocks,
+                     const int32_t* cl, void* out, float* ws, int B, int Hkv, int bs, int S, int max_ctx,
+                     float qscale, hipStream_t st) {
+    float* part_o = ws;
+    float* part_ml = ws + (int64_t)B * Hkv * G * S * PA_D;
+    hipLaunchKernelGGL((pa_split<G>), dim3((unsigned)S, (unsigned)Hkv, (unsigned)B), dim3(PA_THREADS), 0, st,
+                       static_cast<const uint16_t*>(q), q_row, static_cast<const uint16_t*>(kc),
+                       static_cast<const uint16_t*>(vc), bt, max_blocks, cl, static_cast<uint16_t*>(out), part_o,
+                       part_ml, Hkv, bs, S, max_ctx, qscale);
+    if (S > 1)
+        hipLaunchKernelGGL(pa_merge, dim3((unsigned)(Hkv * G), (unsigned)B), dim3(PA_D), 0, st, cl, part_o, part_ml,
+                           static_cast<uint16_t*>(out), Hkv * G, S, max_ctx);
+    return hipGetLastError();
+}
+
+}  // namespace
+}  // namespace nv4
+
+extern "C" int nv4_paged_decode_attention(const void* q, int64_t q_row_stride, const void* k_cache,
+                                          const void* v_cache, const int32_t* block_tables, int64_t max_blocks,
+                                          const int32_t* context_lens, void* out, float* workspace,
+                                          int64_t workspace_bytes, int64_t B, int64_t Hq, int64_t Hkv, int64_t D,
+                                          int64_t block_size, int64_t max_context, float scale, void* stream) {
+    using namespace nv4;
+    if (!q || !k_cache || !v_cache || !block_tables || !context_lens || !out || !workspace) return NV4_E_NULL;
+    if (D != PA_D || B < 1 || Hkv < 1 || Hq < 1 || Hq % Hkv || block_size < 1 || max_blocks < 1 ||
+        max_context < 1 || max_context > max_blocks * block_size || B > 65535 || Hkv > 65535 ||
+        q_row_stride < Hq * D)
+        return NV4_E_SHAPE;
+    const int64_t G = Hq / Hkv;
+    if (G != 1 && G != 2 && G != 4) return NV4_E_SHAPE;  // the merge keeps 16 x G x 128 fp32 in LDS
+    const int64_t S = (max_context + PA_SPLIT - 1) / PA_SPLIT;
+    if (workspace_bytes < B * Hq * S * (D + 2) * 4) return NV4_E_SHAPE;
+    if (reinterpret_cast<uintptr_t>(q) % 16 || reinterpret_cast<uintptr_t>(k_cache) % 16 ||
+        reinterpret_cast<uintptr_t>(v_cache) % 16 || reinterpret_cast<uintptr_t>(out) % 2 ||
+        reinterpret_cast<uintptr_t>(workspace) % 4 || q_row_stride % 8)
+        return NV4_E_ALIGN;
+    const float qscale = scale * 1.4426950408889634f;  // log2(e): softmax in base 2
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    const int b = (int)B, hkv = (int)Hkv, bs = (int)block_size, s = (int)S, mb = (int)max_blocks;
+    switch (G) {
+        case 1: return (int)pa_launch<1>(q, q_row_stride, k_cache, v_cache, block_tables, mb, context_lens, out,
+                                         workspace, b, hkv, bs, s, (int)max_context, qscale, st);
+        case 2: return (int)pa_launch<2>(q, q_row_stride, k_cache, v_cache, block_tables, mb, context_lens, out,
+                                         workspace, b, hkv, bs, s, (int)max_context, qscale, st);
+        default: return (int)pa_launch<4>(q, q_row_stride, k_cache, v_cache, block_tables, mb, context_lens, out,
+                                          workspace, b, hkv, bs, s, (int)max_context, qscale, st);
+    }
+}

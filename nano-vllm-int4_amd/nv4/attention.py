@@ -1,0 +1,111 @@
+"""Paged-KV attention for the Qwen3 decoder on MI355X.
+
+Replaces the reference's Attention (nanovllm/layers/attention.py:44-75),
+whose KV store is a Triton kernel and whose attention is flash-attn, neither
+of which this build uses:
+
+* KV store: each new token's K and V rows go to ``slot_mapping`` slots of
+  the caches ``[num_blocks, block_size, num_kv_heads, head_dim]`` (the
+  reference's store_kvcache, :10-40; slots of -1 are skipped there and never
+  produced here).
+* Prefill (causal, GQA): ``scaled_dot_product_attention`` restricted to its
+  fused flash kernel, one call per sequence of the batch (it raises rather
+  than fall back to the unfused path).
+* Decode: ``paged_decode_attention``, the HIP kernel ``nv4_paged_decode_attention``
+  (split over the context, one workgroup per (sequence, KV head, split);
+  online softmax in fp32; a second pass merges the splits).
+"""
+from __future__ import annotations
+
+import ctypes
+
+import torch
+import torch.nn.functional as F
+from torch import nn
+
+from . import _lib
+from .utils.context import get_context
+
+SPLIT_TOKENS = 256  # context tokens per decode workgroup
+
+
+def decode_workspace(batch: int, num_heads: int, max_context: int, head_dim: int, device) -> torch.Tensor:
+    """fp32 scratch for the split partials of ``paged_decode_attention``."""
+    splits = (max_context + SPLIT_TOKENS - 1) // SPLIT_TOKENS
+    return torch.empty(batch * num_heads * splits * (head_dim + 2), dtype=torch.float32, device=device)
+
+
+def paged_decode_attention(q, k_cache, v_cache, block_tables, context_lens, scale, out=None, workspace=None,
+                           max_context=None):
+    """q [B, Hq, D] bf16 (rows may be strided), caches [nb, bs, Hkv, D] bf16,
+    block_tables [B, max_blocks] int32, context_lens [B] int32 -> [B, Hq, D] bf16.
+    ``max_context`` bounds every context length (default: the block table's
+    capacity)."""
+    B, Hq, D = q.shape
+    nb, bs, Hkv, Dk = k_cache.shape
+    if q.dtype != torch.bfloat16 or k_cache.dtype != torch.bfloat16 or v_cache.dtype != torch.bfloat16:
+        raise TypeError("q and the caches must be BF16")
+    if (Dk != D or v_cache.shape != k_cache.shape or block_tables.dtype != torch.int32
+            or context_lens.dtype != torch.int32 or tuple(context_lens.shape) != (B,)
+            or block_tables.shape[0] != B or q.stride(2) != 1 or q.stride(1) != D):
+        raise ValueError("Inconsistent paged attention arguments")
+    if max_context is None:
+        max_context = block_tables.shape[1] * bs
+    if out is None:
+        out = torch.empty((B, Hq, D), dtype=torch.bfloat16, device=q.device)
+    if workspace is None:
+        workspace = decode_workspace(B, Hq, max_context, D, q.device)
+    lib = _lib.load()
+    stream = torch.cuda.current_stream(q.device).cuda_stream
+    with torch.cuda.device(q.device):
+        rc = lib.nv4_paged_decode_attention(
+            ctypes.c_void_p(q.data_ptr()), q.stride(0), ctypes.c_void_p(k_cache.data_ptr()),
+            ctypes.c_void_p(v_cache.data_ptr()), ctypes.c_void_p(block_tables.data_ptr()), block_tables.shape[1],
+            ctypes.c_void_p(context_lens.data_ptr()), ctypes.c_void_p(out.data_ptr()),
+            ctypes.c_void_p(workspace.data_ptr()), workspace.numel() * 4, B, Hq, Hkv, D, bs, max_context,
+            ctypes.c_float(scale), ctypes.c_void_p(stream))
+    _lib.check(rc, "paged_decode_attention")
+    return out
+
+
+def store_kvcache(key, value, k_cache, v_cache, slot_mapping):
+    N = key.shape[0]
+    kc, vc = k_cache.view(-1, key.shape[1] * key.shape[2]), v_cache.view(-1, value.shape[1] * value.shape[2])
+    idx = slot_mapping.to(torch.int64)
+    kc.index_copy_(0, idx, key.reshape(N, -1))
+    vc.index_copy_(0, idx, value.reshape(N, -1))
+
+
+def prefill_attention(q, k, v, seqlens, scale):
+    """Causal GQA attention over packed sequences of lengths ``seqlens``
+    (q [T, Hq, D], k/v [T, Hkv, D]) with the fused flash kernel only."""
+    from torch.nn.attention import SDPBackend, sdpa_kernel
+    out = torch.empty_like(q)
+    start = 0
+    with sdpa_kernel([SDPBackend.FLASH_ATTENTION]):
+        for n in seqlens:
+            qs = q[start:start + n].transpose(0, 1).unsqueeze(0)
+            ks = k[start:start + n].transpose(0, 1).unsqueeze(0)
+            vs = v[start:start + n].transpose(0, 1).unsqueeze(0)
+            o = F.scaled_dot_product_attention(qs, ks, vs, is_causal=True, scale=scale, enable_gqa=True)
+            out[start:start + n] = o.squeeze(0).transpose(0, 1)
+            start += n
+    return out
+
+
+class Attention(nn.Module):
+    def __init__(self, num_heads, head_dim, scale, num_kv_heads):
+        super().__init__()
+        self.num_heads, self.head_dim, self.scale, self.num_kv_heads = num_heads, head_dim, scale, num_kv_heads
+        self.k_cache = self.v_cache = torch.tensor([])
+        self.workspace = None  # set by the runner for decode
+        self.max_context = None
+
+    def forward(self, q, k, v):
+        ctx = get_context()
+        if self.k_cache.numel() and self.v_cache.numel():
+            store_kvcache(k, v, self.k_cache, self.v_cache, ctx.slot_mapping)
+        if ctx.is_prefill:
+            return prefill_attention(q, k, v, ctx.seqlens_q, self.scale)
+        return paged_decode_attention(q, self.k_cache, self.v_cache, ctx.block_tables, ctx.context_lens,
+                                      self.scale, workspace=self.workspace, max_context=self.max_context)

@@ -1,0 +1,234 @@
+"""A fixed-batch runner for the end-to-end decode workload of the quantized path.
+
+It reproduces the steps the reference's engine takes for its latency
+benchmark (benchmarks/bench_nano_latency.py:32-121 on nanovllm/engine/*):
+requests are prefilled one at a time (serial prefill, each prompt one
+forward), then the whole batch decodes together, one token per sequence per
+step, the decode forward replayed from a HIP graph captured for that batch
+size (nanovllm/engine/model_runner.py:211-276).  A step prepares the
+inputs on the host and copies them in (:144-203), runs the model, the LM
+head on each sequence's last hidden state and the Gumbel-max sampler at the
+request temperature (nanovllm/layers/sampler.py:7-12), and returns the
+tokens to the host; the decode step time is measured around all of it,
+and decode tokens/s = batch * 1000 / mean step ms over the pure-decode
+steps (bench_nano_latency.py:118).
+
+Scope: a fixed set of requests that all fit (the reference's continuous
+batching, preemption and prefix cache are outside the quantized path), the
+KV cache laid out as ``max_num_seqs`` contiguous runs of blocks (sequence
+slot s owns blocks s*B .. s*B+B-1), and one GPU.
+"""
+from __future__ import annotations
+
+import math
+import time
+
+import torch
+
+from .attention import decode_workspace
+from .layers.linear_w4a4 import W4A4Linear
+from .qwen3 import BF16Linear, Qwen3ForCausalLM
+from .utils.context import get_context, reset_context, set_context
+
+
+def qwen3_8b_config(num_hidden_layers: int = 36):
+    """Qwen3-8B dimensions (random weights: nothing is downloaded)."""
+    from transformers import Qwen3Config
+    return Qwen3Config(vocab_size=151936, hidden_size=4096, intermediate_size=12288,
+                       num_hidden_layers=num_hidden_layers, num_attention_heads=32, num_key_value_heads=8,
+                       head_dim=128, max_position_embeddings=40960, rms_norm_eps=1e-6, rope_theta=1_000_000.0,
+                       tie_word_embeddings=False, attention_bias=False, hidden_act="silu", torch_dtype="bfloat16")
+
+
+@torch.no_grad()
+def random_init(model: Qwen3ForCausalLM, seed: int) -> None:
+    """Random-init weights of the workload: embeddings and LM head ~N(0,
+    0.02), norms 1, W4A4 projections with codes uniform in [-8, 7] (random
+    bytes), group-128 scales uniform in [0.005, 0.02] and RHT signs +-1, BF16
+    projections ~N(0, 0.02)."""
+    dev = next(model.parameters()).device
+    g = torch.Generator(device=dev).manual_seed(seed)
+    for name, p in model.named_parameters():
+        if name.endswith("norm.weight"):
+            p.fill_(1.0)
+        else:
+            p.copy_(torch.randn(p.shape, generator=g, device=dev, dtype=torch.float32).mul_(0.02))
+    for m in model.modules():
+        if isinstance(m, W4A4Linear):
+            m.packed_weight.copy_(torch.randint(-128, 128, m.packed_weight.shape, generator=g, device=dev,
+                                                dtype=torch.int16))
+            m.weight_scale.copy_(0.005 + 0.015 * torch.rand(m.weight_scale.shape, generator=g, device=dev))
+            m.signs.copy_(torch.randint(0, 2, m.signs.shape, generator=g, device=dev, dtype=torch.int16) * 2 - 1)
+
+
+class Engine:
+    def __init__(self, hf_config, use_w4a4: bool, max_num_seqs: int, max_model_len: int, block_size: int = 256,
+                 device="cuda:0", model: Qwen3ForCausalLM | None = None, kv_cache: torch.Tensor | None = None,
+                 seed: int = 0):
+        self.cfg, self.device = hf_config, torch.device(device)
+        self.max_num_seqs, self.max_model_len, self.block_size = max_num_seqs, max_model_len, block_size
+        self.blocks_per_seq = math.ceil(max_model_len / block_size)
+        if model is None:
+            prev = torch.get_default_dtype()
+            torch.set_default_dtype(torch.bfloat16)
+            try:
+                with torch.device(self.device):
+                    model = Qwen3ForCausalLM(hf_config, use_w4a4)
+            finally:
+                torch.set_default_dtype(prev)
+            random_init(model, seed)
+        self.model = model.eval()
+        cfg = hf_config
+        head_dim = getattr(cfg, "head_dim", None) or cfg.hidden_size // cfg.num_attention_heads
+        nblocks = max_num_seqs * self.blocks_per_seq
+        shape = (2, cfg.num_hidden_layers, nblocks, block_size, cfg.num_key_value_heads, head_dim)
+        if kv_cache is None or tuple(kv_cache.shape) != shape:
+            kv_cache = torch.empty(shape, dtype=torch.bfloat16, device=self.device)
+        self.kv_cache = kv_cache
+        ws = decode_workspace(max_num_seqs, cfg.num_attention_heads, max_model_len, head_dim, self.device)
+        for i, layer in enumerate(self.model.model.layers):
+            attn = layer.self_attn.attn
+            attn.k_cache, attn.v_cache = kv_cache[0, i], kv_cache[1, i]
+            attn.workspace, attn.max_context = ws, max_model_len
+        self.block_tables = torch.arange(nblocks, dtype=torch.int32, device=self.device).view(
+            max_num_seqs, self.blocks_per_seq)
+        self.graphs: dict[int, torch.cuda.CUDAGraph] = {}
+        self.graph_vars: dict[str, torch.Tensor] = {}
+
+    # ------------------------------------------------------------ helpers
+    def _slots(self, seq_slot: int, start: int, end: int):
+        base = seq_slot * self.blocks_per_seq * self.block_size
+        return list(range(base + start, base + end))
+
+    def _to_dev(self, values, dtype):
+        return torch.tensor(values, dtype=dtype, pin_memory=True).to(self.device, non_blocking=True)
+
+    @staticmethod
+    def sample(logits: torch.Tensor, temperatures: torch.Tensor) -> torch.Tensor:
+        logits = logits.float().div_(temperatures.unsqueeze(dim=1))
+        probs = torch.softmax(logits, dim=-1)
+        return probs.div_(torch.empty_like(probs).exponential_(1).clamp_min_(1e-10)).argmax(dim=-1)
+
+    # -------------------------------------------------------------- steps
+    @torch.inference_mode()
+    def prefill(self, seq_slot: int, token_ids: list[int], temperature: float) -> int:
+        n = len(token_ids)
+        input_ids = self._to_dev(token_ids, torch.int64)
+        positions = self._to_dev(list(range(n)), torch.int64)
+        cu = self._to_dev([0, n], torch.int32)
+        slot_mapping = self._to_dev(self._slots(seq_slot, 0, n), torch.int32)
+        set_context(True, cu, cu, n, n, slot_mapping, None, None, seqlens_q=(n,))
+        logits = self.model.compute_logits(self.model(input_ids, positions))
+        token = self.sample(logits, self._to_dev([temperature], torch.float32)).tolist()[0]
+        reset_context()
+        return token
+
+    def _set_decode_inputs(self, seq_slots, last_tokens, lengths):
+        bs = len(seq_slots)
+        input_ids = self._to_dev(last_tokens, torch.int64)
+        positions = self._to_dev([n - 1 for n in lengths], torch.int64)
+        context_lens = self._to_dev(lengths, torch.int32)
+        slot_mapping = self._to_dev([self._slots(s, n - 1, n)[0] for s, n in zip(seq_slots, lengths)], torch.int32)
+        block_tables = self.block_tables[torch.tensor(seq_slots, device=self.device)] if list(seq_slots) != list(
+            range(bs)) else self.block_tables[:bs]
+        return input_ids, positions, context_lens, slot_mapping, block_tables
+
+    @torch.inference_mode()
+    def capture(self, bs: int) -> None:
+        """Capture the decode forward (model only, as the reference does) for
+        batch size ``bs`` with static input buffers."""
+        gv = {"input_ids": torch.zeros(bs, dtype=torch.int64, device=self.device),
+              "positions": torch.zeros(bs, dtype=torch.int64, device=self.device),
+              "slot_mapping": torch.zeros(bs, dtype=torch.int32, device=self.device),
+              "context_lens": torch.ones(bs, dtype=torch.int32, device=self.device),
+              "block_tables": self.block_tables[:bs].clone()}
+        set_context(False, slot_mapping=gv["slot_mapping"], context_lens=gv["context_lens"],
+                    block_tables=gv["block_tables"])
+        side = torch.cuda.Stream(self.device)
+        side.wait_stream(torch.cuda.current_stream(self.device))
+        with torch.cuda.stream(side):
+            self.model(gv["input_ids"], gv["positions"])  # warm-up outside the graph
+        torch.cuda.current_stream(self.device).wait_stream(side)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            gv["outputs"] = self.model(gv["input_ids"], gv["positions"])
+        reset_context()
+        self.graphs[bs], self.graph_vars[bs] = graph, gv
+
+    @torch.inference_mode()
+    def decode(self, seq_slots, last_tokens, lengths, temperatures: torch.Tensor, eager: bool = False,
+               return_logits: bool = False):
+        """One decode step for the sequences in ``seq_slots`` whose current
+        lengths (prompt + generated, including the new input token) are
+        ``lengths``; returns the sampled tokens (a host list)."""
+        bs = len(seq_slots)
+        input_ids, positions, context_lens, slot_mapping, block_tables = self._set_decode_inputs(
+            seq_slots, last_tokens, lengths)
+        if eager or bs not in self.graphs:
+            set_context(False, slot_mapping=slot_mapping, context_lens=context_lens, block_tables=block_tables)
+            hidden = self.model(input_ids, positions)
+        else:
+            gv = self.graph_vars[bs]
+            gv["input_ids"].copy_(input_ids)
+            gv["positions"].copy_(positions)
+            gv["slot_mapping"].copy_(slot_mapping)
+            gv["context_lens"].copy_(context_lens)
+            gv["block_tables"].copy_(block_tables)
+            self.graphs[bs].replay()
+            hidden = gv["outputs"]
+            set_context(False)
+        logits = self.model.compute_logits(hidden)
+        reset_context()
+        if return_logits:
+            return logits
+        return self.sample(logits, temperatures).tolist()
+
+
+def run_decode_benchmark(engine: Engine, prompts: list[list[int]], output_tokens: int, temperature: float = 0.6,
+                         seed: int = 20261108, check_graph: bool = True) -> dict:
+    """Serial prefill of every prompt, then ``output_tokens - 1`` pure-decode
+    steps of the whole batch; wall-clock milliseconds of each step."""
+    bs = len(prompts)
+    torch.manual_seed(seed)
+    temps = torch.full((bs,), temperature, dtype=torch.float32, device=engine.device)
+    if bs not in engine.graphs:
+        engine.capture(bs)
+    lengths = [len(p) for p in prompts]
+    last, prefill_ms = [], []
+    for s, p in enumerate(prompts):
+        torch.cuda.synchronize(engine.device)
+        t0 = time.perf_counter()
+        last.append(engine.prefill(s, p, temperature))
+        prefill_ms.append((time.perf_counter() - t0) * 1e3)
+    lengths = [n + 1 for n in lengths]
+    result = {"prefill_ms": prefill_ms}
+    if check_graph:  # graph replay must reproduce the eager step exactly
+        slots = list(range(bs))
+        a = engine.decode(slots, last, lengths, temps, eager=True, return_logits=True).clone()
+        b = engine.decode(slots, last, lengths, temps, return_logits=True).clone()
+        result["graph_equals_eager"] = bool(torch.equal(a, b))
+        result["logits_finite"] = bool(torch.isfinite(b).all())
+    decode_ms = []
+    for _ in range(output_tokens - 1):
+        torch.cuda.synchronize(engine.device)
+        t0 = time.perf_counter()
+        last = engine.decode(list(range(bs)), last, lengths, temps)
+        decode_ms.append((time.perf_counter() - t0) * 1e3)
+        lengths = [n + 1 for n in lengths]
+    mean = sum(decode_ms) / len(decode_ms)
+    result.update(decode_ms=decode_ms, decode_ms_mean=mean, tokens_per_s=bs * 1000.0 / mean,
+                  last_tokens=last)
+    return result
+
+
+def seeded_prompts(batch: int, length: int, vocab: int, seed: int = 20261108) -> list[list[int]]:
+    g = torch.Generator("cpu").manual_seed(seed)
+    return torch.randint(0, vocab, (batch, length), generator=g).tolist()
+
+
+def count_w4a4(model) -> int:
+    return sum(isinstance(m, W4A4Linear) for m in model.modules())
+
+
+def count_bf16(model) -> int:
+    return sum(isinstance(m, BF16Linear) for m in model.modules())

@@ -1,0 +1,206 @@
+"""Qwen3 decoder around the quantized linears: the caller side of the hot path.
+
+The module tree, parameter names and numerics follow the reference's
+nanovllm/models/qwen3.py:14-233 (BF16 and W4A4 variants behind
+``use_w4a4``), so state dicts, the BF16 loader and the W4A4 checkpoint
+loader address the same names:
+
+* ``W4A4Linear`` (RHT + group-128 INT4 activations, grouped INT4 GEMM) for
+  the fused qkv / o / gate_up / down projections when ``use_w4a4``; plain
+  BF16 linears (torch ``F.linear``, i.e. hipBLASLt on ROCm) otherwise, with
+  the reference's q/k/v and gate/up shard loaders
+  (nanovllm/layers/linear.py:54-156, one GPU).
+* RMSNorm with the fused residual add (nanovllm/layers/layernorm.py:16-50):
+  fp32 arithmetic, the residual kept in the activation dtype.
+* Rotary embedding from a cos/sin cache (nanovllm/layers/rotary_embedding.py:
+  6-59), SiLU·mul (nanovllm/layers/activation.py:8-11), embedding and LM
+  head, the head reading only each sequence's last position in prefill
+  (nanovllm/layers/embed_head.py:56-66).
+* Attention through ``nv4.attention.Attention`` (paged KV cache).
+
+The reference wraps the small ops in ``torch.compile``; here they are plain
+torch operations (no Triton), and the decode step is captured in a HIP graph
+by the runner instead.
+"""
+from __future__ import annotations
+
+import torch
+import torch.nn.functional as F
+from torch import nn
+
+from .attention import Attention
+from .layers.linear_w4a4 import W4A4Linear
+from .utils.context import get_context
+
+
+class RMSNorm(nn.Module):
+    def __init__(self, hidden_size: int, eps: float = 1e-6) -> None:
+        super().__init__()
+        self.eps = eps
+        self.weight = nn.Parameter(torch.ones(hidden_size))
+
+    def rms_forward(self, x: torch.Tensor) -> torch.Tensor:
+        orig_dtype = x.dtype
+        x = x.float()
+        var = x.pow(2).mean(dim=-1, keepdim=True)
+        x.mul_(torch.rsqrt(var + self.eps))
+        return x.to(orig_dtype).mul_(self.weight)
+
+    def add_rms_forward(self, x: torch.Tensor, residual: torch.Tensor):
+        orig_dtype = x.dtype
+        x = x.float().add_(residual.float())
+        residual = x.to(orig_dtype)
+        var = x.pow(2).mean(dim=-1, keepdim=True)
+        x.mul_(torch.rsqrt(var + self.eps))
+        return x.to(orig_dtype).mul_(self.weight), residual
+
+    def forward(self, x, residual=None):
+        return self.rms_forward(x) if residual is None else self.add_rms_forward(x, residual)
+
+
+def apply_rotary_emb(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.Tensor:
+    x1, x2 = torch.chunk(x.float(), 2, dim=-1)
+    return torch.cat((x1 * cos - x2 * sin, x2 * cos + x1 * sin), dim=-1).to(x.dtype)
+
+
+class RotaryEmbedding(nn.Module):
+    def __init__(self, head_size: int, max_position: int, base: float) -> None:
+        super().__init__()
+        inv_freq = 1.0 / (base ** (torch.arange(0, head_size, 2, dtype=torch.float) / head_size))
+        t = torch.arange(max_position, dtype=torch.float)
+        freqs = t[:, None] * inv_freq[None, :]
+        cache = torch.cat((freqs.cos(), freqs.sin()), dim=-1).unsqueeze_(1)
+        self.register_buffer("cos_sin_cache", cache, persistent=False)
+
+    def forward(self, positions, query, key):
+        cos, sin = self.cos_sin_cache[positions].chunk(2, dim=-1)
+        return apply_rotary_emb(query, cos, sin), apply_rotary_emb(key, cos, sin)
+
+
+class BF16Linear(nn.Module):
+    """One-GPU BF16 linear; ``shards`` maps a shard id to (row offset, rows)
+    for the fused q/k/v or gate/up weight (nanovllm/layers/linear.py:54-156)."""
+
+    def __init__(self, input_size: int, output_size: int, shards: dict | None = None) -> None:
+        super().__init__()
+        self.weight = nn.Parameter(torch.empty(output_size, input_size))
+        self.shards = shards or {}
+        self.weight.weight_loader = self.weight_loader
+
+    def weight_loader(self, param, loaded_weight, shard_id=None):
+        if shard_id is None:
+            param.data.copy_(loaded_weight)
+        else:
+            offset, rows = self.shards[shard_id]
+            param.data.narrow(0, offset, rows).copy_(loaded_weight)
+
+    def forward(self, x):
+        return F.linear(x, self.weight)
+
+
+class Qwen3Attention(nn.Module):
+    def __init__(self, hidden_size, num_heads, num_kv_heads, max_position, head_dim=None, rms_norm_eps=1e-6,
+                 rope_theta=1_000_000.0, use_w4a4=False) -> None:
+        super().__init__()
+        self.num_heads, self.num_kv_heads = num_heads, num_kv_heads
+        self.head_dim = head_dim or hidden_size // num_heads
+        self.q_size, self.kv_size = num_heads * self.head_dim, num_kv_heads * self.head_dim
+        self.scaling = self.head_dim ** -0.5
+        qkv_out = self.q_size + 2 * self.kv_size
+        if use_w4a4:
+            self.qkv_proj = W4A4Linear(hidden_size, qkv_out)
+            self.o_proj = W4A4Linear(self.q_size, hidden_size)
+        else:
+            self.qkv_proj = BF16Linear(hidden_size, qkv_out, {"q": (0, self.q_size),
+                                                              "k": (self.q_size, self.kv_size),
+                                                              "v": (self.q_size + self.kv_size, self.kv_size)})
+            self.o_proj = BF16Linear(self.q_size, hidden_size)
+        self.rotary_emb = RotaryEmbedding(self.head_dim, max_position, rope_theta)
+        self.attn = Attention(num_heads, self.head_dim, self.scaling, num_kv_heads)
+        self.q_norm = RMSNorm(self.head_dim, eps=rms_norm_eps)
+        self.k_norm = RMSNorm(self.head_dim, eps=rms_norm_eps)
+
+    def forward(self, positions, hidden_states):
+        qkv = self.qkv_proj(hidden_states)
+        q, k, v = qkv.split([self.q_size, self.kv_size, self.kv_size], dim=-1)
+        q = self.q_norm(q.reshape(-1, self.num_heads, self.head_dim))
+        k = self.k_norm(k.reshape(-1, self.num_kv_heads, self.head_dim))
+        v = v.reshape(-1, self.num_kv_heads, self.head_dim)
+        q, k = self.rotary_emb(positions, q, k)
+        o = self.attn(q, k, v)
+        return self.o_proj(o.flatten(1, -1))
+
+
+class Qwen3MLP(nn.Module):
+    def __init__(self, hidden_size, intermediate_size, use_w4a4=False) -> None:
+        super().__init__()
+        if use_w4a4:
+            self.gate_up_proj = W4A4Linear(hidden_size, 2 * intermediate_size)
+            self.down_proj = W4A4Linear(intermediate_size, hidden_size)
+        else:
+            self.gate_up_proj = BF16Linear(hidden_size, 2 * intermediate_size,
+                                           {0: (0, intermediate_size), 1: (intermediate_size, intermediate_size)})
+            self.down_proj = BF16Linear(intermediate_size, hidden_size)
+
+    def forward(self, x):
+        gate, up = self.gate_up_proj(x).chunk(2, -1)
+        return self.down_proj(F.silu(gate) * up)
+
+
+class Qwen3DecoderLayer(nn.Module):
+    def __init__(self, config, use_w4a4=False) -> None:
+        super().__init__()
+        self.self_attn = Qwen3Attention(
+            config.hidden_size, config.num_attention_heads, config.num_key_value_heads,
+            config.max_position_embeddings, getattr(config, "head_dim", None), config.rms_norm_eps,
+            getattr(config, "rope_theta", 1_000_000.0), use_w4a4)
+        self.mlp = Qwen3MLP(config.hidden_size, config.intermediate_size, use_w4a4)
+        self.input_layernorm = RMSNorm(config.hidden_size, eps=config.rms_norm_eps)
+        self.post_attention_layernorm = RMSNorm(config.hidden_size, eps=config.rms_norm_eps)
+
+    def forward(self, positions, hidden_states, residual):
+        if residual is None:
+            hidden_states, residual = self.input_layernorm(hidden_states), hidden_states
+        else:
+            hidden_states, residual = self.input_layernorm(hidden_states, residual)
+        hidden_states = self.self_attn(positions, hidden_states)
+        hidden_states, residual = self.post_attention_layernorm(hidden_states, residual)
+        return self.mlp(hidden_states), residual
+
+
+class Qwen3Model(nn.Module):
+    def __init__(self, config, use_w4a4=False) -> None:
+        super().__init__()
+        self.embed_tokens = nn.Embedding(config.vocab_size, config.hidden_size)
+        self.layers = nn.ModuleList([Qwen3DecoderLayer(config, use_w4a4) for _ in range(config.num_hidden_layers)])
+        self.norm = RMSNorm(config.hidden_size, eps=config.rms_norm_eps)
+
+    def forward(self, input_ids, positions):
+        hidden_states, residual = self.embed_tokens(input_ids), None
+        for layer in self.layers:
+            hidden_states, residual = layer(positions, hidden_states, residual)
+        hidden_states, _ = self.norm(hidden_states, residual)
+        return hidden_states
+
+
+class Qwen3ForCausalLM(nn.Module):
+    packed_modules_mapping = {
+        "q_proj": ("qkv_proj", "q"), "k_proj": ("qkv_proj", "k"), "v_proj": ("qkv_proj", "v"),
+        "gate_proj": ("gate_up_proj", 0), "up_proj": ("gate_up_proj", 1),
+    }
+
+    def __init__(self, config, use_w4a4=False) -> None:
+        super().__init__()
+        self.model = Qwen3Model(config, use_w4a4)
+        self.lm_head = nn.Linear(config.hidden_size, config.vocab_size, bias=False)
+        if config.tie_word_embeddings:
+            self.lm_head.weight = self.model.embed_tokens.weight
+
+    def forward(self, input_ids, positions):
+        return self.model(input_ids, positions)
+
+    def compute_logits(self, hidden_states):
+        ctx = get_context()
+        if ctx.is_prefill and ctx.cu_seqlens_q is not None:
+            hidden_states = hidden_states[ctx.cu_seqlens_q[1:] - 1].contiguous()
+        return F.linear(hidden_states, self.lm_head.weight)

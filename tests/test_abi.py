@@ -79,6 +79,24 @@ def test_w4a16_and_linear_rejections():
     assert g(*([P(A16)] * 7), 0, 64, 4096, None) == _lib.NV4_E_SHAPE
 
 
+def test_paged_decode_attention_rejections():
+    f = _lib.load().nv4_paged_decode_attention
+    # q, q_row, k, v, block_tables, max_blocks, context_lens, out, ws, ws_bytes, B, Hq, Hkv, D, bs, max_ctx
+    def call(q_row=4096, max_blocks=17, ws_bytes=1 << 30, B=32, Hq=32, Hkv=8, D=128, bs=256, max_ctx=4352,
+             q=P(A16), ws=P(A16)):
+        return f(q, q_row, P(A16), P(A16), P(A16), max_blocks, P(A16), P(A16), ws, ws_bytes, B, Hq, Hkv, D, bs,
+                 max_ctx, 0.1, None)
+    assert call(q=None) == _lib.NV4_E_NULL
+    assert call(ws=None) == _lib.NV4_E_NULL
+    assert call(D=64) == _lib.NV4_E_SHAPE
+    assert call(Hkv=5) == _lib.NV4_E_SHAPE                    # Hq % Hkv
+    assert call(Hq=64, q_row=8192) == _lib.NV4_E_SHAPE       # GQA group 8
+    assert call(max_blocks=16) == _lib.NV4_E_SHAPE           # 16 blocks of 256 < 4352
+    assert call(ws_bytes=1000) == _lib.NV4_E_SHAPE
+    assert call(q_row=100) == _lib.NV4_E_SHAPE
+    assert call(q=P(A16 + 4)) == _lib.NV4_E_ALIGN
+
+
 def test_python_wrappers_validate_like_the_reference():
     from nv4 import W4A4Linear, rht_quant_pack, w4a4_grouped_gemm
     x = torch.zeros(2, 4096, dtype=torch.bfloat16)

@@ -1,0 +1,135 @@
+"""GPU parity of the decoder's attention against an fp32 reference.
+
+Paged decode attention (``nv4_paged_decode_attention``, the replacement of
+flash_attn_with_kvcache in nanovllm/layers/attention.py:72-74): random bf16
+caches behind shuffled block tables, context lengths at and around the
+256-token split and block boundaries (1, 255, 256, 257, ..., 4352), GQA
+groups 1/2/4, block sizes 256 and 16, and queries read as a strided view of
+a fused qkv tensor; against softmax(scale q.K^T) V computed in fp32.  Bar:
+|out - ref| <= 1e-2 + 1e-2 |ref| (bf16 output).  Prefill attention (causal
+GQA through the fused flash SDPA kernel) against the same fp32 reference on
+short packed sequences, same bar.  The KV store writes exactly the mapped
+slots.
+"""
+import math
+
+import pytest
+import torch
+
+from nv4.attention import paged_decode_attention, prefill_attention, store_kvcache
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda:0"
+
+
+def reference(q, kc, vc, bt, cl, scale):
+    """fp32 attention of each sequence over its first cl[b] slots."""
+    B, Hq, D = q.shape
+    bs, Hkv = kc.shape[1], kc.shape[2]
+    G = Hq // Hkv
+    outs = []
+    for b in range(B):
+        n = int(cl[b])
+        slots = torch.tensor([int(bt[b, t // bs]) * bs + t % bs for t in range(n)], device=q.device)
+        k = kc.reshape(-1, Hkv, D)[slots].float().repeat_interleave(G, dim=1).contiguous()  # [n, Hq, D]
+        v = vc.reshape(-1, Hkv, D)[slots].float().repeat_interleave(G, dim=1).contiguous()
+        s = torch.einsum("hd,nhd->hn", q[b].float(), k) * scale
+        p = torch.softmax(s, dim=-1)
+        outs.append(torch.einsum("hn,nhd->hd", p, v))
+    return torch.stack(outs)
+
+
+def make_case(B, Hq, Hkv, bs, lens, seed, strided=False):
+    g = torch.Generator(device=DEV).manual_seed(seed)
+    max_blocks = max((n + bs - 1) // bs for n in lens)
+    nblocks = B * max_blocks + 3
+    kc = torch.randn(nblocks, bs, Hkv, 128, generator=g, device=DEV).to(torch.bfloat16)
+    vc = torch.randn(nblocks, bs, Hkv, 128, generator=g, device=DEV).to(torch.bfloat16)
+    perm = torch.randperm(nblocks, generator=g, device=DEV)[:B * max_blocks].to(torch.int32)
+    bt = perm.view(B, max_blocks).contiguous()
+    cl = torch.tensor(lens, dtype=torch.int32, device=DEV)
+    if strided:  # q as the leading slice of a fused [B, (Hq + 2 Hkv) * 128] row
+        qkv = torch.randn(B, (Hq + 2 * Hkv) * 128, generator=g, device=DEV).to(torch.bfloat16)
+        q = qkv[:, :Hq * 128].view(B, Hq, 128)
+    else:
+        q = torch.randn(B, Hq, 128, generator=g, device=DEV).to(torch.bfloat16)
+    return q, kc, vc, bt, cl
+
+
+def check(out, ref, what):
+    err = (out.float() - ref).abs()
+    bound = 1e-2 + 1e-2 * ref.abs()
+    bad = (err > bound).sum().item()
+    assert bad == 0, f"{what}: {bad} of {err.numel()} outside the bound, max err {err.max().item():.3e}"
+
+
+@pytest.mark.parametrize("G", [1, 2, 4])
+@pytest.mark.parametrize("bs", [256, 16])
+def test_paged_decode_attention(G, bs):
+    Hkv = 8 // G if G < 8 else 1
+    Hq = Hkv * G
+    lens = [1, 7, 255, 256, 257, 600, 1000, 4352]
+    print(f"[attn] G={G} Hq={Hq} Hkv={Hkv} bs={bs}", flush=True)
+    q, kc, vc, bt, cl = make_case(len(lens), Hq, Hkv, bs, lens, seed=G * 100 + bs)
+    scale = 1 / math.sqrt(128)
+    out = paged_decode_attention(q, kc, vc, bt, cl, scale, max_context=4352)
+    torch.cuda.synchronize()
+    check(out, reference(q, kc, vc, bt, cl, scale), f"G={G} bs={bs}")
+
+
+def test_paged_decode_attention_qwen3_batch_strided():
+    """The decode shape of the end-to-end workload: 32 sequences, 32 query /
+    8 KV heads, contexts near 4096, q read from a fused qkv row."""
+    lens = [4096 + (7 * i) % 257 for i in range(32)]
+    q, kc, vc, bt, cl = make_case(32, 32, 8, 256, lens, seed=7, strided=True)
+    assert q.stride(0) == (32 + 16) * 128
+    scale = 1 / math.sqrt(128)
+    ws = torch.empty(32 * 32 * 18 * 130, dtype=torch.float32, device=DEV)
+    out = paged_decode_attention(q, kc, vc, bt, cl, scale, workspace=ws, max_context=4352)
+    torch.cuda.synchronize()
+    check(out, reference(q, kc, vc, bt, cl, scale), "qwen3 batch")
+
+
+def test_single_split_writes_output_directly():
+    lens = [1, 100, 256]
+    q, kc, vc, bt, cl = make_case(3, 32, 8, 256, lens, seed=11)
+    out = paged_decode_attention(q, kc, vc, bt, cl, 0.1, max_context=256)
+    torch.cuda.synchronize()
+    check(out, reference(q, kc, vc, bt, cl, 0.1), "one split")
+
+
+def test_prefill_attention_flash():
+    g = torch.Generator(device=DEV).manual_seed(3)
+    lens = [1, 17, 300]
+    T = sum(lens)
+    q = torch.randn(T, 32, 128, generator=g, device=DEV).to(torch.bfloat16)
+    k = torch.randn(T, 8, 128, generator=g, device=DEV).to(torch.bfloat16)
+    v = torch.randn(T, 8, 128, generator=g, device=DEV).to(torch.bfloat16)
+    scale = 1 / math.sqrt(128)
+    out = prefill_attention(q, k, v, lens, scale)
+    torch.cuda.synchronize()
+    start = 0
+    for n in lens:
+        qf = q[start:start + n].float().transpose(0, 1).contiguous()
+        kf = k[start:start + n].float().repeat_interleave(4, dim=1).transpose(0, 1).contiguous()
+        vf = v[start:start + n].float().repeat_interleave(4, dim=1).transpose(0, 1).contiguous()
+        s = torch.matmul(qf, kf.transpose(1, 2).contiguous()) * scale
+        s = s + torch.triu(torch.full((n, n), float("-inf"), device=DEV), 1)
+        ref = torch.matmul(torch.softmax(s, dim=-1), vf).transpose(0, 1)
+        check(out[start:start + n], ref, f"prefill n={n}")
+        start += n
+
+
+def test_store_kvcache_writes_mapped_slots():
+    kc = torch.zeros(4, 16, 8, 128, dtype=torch.bfloat16, device=DEV)
+    vc = torch.zeros_like(kc)
+    k = torch.randn(5, 8, 128, device=DEV).to(torch.bfloat16)
+    v = torch.randn(5, 8, 128, device=DEV).to(torch.bfloat16)
+    slots = torch.tensor([3, 17, 40, 41, 63], dtype=torch.int32, device=DEV)
+    store_kvcache(k, v, kc, vc, slots)
+    torch.cuda.synchronize()
+    flat_k, flat_v = kc.view(-1, 8, 128), vc.view(-1, 8, 128)
+    assert torch.equal(flat_k[slots.long()], k) and torch.equal(flat_v[slots.long()], v)
+    mask = torch.ones(64, dtype=torch.bool, device=DEV)
+    mask[slots.long()] = False
+    assert not flat_k[mask].any() and not flat_v[mask].any()

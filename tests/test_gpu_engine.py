@@ -1,0 +1,91 @@
+"""The decoder and fixed-batch runner around the quantized path (GPU).
+
+* BF16 decoder: the decode step (paged KV cache, paged decode attention,
+  rotary positions from the step's context) reproduces the last-position
+  logits of a prefill over the same tokens (flash prefill attention), within
+  bf16 rounding.
+* W4A4 decoder: its first qkv projection inside a prefill forward is
+  bit-exact with the oracle chain on the same normalised activations.
+* Both: the decode step replayed from the captured HIP graph gives logits
+  bit-equal to the eager step (the reference checks the same,
+  benchmarks/bench_nano_latency.py:96-107), finite, and a short run of the
+  benchmark loop completes with in-vocabulary tokens.
+Two decoder layers at the Qwen3-8B widths, vocabulary 1024.
+"""
+import numpy as np
+import pytest
+import torch
+from transformers import Qwen3Config
+
+import oracle
+from conftest import bf16_bits
+from nv4.engine import Engine, run_decode_benchmark, seeded_prompts
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda:0"
+
+
+def cfg():
+    return Qwen3Config(vocab_size=1024, hidden_size=4096, intermediate_size=12288, num_hidden_layers=2,
+                       num_attention_heads=32, num_key_value_heads=8, head_dim=128, max_position_embeddings=4096,
+                       rms_norm_eps=1e-6, rope_theta=1_000_000.0, tie_word_embeddings=False, attention_bias=False)
+
+
+@pytest.fixture(scope="module")
+def engines():
+    c = cfg()
+    bf16 = Engine(c, use_w4a4=False, max_num_seqs=4, max_model_len=1024, device=DEV, seed=1)
+    w4 = Engine(c, use_w4a4=True, max_num_seqs=4, max_model_len=1024, device=DEV, seed=2, kv_cache=bf16.kv_cache)
+    return bf16, w4
+
+
+def test_decode_step_matches_prefill_bf16(engines):
+    eng, _ = engines
+    prompt = seeded_prompts(1, 301, 1024, seed=5)[0]
+    temps = torch.full((1,), 1.0, device=DEV)
+    with torch.inference_mode():
+        # prefill 300 tokens, then decode token 301 at position 300 ...
+        eng.prefill(0, prompt[:300], 1.0)
+        dec = eng.decode([0], [prompt[300]], [301], temps, eager=True, return_logits=True).float()
+        # ... against a prefill of all 301 tokens (slot 1)
+        from nv4.utils.context import reset_context, set_context
+        n = 301
+        ids = torch.tensor(prompt, device=DEV)
+        pos = torch.arange(n, device=DEV)
+        cu = torch.tensor([0, n], dtype=torch.int32, device=DEV)
+        slots = torch.tensor(eng._slots(1, 0, n), dtype=torch.int32, device=DEV)
+        set_context(True, cu, cu, n, n, slots, None, None, seqlens_q=(n,))
+        ref = eng.model.compute_logits(eng.model(ids, pos)).float()
+        reset_context()
+    torch.cuda.synchronize()
+    err = (dec - ref).abs().max().item()
+    scale = ref.abs().max().item()
+    assert err <= 0.03 * scale, f"decode vs prefill logits: max err {err:.4f} of max {scale:.4f}"
+
+
+def test_w4a4_first_projection_matches_oracle(engines):
+    """Capture the qkv projection's input and output inside a real prefill
+    forward of the W4A4 decoder and check the output against the oracle."""
+    _, eng = engines
+    layer = eng.model.model.layers[0]
+    seen = {}
+    h = layer.self_attn.qkv_proj.register_forward_hook(lambda m, i, o: seen.update(x=i[0].clone(), y=o.clone()))
+    try:
+        eng.prefill(2, seeded_prompts(1, 70, 1024, seed=9)[0], 1.0)
+    finally:
+        h.remove()
+    torch.cuda.synchronize()
+    m = layer.self_attn.qkv_proj
+    packed, scale = oracle.rht_quant_pack(bf16_bits(seen["x"]), m.signs.cpu().numpy())
+    ref = oracle.w4a4_gemm(packed, m.packed_weight.cpu().numpy(), scale, bf16_bits(m.weight_scale))
+    assert np.array_equal(bf16_bits(seen["y"]), ref)
+
+
+@pytest.mark.parametrize("which", ["bf16", "w4a4"])
+def test_graph_equals_eager_and_benchmark_loop(engines, which):
+    eng = engines[0] if which == "bf16" else engines[1]
+    prompts = seeded_prompts(4, 200, 1024, seed=11)
+    res = run_decode_benchmark(eng, prompts, output_tokens=6, temperature=0.6)
+    assert res["graph_equals_eager"] and res["logits_finite"]
+    assert len(res["decode_ms"]) == 5 and len(res["prefill_ms"]) == 4
+    assert all(0 <= t < 1024 for t in res["last_tokens"])
