@@ -24,6 +24,14 @@
  *                          (called from W4A16Linear.forward :128-148)
  *   nv4_paged_decode_attention <- flash_attn_with_kvcache in the decode branch of
  *                          nanovllm/layers/attention.py:72-74 (caller of the hot path)
+ *   nv4_rmsnorm         <- RMSNorm.rms_forward / add_rms_forward,
+ *                          nanovllm/layers/layernorm.py:16-50 (caller of the hot path)
+ *   nv4_qk_norm_rope_store <- q_norm/k_norm + rotary_emb in Qwen3Attention.forward,
+ *                          nanovllm/models/qwen3.py:78-94, with
+ *                          nanovllm/layers/rotary_embedding.py:6-48 and store_kvcache,
+ *                          nanovllm/layers/attention.py:10-40 (caller of the hot path)
+ *   nv4_silu_mul        <- SiluAndMul.forward, nanovllm/layers/activation.py:8-11
+ *                          (caller of the hot path)
  */
 #ifndef NV4_H
 #define NV4_H
@@ -138,6 +146,46 @@ int nv4_paged_decode_attention(const void* q, int64_t q_row_stride, const void* 
                                void* out, float* workspace, int64_t workspace_bytes, int64_t B, int64_t Hq,
                                int64_t Hkv, int64_t D, int64_t block_size, int64_t max_context, float scale,
                                void* stream);
+
+/*
+ * RMSNorm over rows of H bf16 values (nanovllm/layers/layernorm.py:16-50):
+ *   residual_in == NULL:  y = bf16(bf16(x * rsqrt(mean(x^2) + eps)) * weight)
+ *   residual_in != NULL:  h = float(x) + float(residual_in); residual_out = bf16(h);
+ *                         y = bf16(bf16(h * rsqrt(mean(h^2) + eps)) * weight)
+ * x, residual_in, residual_out, y: [rows, H] contiguous, 16-byte aligned; weight [H].
+ * residual_in and residual_out are both NULL or both set (they may alias;
+ * x and y may alias).  8 <= H <= 8192, H % 8 == 0.
+ */
+int nv4_rmsnorm(const void* x, const void* residual_in, void* residual_out, const void* weight, void* y,
+                int64_t rows, int64_t H, float eps, void* stream);
+
+/*
+ * Per-head q/k RMSNorm, rotary embedding and KV-cache store for T tokens of a
+ * fused qkv projection (nanovllm/models/qwen3.py:78-94,
+ * nanovllm/layers/rotary_embedding.py:6-48, nanovllm/layers/attention.py:10-40).
+ *   qkv          bf16 [T, row]: Hq query heads, Hkv key heads, Hkv value heads of 128
+ *                (row = qkv_row_stride >= (Hq + 2*Hkv)*128)
+ *   q/k_norm_w   bf16 [128]
+ *   cos_sin      fp32 [max_position, 128]: cos in columns 0..63, sin in 64..127
+ *   positions    int64 [T]; slot_mapping int32 [T]
+ *   q_out        bf16 [T, Hq, 128]: normalised, rotated queries
+ *   k/v_cache    bf16 [num_slots, Hkv, 128] (= [num_blocks, block_size, Hkv, 128]):
+ *                token t's rotated key and its value go to slot slot_mapping[t];
+ *                slots outside [0, num_slots) (the reference's -1) are not stored
+ *   k_out/v_out  optional bf16 [T, Hkv, 128] copies of the rotated keys / values
+ * Positions outside [0, max_position) read row 0 of the table.
+ */
+int nv4_qk_norm_rope_store(const void* qkv, int64_t qkv_row_stride, int64_t T, int64_t Hq, int64_t Hkv,
+                           const void* q_norm_w, const void* k_norm_w, const float* cos_sin, int64_t max_position,
+                           const int64_t* positions, const int32_t* slot_mapping, int64_t num_slots, void* q_out,
+                           void* k_cache, void* v_cache, void* k_out, void* v_out, float eps, void* stream);
+
+/*
+ * SiLU-and-mul (nanovllm/layers/activation.py:8-11): gate_up bf16 [rows, 2*I]
+ * (gate in columns 0..I-1, up in I..2I-1) -> y bf16 [rows, I],
+ * y = bf16(bf16(g / (1 + exp(-g))) * u).  I % 8 == 0; 16-byte aligned.
+ */
+int nv4_silu_mul(const void* gate_up, void* y, int64_t rows, int64_t I, void* stream);
 
 /* Library version string. */
 const char* nv4_version(void);

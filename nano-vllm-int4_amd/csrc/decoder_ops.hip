@@ -1,0 +1,245 @@
+// Fused elementwise / normalisation ops of the Qwen3 decoder around the
+// quantized linears (gfx950).  In the reference these are several
+// torch.compile'd PyTorch ops each; here each is one launch, with the
+// reference's rounding points kept:
+//  * nv4_rmsnorm (nanovllm/layers/layernorm.py:16-40): x = float(x) [+
+//    float(residual), residual_out = bf16(x)]; y = bf16(bf16(x * rsqrt(mean(x^2)
+//    + eps)) * weight).  One workgroup per row; the sum of squares is taken in
+//    fp32 (in a different order than torch's reduction).
+//  * nv4_qk_norm_rope_store (nanovllm/models/qwen3.py:78-94 with
+//    layers/rotary_embedding.py:6-48 and the KV store of
+//    layers/attention.py:10-40): for every token of the fused qkv row, the
+//    query and key heads get the per-head RMSNorm, then the rotary embedding
+//    y1 = bf16(x1*cos - x2*sin), y2 = bf16(x2*cos + x1*sin) (fp32, each product
+//    and the sum rounded separately) on the bf16 normalised values; queries go
+//    to q_out, keys and values to their cache slot (and, when given, to
+//    k_out / v_out).  Slots outside [0, num_slots) -- the reference's -1 --
+//    are not stored; positions outside the cos/sin table read its row 0.  One wave per (token, head): lane l owns dims l and l+64,
+//    the two halves the rotation pairs.
+//  * nv4_silu_mul (nanovllm/layers/activation.py:8-11): bf16(bf16(silu(g)) * u)
+//    with silu(g) = g / (1 + exp(-g)) in fp32.
+#include "nv4_common.h"
+
+namespace nv4 {
+namespace {
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off);
+    return v;
+}
+
+__device__ __forceinline__ float round_bf16(float f) { return bf16_to_f32(f32_to_bf16_rne(f)); }
+
+// rows x H (H % 8 == 0, H <= 8 * 256 * 4); 256 threads per row.
+template <bool RESID>
+__global__ void __launch_bounds__(256)
+rmsnorm_rows(const uint16_t* x, const uint16_t* resid_in, uint16_t* resid_out,
+             const uint16_t* __restrict__ w, uint16_t* y, int H, float eps) {
+    constexpr int MAXV = 4;  // 8-element vectors per thread (H <= 8192)
+    const int64_t row = blockIdx.x;
+    const int t = threadIdx.x;
+    const int nv = H / 8;
+    float v[MAXV][8];
+    float ss = 0.0f;
+#pragma unroll
+    for (int i = 0; i < MAXV; ++i) {
+        const int c = t + i * 256;
+        if (c < nv) {
+            const v4u xv = *reinterpret_cast<const v4u*>(x + row * H + c * 8);
+            v4u rv = {0u, 0u, 0u, 0u};
+            if constexpr (RESID) rv = *reinterpret_cast<const v4u*>(resid_in + row * H + c * 8);
+            v4u ro;
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                const uint32_t xh = (xv[k >> 1] >> (16 * (k & 1))) & 0xffffu;
+                float f = bf16_to_f32(xh);
+                if constexpr (RESID) {
+                    const uint32_t rh = (rv[k >> 1] >> (16 * (k & 1))) & 0xffffu;
+                    f = f + bf16_to_f32(rh);
+                }
+                v[i][k] = f;
+                ss = __builtin_fmaf(f, f, ss);
+            }
+            if constexpr (RESID) {
+#pragma unroll
+                for (int k = 0; k < 4; ++k)
+                    ro[k] = f32_to_bf16_rne(v[i][2 * k]) | (f32_to_bf16_rne(v[i][2 * k + 1]) << 16);
+                *reinterpret_cast<v4u*>(resid_out + row * H + c * 8) = ro;
+            }
+        }
+    }
+    __shared__ float part[4];
+    ss = wave_sum(ss);
+    if ((t & 63) == 0) part[t >> 6] = ss;
+    __syncthreads();
+    const float var = (part[0] + part[1] + part[2] + part[3]) / (float)H;
+    const float r = rsqrtf(var + eps);
+#pragma unroll
+    for (int i = 0; i < MAXV; ++i) {
+        const int c = t + i * 256;
+        if (c < nv) {
+            const v4u wv = *reinterpret_cast<const v4u*>(w + c * 8);
+            v4u out;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                uint32_t pair = 0;
+#pragma unroll
+                for (int e = 0; e < 2; ++e) {
+                    const int kk = 2 * k + e;
+                    const float wf = bf16_to_f32((wv[k] >> (16 * e)) & 0xffffu);
+                    const float nrm = round_bf16(v[i][kk] * r);
+                    pair |= f32_to_bf16_rne(nrm * wf) << (16 * e);
+                }
+                out[k] = pair;
+            }
+            *reinterpret_cast<v4u*>(y + row * H + c * 8) = out;
+        }
+    }
+}
+
+// One wave per (token, head) of the fused qkv row [T, (Hq + 2 Hkv) * 128].
+__global__ void __launch_bounds__(256)
+qk_norm_rope_store(const uint16_t* __restrict__ qkv, int64_t qkv_row, int T, int Hq, int Hkv,
+                   const uint16_t* __restrict__ qw, const uint16_t* __restrict__ kw,
+                   const float* __restrict__ cos_sin, const int64_t* __restrict__ positions,
+                   int64_t max_position, const int32_t* __restrict__ slots, int64_t num_slots,
+                   uint16_t* __restrict__ q_out, uint16_t* __restrict__ k_cache, uint16_t* __restrict__ v_cache,
+                   uint16_t* __restrict__ k_out, uint16_t* __restrict__ v_out, float eps) {
+    const int heads = Hq + 2 * Hkv;
+    const int64_t item = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (item >= (int64_t)T * heads) return;  // whole waves
+    const int64_t tok = item / heads;
+    const int h = (int)(item % heads);
+    const int l = threadIdx.x & 63;
+    const uint16_t* src = qkv + tok * qkv_row + (int64_t)h * 128;
+    float x1 = bf16_to_f32(src[l]), x2 = bf16_to_f32(src[l + 64]);
+    if (h >= Hq + Hkv) {  // value head: copy to its slot (and v_out)
+        const int kvh = h - Hq - Hkv;
+        const int64_t slot = slots[tok];
+        if (slot >= 0 && slot < num_slots) {
+            uint16_t* dst = v_cache + (slot * Hkv + kvh) * 128;
+            dst[l] = src[l];
+            dst[l + 64] = src[l + 64];
+        }
+        if (v_out) {
+            v_out[(tok * Hkv + kvh) * 128 + l] = src[l];
+            v_out[(tok * Hkv + kvh) * 128 + l + 64] = src[l + 64];
+        }
+        return;
+    }
+    const bool is_q = h < Hq;
+    const uint16_t* wt = is_q ? qw : kw;
+    const float var = wave_sum(x1 * x1 + x2 * x2) / 128.0f;
+    const float r = rsqrtf(var + eps);
+    x1 = round_bf16(round_bf16(x1 * r) * bf16_to_f32(wt[l]));
+    x2 = round_bf16(round_bf16(x2 * r) * bf16_to_f32(wt[l + 64]));
+    int64_t pos = positions[tok];
+    if (pos < 0 || pos >= max_position) pos = 0;  // out-of-table positions: never read outside the table
+    const float* cs = cos_sin + pos * 128;
+    const float c = cs[l], s = cs[64 + l];
+    const float a = x1 * c, b = x2 * s, d = x2 * c, e = x1 * s;
+    const uint16_t y1 = (uint16_t)f32_to_bf16_rne(a - b);
+    const uint16_t y2 = (uint16_t)f32_to_bf16_rne(d + e);
+    if (is_q) {
+        uint16_t* dst = q_out + (tok * Hq + h) * 128;
+        dst[l] = y1;
+        dst[l + 64] = y2;
+    } else {
+        const int kvh = h - Hq;
+        const int64_t slot = slots[tok];
+        if (slot >= 0 && slot < num_slots) {
+            uint16_t* dst = k_cache + (slot * Hkv + kvh) * 128;
+            dst[l] = y1;
+            dst[l + 64] = y2;
+        }
+        if (k_out) {
+            k_out[(tok * Hkv + kvh) * 128 + l] = y1;
+            k_out[(tok * Hkv + kvh) * 128 + l + 64] = y2;
+        }
+    }
+}
+
+__global__ void __launch_bounds__(256)
+silu_mul(const uint16_t* __restrict__ gu, uint16_t* __restrict__ y, int64_t rows, int I) {
+    const int64_t n8 = rows * (I / 8);
+    const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (idx >= n8) return;
+    const int64_t row = idx / (I / 8), c = idx % (I / 8);
+    const v4u g = *reinterpret_cast<const v4u*>(gu + row * 2 * I + c * 8);
+    const v4u u = *reinterpret_cast<const v4u*>(gu + row * 2 * I + I + c * 8);
+    v4u out;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        uint32_t pair = 0;
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+            const float gf = bf16_to_f32((g[k] >> (16 * e)) & 0xffffu);
+            const float uf = bf16_to_f32((u[k] >> (16 * e)) & 0xffffu);
+            const float sg = round_bf16(gf / (1.0f + expf(-gf)));
+            pair |= f32_to_bf16_rne(sg * uf) << (16 * e);
+        }
+        out[k] = pair;
+    }
+    *reinterpret_cast<v4u*>(y + row * I + c * 8) = out;
+}
+
+}  // namespace
+}  // namespace nv4
+
+extern "C" int nv4_rmsnorm(const void* x, const void* residual_in, void* residual_out, const void* weight, void* y,
+                           int64_t rows, int64_t H, float eps, void* stream) {
+    using namespace nv4;
+    if (!x || !weight || !y || (residual_in && !residual_out) || (!residual_in && residual_out)) return NV4_E_NULL;
+    if (rows < 1 || rows > 0x7fffffffLL || H < 8 || H % 8 || H > 8192) return NV4_E_SHAPE;
+    if (reinterpret_cast<uintptr_t>(x) % 16 || reinterpret_cast<uintptr_t>(weight) % 16 ||
+        reinterpret_cast<uintptr_t>(y) % 16 || reinterpret_cast<uintptr_t>(residual_in) % 16 ||
+        reinterpret_cast<uintptr_t>(residual_out) % 16)
+        return NV4_E_ALIGN;
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    const auto* xp = static_cast<const uint16_t*>(x);
+    const auto* wp = static_cast<const uint16_t*>(weight);
+    auto* yp = static_cast<uint16_t*>(y);
+    if (residual_in)
+        hipLaunchKernelGGL(rmsnorm_rows<true>, dim3((unsigned)rows), dim3(256), 0, st, xp,
+                           static_cast<const uint16_t*>(residual_in), static_cast<uint16_t*>(residual_out), wp, yp,
+                           (int)H, eps);
+    else
+        hipLaunchKernelGGL(rmsnorm_rows<false>, dim3((unsigned)rows), dim3(256), 0, st, xp, nullptr, nullptr, wp, yp,
+                           (int)H, eps);
+    return (int)hipGetLastError();
+}
+
+extern "C" int nv4_qk_norm_rope_store(const void* qkv, int64_t qkv_row_stride, int64_t T, int64_t Hq, int64_t Hkv,
+                                      const void* q_norm_w, const void* k_norm_w, const float* cos_sin,
+                                      int64_t max_position, const int64_t* positions,
+                                      const int32_t* slot_mapping, int64_t num_slots, void* q_out, void* k_cache,
+                                      void* v_cache, void* k_out, void* v_out, float eps, void* stream) {
+    using namespace nv4;
+    if (!qkv || !q_norm_w || !k_norm_w || !cos_sin || !positions || !slot_mapping || !q_out || !k_cache || !v_cache)
+        return NV4_E_NULL;
+    if (T < 1 || Hq < 1 || Hkv < 1 || max_position < 1 || num_slots < 0 ||
+        qkv_row_stride < (Hq + 2 * Hkv) * 128 || T * (Hq + 2 * Hkv) > 0x7fffffffLL * 4)
+        return NV4_E_SHAPE;
+    const int64_t items = T * (Hq + 2 * Hkv);
+    hipLaunchKernelGGL(qk_norm_rope_store, dim3((unsigned)((items + 3) / 4)), dim3(256), 0,
+                       static_cast<hipStream_t>(stream), static_cast<const uint16_t*>(qkv), qkv_row_stride, (int)T,
+                       (int)Hq, (int)Hkv, static_cast<const uint16_t*>(q_norm_w),
+                       static_cast<const uint16_t*>(k_norm_w), cos_sin, positions, max_position, slot_mapping,
+                       num_slots,
+                       static_cast<uint16_t*>(q_out), static_cast<uint16_t*>(k_cache), static_cast<uint16_t*>(v_cache),
+                       static_cast<uint16_t*>(k_out), static_cast<uint16_t*>(v_out), eps);
+    return (int)hipGetLastError();
+}
+
+extern "C" int nv4_silu_mul(const void* gate_up, void* y, int64_t rows, int64_t I, void* stream) {
+    using namespace nv4;
+    if (!gate_up || !y) return NV4_E_NULL;
+    if (rows < 1 || I < 8 || I % 8) return NV4_E_SHAPE;
+    if (reinterpret_cast<uintptr_t>(gate_up) % 16 || reinterpret_cast<uintptr_t>(y) % 16) return NV4_E_ALIGN;
+    const int64_t n8 = rows * (I / 8);
+    if ((n8 + 255) / 256 > 0x7fffffffLL) return NV4_E_SHAPE;
+    hipLaunchKernelGGL(silu_mul, dim3((unsigned)((n8 + 255) / 256)), dim3(256), 0, static_cast<hipStream_t>(stream),
+                       static_cast<const uint16_t*>(gate_up), static_cast<uint16_t*>(y), rows, (int)I);
+    return (int)hipGetLastError();
+}

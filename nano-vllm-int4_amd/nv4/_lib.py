@@ -35,6 +35,10 @@ SIGNATURES = {
     "nv4_w4a16_gemm": ([_P, _I, _P, _P, _P, _P, _I, _I64, _I64, _I64, _I, _P], _I),
     "nv4_paged_decode_attention": ([_P, _I64, _P, _P, _P, _I64, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64,
                                     _I64, ctypes.c_float, _P], _I),
+    "nv4_rmsnorm": ([_P, _P, _P, _P, _P, _I64, _I64, ctypes.c_float, _P], _I),
+    "nv4_qk_norm_rope_store": ([_P, _I64, _I64, _I64, _I64, _P, _P, _P, _I64, _P, _P, _I64, _P, _P, _P, _P, _P,
+                                ctypes.c_float, _P], _I),
+    "nv4_silu_mul": ([_P, _P, _I64, _I64, _P], _I),
     "nv4_version": ([], ctypes.c_char_p),
     "nv4_strerror": ([_I], ctypes.c_char_p),
 }

@@ -6,8 +6,10 @@ of which this build uses:
 
 * KV store: each new token's K and V rows go to ``slot_mapping`` slots of
   the caches ``[num_blocks, block_size, num_kv_heads, head_dim]`` (the
-  reference's store_kvcache, :10-40; slots of -1 are skipped there and never
-  produced here).
+  reference's store_kvcache, :10-40).  Here the store is fused into the
+  producer of the rotated keys (``nv4.kernels.decoder_ops.qk_norm_rope_store``,
+  called by Qwen3Attention before this module), so ``Attention.forward``
+  receives caches that already hold the step's tokens.
 * Prefill (causal, GQA): ``scaled_dot_product_attention`` restricted to its
   fused flash kernel, one call per sequence of the batch (it raises rather
   than fall back to the unfused path).
@@ -68,14 +70,6 @@ def paged_decode_attention(q, k_cache, v_cache, block_tables, context_lens, scal
     return out
 
 
-def store_kvcache(key, value, k_cache, v_cache, slot_mapping):
-    N = key.shape[0]
-    kc, vc = k_cache.view(-1, key.shape[1] * key.shape[2]), v_cache.view(-1, value.shape[1] * value.shape[2])
-    idx = slot_mapping.to(torch.int64)
-    kc.index_copy_(0, idx, key.reshape(N, -1))
-    vc.index_copy_(0, idx, value.reshape(N, -1))
-
-
 def prefill_attention(q, k, v, seqlens, scale):
     """Causal GQA attention over packed sequences of lengths ``seqlens``
     (q [T, Hq, D], k/v [T, Hkv, D]) with the fused flash kernel only."""
@@ -102,9 +96,9 @@ class Attention(nn.Module):
         self.max_context = None
 
     def forward(self, q, k, v):
+        """q [T, Hq, D]; k, v [T, Hkv, D] in prefill (None in decode, which
+        reads the keys and values from the caches)."""
         ctx = get_context()
-        if self.k_cache.numel() and self.v_cache.numel():
-            store_kvcache(k, v, self.k_cache, self.v_cache, ctx.slot_mapping)
         if ctx.is_prefill:
             return prefill_attention(q, k, v, ctx.seqlens_q, self.scale)
         return paged_decode_attention(q, self.k_cache, self.v_cache, ctx.block_tables, ctx.context_lens,

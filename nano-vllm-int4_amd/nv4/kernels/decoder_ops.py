@@ -1,0 +1,116 @@
+"""Fused decoder elementwise operators around the quantized linears (MI355X).
+
+Each is one HIP launch on torch's current stream (graph-capturable), with the
+rounding points of the reference's PyTorch formulation:
+
+* ``rmsnorm`` -- RMSNorm.rms_forward / add_rms_forward
+  (nanovllm/layers/layernorm.py:16-50), the residual add fused;
+* ``qk_norm_rope_store`` -- the per-head q/k RMSNorm, rotary embedding and KV
+  store of Qwen3Attention.forward (nanovllm/models/qwen3.py:78-94,
+  nanovllm/layers/rotary_embedding.py:6-48, nanovllm/layers/attention.py:10-40);
+* ``silu_mul`` -- SiluAndMul (nanovllm/layers/activation.py:8-11).
+"""
+from __future__ import annotations
+
+import ctypes
+
+import torch
+
+from .. import _lib
+
+
+def _ptr(t):
+    return ctypes.c_void_p(t.data_ptr()) if t is not None else None
+
+
+def _check_dev(tensors, dev):
+    if any(t is not None and (not t.is_cuda or t.device != dev) for t in tensors):
+        raise ValueError("All tensors must be on one CUDA device")
+
+
+def rmsnorm(x, weight, eps, residual=None, out=None):
+    """x bf16 [..., H] -> y (bf16, same shape); with ``residual`` returns
+    (y, x + residual rounded to bf16) and writes the sum into ``residual``."""
+    H = x.shape[-1]
+    if x.dtype != torch.bfloat16 or weight.dtype != torch.bfloat16 or tuple(weight.shape) != (H,):
+        raise TypeError("RMSNorm expects BF16 activations and a BF16 weight [H]")
+    if not x.is_contiguous() or not weight.is_contiguous():
+        raise ValueError("RMSNorm expects contiguous tensors")
+    if residual is not None and (residual.shape != x.shape or residual.dtype != x.dtype
+                                 or not residual.is_contiguous()):
+        raise ValueError("residual must match x")
+    rows = x.numel() // H
+    if out is None:
+        out = torch.empty_like(x)
+    _check_dev((x, weight, residual, out), x.device)
+    lib = _lib.load()
+    stream = torch.cuda.current_stream(x.device).cuda_stream
+    with torch.cuda.device(x.device):
+        rc = lib.nv4_rmsnorm(_ptr(x), _ptr(residual), _ptr(residual), _ptr(weight), _ptr(out), rows, H,
+                             ctypes.c_float(eps), ctypes.c_void_p(stream))
+    _lib.check(rc, "rmsnorm")
+    return out if residual is None else (out, residual)
+
+
+def qk_norm_rope_store(qkv, num_heads, num_kv_heads, q_norm_w, k_norm_w, cos_sin, positions, eps,
+                       slot_mapping=None, k_cache=None, v_cache=None, return_kv=False):
+    """qkv bf16 [T, (Hq + 2 Hkv) * 128] (rows may be strided) -> q [T, Hq, 128]
+    (and, with ``return_kv``, k [T, Hkv, 128], v [T, Hkv, 128]); rotated keys
+    and values go to the cache slots ``slot_mapping`` when caches are given."""
+    T = qkv.shape[0]
+    D = 128
+    if qkv.dtype != torch.bfloat16 or qkv.ndim != 2 or qkv.stride(1) != 1:
+        raise TypeError("qkv must be BF16 [T, heads*128] with unit column stride")
+    if qkv.shape[1] != (num_heads + 2 * num_kv_heads) * D:
+        raise ValueError("qkv width does not match the head counts (head_dim 128)")
+    if cos_sin.dtype != torch.float32 or cos_sin.shape[-1] != D or not cos_sin.is_contiguous():
+        raise TypeError("cos_sin must be a contiguous FP32 [max_position, 128] table")
+    if positions.dtype != torch.int64 or tuple(positions.shape) != (T,):
+        raise TypeError("positions must be int64 [T]")
+    max_position = cos_sin.numel() // D
+    dev = qkv.device
+    q = torch.empty((T, num_heads, D), dtype=torch.bfloat16, device=dev)
+    k = v = None
+    if return_kv:
+        k = torch.empty((T, num_kv_heads, D), dtype=torch.bfloat16, device=dev)
+        v = torch.empty((T, num_kv_heads, D), dtype=torch.bfloat16, device=dev)
+    store = k_cache is not None and k_cache.numel() > 0
+    if store:
+        if (k_cache.dtype != torch.bfloat16 or v_cache.shape != k_cache.shape or k_cache.shape[-2:] != (
+                num_kv_heads, D) or not k_cache.is_contiguous() or not v_cache.is_contiguous()):
+            raise ValueError("caches must be contiguous BF16 [num_blocks, block_size, num_kv_heads, 128]")
+        if slot_mapping is None or slot_mapping.dtype != torch.int32 or tuple(slot_mapping.shape) != (T,):
+            raise TypeError("slot_mapping must be int32 [T]")
+        num_slots = k_cache.numel() // (num_kv_heads * D)
+    else:
+        # No cache: the kernel stores nothing (num_slots 0); pointers are
+        # placeholders that are never dereferenced.
+        num_slots, k_cache, v_cache = 0, q, q
+        slot_mapping = torch.empty((T,), dtype=torch.int32, device=dev) if slot_mapping is None else slot_mapping
+    _check_dev((qkv, q_norm_w, k_norm_w, cos_sin, positions, slot_mapping, k_cache, v_cache), dev)
+    lib = _lib.load()
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    with torch.cuda.device(dev):
+        rc = lib.nv4_qk_norm_rope_store(
+            _ptr(qkv), qkv.stride(0), T, num_heads, num_kv_heads, _ptr(q_norm_w), _ptr(k_norm_w), _ptr(cos_sin),
+            max_position, _ptr(positions), _ptr(slot_mapping), num_slots, _ptr(q), _ptr(k_cache), _ptr(v_cache),
+            _ptr(k), _ptr(v), ctypes.c_float(eps), ctypes.c_void_p(stream))
+    _lib.check(rc, "qk_norm_rope_store")
+    return (q, k, v) if return_kv else q
+
+
+def silu_mul(gate_up, out=None):
+    """gate_up bf16 [..., 2I] -> bf16 [..., I] = silu(gate) * up."""
+    I2 = gate_up.shape[-1]
+    if gate_up.dtype != torch.bfloat16 or I2 % 16 or not gate_up.is_contiguous():
+        raise ValueError("silu_mul expects contiguous BF16 [..., 2I] with I % 8 == 0")
+    rows = gate_up.numel() // I2
+    if out is None:
+        out = torch.empty((*gate_up.shape[:-1], I2 // 2), dtype=torch.bfloat16, device=gate_up.device)
+    _check_dev((gate_up, out), gate_up.device)
+    lib = _lib.load()
+    stream = torch.cuda.current_stream(gate_up.device).cuda_stream
+    with torch.cuda.device(gate_up.device):
+        rc = lib.nv4_silu_mul(_ptr(gate_up), _ptr(out), rows, I2 // 2, ctypes.c_void_p(stream))
+    _lib.check(rc, "silu_mul")
+    return out

@@ -10,60 +10,57 @@ loader address the same names:
   BF16 linears (torch ``F.linear``, i.e. hipBLASLt on ROCm) otherwise, with
   the reference's q/k/v and gate/up shard loaders
   (nanovllm/layers/linear.py:54-156, one GPU).
-* RMSNorm with the fused residual add (nanovllm/layers/layernorm.py:16-50):
-  fp32 arithmetic, the residual kept in the activation dtype.
-* Rotary embedding from a cos/sin cache (nanovllm/layers/rotary_embedding.py:
-  6-59), SiLU·mul (nanovllm/layers/activation.py:8-11), embedding and LM
-  head, the head reading only each sequence's last position in prefill
-  (nanovllm/layers/embed_head.py:56-66).
+* RMSNorm with the fused residual add (nanovllm/layers/layernorm.py:16-50),
+  the per-head q/k RMSNorm + rotary embedding + KV-cache store
+  (nanovllm/models/qwen3.py:78-94, nanovllm/layers/rotary_embedding.py:6-59,
+  nanovllm/layers/attention.py:10-40) and SiLU·mul
+  (nanovllm/layers/activation.py:8-11): one HIP launch each
+  (``nv4.kernels.decoder_ops``), with the rounding points of the
+  reference's PyTorch formulation.
+* Embedding and LM head, the head reading only each sequence's last
+  position in prefill (nanovllm/layers/embed_head.py:56-66).
 * Attention through ``nv4.attention.Attention`` (paged KV cache).
 
-The reference wraps the small ops in ``torch.compile``; here they are plain
-torch operations (no Triton), and the decode step is captured in a HIP graph
-by the runner instead.
+The reference wraps the small ops in ``torch.compile`` (Triton); here they
+are hand-written HIP kernels, and the decode step is captured in a HIP graph
+by the runner.
 """
 from __future__ import annotations
+
+import functools
 
 import torch
 import torch.nn.functional as F
 from torch import nn
 
 from .attention import Attention
+from .kernels.decoder_ops import qk_norm_rope_store, rmsnorm, silu_mul
 from .layers.linear_w4a4 import W4A4Linear
 from .utils.context import get_context
 
 
 class RMSNorm(nn.Module):
+    """RMSNorm with the fused residual add (nanovllm/layers/layernorm.py:16-50)
+    as one HIP launch (``nv4_rmsnorm``): fp32 arithmetic, the normalised
+    value rounded to bf16 before the weight product, the residual kept in
+    bf16.  With ``residual`` the sum is written into ``residual`` in place and
+    returned as the new residual."""
+
     def __init__(self, hidden_size: int, eps: float = 1e-6) -> None:
         super().__init__()
         self.eps = eps
         self.weight = nn.Parameter(torch.ones(hidden_size))
 
-    def rms_forward(self, x: torch.Tensor) -> torch.Tensor:
-        orig_dtype = x.dtype
-        x = x.float()
-        var = x.pow(2).mean(dim=-1, keepdim=True)
-        x.mul_(torch.rsqrt(var + self.eps))
-        return x.to(orig_dtype).mul_(self.weight)
-
-    def add_rms_forward(self, x: torch.Tensor, residual: torch.Tensor):
-        orig_dtype = x.dtype
-        x = x.float().add_(residual.float())
-        residual = x.to(orig_dtype)
-        var = x.pow(2).mean(dim=-1, keepdim=True)
-        x.mul_(torch.rsqrt(var + self.eps))
-        return x.to(orig_dtype).mul_(self.weight), residual
-
     def forward(self, x, residual=None):
-        return self.rms_forward(x) if residual is None else self.add_rms_forward(x, residual)
-
-
-def apply_rotary_emb(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.Tensor:
-    x1, x2 = torch.chunk(x.float(), 2, dim=-1)
-    return torch.cat((x1 * cos - x2 * sin, x2 * cos + x1 * sin), dim=-1).to(x.dtype)
+        return rmsnorm(x.contiguous(), self.weight, self.eps, residual)
 
 
 class RotaryEmbedding(nn.Module):
+    """cos/sin table of the rotary embedding (nanovllm/layers/rotary_embedding.py:
+    6-48): ``cos_sin_cache`` fp32 [max_position, 1, head_size], cos in the first
+    half, sin in the second.  The rotation itself is applied inside
+    ``qk_norm_rope_store``."""
+
     def __init__(self, head_size: int, max_position: int, base: float) -> None:
         super().__init__()
         inv_freq = 1.0 / (base ** (torch.arange(0, head_size, 2, dtype=torch.float) / head_size))
@@ -72,9 +69,17 @@ class RotaryEmbedding(nn.Module):
         cache = torch.cat((freqs.cos(), freqs.sin()), dim=-1).unsqueeze_(1)
         self.register_buffer("cos_sin_cache", cache, persistent=False)
 
-    def forward(self, positions, query, key):
-        cos, sin = self.cos_sin_cache[positions].chunk(2, dim=-1)
-        return apply_rotary_emb(query, cos, sin), apply_rotary_emb(key, cos, sin)
+
+@functools.lru_cache(maxsize=None)
+def _rope(head_size: int, max_position: int, base: float, device: str) -> RotaryEmbedding:
+    # One table shared by every layer, as the reference's lru_cache'd get_rope
+    # (nanovllm/layers/rotary_embedding.py:51-59); 20 MiB at 40960 positions.
+    with torch.device(device):
+        return RotaryEmbedding(head_size, max_position, base)
+
+
+def get_rope(head_size: int, max_position: int, base: float) -> RotaryEmbedding:
+    return _rope(head_size, max_position, float(base), str(torch.empty(0).device))
 
 
 class BF16Linear(nn.Module):
@@ -115,18 +120,21 @@ class Qwen3Attention(nn.Module):
                                                               "k": (self.q_size, self.kv_size),
                                                               "v": (self.q_size + self.kv_size, self.kv_size)})
             self.o_proj = BF16Linear(self.q_size, hidden_size)
-        self.rotary_emb = RotaryEmbedding(self.head_dim, max_position, rope_theta)
+        self.rotary_emb = get_rope(self.head_dim, max_position, rope_theta)
         self.attn = Attention(num_heads, self.head_dim, self.scaling, num_kv_heads)
         self.q_norm = RMSNorm(self.head_dim, eps=rms_norm_eps)
         self.k_norm = RMSNorm(self.head_dim, eps=rms_norm_eps)
 
     def forward(self, positions, hidden_states):
         qkv = self.qkv_proj(hidden_states)
-        q, k, v = qkv.split([self.q_size, self.kv_size, self.kv_size], dim=-1)
-        q = self.q_norm(q.reshape(-1, self.num_heads, self.head_dim))
-        k = self.k_norm(k.reshape(-1, self.num_kv_heads, self.head_dim))
-        v = v.reshape(-1, self.num_kv_heads, self.head_dim)
-        q, k = self.rotary_emb(positions, q, k)
+        ctx = get_context()
+        # q/k RMSNorm + rotary + KV-cache store in one launch; prefill also
+        # needs the rotated keys and the values as tensors.
+        out = qk_norm_rope_store(qkv, self.num_heads, self.num_kv_heads, self.q_norm.weight, self.k_norm.weight,
+                                 self.rotary_emb.cos_sin_cache, positions, self.q_norm.eps,
+                                 slot_mapping=ctx.slot_mapping, k_cache=self.attn.k_cache,
+                                 v_cache=self.attn.v_cache, return_kv=ctx.is_prefill)
+        q, k, v = out if ctx.is_prefill else (out, None, None)
         o = self.attn(q, k, v)
         return self.o_proj(o.flatten(1, -1))
 
@@ -143,8 +151,7 @@ class Qwen3MLP(nn.Module):
             self.down_proj = BF16Linear(intermediate_size, hidden_size)
 
     def forward(self, x):
-        gate, up = self.gate_up_proj(x).chunk(2, -1)
-        return self.down_proj(F.silu(gate) * up)
+        return self.down_proj(silu_mul(self.gate_up_proj(x)))
 
 
 class Qwen3DecoderLayer(nn.Module):

@@ -97,6 +97,29 @@ def test_paged_decode_attention_rejections():
     assert call(q=P(A16 + 4)) == _lib.NV4_E_ALIGN
 
 
+def test_decoder_ops_rejections():
+    lib = _lib.load()
+    rms = lib.nv4_rmsnorm
+    assert rms(None, None, None, P(A16), P(A16), 4, 4096, 1e-6, None) == _lib.NV4_E_NULL
+    assert rms(P(A16), P(A16), None, P(A16), P(A16), 4, 4096, 1e-6, None) == _lib.NV4_E_NULL  # residual pair
+    assert rms(P(A16), None, None, P(A16), P(A16), 4, 4100, 1e-6, None) == _lib.NV4_E_SHAPE   # H % 8
+    assert rms(P(A16), None, None, P(A16), P(A16), 4, 16384, 1e-6, None) == _lib.NV4_E_SHAPE  # H > 8192
+    assert rms(P(A16), None, None, P(A16), P(A16), 0, 4096, 1e-6, None) == _lib.NV4_E_SHAPE
+    assert rms(P(A16 + 2), None, None, P(A16), P(A16), 4, 4096, 1e-6, None) == _lib.NV4_E_ALIGN
+    qk = lib.nv4_qk_norm_rope_store
+    def call(qkv=P(A16), row=6144, T=4, Hq=32, Hkv=8, max_pos=4096, num_slots=1024):
+        return qk(qkv, row, T, Hq, Hkv, P(A16), P(A16), P(A16), max_pos, P(A16), P(A16), num_slots, P(A16),
+                  P(A16), P(A16), None, None, 1e-6, None)
+    assert call(qkv=None) == _lib.NV4_E_NULL
+    assert call(row=6000) == _lib.NV4_E_SHAPE
+    assert call(T=0) == _lib.NV4_E_SHAPE
+    assert call(max_pos=0) == _lib.NV4_E_SHAPE
+    silu = lib.nv4_silu_mul
+    assert silu(None, P(A16), 4, 12288, None) == _lib.NV4_E_NULL
+    assert silu(P(A16), P(A16), 4, 12, None) == _lib.NV4_E_SHAPE
+    assert silu(P(A16 + 8), P(A16), 4, 12288, None) == _lib.NV4_E_ALIGN
+
+
 def test_python_wrappers_validate_like_the_reference():
     from nv4 import W4A4Linear, rht_quant_pack, w4a4_grouped_gemm
     x = torch.zeros(2, 4096, dtype=torch.bfloat16)

@@ -8,15 +8,14 @@ groups 1/2/4, block sizes 256 and 16, and queries read as a strided view of
 a fused qkv tensor; against softmax(scale q.K^T) V computed in fp32.  Bar:
 |out - ref| <= 1e-2 + 1e-2 |ref| (bf16 output).  Prefill attention (causal
 GQA through the fused flash SDPA kernel) against the same fp32 reference on
-short packed sequences, same bar.  The KV store writes exactly the mapped
-slots.
+short packed sequences, same bar.
 """
 import math
 
 import pytest
 import torch
 
-from nv4.attention import paged_decode_attention, prefill_attention, store_kvcache
+from nv4.attention import paged_decode_attention, prefill_attention
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda:0"
@@ -118,18 +117,3 @@ def test_prefill_attention_flash():
         ref = torch.matmul(torch.softmax(s, dim=-1), vf).transpose(0, 1)
         check(out[start:start + n], ref, f"prefill n={n}")
         start += n
-
-
-def test_store_kvcache_writes_mapped_slots():
-    kc = torch.zeros(4, 16, 8, 128, dtype=torch.bfloat16, device=DEV)
-    vc = torch.zeros_like(kc)
-    k = torch.randn(5, 8, 128, device=DEV).to(torch.bfloat16)
-    v = torch.randn(5, 8, 128, device=DEV).to(torch.bfloat16)
-    slots = torch.tensor([3, 17, 40, 41, 63], dtype=torch.int32, device=DEV)
-    store_kvcache(k, v, kc, vc, slots)
-    torch.cuda.synchronize()
-    flat_k, flat_v = kc.view(-1, 8, 128), vc.view(-1, 8, 128)
-    assert torch.equal(flat_k[slots.long()], k) and torch.equal(flat_v[slots.long()], v)
-    mask = torch.ones(64, dtype=torch.bool, device=DEV)
-    mask[slots.long()] = False
-    assert not flat_k[mask].any() and not flat_v[mask].any()

@@ -1,0 +1,161 @@
+"""GPU parity of the fused decoder elementwise kernels against fp32 PyTorch.
+
+Each kernel is compared with the reference's PyTorch formulation of the
+same op, written out below in fp32 with the reference's bf16 rounding
+points (nanovllm/layers/layernorm.py:16-50, nanovllm/layers/rotary_embedding.py:
+6-48, nanovllm/models/qwen3.py:78-94, nanovllm/layers/activation.py:8-11,
+nanovllm/layers/attention.py:10-40):
+
+* bit-exact where no reduction or transcendental is involved (the residual
+  sum, the value copy into the cache, untouched cache slots);
+* elsewhere within one bf16 ulp, with at most 1% of the elements off by that
+  ulp: the kernels sum x^2 in another order than torch's reduction (so the
+  reciprocal RMS can differ in its last fp32 bit) and exp may differ by an
+  ulp between implementations, which moves a bf16 rounding now and then.
+  A rotated output y1 = x1 cos - x2 sin inherits a one-ulp change of the
+  normalised x1 or x2 without the cancellation shrinking it, so its bound
+  adds 2^-7 (|x1| + |x2|).
+"""
+import pytest
+import torch
+import torch.nn.functional as F
+
+from nv4.kernels.decoder_ops import qk_norm_rope_store, rmsnorm, silu_mul
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda:0"
+EPS = 1e-6
+
+
+def close_bf16(out, ref, what, frac=0.01, extra=None):
+    """|out - ref| <= 1 bf16 ulp of ref (+ ``extra``) everywhere; mismatches <= frac."""
+    o, r = out.float(), ref.float()
+    ulp = torch.where(r == 0, torch.full_like(r, 2.0 ** -133), r.abs() * 2.0 ** -7)
+    if extra is not None:
+        ulp = ulp + extra
+    bad = (o - r).abs() > ulp * 1.001
+    assert not bad.any(), f"{what}: {int(bad.sum())} elements off by more than one ulp"
+    mism = (o != r).float().mean().item()
+    assert mism <= frac, f"{what}: {mism:.4f} of the elements differ by an ulp"
+
+
+def ref_rms(x, w, residual=None):
+    h = x.float()
+    if residual is not None:
+        h = h + residual.float()
+    res = h.to(torch.bfloat16)
+    r = torch.rsqrt(h.pow(2).mean(dim=-1, keepdim=True) + EPS)
+    y = ((h * r).to(torch.bfloat16).float() * w.float()).to(torch.bfloat16)
+    return y, res
+
+
+@pytest.mark.parametrize("rows,H", [(1, 4096), (7, 4096), (64, 4096), (300, 1024), (3, 8192), (5, 136)])
+@pytest.mark.parametrize("with_residual", [False, True])
+def test_rmsnorm(rows, H, with_residual):
+    g = torch.Generator(device=DEV).manual_seed(rows * 31 + H)
+    x = (torch.randn(rows, H, generator=g, device=DEV) * 3).to(torch.bfloat16)
+    w = (1 + 0.1 * torch.randn(H, generator=g, device=DEV)).to(torch.bfloat16)
+    res = torch.randn(rows, H, generator=g, device=DEV).to(torch.bfloat16) if with_residual else None
+    ref_y, ref_res = ref_rms(x, w, res)
+    if with_residual:
+        y, new_res = rmsnorm(x, w, EPS, residual=res)
+        assert new_res.data_ptr() == res.data_ptr()
+        assert torch.equal(new_res, ref_res)
+    else:
+        y = rmsnorm(x, w, EPS)
+    close_bf16(y, ref_y, f"rmsnorm rows={rows} H={H}")
+
+
+def test_rmsnorm_in_place_output():
+    g = torch.Generator(device=DEV).manual_seed(4)
+    x = torch.randn(9, 4096, generator=g, device=DEV).to(torch.bfloat16)
+    w = torch.ones(4096, dtype=torch.bfloat16, device=DEV)
+    ref_y, _ = ref_rms(x, w)
+    y = rmsnorm(x, w, EPS, out=x)
+    assert y.data_ptr() == x.data_ptr()
+    close_bf16(y, ref_y, "rmsnorm in place")
+
+
+def ref_qk(qkv, Hq, Hkv, qw, kw, cos_sin, positions):
+    D = 128
+    T = qkv.shape[0]
+    q = qkv[:, :Hq * D].reshape(T, Hq, D)
+    k = qkv[:, Hq * D:(Hq + Hkv) * D].reshape(T, Hkv, D)
+    v = qkv[:, (Hq + Hkv) * D:(Hq + 2 * Hkv) * D].reshape(T, Hkv, D)
+    q, _ = ref_rms(q, qw)
+    k, _ = ref_rms(k, kw)
+    cos, sin = cos_sin[positions].chunk(2, dim=-1)  # [T, 1, 64]
+
+    def rot(x):
+        x1, x2 = x.float().chunk(2, dim=-1)
+        return torch.cat((x1 * cos - x2 * sin, x2 * cos + x1 * sin), dim=-1).to(torch.bfloat16)
+
+    def slack(x):  # one-ulp change of either rotated input
+        x1, x2 = x.float().abs().chunk(2, dim=-1)
+        return (x1 + x2).repeat(1, 1, 2) * 2.0 ** -7
+
+    return rot(q), rot(k), v.contiguous(), slack(q), slack(k)
+
+
+def rope_table(max_pos, base=1_000_000.0):
+    inv = 1.0 / (base ** (torch.arange(0, 128, 2, dtype=torch.float) / 128))
+    f = torch.arange(max_pos, dtype=torch.float)[:, None] * inv[None, :]
+    return torch.cat((f.cos(), f.sin()), dim=-1).unsqueeze_(1).to(DEV)
+
+
+@pytest.mark.parametrize("T,Hq,Hkv", [(1, 32, 8), (3, 32, 8), (33, 32, 8), (260, 32, 8), (5, 8, 8), (4, 4, 1)])
+def test_qk_norm_rope_store(T, Hq, Hkv):
+    g = torch.Generator(device=DEV).manual_seed(T * 7 + Hq)
+    width = (Hq + 2 * Hkv) * 128
+    qkv_full = (torch.randn(T, width + 256, generator=g, device=DEV) * 2).to(torch.bfloat16)
+    qkv = qkv_full[:, :width]  # strided rows, as a slice of a wider projection output
+    qw = (1 + 0.2 * torch.randn(128, generator=g, device=DEV)).to(torch.bfloat16)
+    kw = (1 + 0.2 * torch.randn(128, generator=g, device=DEV)).to(torch.bfloat16)
+    table = rope_table(4096)
+    positions = torch.randint(0, 4096, (T,), generator=g, device=DEV)
+    nb, bs = 6, 64
+    kc = torch.zeros(nb, bs, Hkv, 128, dtype=torch.bfloat16, device=DEV)
+    vc = torch.zeros_like(kc)
+    slots = torch.randperm(nb * bs, generator=g, device=DEV)[:T].to(torch.int32)
+    if T > 2:
+        slots[1] = -1  # the reference's padding slot: not stored
+    rq, rk, rv, sq, sk = ref_qk(qkv, Hq, Hkv, qw, kw, table, positions)
+    q, k, v = qk_norm_rope_store(qkv, Hq, Hkv, qw, kw, table, positions, EPS, slot_mapping=slots, k_cache=kc,
+                                 v_cache=vc, return_kv=True)
+    close_bf16(q, rq, "q", extra=sq)
+    close_bf16(k, rk, "k", extra=sk)
+    assert torch.equal(v, rv)
+    keep = slots >= 0
+    idx = slots[keep].long()
+    flat_k, flat_v = kc.view(-1, Hkv, 128), vc.view(-1, Hkv, 128)
+    assert torch.equal(flat_k[idx], k[keep]) and torch.equal(flat_v[idx], v[keep])
+    mask = torch.ones(nb * bs, dtype=torch.bool, device=DEV)
+    mask[idx] = False
+    assert not flat_k[mask].any() and not flat_v[mask].any()
+    # decode form: no k/v outputs, same queries and cache contents
+    kc2, vc2 = torch.zeros_like(kc), torch.zeros_like(vc)
+    q2 = qk_norm_rope_store(qkv, Hq, Hkv, qw, kw, table, positions, EPS, slot_mapping=slots, k_cache=kc2,
+                            v_cache=vc2)
+    assert torch.equal(q2, q) and torch.equal(kc2, kc) and torch.equal(vc2, vc)
+
+
+@pytest.mark.parametrize("rows,I", [(1, 12288), (32, 12288), (70, 12288), (3, 8)])
+def test_silu_mul(rows, I):
+    g = torch.Generator(device=DEV).manual_seed(rows + I)
+    gu = (torch.randn(rows, 2 * I, generator=g, device=DEV) * 4).to(torch.bfloat16)
+    gate, up = gu.float().chunk(2, -1)
+    ref = (F.silu(gate).to(torch.bfloat16).float() * up).to(torch.bfloat16)
+    close_bf16(silu_mul(gu), ref, f"silu_mul rows={rows}")
+
+
+def test_silu_mul_extremes():
+    vals = torch.tensor([0.0, -0.0, 1.0, -1.0, 20.0, -20.0, 88.0, -88.0, 100.0, -100.0, 3e38, -3e38, 1e-30, -1e-30,
+                         float("inf"), float("-inf")], device=DEV)
+    g = vals.repeat(8)[:128 // 2 * 2]
+    gu = torch.cat([g, torch.full_like(g, 1.5)]).view(1, -1).to(torch.bfloat16)
+    gate, up = gu.float().chunk(2, -1)
+    ref = (F.silu(gate).to(torch.bfloat16).float() * up).to(torch.bfloat16)
+    out = silu_mul(gu)
+    fin = torch.isfinite(ref.float())
+    close_bf16(out[fin], ref[fin], "silu extremes", frac=0.05)
+    assert torch.equal(out[~fin].float().nan_to_num(0.0), ref[~fin].float().nan_to_num(0.0))
