@@ -22,6 +22,10 @@ Timing rules:
   the roofline fraction against the 8 TB/s HBM peak.
 * The CPU baseline is the repository's C oracle (the same chain), timed on
   this host's cores on a bounded number of steps.
+* ``e2e_decode``: the decoder around the hot path, end to end -- the
+  reference's latency benchmark (32 x 4096-token prompts, serial prefill,
+  bs32 decode of 256 tokens with HIP-graph steps) on the Qwen3-8B-shaped
+  model with random weights, W4A4 projections against BF16 hipBLASLt ones.
 
 Prints ONE JSON line.  ``--gpus`` above 1 is rejected: this path runs on one
 GPU (rows of M are independent; see the design notes for sharding).
@@ -49,6 +53,9 @@ INT8_PEAK_TOPS = 5000.0        # MI355X dense int8 MFMA, published (no sparsity)
 PUBLISHED_CHAIN_M32_US = {"qkv": 28.12, "o": 21.87, "gate_up": 86.85, "down": 64.65}
 PUBLISHED_GEMM_M32_US = {"qkv": 21.25, "o": 14.97, "gate_up": 79.86, "down": 46.06}
 PUBLISHED_GEMM_M4096_US = {"qkv": 861.77, "o": 505.62, "gate_up": 3293.68, "down": 1550.64}
+# Published bs32 decode tokens/s of the real Qwen3-8B (one RTX A6000, 32 x 4096
+# prompts, 256 output tokens), benchmarks/README.md:65.
+PUBLISHED_E2E_TOKS = {"bf16": 564.57, "w4a4": 766.71}
 
 
 def k2_bytes(M, N, K):
@@ -69,6 +76,9 @@ def parse_args():
     ap.add_argument("--no-detail", action="store_true", help="skip the per-projection M=32/M=4096 table")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
     ap.add_argument("--cpu-seconds", type=float, default=15.0, help="target CPU baseline sample length")
+    ap.add_argument("--no-e2e", action="store_true", help="skip the end-to-end bs32 decode of the decoder")
+    ap.add_argument("--e2e-layers", type=int, default=36, help="decoder layers of the end-to-end model")
+    ap.add_argument("--e2e-tokens", type=int, default=256, help="output tokens per request (end to end)")
     ap.add_argument("--pmc-pass", action="store_true",
                     help="for rocprofv3 --pmc: eager decode GEMM launches (3 rounds over the rotating sets) "
                          "and three plain 256 MiB device copies as the counter calibration, then exit")
@@ -162,6 +172,43 @@ def measured_traffic():
             return json.load(f)
     except (OSError, ValueError):
         return None
+
+
+# -------------------------------------------------------------- end to end
+def e2e_decode(torch, layers, out_tokens):
+    """The reference's latency benchmark on the Qwen3-8B-shaped decoder with
+    random weights: 32 requests of 4096 seeded token ids, serial prefill, then
+    bs32 decode of ``out_tokens`` tokens (HIP-graph steps), for the W4A4 and
+    the BF16 (hipBLASLt) projections; decode tokens/s = 32 * 1000 / mean step
+    ms over the pure-decode steps (benchmarks/bench_nano_latency.py:32-121)."""
+    from nv4.engine import Engine, qwen3_8b_config, run_decode_benchmark, seeded_prompts
+    cfg = qwen3_8b_config(layers)
+    prompts = seeded_prompts(32, 4096, cfg.vocab_size)
+    res, kv = {}, None
+    for which in ("w4a4", "bf16"):
+        eng = Engine(cfg, use_w4a4=(which == "w4a4"), max_num_seqs=32, max_model_len=4096 + out_tokens,
+                     device="cuda:0", seed=1, kv_cache=kv)
+        kv = eng.kv_cache
+        r = run_decode_benchmark(eng, prompts, output_tokens=out_tokens)
+        if not (r["graph_equals_eager"] and r["logits_finite"]):
+            raise RuntimeError(f"end-to-end {which}: graph replay differs from eager or logits not finite")
+        steps = sorted(r["decode_ms"])
+        res[which] = {"tokens_per_s": round(r["tokens_per_s"], 1), "decode_ms_mean": round(r["decode_ms_mean"], 4),
+                      "decode_ms_p50": round(steps[len(steps) // 2], 4),
+                      "prefill_ms_mean": round(sum(r["prefill_ms"][1:]) / (len(r["prefill_ms"]) - 1), 2),
+                      "published_a6000_tokens_per_s": PUBLISHED_E2E_TOKS[which]}
+        print(f"[e2e] {which}: {res[which]['tokens_per_s']} tok/s, {res[which]['decode_ms_mean']} ms/step",
+              file=sys.stderr, flush=True)
+        del eng
+        torch.cuda.empty_cache()
+    del kv
+    torch.cuda.empty_cache()
+    res["w4a4_over_bf16"] = round(res["w4a4"]["tokens_per_s"] / res["bf16"]["tokens_per_s"], 4)
+    res["workload"] = (f"Qwen3-8B-shaped decoder ({layers} layers, hidden 4096, intermediate 12288, 32 q / 8 kv "
+                       "heads, vocab 151936), random weights; 32 requests x 4096 seeded token ids, serial "
+                       f"prefill, bs32 decode of {out_tokens} tokens (HIP graph), KV cache bf16 paged "
+                       "(block 256); tokens/s over the pure-decode steps")
+    return res
 
 
 # ---------------------------------------------------------------- CPU leg
@@ -329,6 +376,10 @@ def main():
 
     if not args.no_detail:
         line["detail"] = detail_table(torch, nv4, W, dev, R)
+    del graphs, sets, acts
+    torch.cuda.empty_cache()
+    if not args.no_e2e:
+        line["e2e_decode"] = e2e_decode(torch, args.e2e_layers, args.e2e_tokens)
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(M, args.cpu_seconds)
         line["cpu_baseline"]["gpu_speedup"] = round(line["cpu_baseline"]["value"] / step_us, 1)
