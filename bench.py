@@ -88,13 +88,15 @@ def parse_args():
 # ----------------------------------------------------------------- inputs
 def make_layer_sets(torch, W, M, rotate, dev):
     """Weight sets: set 0 is the seeded CPU workload (shared with the oracle),
-    the others are drawn on the GPU with the same recipe."""
+    the others are drawn on the GPU with the same recipe.  Packed weights are
+    stored in the MFMA-tiled order, as W4A4Linear keeps them after loading."""
+    import nv4
     acts, sets = {}, []
     base = {}
     for p in PROJECTIONS:
         case = W.w4a4_case(p, M)
         acts[p] = case.x.to(dev)
-        base[p] = (case.signs.to(dev), case.w_packed.to(dev), case.w_scale.to(dev))
+        base[p] = (case.signs.to(dev), nv4.tile_weights(case.w_packed.to(dev)), case.w_scale.to(dev))
     sets.append(base)
     g = torch.Generator(device=dev)
     g.manual_seed(W.BASE_SEED + 1000)
@@ -105,7 +107,7 @@ def make_layer_sets(torch, W, M, rotate, dev):
             sg = (torch.randint(0, 2, (K,), generator=g, device=dev, dtype=torch.int8) * 2 - 1)
             wp = torch.randint(-128, 128, (N, K // 2), generator=g, device=dev, dtype=torch.int16).to(torch.int8)
             sw = (0.005 + 0.015 * torch.rand(N, K // 128, generator=g, device=dev)).to(torch.bfloat16)
-            layer[p] = (sg.contiguous(), wp.contiguous(), sw.contiguous())
+            layer[p] = (sg.contiguous(), nv4.tile_weights(wp.contiguous()), sw.contiguous())
         sets.append(layer)
     return acts, sets
 
@@ -280,12 +282,12 @@ def main():
     sc = {p: torch.empty((M, W.PROJECTIONS[p][1] // 128), dtype=torch.bfloat16, device=dev) for p in PROJECTIONS}
     out = {p: torch.empty((M, W.PROJECTIONS[p][0]), dtype=torch.bfloat16, device=dev) for p in PROJECTIONS}
 
-    def linear(l, p):  # W4A4Linear.forward: RHT+quant+pack, then the grouped GEMM
+    def linear(l, p):  # W4A4Linear.forward: RHT+quant+pack, then the grouped GEMM (tiled weights)
         nv4.w4a4_linear(acts[p], sets[l][p][0], sets[l][p][1], sets[l][p][2],
-                        out=out[p], out_packed=pk[p], out_scale=sc[p])
+                        out=out[p], out_packed=pk[p], out_scale=sc[p], weights_tiled=True)
 
     def gemm(l, p):  # the GEMM alone, on the codes the last linear call left in pk/sc
-        nv4.w4a4_grouped_gemm(pk[p], sets[l][p][1], sc[p], sets[l][p][2], out=out[p])
+        nv4.w4a4_grouped_gemm(pk[p], sets[l][p][1], sc[p], sets[l][p][2], out=out[p], weights_tiled=True)
 
     def step(l):
         for p in PROJECTIONS:
@@ -362,7 +364,8 @@ def main():
             "M": M, "rotate": R,
         },
         "roofline": {
-            "kernel": "decode grouped INT4 GEMM (k2_decode for qkv/o/down, k2_wide for gate_up), M=32",
+            "kernel": ("decode grouped INT4 GEMM on MFMA-tiled weights (k2_dec for qkv/o/down, k2_wide for "
+                       "gate_up), M=32"),
             "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
             "traffic": (traffic or {}).get("bytes_per_launch"),
@@ -407,12 +410,13 @@ def detail_table(torch, nv4, W, dev, R):
                 wp = torch.randint(-128, 128, (N, K // 2), generator=g, device=dev,
                                    dtype=torch.int16).to(torch.int8)
                 sw = (0.005 + 0.015 * torch.rand(N, K // 128, generator=g, device=dev)).to(torch.bfloat16)
-                wsets.append((wp, sw))
+                wsets.append((nv4.tile_weights(wp), sw))
             pkb = torch.empty((M, K // 2), dtype=torch.int8, device=dev)
             scb = torch.empty((M, K // 128), dtype=torch.bfloat16, device=dev)
             ob = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
             l1 = [lambda: nv4.rht_quant_pack(x, sg, out_packed=pkb, out_scale=scb)] * rot
-            l2 = [lambda w=w: nv4.w4a4_grouped_gemm(pkb, w[0], scb, w[1], out=ob) for w in wsets]
+            l2 = [lambda w=w: nv4.w4a4_grouped_gemm(pkb, w[0], scb, w[1], out=ob, weights_tiled=True)
+                  for w in wsets]
             us1 = graph_launch_us(torch, l1, reps)
             us2 = graph_launch_us(torch, l2, reps)
             del wsets

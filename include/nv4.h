@@ -20,6 +20,11 @@
  *                          and :32 compile_grouped_gemm(..., output_fp32, weight_grouped)
  *   nv4_w4a4_linear     <- nanovllm/layers/linear_w4a4.py:27-35 W4A4Linear.forward
  *                          (rht_quant_pack + w4a4_grouped_gemm)
+ *   nv4_w4a4_gemm_tiled, nv4_w4a4_linear_tiled, nv4_w4a4_tile_weights,
+ *   nv4_w4a4_untile_weights <- the same two operators on weights stored in an
+ *                          MFMA-tiled order (no counterpart in the reference,
+ *                          whose kernels read [N,K/2]; W4A4Linear keeps the
+ *                          reference layout in its state dict)
  *   nv4_w4a16_gemm      <- nanovllm/layers/linear_w4a16.py:11 tl_dequant_matmul_w4a16
  *                          (called from W4A16Linear.forward :128-148)
  *   nv4_paged_decode_attention <- flash_attn_with_kvcache in the decode branch of
@@ -110,6 +115,30 @@ int nv4_w4a4_gemm(const int8_t* a, const int8_t* w, const void* sa, const void* 
 int nv4_w4a4_linear(const void* x, const int8_t* signs, const int8_t* w, const void* sw,
                     void* out, int8_t* a_packed, void* a_scale,
                     int64_t M, int64_t N, int64_t K, void* stream);
+
+/*
+ * MFMA-tiled packed weights.  The same N*K/2 bytes as [N,K/2], reordered so
+ * that the 16 columns x 128 k of one column block and K group are 1 KiB of
+ * consecutive memory in the order the matrix-core lanes consume them:
+ *   16-byte unit u = (cb*(K/128) + g)*64 + l  holds packed bytes
+ *   64*g + 16*(l/16) .. +15 of column 16*cb + l%16          (l = 0..63).
+ * Decode-sized GEMMs then load whole cache lines instead of half lines.
+ * N % 16 == 0, K % 128 == 0; both buffers 16-byte aligned and not overlapping.
+ */
+int nv4_w4a4_tile_weights(const int8_t* w, int8_t* w_tiled, int64_t N, int64_t K, void* stream);
+int nv4_w4a4_untile_weights(const int8_t* w_tiled, int8_t* w, int64_t N, int64_t K, void* stream);
+
+/*
+ * nv4_w4a4_gemm / nv4_w4a4_linear on MFMA-tiled weights (N % 16 == 0 as well);
+ * results are bit-identical to the reference-layout calls on the untiled
+ * weights.
+ */
+int nv4_w4a4_gemm_tiled(const int8_t* a, const int8_t* w_tiled, const void* sa, const void* sw,
+                        int sw_grouped, void* out, int out_fp32,
+                        int64_t M, int64_t N, int64_t K, void* stream);
+int nv4_w4a4_linear_tiled(const void* x, const int8_t* signs, const int8_t* w_tiled, const void* sw,
+                          void* out, int8_t* a_packed, void* a_scale,
+                          int64_t M, int64_t N, int64_t K, void* stream);
 
 /*
  * W4A16 GEMM with GPTQ weights (zero-point convention w = (q - z - 1) * s).

@@ -17,13 +17,17 @@
 // a group is irrelevant for an exact integer sum, so A and W are unpacked by
 // the same routine and fed to v_mfma_i32_*_i8 in matching lanes.
 //
+// Weights come in the reference layout [N][K/2] or in the MFMA-tiled layout
+// (nv4_w4a4_tile_weights: 16 columns x 128 k of one column block and group
+// as 1 KiB in lane order), which lets every weight load be whole cache
+// lines; the results are the same bits.
+//
 // Three kernels, no split-K, no atomics:
-//  * k2_decode (M <= 64): one workgroup per 16 (or 32) output columns and all
-//    M rows.  Its eight waves each take one K-group per sub-round, compute
-//    the exact int32 group dots with v_mfma_i32_16x16x64_i8 and hand them to
-//    the whole workgroup through LDS, which runs the fp32 epilogue in group
-//    order.  Loads run several sub-rounds ahead.  The weight stream
-//    (N*K/2 bytes) dominates, so this kernel is HBM-bound.
+//  * k2_dec (M <= 64): one workgroup per 16 output columns and all M rows.
+//    Its eight waves each take one K group per round, compute the exact
+//    int32 group dots with v_mfma_i32_16x16x64_i8 and hand them through LDS
+//    to the whole workgroup, which runs the fp32 epilogue in group order.
+//    Loads run several rounds ahead.
 //  * k2_wide (M <= 32, wide N): waves own column blocks over the whole K,
 //    activations widened once per CU into LDS.
 //  * k2_prefill (M > 64, w4a4_prefill.hip): LDS-staged 128x128 tiles.
@@ -43,101 +47,117 @@ __device__ __forceinline__ void store_out(void* out, int64_t idx, float v) {
 }
 
 // ----------------------------------------------------------------------------
-// Decode kernel (M <= 64).  Workgroup = 8 waves, output tile = all M rows
-// (MB blocks of 16) x BN = 16*NB columns, whole K.  Groups are handed out in
-// sub-rounds of 8: in sub-round j wave w computes the exact int32 dots of
-// group 8j+w for the whole tile, the dots go through LDS, and every thread
-// then runs the in-order fp32 epilogue of those 8 groups for the outputs it
-// owns.  Loads run D sub-rounds ahead of use in a register ring; for
-// K = 4096 every byte the workgroup needs is requested before the first MFMA.
+// Decode kernel (M <= 64).  Workgroup = one 16-column block, all M rows
+// (MB row blocks of 16), whole K; its eight waves split the K groups: in
+// round r wave w takes group 8r + w.  Per group the wave computes the exact
+// int32 dots of the 16-column x ROWS tile (v_mfma_i32_16x16x64_i8, two per
+// row block) and writes them to LDS as int16; after the round's barrier each
+// thread advances the in-order fp32 epilogue of the output(s) it owns over
+// the round's eight groups while later rounds' loads are in flight.  Dots,
+// activation slices and scales are double buffered, so one barrier per round
+// suffices.
 //
-// Weights go straight from the ring into MFMA operands: lane l loads 16 bytes
-// of column l%16 (a quarter of the group's 64 bytes).  The activation slice
-// of a sub-round (all rows x 512 bytes) is shared by the eight waves, so it
-// is loaded cooperatively in whole 128-byte lines (8 lanes per line), staged
-// in LDS one sub-round ahead and read back as MFMA operands: half-line
-// per-lane loads would double the L1 misses of the activation re-reads, which
-// every workgroup of the launch makes.
+// Loads are shaped for the CU's load path, which moves whole contiguous
+// 128-byte lines several times faster than the 16 half-lines of a per-lane
+// MFMA operand load:
+//  * weights: with the MFMA-tiled layout (TW) one group of a column block is
+//    1 KiB, lane l's 16 bytes at l*16, so a wave loads whole lines; with the
+//    reference layout [N][K/2] lane l loads column l%16, bytes 16*(l/16) of
+//    the group's 64;
+//  * activations: the round's slice (ROWS rows x 512 bytes) is loaded in
+//    whole lines by all threads, staged in LDS one round ahead and read back
+//    as MFMA operands.
+// All loads of a round ride in a register ring D rounds deep (every byte of
+// a K = 4096 projection is requested before the first MFMA), together with
+// the round's scales (sa of every row and sw of the 16 columns, 8 groups).
 //
-// MFMA 16x16x64 i8 layout used here (checked by the parity tests):
-//   A operand: lane l supplies row l%16, B operand: lane l supplies column
-//   l%16; both take the same 16 k-slots (set l/16), so identical unpacking
-//   pairs every k.  Result: lane l holds C[4*(l/16) + i][l%16], i = 0..3.
-// LDS activation slice: row r at r*512 bytes, its 16-byte chunk c stored at
-// chunk (c & ~7) | ((c ^ r) & 7), so the 16 rows of one operand load fall in
-// distinct bank groups.
+// Layouts.  MFMA 16x16x64 i8: A operand lane l supplies row l%16, B operand
+// column l%16, both the k-slots of set l/16; lane l of the result holds
+// C[4*(l/16) + i][l%16], i = 0..3.  LDS activation slice: row r at r*512
+// bytes, its 16-byte chunk c at chunk (c & ~7) | ((c ^ r) & 7), so the 16
+// rows of one operand load fall in distinct bank groups.  Tile output
+// o = rb*256 + 4*l + i (row block rb, MFMA lane l, result i) is row
+// 16 rb + 4 (l/16) + i, column l%16: the epilogue's dot reads are
+// consecutive int16 over the threads.  Round scales: sal[row][group % 8]
+// and swl[column][group % 8], so a thread reads its eight in two 16-byte
+// loads.  Each phase issues all of its LDS reads before their first use
+// (the compiler would otherwise wait on each read in turn).
 //
 // Every global load is unconditional (indices clamped into range): a load
 // under a thread-dependent branch makes the compiler drain all outstanding
 // loads at the branch join, which would serialise the ring.
 // ----------------------------------------------------------------------------
-constexpr int DEC_WAVES = 8;
-constexpr int DEC_THREADS = DEC_WAVES * 64;
+constexpr int DC_WAVES = 8;
+constexpr int DC_T = DC_WAVES * 64;
 
-template <int MB, int NB, int D, bool SW_GROUPED, bool OUT_F32>
-__global__ void __launch_bounds__(DEC_THREADS)
-k2_decode(const int8_t* __restrict__ a, const int8_t* __restrict__ w,
-          const uint16_t* __restrict__ sa, const uint16_t* __restrict__ sw,
-          void* __restrict__ out, int M, int N, int K) {
-    constexpr int BN = 16 * NB, NBLK = MB * NB, ROWS = MB * 16;
-    constexpr int OPT = (NBLK * 256 + DEC_THREADS - 1) / DEC_THREADS;  // outputs per thread
-    constexpr int N_SA = ROWS * 8;                                      // scale entries per sub-round
-    constexpr int N_SW = SW_GROUPED ? BN * 8 : 0;
-    constexpr int SPT = (N_SA + N_SW + DEC_THREADS - 1) / DEC_THREADS;  // scale entries per thread
-    constexpr int APT = ROWS * 32 / DEC_THREADS;                        // activation chunks per thread (= MB)
+__device__ __forceinline__ int dc_swz(int r, int c) { return r * 512 + (((c & ~7) | ((c ^ r) & 7)) << 4); }
+
+template <int MB, int D, bool TW, bool SW_GROUPED, bool OUT_F32>
+__global__ void __launch_bounds__(DC_T, 2)
+k2_dec(const int8_t* __restrict__ a, const int8_t* __restrict__ w,
+       const uint16_t* __restrict__ sa, const uint16_t* __restrict__ sw,
+       void* __restrict__ out, int M, int N, int K) {
+    constexpr int ROWS = MB * 16, NOUT = ROWS * 16;
+    constexpr int OPT = (NOUT + DC_T - 1) / DC_T;                      // outputs per thread
+    constexpr int APT = ROWS * 32 / DC_T;                               // activation chunks per thread
+    constexpr int N_SA = ROWS * 8;                                      // scale entries per round
+    constexpr int N_SW = SW_GROUPED ? 16 * 8 : 0;
+    constexpr int SPT = (N_SA + N_SW + DC_T - 1) / DC_T;
+    static_assert(APT * DC_T == ROWS * 32, "activation slice must split evenly");
     __shared__ __align__(16) uint8_t a_l[2][ROWS * 512];
-    __shared__ int16_t dots[2][8][NBLK][256];
-    __shared__ float sal[2][8][ROWS];
-    __shared__ float swl[2][8][BN];
+    __shared__ __align__(16) int16_t dots[2][DC_WAVES][NOUT];
+    __shared__ __align__(16) float sal[2][ROWS][8];  // a row's 8 scales of the round together
+    __shared__ __align__(16) float swl[2][16][8];
     __shared__ float ssink[1];
 
     const int t = threadIdx.x;
     const int lane = t & 63, wave = t >> 6;
-    const int n0 = blockIdx.x * BN;
+    const int n0 = blockIdx.x * 16;
     const int G = K >> 7;
-    const int S = (G + 7) >> 3;  // sub-rounds
-    const int KB = K >> 1;       // packed bytes per row
-
+    const int R = (G + 7) >> 3;  // rounds
+    const int KB = K >> 1;
     const int rc = lane & 15, part = lane >> 4;
-    const int8_t* wp[NB];
-#pragma unroll
-    for (int nb = 0; nb < NB; ++nb)
-        wp[nb] = w + (int64_t)min(n0 + nb * 16 + rc, N - 1) * KB + part * 16;
+
+    // Weights: the tiled layout is [N/16][G][64 lanes][16 bytes].
+    const int8_t* wbase = TW ? w + (int64_t)blockIdx.x * G * 1024 + lane * 16
+                             : w + (int64_t)min(n0 + rc, N - 1) * KB + part * 16;
+    const int wstep = TW ? 1024 : 64;
 
     // Activation staging: thread t moves chunks q = t + 512 i (row q/32,
-    // chunk q%32 of the row's 512-byte slice).
+    // chunk q%32 of the row's 512-byte slice).  The slice of round r starts
+    // at byte 512 r, moved back so that it ends at the row end when the last
+    // round is partial.
     const int8_t* arow[APT];
     int a_c16[APT], a_dst[APT];
 #pragma unroll
     for (int i = 0; i < APT; ++i) {
-        const int q = t + i * DEC_THREADS;
+        const int q = t + i * DC_T;
         const int r = q >> 5, c = q & 31;
         arow[i] = a + (int64_t)min(r, M - 1) * KB;
         a_c16[i] = c * 16;
-        a_dst[i] = r * 512 + (((c & ~7) | ((c ^ r) & 7)) << 4);
+        a_dst[i] = dc_swz(r, c);
     }
-    // Start of the 512-byte slice staged for sub-round j: 512 j, moved back
-    // so that it ends at the row end when the last sub-round is partial.
-    auto slice_start = [&](int j) { return max(0, min(j * 512, KB - 512)); };
+    auto slice_start = [&](int r) { return max(0, min(r * 512, KB - 512)); };
 
-    // Scale staging: entry e < N_SA is sa[row = e/8][8j + e%8], then sw.
+    // Scale staging: entry e < N_SA is sa[row = e/8][8r + e%8] (stored at
+    // sal[.][e/8][e%8]), then sw.
     const uint16_t* sp[SPT];
     float* sdst[SPT];
     int sgl[SPT], sstride[SPT];
 #pragma unroll
     for (int q = 0; q < SPT; ++q) {
-        const int e = t + q * DEC_THREADS;
+        const int e = t + q * DC_T;
         sgl[q] = e & 7;
         if (e < N_SA) {
             const int row = e >> 3;
             sp[q] = sa + (int64_t)min(row, M - 1) * G;
-            sdst[q] = &sal[0][sgl[q]][row];
+            sdst[q] = &sal[0][row][sgl[q]];
             sstride[q] = 8 * ROWS;
         } else if (e < N_SA + N_SW) {
             const int col = (e - N_SA) >> 3;
             sp[q] = sw + (int64_t)min(n0 + col, N - 1) * G;
-            sdst[q] = &swl[0][sgl[q]][col];
-            sstride[q] = 8 * BN;
+            sdst[q] = &swl[0][col][sgl[q]];
+            sstride[q] = 8 * 16;
         } else {  // nothing to stage: load a valid scale, store to the sink
             sp[q] = sa;
             sdst[q] = ssink;
@@ -145,87 +165,84 @@ k2_decode(const int8_t* __restrict__ a, const int8_t* __restrict__ w,
         }
     }
 
-    v4u rw[D][NB], ra[D][APT];
+    v4u rw[D], ra[D][APT];
     uint16_t rs[D][SPT];
-
-    auto issue = [&](int j, v4u (&w_out)[NB], v4u (&a_out)[APT], uint16_t (&s_out)[SPT]) {
-        const int64_t g = min(j * 8 + wave, G - 1);
-#pragma unroll
-        for (int nb = 0; nb < NB; ++nb) w_out[nb] = *reinterpret_cast<const v4u*>(wp[nb] + g * 64);
-        const int aoff = slice_start(min(j, S - 1));
+    auto issue = [&](int r, v4u& w_out, v4u (&a_out)[APT], uint16_t (&s_out)[SPT]) {
+        w_out = *reinterpret_cast<const v4u*>(wbase + (int64_t)min(r * 8 + wave, G - 1) * wstep);
+        const int aoff = slice_start(min(r, R - 1));
 #pragma unroll
         for (int i = 0; i < APT; ++i)
             a_out[i] = *reinterpret_cast<const v4u*>(arow[i] + min(aoff + a_c16[i], KB - 16));
 #pragma unroll
-        for (int q = 0; q < SPT; ++q) s_out[q] = sp[q][min(j * 8 + sgl[q], G - 1)];
+        for (int q = 0; q < SPT; ++q) s_out[q] = sp[q][min(r * 8 + sgl[q], G - 1)];
     };
-    auto stage_a = [&](int j, const v4u (&a_in)[APT]) {
+    auto stage_a = [&](int r, const v4u (&a_in)[APT]) {
 #pragma unroll
-        for (int i = 0; i < APT; ++i) *reinterpret_cast<v4u*>(&a_l[j & 1][a_dst[i]]) = a_in[i];
+        for (int i = 0; i < APT; ++i) *reinterpret_cast<v4u*>(&a_l[r & 1][a_dst[i]]) = a_in[i];
+    };
+    auto mma = [&](int r, const v4u& w_in, const uint16_t (&s_in)[SPT]) {
+        const int buf = r & 1;
+        if (r * 8 + wave < G) {  // uniform over the wave
+            const int cbase = (wave * 64 + r * 512 - slice_start(r)) >> 4;  // group's chunk in the slice
+            v4u av[MB];  // every operand read issued before the first use
+#pragma unroll
+            for (int mb = 0; mb < MB; ++mb)
+                av[mb] = *reinterpret_cast<const v4u*>(&a_l[buf][dc_swz(mb * 16 + rc, cbase + part)]);
+            __builtin_amdgcn_sched_barrier(0);
+            const v4i w0 = unpack8_x16(w_in[0], w_in[1]);
+            const v4i w1 = unpack8_x16(w_in[2], w_in[3]);
+#pragma unroll
+            for (int mb = 0; mb < MB; ++mb) {
+                const v4i a0 = unpack8_x16(av[mb][0], av[mb][1]);
+                const v4i a1 = unpack8_x16(av[mb][2], av[mb][3]);
+                v4i acc = {0, 0, 0, 0};
+                acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, w0, acc, 0, 0, 0);
+                acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, w1, acc, 0, 0, 0);
+                // 256 * dot -> dot (exact); |dot| <= 8192 fits int16.
+                const uint32_t lo = ((uint32_t)(acc[0] >> 8) & 0xffffu) | ((uint32_t)(acc[1] >> 8) << 16);
+                const uint32_t hi = ((uint32_t)(acc[2] >> 8) & 0xffffu) | ((uint32_t)(acc[3] >> 8) << 16);
+                *reinterpret_cast<uint2*>(&dots[buf][wave][mb * 256 + lane * 4]) = make_uint2(lo, hi);
+            }
+        }
+#pragma unroll
+        for (int q = 0; q < SPT; ++q) sdst[q][buf * sstride[q]] = bf16_to_f32(s_in[q]);
     };
 
     float total[OPT];
 #pragma unroll
     for (int oi = 0; oi < OPT; ++oi) total[oi] = 0.0f;
-
-    auto consume = [&](int j, const v4u (&w_in)[NB], const v4u (&a_next)[APT], const uint16_t (&s_in)[SPT]) {
-        const int buf = j & 1;
-        const int g = j * 8 + wave;
-        if (g < G) {  // uniform over the wave
-            // Chunk of this group inside the staged slice.
-            const int shift = j * 512 - slice_start(j);  // bytes the slice was moved back
-            const int cbase = (wave * 64 + shift) >> 4;
-            v4i w0[NB], w1[NB];
-#pragma unroll
-            for (int nb = 0; nb < NB; ++nb) {
-                w0[nb] = unpack8_x16(w_in[nb][0], w_in[nb][1]);
-                w1[nb] = unpack8_x16(w_in[nb][2], w_in[nb][3]);
-            }
-#pragma unroll
-            for (int mb = 0; mb < MB; ++mb) {
-                const int r = mb * 16 + rc;
-                const int c = cbase + part;
-                const v4u av = *reinterpret_cast<const v4u*>(
-                    &a_l[buf][r * 512 + (((c & ~7) | ((c ^ r) & 7)) << 4)]);
-                const v4i a0 = unpack8_x16(av[0], av[1]);
-                const v4i a1 = unpack8_x16(av[2], av[3]);
-#pragma unroll
-                for (int nb = 0; nb < NB; ++nb) {
-                    v4i acc = {0, 0, 0, 0};
-                    acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, w0[nb], acc, 0, 0, 0);
-                    acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, w1[nb], acc, 0, 0, 0);
-                    // 256 * dot -> dot (exact); |dot| <= 8192 fits int16.
-                    const uint32_t lo = ((uint32_t)(acc[0] >> 8) & 0xffffu) | ((uint32_t)(acc[1] >> 8) << 16);
-                    const uint32_t hi = ((uint32_t)(acc[2] >> 8) & 0xffffu) | ((uint32_t)(acc[3] >> 8) << 16);
-                    *reinterpret_cast<uint2*>(&dots[buf][wave][mb * NB + nb][lane * 4]) = make_uint2(lo, hi);
-                }
-            }
-        }
-#pragma unroll
-        for (int q = 0; q < SPT; ++q) sdst[q][buf * sstride[q]] = bf16_to_f32(s_in[q]);
-        if (j + 1 < S) stage_a(j + 1, a_next);  // uniform
-        __syncthreads();
-        const int ng = min(8, G - j * 8);  // groups in this sub-round
+    auto epilogue = [&](int r) {
+        const int buf = r & 1;
+        const int ng = min(8, G - r * 8);
 #pragma unroll
         for (int oi = 0; oi < OPT; ++oi) {
-            const int o = t + oi * DEC_THREADS;
-            if (o < NBLK * 256) {
-                const int row = o / BN, col = o % BN;
-                const int blk = (row >> 4) * NB + (col >> 4);
-                const int e = ((((row & 15) >> 2) * 16 + (col & 15)) << 2) + (row & 3);
+            const int o = t + oi * DC_T;
+            if (o < NOUT) {
+                const int l = (o >> 2) & 63;
+                const int row = (o >> 8) * 16 + 4 * (l >> 4) + (o & 3), col = l & 15;
                 if (ng == 8) {
-                    float d[8], s[8];
+                    // All LDS reads first (one wait), then the in-order chain.
+                    int dr[8];
+#pragma unroll
+                    for (int gl = 0; gl < 8; ++gl) dr[gl] = dots[buf][gl][o];
+                    const v4f a0 = *reinterpret_cast<const v4f*>(&sal[buf][row][0]);
+                    const v4f a1 = *reinterpret_cast<const v4f*>(&sal[buf][row][4]);
+                    v4f w0 = {1.0f, 1.0f, 1.0f, 1.0f}, w1 = w0;
+                    if constexpr (SW_GROUPED) {
+                        w0 = *reinterpret_cast<const v4f*>(&swl[buf][col][0]);
+                        w1 = *reinterpret_cast<const v4f*>(&swl[buf][col][4]);
+                    }
+                    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
                     for (int gl = 0; gl < 8; ++gl) {
-                        d[gl] = (float)dots[buf][gl][blk][e];
-                        s[gl] = SW_GROUPED ? sal[buf][gl][row] * swl[buf][gl][col] : sal[buf][gl][row];
+                        const float sa_g = gl < 4 ? a0[gl & 3] : a1[gl & 3];
+                        const float s = SW_GROUPED ? sa_g * (gl < 4 ? w0[gl & 3] : w1[gl & 3]) : sa_g;
+                        total[oi] = __builtin_fmaf((float)dr[gl], s, total[oi]);
                     }
-#pragma unroll
-                    for (int gl = 0; gl < 8; ++gl) total[oi] = __builtin_fmaf(d[gl], s[gl], total[oi]);
                 } else {
                     for (int gl = 0; gl < ng; ++gl) {
-                        const float d = (float)dots[buf][gl][blk][e];
-                        const float s = SW_GROUPED ? sal[buf][gl][row] * swl[buf][gl][col] : sal[buf][gl][row];
+                        const float d = (float)dots[buf][gl][o];
+                        const float s = SW_GROUPED ? sal[buf][row][gl] * swl[buf][col][gl] : sal[buf][row][gl];
                         total[oi] = __builtin_fmaf(d, s, total[oi]);
                     }
                 }
@@ -236,29 +253,36 @@ k2_decode(const int8_t* __restrict__ a, const int8_t* __restrict__ w,
     static_for<0, D>([&](auto U) { issue(U, rw[U], ra[U], rs[U]); });
     stage_a(0, ra[0]);
     __syncthreads();
-
-    // Steady state: consume a slot, refill it D sub-rounds ahead.  The
-    // activation slice of sub-round j+1 (slot u+1) is staged during j.
-    int j0 = 0;
-    for (; j0 + D < S; j0 += D) {
+    // Steady state: round r uses slot r % D, stages the activation slice of
+    // round r + 1 (slot (r+1) % D) and refills slot r % D with round r + D.
+    int r0 = 0;
+    for (; r0 + D < R; r0 += D) {
         static_for<0, D>([&](auto U) {
             constexpr int u = U, un = (u + 1) % D;
-            consume(j0 + u, rw[u], ra[un], rs[u]);
-            issue(j0 + u + D, rw[u], ra[u], rs[u]);
+            mma(r0 + u, rw[u], rs[u]);
+            stage_a(r0 + u + 1, ra[un]);
+            issue(r0 + u + D, rw[u], ra[u], rs[u]);
+            __syncthreads();
+            epilogue(r0 + u);
         });
     }
-    // Tail: the last (at most D) sub-rounds are already in flight.
+    // Tail: the last (at most D) rounds are already in flight.
     static_for<0, D>([&](auto U) {
         constexpr int u = U, un = (u + 1) % D;
-        if (j0 + u < S) consume(j0 + u, rw[u], ra[un], rs[u]);
+        if (r0 + u < R) {
+            mma(r0 + u, rw[u], rs[u]);
+            if (r0 + u + 1 < R) stage_a(r0 + u + 1, ra[un]);
+            __syncthreads();
+            epilogue(r0 + u);
+        }
     });
 
 #pragma unroll
     for (int oi = 0; oi < OPT; ++oi) {
-        const int o = t + oi * DEC_THREADS;
-        const int row = o / BN, col = o % BN;
-        const int n = n0 + col;
-        if (o < NBLK * 256 && row < M && n < N) {
+        const int o = t + oi * DC_T;
+        const int l = (o >> 2) & 63;
+        const int row = (o >> 8) * 16 + 4 * (l >> 4) + (o & 3), n = n0 + (l & 15);
+        if (o < NOUT && row < M && n < N) {
             float v = total[oi];
             if constexpr (!SW_GROUPED) v = v * bf16_to_f32(sw[n]);
             store_out<OUT_F32>(out, (int64_t)row * N + n, v);
@@ -293,7 +317,7 @@ constexpr int WIDE_A_BYTES = 128 * 1024;  // widened activation block limit (M x
 constexpr int WIDE_SCALES = 1024;         // G * ROWS limit
 constexpr int WIDE_WSCALES = 3072;        // G * CBW * 16 limit
 
-template <int MB, int CBW, int D, bool SW_GROUPED, bool OUT_F32>
+template <int MB, int CBW, int D, bool TW, bool SW_GROUPED, bool OUT_F32>
 __global__ void __launch_bounds__(CBW * MB * 64)
 k2_wide(const int8_t* __restrict__ a, const int8_t* __restrict__ w,
         const uint16_t* __restrict__ sa, const uint16_t* __restrict__ sw,
@@ -316,7 +340,10 @@ k2_wide(const int8_t* __restrict__ a, const int8_t* __restrict__ w,
     const int rc = lane & 15, part = lane >> 4;
     const int col0 = blockIdx.x * COLS;
     const int col = col0 + cbl * 16 + rc;
-    const int8_t* wp = w + (int64_t)min(col, N - 1) * KB + part * 16;
+    // Weights: tiled layout [N/16][G][64 lanes][16 bytes] (TW) or [N][K/2].
+    const int8_t* wp = TW ? w + (int64_t)min(blockIdx.x * CBW + cbl, (N >> 4) - 1) * G * 1024 + lane * 16
+                          : w + (int64_t)min(col, N - 1) * KB + part * 16;
+    constexpr int WSTEP = TW ? 1024 : 64;
 
     // ---- activation block + scales: loads first, then the weight ring.
     v4u ra[AC];
@@ -339,7 +366,7 @@ k2_wide(const int8_t* __restrict__ a, const int8_t* __restrict__ w,
     }
     v4u rw[D];
     auto issue = [&](int g, v4u& w_out) {
-        w_out = *reinterpret_cast<const v4u*>(wp + (int64_t)min(g, G - 1) * 64);
+        w_out = *reinterpret_cast<const v4u*>(wp + (int64_t)min(g, G - 1) * WSTEP);
     };
     static_for<0, D>([&](auto U) { issue(U, rw[U]); });
     // Widen and store: packed chunk c of row r -> units 2c, 2c+1.
@@ -418,17 +445,12 @@ k2_wide(const int8_t* __restrict__ a, const int8_t* __restrict__ w,
     }
 }
 
-template <int MB, int NB, bool SG, bool OF>
-hipError_t launch_decode(const int8_t* a, const int8_t* w, const void* sa, const void* sw, void* out,
-                         int M, int N, int K, hipStream_t st) {
-    // Sub-rounds in flight: all of them for K <= 4096, six beyond.
-    const dim3 grid((unsigned)((N + 16 * NB - 1) / (16 * NB)));
-    const uint16_t* sap = static_cast<const uint16_t*>(sa);
-    const uint16_t* swp = static_cast<const uint16_t*>(sw);
-    if (K <= 4096)
-        hipLaunchKernelGGL((k2_decode<MB, NB, 4, SG, OF>), grid, dim3(DEC_THREADS), 0, st, a, w, sap, swp, out, M, N, K);
-    else
-        hipLaunchKernelGGL((k2_decode<MB, NB, 6, SG, OF>), grid, dim3(DEC_THREADS), 0, st, a, w, sap, swp, out, M, N, K);
+template <int MB, bool TW, bool SG, bool OF>
+hipError_t launch_dec(const int8_t* a, const int8_t* w, const void* sa, const void* sw, void* out,
+                      int M, int N, int K, hipStream_t st) {
+    constexpr int D = 4;  // rounds in flight: all of them for K <= 4096
+    hipLaunchKernelGGL((k2_dec<MB, D, TW, SG, OF>), dim3((unsigned)((N + 15) / 16)), dim3(DC_T), 0, st, a, w,
+                       static_cast<const uint16_t*>(sa), static_cast<const uint16_t*>(sw), out, M, N, K);
     return hipGetLastError();
 }
 
@@ -455,66 +477,64 @@ bool wide_fits(int M, int N, int K) {
            (int64_t)(K / 128) * 16 * (per_cu <= 4 ? 4 : per_cu <= 6 ? 6 : 8) <= WIDE_WSCALES;
 }
 
-template <int MB, int CBW, bool SG, bool OF>
+template <int MB, int CBW, bool TW, bool SG, bool OF>
 hipError_t launch_wide_cbw(const int8_t* a, const int8_t* w, const void* sa, const void* sw, void* out,
                            int M, int N, int K, hipStream_t st) {
     constexpr int D = 8;  // groups in flight per wave
     const int ncb = (N + 15) / 16;
-    hipLaunchKernelGGL((k2_wide<MB, CBW, D, SG, OF>), dim3((unsigned)((ncb + CBW - 1) / CBW)), dim3(CBW * MB * 64),
+    hipLaunchKernelGGL((k2_wide<MB, CBW, D, TW, SG, OF>), dim3((unsigned)((ncb + CBW - 1) / CBW)), dim3(CBW * MB * 64),
                        0, st, a, w, static_cast<const uint16_t*>(sa), static_cast<const uint16_t*>(sw), out, M, N, K);
     return hipGetLastError();
 }
 
-template <int MB, bool SG, bool OF>
+template <int MB, bool TW, bool SG, bool OF>
 hipError_t launch_wide(const int8_t* a, const int8_t* w, const void* sa, const void* sw, void* out,
                        int M, int N, int K, hipStream_t st) {
     // Column blocks per workgroup: enough that one workgroup per CU covers N.
     const int per_cu = ((N + 15) / 16 + cu_count() - 1) / cu_count();
-    if (per_cu <= 4) return launch_wide_cbw<MB, 4, SG, OF>(a, w, sa, sw, out, M, N, K, st);
-    if (per_cu <= 6) return launch_wide_cbw<MB, 6, SG, OF>(a, w, sa, sw, out, M, N, K, st);
-    return launch_wide_cbw<MB, 8, SG, OF>(a, w, sa, sw, out, M, N, K, st);
+    if (per_cu <= 4) return launch_wide_cbw<MB, 4, TW, SG, OF>(a, w, sa, sw, out, M, N, K, st);
+    if (per_cu <= 6) return launch_wide_cbw<MB, 6, TW, SG, OF>(a, w, sa, sw, out, M, N, K, st);
+    return launch_wide_cbw<MB, 8, TW, SG, OF>(a, w, sa, sw, out, M, N, K, st);
 }
 
-template <bool SG, bool OF>
+template <bool TW, bool SG, bool OF>
 hipError_t dispatch(const int8_t* a, const int8_t* w, const void* sa, const void* sw, void* out,
                     int M, int N, int K, hipStream_t st) {
     // Wide N: waves own column blocks, activations fetched once per CU.
     if (wide_fits(M, N, K)) {
-        return M <= 16 ? launch_wide<1, SG, OF>(a, w, sa, sw, out, M, N, K, st)
-                       : launch_wide<2, SG, OF>(a, w, sa, sw, out, M, N, K, st);
+        return M <= 16 ? launch_wide<1, TW, SG, OF>(a, w, sa, sw, out, M, N, K, st)
+                       : launch_wide<2, TW, SG, OF>(a, w, sa, sw, out, M, N, K, st);
     }
-    // Otherwise 32 columns per workgroup for wide N halves the activation
-    // re-reads while still giving every CU several workgroups.
-    const bool wide = N >= 16384;
-    if (M <= 16) return wide ? launch_decode<1, 2, SG, OF>(a, w, sa, sw, out, M, N, K, st)
-                             : launch_decode<1, 1, SG, OF>(a, w, sa, sw, out, M, N, K, st);
-    if (M <= 32) return wide ? launch_decode<2, 2, SG, OF>(a, w, sa, sw, out, M, N, K, st)
-                             : launch_decode<2, 1, SG, OF>(a, w, sa, sw, out, M, N, K, st);
-    if (M <= 48) return launch_decode<3, 1, SG, OF>(a, w, sa, sw, out, M, N, K, st);
-    if (M <= 64) return launch_decode<4, 1, SG, OF>(a, w, sa, sw, out, M, N, K, st);
-    return k2_prefill_launch(a, w, sa, sw, SG, out, OF, M, N, K, st);
+    if (M <= 16) return launch_dec<1, TW, SG, OF>(a, w, sa, sw, out, M, N, K, st);
+    if (M <= 32) return launch_dec<2, TW, SG, OF>(a, w, sa, sw, out, M, N, K, st);
+    if (M <= 48) return launch_dec<3, TW, SG, OF>(a, w, sa, sw, out, M, N, K, st);
+    if (M <= 64) return launch_dec<4, TW, SG, OF>(a, w, sa, sw, out, M, N, K, st);
+    return k2_prefill_launch(a, w, sa, sw, SG, out, OF, TW, M, N, K, st);
 }
 
-}  // namespace
-}  // namespace nv4
-
-extern "C" int nv4_w4a4_linear(const void* x, const int8_t* signs, const int8_t* w, const void* sw,
-                               void* out, int8_t* a_packed, void* a_scale,
-                               int64_t M, int64_t N, int64_t K, void* stream) {
-    using namespace nv4;
-    if (!x || !signs || !w || !sw || !out || !a_packed || !a_scale) return NV4_E_NULL;
-    if (K != 4096 && K != 12288) return NV4_E_SHAPE;
-    const int rc = nv4_rht_quant_pack(x, signs, a_packed, a_scale, M, K, NV4_LAYOUT_REFERENCE, stream);
-    if (rc != NV4_OK) return rc;
-    return nv4_w4a4_gemm(a_packed, w, a_scale, sw, 1, out, 0, M, N, K, stream);
+// MFMA-tiled weight layout <-> reference layout [N][K/2]: 16-byte unit
+// u = (cb*G + g)*64 + l of the tiled buffer is bytes 64 g + 16 (l/16) ..
+// +15 of column 16 cb + l%16.  One thread per unit, both directions.
+template <bool TO_TILED>
+__global__ void __launch_bounds__(256)
+tile_weights(const int8_t* __restrict__ src, int8_t* __restrict__ dst, int64_t units, int G, int KB) {
+    const int64_t u = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (u >= units) return;
+    const int l = (int)(u & 63);
+    const int64_t cg = u >> 6;  // cb * G + g
+    const int64_t cb = cg / G;
+    const int g = (int)(cg - cb * G);
+    const int64_t ref = (cb * 16 + (l & 15)) * KB + g * 64 + (l >> 4) * 16;
+    if constexpr (TO_TILED)
+        *reinterpret_cast<v4u*>(dst + u * 16) = *reinterpret_cast<const v4u*>(src + ref);
+    else
+        *reinterpret_cast<v4u*>(dst + ref) = *reinterpret_cast<const v4u*>(src + u * 16);
 }
 
-extern "C" int nv4_w4a4_gemm(const int8_t* a, const int8_t* w, const void* sa, const void* sw,
-                             int sw_grouped, void* out, int out_fp32,
-                             int64_t M, int64_t N, int64_t K, void* stream) {
-    using namespace nv4;
+int gemm_impl(const int8_t* a, const int8_t* w, const void* sa, const void* sw, int sw_grouped, void* out,
+              int out_fp32, bool tiled, int64_t M, int64_t N, int64_t K, void* stream) {
     if (!a || !w || !sa || !sw || !out) return NV4_E_NULL;
-    if (M < 1 || N < 1 || K < 128 || K % 128 || N % 8) return NV4_E_SHAPE;
+    if (M < 1 || N < 1 || K < 128 || K % 128 || N % 8 || (tiled && N % 16)) return NV4_E_SHAPE;
     if (M > 0x7fffffffLL || N > 0x7fffffffLL || K > (1LL << 20)) return NV4_E_SHAPE;
     if (M * (K / 128) > 0x7fffffffLL || N * (K / 128) > 0x7fffffffLL) return NV4_E_SHAPE;
     if (((M + 127) / 128) * ((N + 127) / 128) > 0x7fffffffLL) return NV4_E_SHAPE;
@@ -525,12 +545,80 @@ extern "C" int nv4_w4a4_gemm(const int8_t* a, const int8_t* w, const void* sa, c
     hipStream_t st = static_cast<hipStream_t>(stream);
     const int m = (int)M, n = (int)N, k = (int)K;
     hipError_t e;
-    if (sw_grouped) {
-        e = out_fp32 ? dispatch<true, true>(a, w, sa, sw, out, m, n, k, st)
-                     : dispatch<true, false>(a, w, sa, sw, out, m, n, k, st);
+    if (tiled) {
+        if (sw_grouped)
+            e = out_fp32 ? dispatch<true, true, true>(a, w, sa, sw, out, m, n, k, st)
+                         : dispatch<true, true, false>(a, w, sa, sw, out, m, n, k, st);
+        else
+            e = out_fp32 ? dispatch<true, false, true>(a, w, sa, sw, out, m, n, k, st)
+                         : dispatch<true, false, false>(a, w, sa, sw, out, m, n, k, st);
     } else {
-        e = out_fp32 ? dispatch<false, true>(a, w, sa, sw, out, m, n, k, st)
-                     : dispatch<false, false>(a, w, sa, sw, out, m, n, k, st);
+        if (sw_grouped)
+            e = out_fp32 ? dispatch<false, true, true>(a, w, sa, sw, out, m, n, k, st)
+                         : dispatch<false, true, false>(a, w, sa, sw, out, m, n, k, st);
+        else
+            e = out_fp32 ? dispatch<false, false, true>(a, w, sa, sw, out, m, n, k, st)
+                         : dispatch<false, false, false>(a, w, sa, sw, out, m, n, k, st);
     }
     return (int)e;
+}
+
+int linear_impl(const void* x, const int8_t* signs, const int8_t* w, const void* sw, void* out,
+                int8_t* a_packed, void* a_scale, bool tiled, int64_t M, int64_t N, int64_t K, void* stream) {
+    if (!x || !signs || !w || !sw || !out || !a_packed || !a_scale) return NV4_E_NULL;
+    if (K != 4096 && K != 12288) return NV4_E_SHAPE;
+    if (N < 1 || N % 8 || (tiled && N % 16)) return NV4_E_SHAPE;  // checked before K1 runs
+    const int rc = nv4_rht_quant_pack(x, signs, a_packed, a_scale, M, K, NV4_LAYOUT_REFERENCE, stream);
+    if (rc != NV4_OK) return rc;
+    return gemm_impl(a_packed, w, a_scale, sw, 1, out, 0, tiled, M, N, K, stream);
+}
+
+int tile_impl(const int8_t* src, int8_t* dst, bool to_tiled, int64_t N, int64_t K, void* stream) {
+    if (!src || !dst) return NV4_E_NULL;
+    if (N < 16 || N % 16 || K < 128 || K % 128 || K > (1LL << 20) || N > 0x7fffffffLL) return NV4_E_SHAPE;
+    if (reinterpret_cast<uintptr_t>(src) % 16 || reinterpret_cast<uintptr_t>(dst) % 16) return NV4_E_ALIGN;
+    const int64_t units = N * K / 32;
+    if ((units + 255) / 256 > 0x7fffffffLL) return NV4_E_SHAPE;
+    const dim3 grid((unsigned)((units + 255) / 256));
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    if (to_tiled)
+        hipLaunchKernelGGL(tile_weights<true>, grid, dim3(256), 0, st, src, dst, units, (int)(K / 128), (int)(K / 2));
+    else
+        hipLaunchKernelGGL(tile_weights<false>, grid, dim3(256), 0, st, src, dst, units, (int)(K / 128), (int)(K / 2));
+    return (int)hipGetLastError();
+}
+
+}  // namespace
+}  // namespace nv4
+
+extern "C" int nv4_w4a4_linear(const void* x, const int8_t* signs, const int8_t* w, const void* sw,
+                               void* out, int8_t* a_packed, void* a_scale,
+                               int64_t M, int64_t N, int64_t K, void* stream) {
+    return nv4::linear_impl(x, signs, w, sw, out, a_packed, a_scale, false, M, N, K, stream);
+}
+
+extern "C" int nv4_w4a4_linear_tiled(const void* x, const int8_t* signs, const int8_t* w_tiled, const void* sw,
+                                     void* out, int8_t* a_packed, void* a_scale,
+                                     int64_t M, int64_t N, int64_t K, void* stream) {
+    return nv4::linear_impl(x, signs, w_tiled, sw, out, a_packed, a_scale, true, M, N, K, stream);
+}
+
+extern "C" int nv4_w4a4_gemm(const int8_t* a, const int8_t* w, const void* sa, const void* sw,
+                             int sw_grouped, void* out, int out_fp32,
+                             int64_t M, int64_t N, int64_t K, void* stream) {
+    return nv4::gemm_impl(a, w, sa, sw, sw_grouped, out, out_fp32, false, M, N, K, stream);
+}
+
+extern "C" int nv4_w4a4_gemm_tiled(const int8_t* a, const int8_t* w_tiled, const void* sa, const void* sw,
+                                   int sw_grouped, void* out, int out_fp32,
+                                   int64_t M, int64_t N, int64_t K, void* stream) {
+    return nv4::gemm_impl(a, w_tiled, sa, sw, sw_grouped, out, out_fp32, true, M, N, K, stream);
+}
+
+extern "C" int nv4_w4a4_tile_weights(const int8_t* w, int8_t* w_tiled, int64_t N, int64_t K, void* stream) {
+    return nv4::tile_impl(w, w_tiled, true, N, K, stream);
+}
+
+extern "C" int nv4_w4a4_untile_weights(const int8_t* w_tiled, int8_t* w, int64_t N, int64_t K, void* stream) {
+    return nv4::tile_impl(w_tiled, w, false, N, K, stream);
 }

@@ -99,7 +99,7 @@ __device__ __forceinline__ void pf_store(void* out, int64_t idx, float v) {
     }
 }
 
-template <bool FAST, bool SG, bool OF, bool WIN>
+template <bool FAST, bool SG, bool OF, bool WIN, bool TW>
 __device__ __forceinline__ void pf_body(const int8_t* __restrict__ a, const int8_t* __restrict__ w,
                                         const uint16_t* __restrict__ sa, const uint16_t* __restrict__ sw,
                                         void* __restrict__ out, int M, int N, int K, int m0, int n0,
@@ -121,16 +121,26 @@ __device__ __forceinline__ void pf_body(const int8_t* __restrict__ a, const int8
     // window is written every 8 groups; otherwise each group's scale is
     // loaded and written on its own -- a 2-byte load per row and group would
     // otherwise cost as many cache requests as all the operand data.
+    // With the MFMA-tiled weight layout (TW: [N/16][G][64 lanes][16 bytes])
+    // thread q instead moves lane q%64 of the tile's column block q/64 (tile
+    // row 16 (q/64) + q%16, chunk (q%64)/16): whole 1 KiB blocks per wave.
     const int8_t* a_t = a + (int64_t)m0 * KB;
-    const int8_t* w_t = w + (int64_t)n0 * KB;
+    const int8_t* w_t = TW ? w + (int64_t)(n0 >> 4) * G * 1024 : w + (int64_t)n0 * KB;
     uint32_t offa[2], offw[2];
-    int la[2];
+    int la[2], lw[2];
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
         const int q = t + i * PF_T, r = q >> 2, c = q & 3;
         offa[i] = (uint32_t)(min(r, M - 1 - m0) * KB + c * 16);
-        offw[i] = (uint32_t)(min(r, N - 1 - n0) * KB + c * 16);
         la[i] = pf_swz(r, 2 * c);  // chunk 2c+1 lands at la ^ 16
+        if constexpr (TW) {
+            const int j = q >> 6, l = q & 63;
+            offw[i] = (uint32_t)(min(j, ((N - n0) >> 4) - 1) * G * 1024 + l * 16);
+            lw[i] = pf_swz(j * 16 + (l & 15), 2 * (l >> 4));
+        } else {
+            offw[i] = (uint32_t)(min(r, N - 1 - n0) * KB + c * 16);
+            lw[i] = la[i];
+        }
     }
     const bool is_sa = t < PF_BM;
     const uint16_t* s_t = is_sa ? sa + (int64_t)m0 * G : (SG ? sw + (int64_t)n0 * G : sa + (int64_t)m0 * G);
@@ -144,7 +154,7 @@ __device__ __forceinline__ void pf_body(const int8_t* __restrict__ a, const int8
     uint32_t rs;
     auto load = [&](int g) {
         const int8_t* ag = a_t + g * 64;
-        const int8_t* wg = w_t + g * 64;
+        const int8_t* wg = w_t + g * (TW ? 1024 : 64);
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
             ra[i] = *reinterpret_cast<const v4u*>(ag + offa[i]);
@@ -160,8 +170,9 @@ __device__ __forceinline__ void pf_body(const int8_t* __restrict__ a, const int8
             const int l0 = la[i], l1 = la[i] ^ 16;
             *reinterpret_cast<v4i*>(st + l0) = unpack8_x16(ra[i][0], ra[i][1]);
             *reinterpret_cast<v4i*>(st + l1) = unpack8_x16(ra[i][2], ra[i][3]);
-            *reinterpret_cast<v4i*>(st + PF_A + l0) = unpack8_x16(rw[i][0], rw[i][1]);
-            *reinterpret_cast<v4i*>(st + PF_A + l1) = unpack8_x16(rw[i][2], rw[i][3]);
+            const int m0w = lw[i], m1w = lw[i] ^ 16;
+            *reinterpret_cast<v4i*>(st + PF_A + m0w) = unpack8_x16(rw[i][0], rw[i][1]);
+            *reinterpret_cast<v4i*>(st + PF_A + m1w) = unpack8_x16(rw[i][2], rw[i][3]);
         }
         if constexpr (!WIN) *reinterpret_cast<float*>(smem + slot(x) + t * 4) = bf16_to_f32(rs) * sfac;
     };
@@ -294,7 +305,7 @@ __device__ __forceinline__ void pf_body(const int8_t* __restrict__ a, const int8
     }
 }
 
-template <bool SG, bool OF, bool WIN>
+template <bool SG, bool OF, bool WIN, bool TW>
 __global__ void __launch_bounds__(PF_T, 2)
 k2_prefill(const int8_t* __restrict__ a, const int8_t* __restrict__ w, const uint16_t* __restrict__ sa,
            const uint16_t* __restrict__ sw, void* __restrict__ out, int M, int N, int K, int tm, int tn) {
@@ -325,12 +336,12 @@ k2_prefill(const int8_t* __restrict__ a, const int8_t* __restrict__ w, const uin
         __syncthreads();
     }
     if (fast)
-        pf_body<true, SG, OF, WIN>(a, w, sa, sw, out, M, N, K, m0, n0, smem);
+        pf_body<true, SG, OF, WIN, TW>(a, w, sa, sw, out, M, N, K, m0, n0, smem);
     else
-        pf_body<false, SG, OF, WIN>(a, w, sa, sw, out, M, N, K, m0, n0, smem);
+        pf_body<false, SG, OF, WIN, TW>(a, w, sa, sw, out, M, N, K, m0, n0, smem);
 }
 
-template <bool SG, bool OF>
+template <bool SG, bool OF, bool TW>
 hipError_t launch(const int8_t* a, const int8_t* w, const void* sa, const void* sw, void* out, int M, int N,
                   int K, hipStream_t st) {
     const int tm = (M + PF_BM - 1) / PF_BM, tn = (N + PF_BN - 1) / PF_BN;
@@ -340,10 +351,10 @@ hipError_t launch(const int8_t* a, const int8_t* w, const void* sa, const void* 
     const bool win = (K / 128) % 8 == 0 && reinterpret_cast<uintptr_t>(sa) % 16 == 0 &&
                      (!SG || reinterpret_cast<uintptr_t>(sw) % 16 == 0);
     if (win)
-        hipLaunchKernelGGL((k2_prefill<SG, OF, true>), dim3((unsigned)(tm * tn)), dim3(PF_T), 0, st, a, w, sap, swp,
-                           out, M, N, K, tm, tn);
+        hipLaunchKernelGGL((k2_prefill<SG, OF, true, TW>), dim3((unsigned)(tm * tn)), dim3(PF_T), 0, st, a, w, sap,
+                           swp, out, M, N, K, tm, tn);
     else
-        hipLaunchKernelGGL((k2_prefill<SG, OF, false>), dim3((unsigned)(tm * tn)), dim3(PF_T), 0, st, a, w, sap,
+        hipLaunchKernelGGL((k2_prefill<SG, OF, false, TW>), dim3((unsigned)(tm * tn)), dim3(PF_T), 0, st, a, w, sap,
                            swp, out, M, N, K, tm, tn);
     return hipGetLastError();
 }
@@ -351,13 +362,20 @@ hipError_t launch(const int8_t* a, const int8_t* w, const void* sa, const void* 
 }  // namespace
 
 hipError_t k2_prefill_launch(const int8_t* a, const int8_t* w, const void* sa, const void* sw,
-                             bool sw_grouped, void* out, bool out_fp32, int M, int N, int K,
+                             bool sw_grouped, void* out, bool out_fp32, bool w_tiled, int M, int N, int K,
                              hipStream_t st) {
+    if (w_tiled) {
+        if (sw_grouped)
+            return out_fp32 ? launch<true, true, true>(a, w, sa, sw, out, M, N, K, st)
+                            : launch<true, false, true>(a, w, sa, sw, out, M, N, K, st);
+        return out_fp32 ? launch<false, true, true>(a, w, sa, sw, out, M, N, K, st)
+                        : launch<false, false, true>(a, w, sa, sw, out, M, N, K, st);
+    }
     if (sw_grouped)
-        return out_fp32 ? launch<true, true>(a, w, sa, sw, out, M, N, K, st)
-                        : launch<true, false>(a, w, sa, sw, out, M, N, K, st);
-    return out_fp32 ? launch<false, true>(a, w, sa, sw, out, M, N, K, st)
-                    : launch<false, false>(a, w, sa, sw, out, M, N, K, st);
+        return out_fp32 ? launch<true, true, false>(a, w, sa, sw, out, M, N, K, st)
+                        : launch<true, false, false>(a, w, sa, sw, out, M, N, K, st);
+    return out_fp32 ? launch<false, true, false>(a, w, sa, sw, out, M, N, K, st)
+                    : launch<false, false, false>(a, w, sa, sw, out, M, N, K, st);
 }
 
 }  // namespace nv4

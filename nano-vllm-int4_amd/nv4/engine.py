@@ -45,7 +45,8 @@ def random_init(model: Qwen3ForCausalLM, seed: int) -> None:
     """Random-init weights of the workload: embeddings and LM head ~N(0,
     0.02), norms 1, W4A4 projections with codes uniform in [-8, 7] (random
     bytes), group-128 scales uniform in [0.005, 0.02] and RHT signs +-1, BF16
-    projections ~N(0, 0.02)."""
+    projections ~N(0, 0.02).  W4A4 weights end in the MFMA-tiled order, as
+    after the checkpoint loader."""
     dev = next(model.parameters()).device
     g = torch.Generator(device=dev).manual_seed(seed)
     for name, p in model.named_parameters():
@@ -59,6 +60,8 @@ def random_init(model: Qwen3ForCausalLM, seed: int) -> None:
                                                 dtype=torch.int16))
             m.weight_scale.copy_(0.005 + 0.015 * torch.rand(m.weight_scale.shape, generator=g, device=dev))
             m.signs.copy_(torch.randint(0, 2, m.signs.shape, generator=g, device=dev, dtype=torch.int16) * 2 - 1)
+            m.weights_tiled = False
+            m.tile_weights_()
 
 
 class Engine:

@@ -43,16 +43,44 @@ def _validate_config(cfg: GroupedConfig) -> None:
         raise ValueError("Require positive dimensions, K divisible by 128, N divisible by 8, and whole warps")
 
 
-def _launch(a_packed, w_packed, a_scale, w_scale, out, output_fp32, weight_grouped):
+def _launch(a_packed, w_packed, a_scale, w_scale, out, output_fp32, weight_grouped, weights_tiled=False):
     M, N, K = a_packed.shape[0], w_packed.shape[0], a_packed.shape[1] * 2
     lib = _lib.load()
+    fn = lib.nv4_w4a4_gemm_tiled if weights_tiled else lib.nv4_w4a4_gemm
     stream = torch.cuda.current_stream(a_packed.device).cuda_stream
     with torch.cuda.device(a_packed.device):
-        rc = lib.nv4_w4a4_gemm(ctypes.c_void_p(a_packed.data_ptr()), ctypes.c_void_p(w_packed.data_ptr()),
-                               ctypes.c_void_p(a_scale.data_ptr()), ctypes.c_void_p(w_scale.data_ptr()),
-                               1 if weight_grouped else 0, ctypes.c_void_p(out.data_ptr()),
-                               1 if output_fp32 else 0, M, N, K, ctypes.c_void_p(stream))
+        rc = fn(ctypes.c_void_p(a_packed.data_ptr()), ctypes.c_void_p(w_packed.data_ptr()),
+                ctypes.c_void_p(a_scale.data_ptr()), ctypes.c_void_p(w_scale.data_ptr()),
+                1 if weight_grouped else 0, ctypes.c_void_p(out.data_ptr()),
+                1 if output_fp32 else 0, M, N, K, ctypes.c_void_p(stream))
     _lib.check(rc, "w4a4_grouped_gemm")
+
+
+def _tile(src, to_tiled):
+    if src.ndim != 2 or src.dtype != torch.int8 or not src.is_cuda or not src.is_contiguous():
+        raise ValueError("Packed weights must be a contiguous int8 CUDA tensor [N,K/2]")
+    N, K = src.shape[0], src.shape[1] * 2
+    if N % 16 or K % GROUP_SIZE or min(N, K) < 1:
+        raise ValueError("The tiled weight layout needs N divisible by 16 and K divisible by 128")
+    dst = torch.empty_like(src)
+    lib = _lib.load()
+    fn = lib.nv4_w4a4_tile_weights if to_tiled else lib.nv4_w4a4_untile_weights
+    stream = torch.cuda.current_stream(src.device).cuda_stream
+    with torch.cuda.device(src.device):
+        rc = fn(ctypes.c_void_p(src.data_ptr()), ctypes.c_void_p(dst.data_ptr()), N, K, ctypes.c_void_p(stream))
+    _lib.check(rc, "tile_weights" if to_tiled else "untile_weights")
+    return dst
+
+
+def tile_weights(w_packed):
+    """[N,K/2] packed weights -> the same bytes in the MFMA-tiled order read
+    by the decode kernels (1 KiB per 16 columns x 128 k, lane-major)."""
+    return _tile(w_packed, True)
+
+
+def untile_weights(w_tiled):
+    """Inverse of ``tile_weights``."""
+    return _tile(w_tiled, False)
 
 
 @lru_cache(None)
@@ -84,8 +112,10 @@ def best_grouped_config(M, N, K, weight_grouped=False):
     return GroupedConfig() if M <= 32 else GroupedConfig(64, 128, 2, 128)
 
 
-def w4a4_grouped_gemm(a_packed, w_packed, a_scale, w_scale, out=None, config=None):
-    """Packed INT4; BF16 Sa[M,K/128], Sw[N] or Sw[N,K/128], output[M,N]."""
+def w4a4_grouped_gemm(a_packed, w_packed, a_scale, w_scale, out=None, config=None, *, weights_tiled=False):
+    """Packed INT4; BF16 Sa[M,K/128], Sw[N] or Sw[N,K/128], output[M,N].
+    ``weights_tiled``: ``w_packed`` holds ``tile_weights`` output (N % 16 == 0);
+    the result is bit-identical."""
     if a_packed.ndim != 2 or w_packed.ndim != 2 or a_packed.shape[1] != w_packed.shape[1]:
         raise ValueError("Packed inputs must have compatible [M,K/2] and [N,K/2] shapes")
     M, K = a_packed.shape[0], a_packed.shape[1] * 2
@@ -111,5 +141,7 @@ def w4a4_grouped_gemm(a_packed, w_packed, a_scale, w_scale, out=None, config=Non
         raise ValueError("Output must be contiguous BF16 [M,N] on the input device")
     if config is not None:
         _validate_config(config)
-    _launch(a_packed, w_packed, a_scale, w_scale, out, False, weight_grouped)
+    if weights_tiled and N % 16:
+        raise ValueError("The tiled weight layout needs N divisible by 16")
+    _launch(a_packed, w_packed, a_scale, w_scale, out, False, weight_grouped, weights_tiled)
     return out

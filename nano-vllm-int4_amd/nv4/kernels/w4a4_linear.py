@@ -16,8 +16,9 @@ import torch
 from .. import _lib
 
 
-def w4a4_linear(x, signs, w_packed, w_scale, *, out=None, out_packed=None, out_scale=None):
-    """x bf16 [M,K] (K = 4096 or 12288) -> bf16 [M,N]."""
+def w4a4_linear(x, signs, w_packed, w_scale, *, out=None, out_packed=None, out_scale=None, weights_tiled=False):
+    """x bf16 [M,K] (K = 4096 or 12288) -> bf16 [M,N].  ``weights_tiled``:
+    ``w_packed`` is in the MFMA-tiled order (``tile_weights``)."""
     if x.ndim != 2 or x.dtype != torch.bfloat16 or x.shape[1] not in (4096, 12288) or x.shape[0] < 1:
         raise ValueError("Expected BF16 X[M,K], M>0, K=4096/12288")
     M, K = x.shape
@@ -28,6 +29,8 @@ def w4a4_linear(x, signs, w_packed, w_scale, *, out=None, out_packed=None, out_s
     N = w_packed.shape[0] if w_packed.ndim == 2 else -1
     if tuple(signs.shape) != (K,) or tuple(w_packed.shape) != (N, K // 2) or N % 8 or N < 8:
         raise ValueError("Expected signs[K] and packed weights [N,K/2] with N divisible by 8")
+    if weights_tiled and N % 16:
+        raise ValueError("The tiled weight layout needs N divisible by 16")
     if tuple(w_scale.shape) != (N, K // 128):
         raise ValueError("Expected weight scales [N,K/128]")
     dev = x.device
@@ -46,10 +49,11 @@ def w4a4_linear(x, signs, w_packed, w_scale, *, out=None, out_packed=None, out_s
         raise ValueError("All tensors must be contiguous on one CUDA device")
     lib = _lib.load()
     stream = torch.cuda.current_stream(dev).cuda_stream
+    fn = lib.nv4_w4a4_linear_tiled if weights_tiled else lib.nv4_w4a4_linear
     with torch.cuda.device(dev):
-        rc = lib.nv4_w4a4_linear(ctypes.c_void_p(x.data_ptr()), ctypes.c_void_p(signs.data_ptr()),
-                                 ctypes.c_void_p(w_packed.data_ptr()), ctypes.c_void_p(w_scale.data_ptr()),
-                                 ctypes.c_void_p(out.data_ptr()), ctypes.c_void_p(out_packed.data_ptr()),
-                                 ctypes.c_void_p(out_scale.data_ptr()), M, N, K, ctypes.c_void_p(stream))
+        rc = fn(ctypes.c_void_p(x.data_ptr()), ctypes.c_void_p(signs.data_ptr()),
+                ctypes.c_void_p(w_packed.data_ptr()), ctypes.c_void_p(w_scale.data_ptr()),
+                ctypes.c_void_p(out.data_ptr()), ctypes.c_void_p(out_packed.data_ptr()),
+                ctypes.c_void_p(out_scale.data_ptr()), M, N, K, ctypes.c_void_p(stream))
     _lib.check(rc, "w4a4_linear")
     return out

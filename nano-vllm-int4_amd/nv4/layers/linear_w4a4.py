@@ -8,11 +8,18 @@ carry over, and the same forward: RHT + quantize + pack the activations
 (K1), then the grouped INT4 GEMM (K2), on the current stream through one C
 ABI call (``nv4_w4a4_linear``).  Temporary buffers come from torch's caching
 allocator, so the forward can be captured in a HIP graph.
+
+``tile_weights_()`` (called by the loaders once the weights are in) reorders
+``packed_weight`` in place into the MFMA-tiled order that the decode
+kernels read in whole cache lines; the forward then uses the tiled entry
+point, with bit-identical results.  ``state_dict()`` and
+``load_state_dict()`` still see the reference [out, in/2] layout.
 """
 import torch
 from torch import nn
 import torch.distributed as dist
 
+from ..kernels.w4a4_grouped import tile_weights, untile_weights
 from ..kernels.w4a4_linear import w4a4_linear
 
 
@@ -27,6 +34,26 @@ class W4A4Linear(nn.Module):
         self.register_buffer("packed_weight", torch.empty(output_size, input_size // 2, dtype=torch.int8))
         self.register_buffer("weight_scale", torch.empty(output_size, input_size // 128, dtype=torch.bfloat16))
         self.register_buffer("signs", torch.empty(input_size, dtype=torch.int8))
+        self.weights_tiled = False
+
+    @torch.no_grad()
+    def tile_weights_(self) -> "W4A4Linear":
+        """Reorder ``packed_weight`` into the MFMA-tiled layout (GPU, once)."""
+        if not self.weights_tiled and self.out_features % 16 == 0 and self.packed_weight.is_cuda:
+            self.packed_weight.copy_(tile_weights(self.packed_weight))
+            self.weights_tiled = True
+        return self
+
+    def _save_to_state_dict(self, destination, prefix, keep_vars):
+        super()._save_to_state_dict(destination, prefix, keep_vars)
+        if self.weights_tiled:
+            destination[prefix + "packed_weight"] = untile_weights(self.packed_weight)
+
+    def _load_from_state_dict(self, state_dict, prefix, *args, **kwargs):
+        super()._load_from_state_dict(state_dict, prefix, *args, **kwargs)
+        if self.weights_tiled and prefix + "packed_weight" in state_dict:
+            with torch.no_grad():
+                self.packed_weight.copy_(tile_weights(self.packed_weight))
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         if x.shape[-1] != self.in_features or x.dtype != torch.bfloat16:
@@ -35,5 +62,5 @@ class W4A4Linear(nn.Module):
         # RHT + quantize + pack, then the grouped INT4 GEMM; packed codes and
         # scales come from the caching allocator, so the forward can be
         # captured in a HIP graph.
-        out = w4a4_linear(flat, self.signs, self.packed_weight, self.weight_scale)
+        out = w4a4_linear(flat, self.signs, self.packed_weight, self.weight_scale, weights_tiled=self.weights_tiled)
         return out.reshape(*x.shape[:-1], self.out_features)

@@ -120,7 +120,11 @@ def load_w4a4_model(model, model_path, checkpoint_path):
                 module.packed_weight.copy_(packed)
                 module.weight_scale.copy_(scale)
                 module.signs.copy_(signs)
+                module.weights_tiled = False  # the buffer now holds the reference layout
                 count += len(sources)
+    for module in model.modules():  # decode-kernel weight order (GPU modules; bit-identical results)
+        if isinstance(module, W4A4Linear):
+            module.tile_weights_()
     return {"format": FORMAT, "projections": count, "native_linear_modules": len(layers) * 4,
             "checkpoint_manifest_sha256": sha256(checkpoint / "manifest.json"),
             "weight_group_size": 128, "activation_group_size": 128, "activation_clipping": 0.9,

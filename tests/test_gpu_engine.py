@@ -76,8 +76,10 @@ def test_w4a4_first_projection_matches_oracle(engines):
         h.remove()
     torch.cuda.synchronize()
     m = layer.self_attn.qkv_proj
-    packed, scale = oracle.rht_quant_pack(bf16_bits(seen["x"]), m.signs.cpu().numpy())
-    ref = oracle.w4a4_gemm(packed, m.packed_weight.cpu().numpy(), scale, bf16_bits(m.weight_scale))
+    assert m.weights_tiled  # the runner's projections read the MFMA-tiled layout
+    sd = m.state_dict()  # reference [out, in/2] layout
+    packed, scale = oracle.rht_quant_pack(bf16_bits(seen["x"]), sd["signs"].cpu().numpy())
+    ref = oracle.w4a4_gemm(packed, sd["packed_weight"].cpu().numpy(), scale, bf16_bits(sd["weight_scale"]))
     assert np.array_equal(bf16_bits(seen["y"]), ref)
 
 

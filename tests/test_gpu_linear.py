@@ -5,7 +5,9 @@ is rht_quant_pack followed by w4a4_grouped_gemm; the one-call operator must
 give the same bits as the oracle chain -- codes, scales and bf16 outputs --
 for the four Qwen3-8B projections across the decode and prefill kernels,
 repeated calls, a non-default stream and HIP-graph replay after the inputs
-change.  Bar: bit-exact.
+change -- with the weights in the reference layout and in the MFMA-tiled
+layout that ``W4A4Linear.tile_weights_()`` switches the module to (its
+state dict keeps the reference layout).  Bar: bit-exact.
 """
 import numpy as np
 import pytest
@@ -13,7 +15,7 @@ import torch
 
 import oracle
 from conftest import bf16_bits
-from nv4 import w4a4_linear
+from nv4 import W4A4Linear, tile_weights, w4a4_linear
 from nv4 import workloads as W
 
 pytestmark = pytest.mark.gpu
@@ -26,15 +28,17 @@ def expected(case):
     return packed, scale, oracle.w4a4_gemm(packed, case.w_packed.numpy(), scale, bf16_bits(case.w_scale))
 
 
-def run(case, stream=None):
+def run(case, stream=None, tiled=False):
     M, N, K = case.shape
     x, signs = case.x.to(DEV), case.signs.to(DEV)
     wp, ws = case.w_packed.to(DEV), case.w_scale.to(DEV)
+    if tiled:
+        wp = tile_weights(wp)
     packed = torch.full((M, K // 2), 85, dtype=torch.int8, device=DEV)
     scale = torch.full((M, K // 128), float("nan"), dtype=torch.bfloat16, device=DEV)
     out = torch.full((M, N), float("nan"), dtype=torch.bfloat16, device=DEV)
     with torch.cuda.stream(stream or torch.cuda.current_stream()):
-        w4a4_linear(x, signs, wp, ws, out=out, out_packed=packed, out_scale=scale)
+        w4a4_linear(x, signs, wp, ws, out=out, out_packed=packed, out_scale=scale, weights_tiled=tiled)
     torch.cuda.synchronize()
     return packed, scale, out
 
@@ -48,12 +52,13 @@ def check(case, got, what):
     assert bad.size == 0, f"{what}: {len(bad)} outputs differ, first {bad[:5].tolist()}"
 
 
+@pytest.mark.parametrize("tiled", [False, True])
 @pytest.mark.parametrize("proj", ["o", "qkv", "gate_up", "down"])
 @pytest.mark.parametrize("M", [1, 7, 32])
-def test_linear_qwen3_shapes(proj, M):
-    print(f"[linear] {proj} M={M}", flush=True)
+def test_linear_qwen3_shapes(proj, M, tiled):
+    print(f"[linear] {proj} M={M} tiled={tiled}", flush=True)
     case = W.w4a4_case(proj, M)
-    check(case, run(case), f"{proj} M={M}")
+    check(case, run(case, tiled=tiled), f"{proj} M={M} tiled={tiled}")
 
 
 @pytest.mark.parametrize("M", [16, 17, 33, 48, 64, 65])
@@ -63,6 +68,31 @@ def test_linear_m_blocks(M):
         print(f"[linear] {proj} M={M}", flush=True)
         case = W.w4a4_case(proj, M, seed=W.BASE_SEED + M)
         check(case, run(case), f"{proj} M={M}")
+        check(case, run(case, tiled=True), f"{proj} M={M} tiled")
+
+
+def test_module_tiled_weights_and_state_dict():
+    """W4A4Linear.tile_weights_(): same outputs; state_dict() returns and
+    load_state_dict() accepts the reference [out, in/2] layout."""
+    case = W.w4a4_case("qkv", 32)
+    x = case.x.to(DEV)
+    m = W4A4Linear(4096, 6144).to(DEV)
+    with torch.no_grad():
+        m.packed_weight.copy_(case.w_packed)
+        m.weight_scale.copy_(case.w_scale)
+        m.signs.copy_(case.signs)
+    plain = m(x)
+    _, _, o_ref = expected(case)
+    assert np.array_equal(bf16_bits(plain), o_ref)
+    m.tile_weights_()
+    assert m.weights_tiled and not torch.equal(m.packed_weight.cpu(), case.w_packed)
+    assert torch.equal(m(x), plain)
+    sd = m.state_dict()
+    assert torch.equal(sd["packed_weight"].cpu(), case.w_packed)
+    m2 = W4A4Linear(4096, 6144).to(DEV).tile_weights_()
+    m2.load_state_dict(sd)
+    assert m2.weights_tiled and torch.equal(m2.packed_weight, m.packed_weight)
+    assert torch.equal(m2(x), plain)
 
 
 def test_linear_repeated_calls_and_stream():

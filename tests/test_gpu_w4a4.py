@@ -8,7 +8,10 @@ three repeated calls, and the constant-scale reductions to the per-channel
 API.  Adds an M sweep across the kernel boundaries (skinny M <= 64, tiled
 above; tails in M and N) and the four Qwen3-8B projections at M = 32 (every
 element) and M = 4096 (a row sample, like the reference's pipeline audit,
-benchmarks/bench_rht_a4.py:184-190).  Bar: bit-exact.
+benchmarks/bench_rht_a4.py:184-190).  Every case with N % 16 == 0 runs again
+on the same weights in the MFMA-tiled layout (``tile_weights``), whose
+results must equal the reference-layout results bit for bit, and the tiled
+layout itself is pinned against its definition.  Bar: bit-exact.
 """
 import numpy as np
 import pytest
@@ -16,7 +19,7 @@ import torch
 
 import oracle
 from conftest import bf16_bits, bits_to_bf16
-from nv4 import compile_grouped_gemm, rht_quant_pack, w4a4_grouped_gemm
+from nv4 import compile_grouped_gemm, rht_quant_pack, tile_weights, untile_weights, w4a4_grouped_gemm
 from nv4 import workloads as W
 
 pytestmark = pytest.mark.gpu
@@ -77,7 +80,30 @@ def run_case(M, N, K, seed, grouped=True):
     compile_grouped_gemm(M, N, K, output_fp32=True, weight_grouped=grouped)(a, w, s_a, s_w, out32)
     torch.cuda.synchronize()
     assert_bits_equal(out32.cpu().numpy().view(np.uint32), exp_f32.view(np.uint32), "fp32 output")
+    if N % 16 == 0:
+        wt = tile_weights(w)
+        out.fill_(float("nan"))
+        w4a4_grouped_gemm(a, wt, s_a, s_w, out=out, weights_tiled=True)
+        torch.cuda.synchronize()
+        assert_bits_equal(bf16_bits(out), exp_bf16, "bf16 output, tiled weights")
+        assert torch.equal(storage[:64], sentinel) and torch.equal(storage[-64:], sentinel)
     return ap, wp, sa, sw, a, w, s_a, s_w
+
+
+@pytest.mark.parametrize("N,K", [(16, 128), (48, 384), (6144, 4096), (4096, 12288)])
+def test_tiled_weight_layout(N, K):
+    """The tiled order is the documented permutation: unit (cb*G + g)*64 + l
+    holds bytes 64 g + 16 (l/16) .. +15 of column 16 cb + l%16; untiling
+    restores the input."""
+    rng = np.random.default_rng(N + K)
+    w = rng.integers(-128, 128, (N, K // 2), dtype=np.int8)
+    ref = w.reshape(N // 16, 16, K // 128, 4, 16).transpose(0, 2, 3, 1, 4).reshape(N, K // 2)
+    wt = tile_weights(torch.from_numpy(w).to(DEV))
+    torch.cuda.synchronize()
+    assert np.array_equal(wt.cpu().numpy(), ref)
+    assert np.array_equal(untile_weights(wt).cpu().numpy(), w)
+    with pytest.raises(ValueError):
+        tile_weights(torch.zeros((24, 64), dtype=torch.int8, device=DEV))
 
 
 @pytest.mark.parametrize("M,N,K", [(17, 96, 512), (33, 136, 4096), (32, 128, 12288)])
@@ -110,14 +136,16 @@ def test_k2_per_channel_scale(M, N, K):
 def test_k2_m_sweep(M):
     run_case(M, 136, 1024, 1000 + M)
     run_case(M, 264, 256, 2000 + M, grouped=False)
+    run_case(M, 272, 512, 2500 + M)  # 17 column blocks: tiled weights, column-block tail in a prefill tile
 
 
 @pytest.mark.parametrize("M,N,K", [(1, 4104, 4096), (16, 4104, 4096), (17, 4104, 4096), (32, 4104, 4096),
                                    (33, 4104, 4096), (48, 264, 4096), (8, 520, 12288), (16, 264, 8192)])
 def test_k2_decode_activations_in_lds(M, N, K):
-    """Shapes served by the persistent decode kernel that keeps the packed
-    activations in LDS: every M block, a column tail, more 16-column tiles
-    than compute units (a workgroup walks several tiles), K = 8192 and 12288."""
+    """Shapes served by the decode kernel (one workgroup per 16 columns, the
+    K groups split over its waves, activation slices staged in LDS): every
+    M block, a column tail, more 16-column blocks than compute units, K =
+    8192 and 12288 (rounds beyond the load ring)."""
     run_case(M, N, K, 3000 + M + K)
     if M in (17, 48):
         run_case(M, N, K, 4000 + M + K, grouped=False)
@@ -141,17 +169,20 @@ def chain_expected(case, rows=None):
     return packed, scale, oracle.w4a4_gemm(packed, case.w_packed.numpy(), scale, bf16_bits(case.w_scale))
 
 
+@pytest.mark.parametrize("tiled", [False, True])
 @pytest.mark.parametrize("proj", ["o", "qkv", "gate_up", "down"])
-def test_k2_chain_qwen3_shapes_m32(proj):
+def test_k2_chain_qwen3_shapes_m32(proj, tiled):
     case = W.w4a4_case(proj, 32)
     M, N, K = case.shape
-    print(f"[chain] {proj} M={M} N={N} K={K}", flush=True)
+    print(f"[chain] {proj} M={M} N={N} K={K} tiled={tiled}", flush=True)
     x, signs = case.x.to(DEV), case.signs.to(DEV)
     wpk, wsc = case.w_packed.to(DEV), case.w_scale.to(DEV)
+    if tiled:
+        wpk = tile_weights(wpk)
     packed = torch.empty((M, K // 2), dtype=torch.int8, device=DEV)
     scale = torch.empty((M, K // 128), dtype=torch.bfloat16, device=DEV)
     rht_quant_pack(x, signs, out_packed=packed, out_scale=scale)
-    out = w4a4_grouped_gemm(packed, wpk, scale, wsc)
+    out = w4a4_grouped_gemm(packed, wpk, scale, wsc, weights_tiled=tiled)
     torch.cuda.synchronize()
     p_ref, s_ref, o_ref = chain_expected(case)
     assert np.array_equal(packed.cpu().numpy(), p_ref)
@@ -159,17 +190,20 @@ def test_k2_chain_qwen3_shapes_m32(proj):
     assert_bits_equal(bf16_bits(out), o_ref, f"{proj} M=32 chain")
 
 
+@pytest.mark.parametrize("tiled", [False, True])
 @pytest.mark.parametrize("proj", ["o", "qkv", "gate_up", "down"])
-def test_k2_chain_qwen3_shapes_m4096_sampled(proj):
+def test_k2_chain_qwen3_shapes_m4096_sampled(proj, tiled):
     case = W.w4a4_case(proj, 4096)
     M, N, K = case.shape
-    print(f"[chain] {proj} M={M} N={N} K={K} (row sample)", flush=True)
+    print(f"[chain] {proj} M={M} N={N} K={K} tiled={tiled} (row sample)", flush=True)
     x, signs = case.x.to(DEV), case.signs.to(DEV)
     wpk, wsc = case.w_packed.to(DEV), case.w_scale.to(DEV)
+    if tiled:
+        wpk = tile_weights(wpk)
     packed = torch.empty((M, K // 2), dtype=torch.int8, device=DEV)
     scale = torch.empty((M, K // 128), dtype=torch.bfloat16, device=DEV)
     rht_quant_pack(x, signs, out_packed=packed, out_scale=scale)
-    out = w4a4_grouped_gemm(packed, wpk, scale, wsc)
+    out = w4a4_grouped_gemm(packed, wpk, scale, wsc, weights_tiled=tiled)
     torch.cuda.synchronize()
     rows = np.unique(np.concatenate([np.arange(0, 3), np.linspace(0, M - 1, 21).round().astype(int),
                                      np.arange(M - 3, M), [127, 128, 129]]))
@@ -191,7 +225,7 @@ def extreme_scales(rng, rows, G, frac=0.05):
 
 
 @pytest.mark.parametrize("M,N,K,rows_special", [(200, 264, 1024, True), (257, 392, 2048, False),
-                                                 (150, 136, 12288, True)])
+                                                 (150, 136, 12288, True), (130, 400, 1024, False)])
 def test_k2_prefill_extreme_scales(M, N, K, rows_special):
     """Prefill tiles whose scales leave the range where the kernel folds the
     x256 of the widened nibbles into the activation scale must take the
@@ -220,6 +254,10 @@ def test_k2_prefill_extreme_scales(M, N, K, rows_special):
             out = w4a4_grouped_gemm(a, w, s_a, s_w)
             torch.cuda.synchronize()
             assert_bits_equal(bf16_bits(out), exp, "bf16 output")
+            if N % 16 == 0:
+                out = w4a4_grouped_gemm(a, tile_weights(w), s_a, s_w, weights_tiled=True)
+                torch.cuda.synchronize()
+                assert_bits_equal(bf16_bits(out), exp, "bf16 output, tiled weights")
 
 
 @pytest.mark.parametrize("M,N,K", [(1000, 1032, 512), (300, 520, 1024), (4096, 264, 2048)])
