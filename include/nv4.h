@@ -37,6 +37,12 @@
  *                          nanovllm/layers/attention.py:10-40 (caller of the hot path)
  *   nv4_silu_mul        <- SiluAndMul.forward, nanovllm/layers/activation.py:8-11
  *                          (caller of the hot path)
+ *   nv4_rmsnorm_rht_quant_pack, nv4_silu_mul_rht_quant_pack <- the producer of
+ *                          W4A4Linear's input fused into rht_quant_pack:
+ *                          add+RMSNorm (layernorm.py:28-40) before the qkv and
+ *                          gate_up projections, SiluAndMul (activation.py:8-11)
+ *                          before down (nanovllm/models/qwen3.py:96-135 with
+ *                          nanovllm/layers/linear_w4a4.py:30-34)
  */
 #ifndef NV4_H
 #define NV4_H
@@ -183,7 +189,8 @@ int nv4_paged_decode_attention(const void* q, int64_t q_row_stride, const void* 
  *                         y = bf16(bf16(h * rsqrt(mean(h^2) + eps)) * weight)
  * x, residual_in, residual_out, y: [rows, H] contiguous, 16-byte aligned; weight [H].
  * residual_in and residual_out are both NULL or both set (they may alias;
- * x and y may alias).  8 <= H <= 8192, H % 8 == 0.
+ * x and y may alias).  16 <= H <= 8192, H % 16 == 0.  The sum of squares is
+ * taken in one fixed order, shared with nv4_rmsnorm_rht_quant_pack.
  */
 int nv4_rmsnorm(const void* x, const void* residual_in, void* residual_out, const void* weight, void* y,
                 int64_t rows, int64_t H, float eps, void* stream);
@@ -215,6 +222,26 @@ int nv4_qk_norm_rope_store(const void* qkv, int64_t qkv_row_stride, int64_t T, i
  * y = bf16(bf16(g / (1 + exp(-g))) * u).  I % 8 == 0; 16-byte aligned.
  */
 int nv4_silu_mul(const void* gate_up, void* y, int64_t rows, int64_t I, void* stream);
+
+/*
+ * Fused prologue + K1: the RMSNorm (or SiLU-mul) output is computed, rounded
+ * to bf16 exactly as nv4_rmsnorm (nv4_silu_mul) stores it, and quantized as
+ * nv4_rht_quant_pack (reference layout) would quantize that stored tensor,
+ * without writing it: packed codes and scales are bit-identical to the
+ * two-step sequence.
+ * nv4_rmsnorm_rht_quant_pack: x bf16 [M,4096]; residual_in/residual_out as
+ *   nv4_rmsnorm (both NULL, or both set; they may alias); norm_weight bf16
+ *   [4096]; K == 4096.
+ * nv4_silu_mul_rht_quant_pack: gate_up bf16 [M,2K] (gate in columns 0..K-1,
+ *   up in K..2K-1); K in {4096, 12288}.
+ * signs int8 [K]; packed int8 [M,K/2]; scale bf16 [M,K/128]; alignments as
+ * nv4_rht_quant_pack (activations 16 bytes).
+ */
+int nv4_rmsnorm_rht_quant_pack(const void* x, const void* residual_in, void* residual_out, const void* norm_weight,
+                               float eps, const int8_t* signs, int8_t* packed, void* scale, int64_t M, int64_t K,
+                               void* stream);
+int nv4_silu_mul_rht_quant_pack(const void* gate_up, const int8_t* signs, int8_t* packed, void* scale, int64_t M,
+                                int64_t K, void* stream);
 
 /* Library version string. */
 const char* nv4_version(void);

@@ -5,7 +5,8 @@
 //  * nv4_rmsnorm (nanovllm/layers/layernorm.py:16-40): x = float(x) [+
 //    float(residual), residual_out = bf16(x)]; y = bf16(bf16(x * rsqrt(mean(x^2)
 //    + eps)) * weight).  One workgroup per row; the sum of squares is taken in
-//    fp32 (in a different order than torch's reduction).
+//    fp32 in the fixed order of norm_ops.h (not torch's), which the fused K1
+//    prologue shares.
 //  * nv4_qk_norm_rope_store (nanovllm/models/qwen3.py:78-94 with
 //    layers/rotary_embedding.py:6-48 and the KV store of
 //    layers/attention.py:10-40): for every token of the fused qkv row, the
@@ -14,86 +15,54 @@
 //    and the sum rounded separately) on the bf16 normalised values; queries go
 //    to q_out, keys and values to their cache slot (and, when given, to
 //    k_out / v_out).  Slots outside [0, num_slots) -- the reference's -1 --
-//    are not stored; positions outside the cos/sin table read its row 0.  One wave per (token, head): lane l owns dims l and l+64,
-//    the two halves the rotation pairs.
+//    are not stored; positions outside the cos/sin table read its row 0.  One
+//    wave per (token, head): lane l owns dims l and l+64, the two halves the
+//    rotation pairs.
 //  * nv4_silu_mul (nanovllm/layers/activation.py:8-11): bf16(bf16(silu(g)) * u)
 //    with silu(g) = g / (1 + exp(-g)) in fp32.
-#include "nv4_common.h"
+#include "norm_ops.h"
 
 namespace nv4 {
 namespace {
 
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off);
-    return v;
-}
-
-__device__ __forceinline__ float round_bf16(float f) { return bf16_to_f32(f32_to_bf16_rne(f)); }
-
-// rows x H (H % 8 == 0, H <= 8 * 256 * 4); 256 threads per row.
+// rows x H (H % 16 == 0, H <= 8192); 256 threads per row, thread t owning
+// the 16-value units t and t + 256 (the fixed reduction order of
+// norm_ops.h, shared with the fused K1 prologue).
 template <bool RESID>
 __global__ void __launch_bounds__(256)
 rmsnorm_rows(const uint16_t* x, const uint16_t* resid_in, uint16_t* resid_out,
              const uint16_t* __restrict__ w, uint16_t* y, int H, float eps) {
-    constexpr int MAXV = 4;  // 8-element vectors per thread (H <= 8192)
+    constexpr int MAXU = 2;
+    __shared__ float red[4];
     const int64_t row = blockIdx.x;
     const int t = threadIdx.x;
-    const int nv = H / 8;
-    float v[MAXV][8];
+    const int nu = H / 16;
+    float h[MAXU][16];
     float ss = 0.0f;
 #pragma unroll
-    for (int i = 0; i < MAXV; ++i) {
-        const int c = t + i * 256;
-        if (c < nv) {
-            const v4u xv = *reinterpret_cast<const v4u*>(x + row * H + c * 8);
-            v4u rv = {0u, 0u, 0u, 0u};
-            if constexpr (RESID) rv = *reinterpret_cast<const v4u*>(resid_in + row * H + c * 8);
-            v4u ro;
-#pragma unroll
-            for (int k = 0; k < 8; ++k) {
-                const uint32_t xh = (xv[k >> 1] >> (16 * (k & 1))) & 0xffffu;
-                float f = bf16_to_f32(xh);
-                if constexpr (RESID) {
-                    const uint32_t rh = (rv[k >> 1] >> (16 * (k & 1))) & 0xffffu;
-                    f = f + bf16_to_f32(rh);
-                }
-                v[i][k] = f;
-                ss = __builtin_fmaf(f, f, ss);
-            }
-            if constexpr (RESID) {
-#pragma unroll
-                for (int k = 0; k < 4; ++k)
-                    ro[k] = f32_to_bf16_rne(v[i][2 * k]) | (f32_to_bf16_rne(v[i][2 * k + 1]) << 16);
-                *reinterpret_cast<v4u*>(resid_out + row * H + c * 8) = ro;
-            }
+    for (int j = 0; j < MAXU; ++j) {
+        const int u = t + j * 256;
+        if (u < nu) {
+            const int64_t off = row * H + u * 16;
+            rms_load16<RESID>(x + off, RESID ? resid_in + off : nullptr, RESID ? resid_out + off : nullptr, h[j],
+                              ss);
         }
     }
-    __shared__ float part[4];
-    ss = wave_sum(ss);
-    if ((t & 63) == 0) part[t >> 6] = ss;
-    __syncthreads();
-    const float var = (part[0] + part[1] + part[2] + part[3]) / (float)H;
-    const float r = rsqrtf(var + eps);
+    const float r = rms_rsqrt256(ss, red, H, eps);
 #pragma unroll
-    for (int i = 0; i < MAXV; ++i) {
-        const int c = t + i * 256;
-        if (c < nv) {
-            const v4u wv = *reinterpret_cast<const v4u*>(w + c * 8);
-            v4u out;
+    for (int j = 0; j < MAXU; ++j) {
+        const int u = t + j * 256;
+        if (u < nu) {
+            float v[16];
+            rms_apply16(h[j], r, w + u * 16, v);
+            v4u o0, o1;
 #pragma unroll
             for (int k = 0; k < 4; ++k) {
-                uint32_t pair = 0;
-#pragma unroll
-                for (int e = 0; e < 2; ++e) {
-                    const int kk = 2 * k + e;
-                    const float wf = bf16_to_f32((wv[k] >> (16 * e)) & 0xffffu);
-                    const float nrm = round_bf16(v[i][kk] * r);
-                    pair |= f32_to_bf16_rne(nrm * wf) << (16 * e);
-                }
-                out[k] = pair;
+                o0[k] = f32_to_bf16_rne(v[2 * k]) | (f32_to_bf16_rne(v[2 * k + 1]) << 16);
+                o1[k] = f32_to_bf16_rne(v[8 + 2 * k]) | (f32_to_bf16_rne(v[8 + 2 * k + 1]) << 16);
             }
-            *reinterpret_cast<v4u*>(y + row * H + c * 8) = out;
+            *reinterpret_cast<v4u*>(y + row * H + u * 16) = o0;
+            *reinterpret_cast<v4u*>(y + row * H + u * 16 + 8) = o1;
         }
     }
 }
@@ -176,8 +145,7 @@ silu_mul(const uint16_t* __restrict__ gu, uint16_t* __restrict__ y, int64_t rows
         for (int e = 0; e < 2; ++e) {
             const float gf = bf16_to_f32((g[k] >> (16 * e)) & 0xffffu);
             const float uf = bf16_to_f32((u[k] >> (16 * e)) & 0xffffu);
-            const float sg = round_bf16(gf / (1.0f + expf(-gf)));
-            pair |= f32_to_bf16_rne(sg * uf) << (16 * e);
+            pair |= f32_to_bf16_rne(silu_mul1(gf, uf)) << (16 * e);
         }
         out[k] = pair;
     }
@@ -191,7 +159,7 @@ extern "C" int nv4_rmsnorm(const void* x, const void* residual_in, void* residua
                            int64_t rows, int64_t H, float eps, void* stream) {
     using namespace nv4;
     if (!x || !weight || !y || (residual_in && !residual_out) || (!residual_in && residual_out)) return NV4_E_NULL;
-    if (rows < 1 || rows > 0x7fffffffLL || H < 8 || H % 8 || H > 8192) return NV4_E_SHAPE;
+    if (rows < 1 || rows > 0x7fffffffLL || H < 16 || H % 16 || H > 8192) return NV4_E_SHAPE;
     if (reinterpret_cast<uintptr_t>(x) % 16 || reinterpret_cast<uintptr_t>(weight) % 16 ||
         reinterpret_cast<uintptr_t>(y) % 16 || reinterpret_cast<uintptr_t>(residual_in) % 16 ||
         reinterpret_cast<uintptr_t>(residual_out) % 16)

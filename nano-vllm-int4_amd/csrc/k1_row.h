@@ -63,18 +63,24 @@ __device__ __forceinline__ void wave_lds_sync() {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-// 16 contiguous bf16 values times their int8 signs.
-__device__ __forceinline__ void load_signed16(const uint16_t* __restrict__ xp, const int8_t* __restrict__ sp,
-                                              float (&a)[16]) {
+// 16 contiguous bf16 values as fp32.
+__device__ __forceinline__ void load_bf16x16(const uint16_t* __restrict__ xp, float (&a)[16]) {
     const v4u x0 = *reinterpret_cast<const v4u*>(xp);
     const v4u x1 = *reinterpret_cast<const v4u*>(xp + 8);
-    const v4u sv = *reinterpret_cast<const v4u*>(sp);
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
         const uint32_t xw = i < 8 ? x0[(i & 7) >> 1] : x1[(i & 7) >> 1];
-        const uint32_t h = (xw >> (16 * (i & 1))) & 0xffffu;
+        a[i] = bf16_to_f32((xw >> (16 * (i & 1))) & 0xffffu);
+    }
+}
+
+// a[i] *= sign[i] for 16 contiguous int8 signs (exact).
+__device__ __forceinline__ void apply_signs16(const int8_t* __restrict__ sp, float (&a)[16]) {
+    const v4u sv = *reinterpret_cast<const v4u*>(sp);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
         const int sg = (int)(int8_t)((sv[i >> 2] >> (8 * (i & 3))) & 0xffu);
-        a[i] = bf16_to_f32(h) * (float)sg;
+        a[i] = a[i] * (float)sg;
     }
 }
 
@@ -188,13 +194,21 @@ __device__ __forceinline__ void chunk1024_bits0_9(float (&a)[16], float* __restr
 constexpr int K12_THREADS = 1024;
 constexpr int K12_LDS = 12 * 1024;
 
-__device__ __forceinline__ void k1_row12288(const uint16_t* __restrict__ xr, const int8_t* __restrict__ signs,
+//
+// The row's values come from a prologue: prologue(col0, v) fills v[0..15]
+// with the fp32 values of columns col0..col0+15 (bf16 x, or the output of a
+// fused RMSNorm / SiLU-mul rounded to bf16); they are multiplied by the
+// signs here.  Threads 0-767 (waves 0-11) call it once each, with
+// col0 = 16 t.
+template <class Prologue>
+__device__ __forceinline__ void k1_row12288(Prologue&& prologue, const int8_t* __restrict__ signs,
                                             int8_t* __restrict__ prow, uint16_t* __restrict__ srow,
                                             float* __restrict__ buf) {
     const int t = threadIdx.x, w = t >> 6, l = t & 63;
     if (w < 12) {
         float a[16];
-        load_signed16(xr + w * 1024 + 16 * l, signs + w * 1024 + 16 * l, a);
+        prologue(w * 1024 + 16 * l, a);
+        apply_signs16(signs + w * 1024 + 16 * l, a);
         float* blk = buf + w * 1024;
         chunk1024_bits0_9(a, blk, l);
 #pragma unroll
@@ -226,15 +240,18 @@ __device__ __forceinline__ void k1_row12288(const uint16_t* __restrict__ xr, con
 
 // K = 4096 (one 4096-point chunk) by 256 threads: each wave runs bits 0-9 of
 // its 1024-column quarter, one workgroup transpose brings bits 8-11 into
-// registers (thread t: columns t | r << 8).
+// registers (thread t: columns t | r << 8).  Every thread calls the
+// prologue once, with col0 = 16 t.
 constexpr int K4_LDS = 4 * 1024;
 
-__device__ __forceinline__ void k1_row4096(const uint16_t* __restrict__ xr, const int8_t* __restrict__ signs,
+template <class Prologue>
+__device__ __forceinline__ void k1_row4096(Prologue&& prologue, const int8_t* __restrict__ signs,
                                            int8_t* __restrict__ prow, uint16_t* __restrict__ srow,
                                            float* __restrict__ buf) {
     const int t = threadIdx.x, w = t >> 6, l = t & 63;
     float a[16];
-    load_signed16(xr + w * 1024 + 16 * l, signs + w * 1024 + 16 * l, a);
+    prologue(w * 1024 + 16 * l, a);
+    apply_signs16(signs + w * 1024 + 16 * l, a);
     float* blk = buf + w * 1024;
     reg_butterflies(a);
 #pragma unroll

@@ -1,0 +1,109 @@
+// Elementwise / normalisation pieces shared by the standalone decoder kernels
+// (decoder_ops.hip) and the fused prologues of K1 (rht_quant_pack.hip), so
+// that "op, then K1" and "op fused into K1" produce the same bits.
+//
+// RMSNorm (nanovllm/layers/layernorm.py:16-50) in one fixed order: thread t
+// of a 256-thread workgroup owns the 16-value units u = t, t + 256, ... of
+// the row and accumulates fmaf(h, h, ss) over its values in column order;
+// the wave sums by xor-shuffles 32, 16, .., 1; the workgroup adds the four
+// wave partials left to right.  r = rsqrtf(ss / H + eps) and
+// y = bf16(bf16(h * r) * w).
+// SiLU-and-mul (nanovllm/layers/activation.py:8-11): y = bf16(bf16(g /
+// (1 + expf(-g))) * u), fp32 arithmetic.
+#pragma once
+
+#include "nv4_common.h"
+
+namespace nv4 {
+namespace {
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off);
+    return v;
+}
+
+__device__ __forceinline__ float round_bf16(float f) { return bf16_to_f32(f32_to_bf16_rne(f)); }
+
+// h = float(x) (+ float(res)) for 16 contiguous values; with a residual the
+// rounded sum goes to res_out.  Accumulates the sum of squares into ss.
+template <bool RESID>
+__device__ __forceinline__ void rms_load16(const uint16_t* __restrict__ x, const uint16_t* res, uint16_t* res_out,
+                                           float (&h)[16], float& ss) {
+    const v4u x0 = *reinterpret_cast<const v4u*>(x);
+    const v4u x1 = *reinterpret_cast<const v4u*>(x + 8);
+    v4u r0 = {0u, 0u, 0u, 0u}, r1 = r0;
+    if constexpr (RESID) {
+        r0 = *reinterpret_cast<const v4u*>(res);
+        r1 = *reinterpret_cast<const v4u*>(res + 8);
+    }
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        const uint32_t xw = i < 8 ? x0[(i & 7) >> 1] : x1[(i & 7) >> 1];
+        float f = bf16_to_f32((xw >> (16 * (i & 1))) & 0xffffu);
+        if constexpr (RESID) {
+            const uint32_t rw = i < 8 ? r0[(i & 7) >> 1] : r1[(i & 7) >> 1];
+            f = f + bf16_to_f32((rw >> (16 * (i & 1))) & 0xffffu);
+        }
+        h[i] = f;
+        ss = __builtin_fmaf(f, f, ss);
+    }
+    if constexpr (RESID) {
+        v4u o0, o1;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            o0[k] = f32_to_bf16_rne(h[2 * k]) | (f32_to_bf16_rne(h[2 * k + 1]) << 16);
+            o1[k] = f32_to_bf16_rne(h[8 + 2 * k]) | (f32_to_bf16_rne(h[8 + 2 * k + 1]) << 16);
+        }
+        *reinterpret_cast<v4u*>(res_out) = o0;
+        *reinterpret_cast<v4u*>(res_out + 8) = o1;
+    }
+}
+
+// Workgroup (256 threads) reduction of the per-thread sums of squares and
+// the reciprocal RMS.  red: 4 floats of LDS; ends with a barrier after which
+// red may be reused.
+__device__ __forceinline__ float rms_rsqrt256(float ss, float* red, int H, float eps) {
+    ss = wave_sum(ss);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
+    __syncthreads();
+    const float tot = ((red[0] + red[1]) + red[2]) + red[3];
+    return rsqrtf(tot / (float)H + eps);
+}
+
+// y = bf16(bf16(h * r) * w) for 16 contiguous values, as fp32.
+__device__ __forceinline__ void rms_apply16(const float (&h)[16], float r, const uint16_t* __restrict__ w,
+                                            float (&y)[16]) {
+    const v4u w0 = *reinterpret_cast<const v4u*>(w);
+    const v4u w1 = *reinterpret_cast<const v4u*>(w + 8);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        const uint32_t ww = i < 8 ? w0[(i & 7) >> 1] : w1[(i & 7) >> 1];
+        const float wf = bf16_to_f32((ww >> (16 * (i & 1))) & 0xffffu);
+        y[i] = round_bf16(round_bf16(h[i] * r) * wf);
+    }
+}
+
+__device__ __forceinline__ float silu_mul1(float g, float u) { return round_bf16(round_bf16(g / (1.0f + expf(-g))) * u); }
+
+// y = silu(g) * u (bf16 rounding points above) for 16 contiguous values.
+__device__ __forceinline__ void silu_mul16(const uint16_t* __restrict__ g, const uint16_t* __restrict__ u,
+                                           float (&y)[16]) {
+    float gf[16], uf[16];
+    const v4u g0 = *reinterpret_cast<const v4u*>(g);
+    const v4u g1 = *reinterpret_cast<const v4u*>(g + 8);
+    const v4u u0 = *reinterpret_cast<const v4u*>(u);
+    const v4u u1 = *reinterpret_cast<const v4u*>(u + 8);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        const uint32_t gw = i < 8 ? g0[(i & 7) >> 1] : g1[(i & 7) >> 1];
+        const uint32_t uw = i < 8 ? u0[(i & 7) >> 1] : u1[(i & 7) >> 1];
+        gf[i] = bf16_to_f32((gw >> (16 * (i & 1))) & 0xffffu);
+        uf[i] = bf16_to_f32((uw >> (16 * (i & 1))) & 0xffffu);
+    }
+#pragma unroll
+    for (int i = 0; i < 16; ++i) y[i] = silu_mul1(gf[i], uf[i]);
+}
+
+}  // namespace
+}  // namespace nv4

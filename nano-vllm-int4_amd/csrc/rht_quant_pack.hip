@@ -1,7 +1,12 @@
 // K1: fused randomized Hadamard transform + group-128 INT4 quantization +
 // nibble packing, for gfx950.  The reference-layout row transforms live in
-// k1_row.h; this file holds the kernels and the C ABI entry point.
+// k1_row.h; this file holds the kernels and the C ABI entry points,
+// including K1 with the producer of its input fused in front (add+RMSNorm
+// for the qkv and gate_up inputs, SiLU-mul for the down input): the row is
+// computed, rounded to bf16 as the separate op would store it, and fed to the
+// transform without the round trip through memory.
 #include "k1_row.h"
+#include "norm_ops.h"
 
 namespace nv4 {
 namespace {
@@ -12,7 +17,9 @@ k1_k12288(const uint16_t* __restrict__ x, const int8_t* __restrict__ signs,
           int8_t* __restrict__ packed, uint16_t* __restrict__ scale) {
     __shared__ float buf[K12_LDS];
     const int64_t row = blockIdx.x;
-    k1_row12288(x + row * 12288, signs, packed + row * 6144, scale + row * 96, buf);
+    const uint16_t* xr = x + row * 12288;
+    k1_row12288([&](int c0, float (&v)[16]) { load_bf16x16(xr + c0, v); }, signs, packed + row * 6144,
+                scale + row * 96, buf);
 }
 
 // K = 4096: one workgroup of 256 threads per row.
@@ -21,7 +28,51 @@ k1_k4096(const uint16_t* __restrict__ x, const int8_t* __restrict__ signs,
          int8_t* __restrict__ packed, uint16_t* __restrict__ scale) {
     __shared__ float buf[K4_LDS];
     const int64_t row = blockIdx.x;
-    k1_row4096(x + row * 4096, signs, packed + row * 2048, scale + row * 32, buf);
+    const uint16_t* xr = x + row * 4096;
+    k1_row4096([&](int c0, float (&v)[16]) { load_bf16x16(xr + c0, v); }, signs, packed + row * 2048,
+               scale + row * 32, buf);
+}
+
+// K = 4096 behind add+RMSNorm (same bits as nv4_rmsnorm followed by K1):
+// thread t's prologue unit is columns 16t..16t+15, the unit nv4_rmsnorm's
+// thread t owns for a 4096-wide row.
+template <bool RESID>
+__global__ void __launch_bounds__(256)
+k1_k4096_rmsnorm(const uint16_t* x, const uint16_t* res_in, uint16_t* res_out, const uint16_t* __restrict__ nw,
+                 float eps, const int8_t* __restrict__ signs, int8_t* __restrict__ packed,
+                 uint16_t* __restrict__ scale) {
+    __shared__ float buf[K4_LDS];
+    __shared__ float red[4];
+    const int64_t off = (int64_t)blockIdx.x * 4096;
+    k1_row4096(
+        [&](int c0, float (&v)[16]) {
+            float h[16], ss = 0.0f;
+            rms_load16<RESID>(x + off + c0, RESID ? res_in + off + c0 : nullptr,
+                              RESID ? res_out + off + c0 : nullptr, h, ss);
+            const float r = rms_rsqrt256(ss, red, 4096, eps);
+            rms_apply16(h, r, nw + c0, v);
+        },
+        signs, packed + (int64_t)blockIdx.x * 2048, scale + (int64_t)blockIdx.x * 32, buf);
+}
+
+// K1 behind SiLU-and-mul of a [M, 2K] gate/up row (same bits as nv4_silu_mul
+// followed by K1).
+__global__ void __launch_bounds__(256)
+k1_k4096_silu(const uint16_t* __restrict__ gu, const int8_t* __restrict__ signs, int8_t* __restrict__ packed,
+              uint16_t* __restrict__ scale) {
+    __shared__ float buf[K4_LDS];
+    const uint16_t* g = gu + (int64_t)blockIdx.x * 8192;
+    k1_row4096([&](int c0, float (&v)[16]) { silu_mul16(g + c0, g + 4096 + c0, v); }, signs,
+               packed + (int64_t)blockIdx.x * 2048, scale + (int64_t)blockIdx.x * 32, buf);
+}
+
+__global__ void __launch_bounds__(K12_THREADS)
+k1_k12288_silu(const uint16_t* __restrict__ gu, const int8_t* __restrict__ signs, int8_t* __restrict__ packed,
+               uint16_t* __restrict__ scale) {
+    __shared__ float buf[K12_LDS];
+    const uint16_t* g = gu + (int64_t)blockIdx.x * 24576;
+    k1_row12288([&](int c0, float (&v)[16]) { silu_mul16(g + c0, g + 12288 + c0, v); }, signs,
+                packed + (int64_t)blockIdx.x * 6144, scale + (int64_t)blockIdx.x * 96, buf);
 }
 
 // block128 layout: every aligned 128-block gets its own 128-point Sylvester
@@ -110,4 +161,47 @@ extern "C" int nv4_rht_quant_pack(const void* x, const int8_t* signs, int8_t* pa
         return (int)hipGetLastError();
     }
     return NV4_E_LAYOUT;
+}
+
+extern "C" int nv4_rmsnorm_rht_quant_pack(const void* x, const void* residual_in, void* residual_out,
+                                          const void* norm_weight, float eps, const int8_t* signs, int8_t* packed,
+                                          void* scale, int64_t M, int64_t K, void* stream) {
+    using namespace nv4;
+    if (!x || !norm_weight || !signs || !packed || !scale || (!residual_in) != (!residual_out)) return NV4_E_NULL;
+    if (M < 1 || M > 0x7fffffffLL || K != 4096) return NV4_E_SHAPE;
+    if (reinterpret_cast<uintptr_t>(x) % 16 || reinterpret_cast<uintptr_t>(residual_in) % 16 ||
+        reinterpret_cast<uintptr_t>(residual_out) % 16 || reinterpret_cast<uintptr_t>(norm_weight) % 16 ||
+        reinterpret_cast<uintptr_t>(packed) % 8 || reinterpret_cast<uintptr_t>(scale) % 2 ||
+        reinterpret_cast<uintptr_t>(signs) % 16)
+        return NV4_E_ALIGN;
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    const auto* xp = static_cast<const uint16_t*>(x);
+    const auto* wp = static_cast<const uint16_t*>(norm_weight);
+    auto* sp = static_cast<uint16_t*>(scale);
+    if (residual_in)
+        hipLaunchKernelGGL(k1_k4096_rmsnorm<true>, dim3((unsigned)M), dim3(256), 0, st, xp,
+                           static_cast<const uint16_t*>(residual_in), static_cast<uint16_t*>(residual_out), wp, eps,
+                           signs, packed, sp);
+    else
+        hipLaunchKernelGGL(k1_k4096_rmsnorm<false>, dim3((unsigned)M), dim3(256), 0, st, xp, nullptr, nullptr, wp,
+                           eps, signs, packed, sp);
+    return (int)hipGetLastError();
+}
+
+extern "C" int nv4_silu_mul_rht_quant_pack(const void* gate_up, const int8_t* signs, int8_t* packed, void* scale,
+                                           int64_t M, int64_t K, void* stream) {
+    using namespace nv4;
+    if (!gate_up || !signs || !packed || !scale) return NV4_E_NULL;
+    if (M < 1 || M > 0x7fffffffLL || (K != 4096 && K != 12288)) return NV4_E_SHAPE;
+    if (reinterpret_cast<uintptr_t>(gate_up) % 16 || reinterpret_cast<uintptr_t>(packed) % 8 ||
+        reinterpret_cast<uintptr_t>(scale) % 2 || reinterpret_cast<uintptr_t>(signs) % 16)
+        return NV4_E_ALIGN;
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    const auto* gp = static_cast<const uint16_t*>(gate_up);
+    auto* sp = static_cast<uint16_t*>(scale);
+    if (K == 4096)
+        hipLaunchKernelGGL(k1_k4096_silu, dim3((unsigned)M), dim3(256), 0, st, gp, signs, packed, sp);
+    else
+        hipLaunchKernelGGL(k1_k12288_silu, dim3((unsigned)M), dim3(K12_THREADS), 0, st, gp, signs, packed, sp);
+    return (int)hipGetLastError();
 }

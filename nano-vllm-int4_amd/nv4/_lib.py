@@ -43,6 +43,8 @@ SIGNATURES = {
     "nv4_qk_norm_rope_store": ([_P, _I64, _I64, _I64, _I64, _P, _P, _P, _I64, _P, _P, _I64, _P, _P, _P, _P, _P,
                                 ctypes.c_float, _P], _I),
     "nv4_silu_mul": ([_P, _P, _I64, _I64, _P], _I),
+    "nv4_rmsnorm_rht_quant_pack": ([_P, _P, _P, _P, ctypes.c_float, _P, _P, _P, _I64, _I64, _P], _I),
+    "nv4_silu_mul_rht_quant_pack": ([_P, _P, _P, _P, _I64, _I64, _P], _I),
     "nv4_version": ([], ctypes.c_char_p),
     "nv4_strerror": ([_I], ctypes.c_char_p),
 }

@@ -8,7 +8,12 @@ rounding points of the reference's PyTorch formulation:
 * ``qk_norm_rope_store`` -- the per-head q/k RMSNorm, rotary embedding and KV
   store of Qwen3Attention.forward (nanovllm/models/qwen3.py:78-94,
   nanovllm/layers/rotary_embedding.py:6-48, nanovllm/layers/attention.py:10-40);
-* ``silu_mul`` -- SiluAndMul (nanovllm/layers/activation.py:8-11).
+* ``silu_mul`` -- SiluAndMul (nanovllm/layers/activation.py:8-11);
+* ``rmsnorm_rht_quant_pack`` / ``silu_mul_rht_quant_pack`` -- the same two
+  producers fused in front of ``rht_quant_pack`` (the quantization of a
+  W4A4Linear's input): codes and scales bit-identical to running the
+  producer, then ``rht_quant_pack`` on its bf16 output, without writing
+  that output.
 """
 from __future__ import annotations
 
@@ -114,3 +119,62 @@ def silu_mul(gate_up, out=None):
         rc = lib.nv4_silu_mul(_ptr(gate_up), _ptr(out), rows, I2 // 2, ctypes.c_void_p(stream))
     _lib.check(rc, "silu_mul")
     return out
+
+
+def _k1_outputs(M, K, dev, out_packed, out_scale):
+    if out_packed is None:
+        out_packed = torch.empty((M, K // 2), dtype=torch.int8, device=dev)
+    if out_scale is None:
+        out_scale = torch.empty((M, K // 128), dtype=torch.bfloat16, device=dev)
+    if (tuple(out_packed.shape) != (M, K // 2) or out_packed.dtype != torch.int8 or not out_packed.is_contiguous()
+            or tuple(out_scale.shape) != (M, K // 128) or out_scale.dtype != torch.bfloat16
+            or not out_scale.is_contiguous()):
+        raise ValueError("Outputs must be contiguous INT8 [M,K/2] and BF16 [M,K/128]")
+    return out_packed, out_scale
+
+
+def rmsnorm_rht_quant_pack(x, weight, eps, signs, residual=None, out_packed=None, out_scale=None):
+    """x bf16 [M, 4096] -> (packed, scale) of rht_quant_pack(rmsnorm(x)); with
+    ``residual`` the norm input is x + residual, whose bf16 rounding is written
+    into ``residual`` and returned as a third element."""
+    if x.ndim != 2 or x.shape[1] != 4096 or x.dtype != torch.bfloat16 or not x.is_contiguous():
+        raise ValueError("Expected contiguous BF16 x[M,4096]")
+    if weight.dtype != torch.bfloat16 or tuple(weight.shape) != (4096,) or signs.dtype != torch.int8 \
+            or tuple(signs.shape) != (4096,):
+        raise TypeError("Expected a BF16 norm weight [4096] and int8 signs [4096]")
+    if residual is not None and (residual.shape != x.shape or residual.dtype != x.dtype
+                                 or not residual.is_contiguous()):
+        raise ValueError("residual must match x")
+    M, K = x.shape
+    dev = x.device
+    out_packed, out_scale = _k1_outputs(M, K, dev, out_packed, out_scale)
+    _check_dev((x, weight, signs, residual, out_packed, out_scale), dev)
+    lib = _lib.load()
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    with torch.cuda.device(dev):
+        rc = lib.nv4_rmsnorm_rht_quant_pack(_ptr(x), _ptr(residual), _ptr(residual), _ptr(weight),
+                                            ctypes.c_float(eps), _ptr(signs), _ptr(out_packed), _ptr(out_scale),
+                                            M, K, ctypes.c_void_p(stream))
+    _lib.check(rc, "rmsnorm_rht_quant_pack")
+    return (out_packed, out_scale) if residual is None else (out_packed, out_scale, residual)
+
+
+def silu_mul_rht_quant_pack(gate_up, signs, out_packed=None, out_scale=None):
+    """gate_up bf16 [M, 2K] (K = 4096 or 12288) -> (packed, scale) of
+    rht_quant_pack(silu_mul(gate_up))."""
+    if gate_up.ndim != 2 or gate_up.dtype != torch.bfloat16 or not gate_up.is_contiguous() \
+            or gate_up.shape[1] not in (8192, 24576):
+        raise ValueError("Expected contiguous BF16 gate_up[M,2K], K = 4096 or 12288")
+    M, K = gate_up.shape[0], gate_up.shape[1] // 2
+    if signs.dtype != torch.int8 or tuple(signs.shape) != (K,):
+        raise TypeError("Expected int8 signs [K]")
+    dev = gate_up.device
+    out_packed, out_scale = _k1_outputs(M, K, dev, out_packed, out_scale)
+    _check_dev((gate_up, signs, out_packed, out_scale), dev)
+    lib = _lib.load()
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    with torch.cuda.device(dev):
+        rc = lib.nv4_silu_mul_rht_quant_pack(_ptr(gate_up), _ptr(signs), _ptr(out_packed), _ptr(out_scale), M, K,
+                                             ctypes.c_void_p(stream))
+    _lib.check(rc, "silu_mul_rht_quant_pack")
+    return out_packed, out_scale

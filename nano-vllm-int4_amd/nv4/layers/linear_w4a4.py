@@ -19,7 +19,7 @@ import torch
 from torch import nn
 import torch.distributed as dist
 
-from ..kernels.w4a4_grouped import tile_weights, untile_weights
+from ..kernels.w4a4_grouped import tile_weights, untile_weights, w4a4_grouped_gemm
 from ..kernels.w4a4_linear import w4a4_linear
 
 
@@ -64,3 +64,11 @@ class W4A4Linear(nn.Module):
         # captured in a HIP graph.
         out = w4a4_linear(flat, self.signs, self.packed_weight, self.weight_scale, weights_tiled=self.weights_tiled)
         return out.reshape(*x.shape[:-1], self.out_features)
+
+    def forward_quantized(self, packed: torch.Tensor, scale: torch.Tensor) -> torch.Tensor:
+        """The GEMM half of ``forward`` on activations already quantized by
+        ``rht_quant_pack`` (or a fused producer + K1: ``nv4.kernels.decoder_ops``)
+        with this module's signs: packed int8 [M, in/2], scale bf16 [M, in/128]
+        -> bf16 [M, out]."""
+        return w4a4_grouped_gemm(packed, self.packed_weight, scale, self.weight_scale,
+                                 weights_tiled=self.weights_tiled)

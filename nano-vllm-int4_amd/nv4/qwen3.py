@@ -17,6 +17,10 @@ loader address the same names:
   (nanovllm/layers/activation.py:8-11): one HIP launch each
   (``nv4.kernels.decoder_ops``), with the rounding points of the
   reference's PyTorch formulation.
+* W4A4 layers fuse the input and post-attention add+RMSNorm into the qkv
+  and gate_up activation quantization, and SiLU-mul into down's
+  (``rmsnorm_rht_quant_pack``, ``silu_mul_rht_quant_pack``): same bits,
+  one launch and one activation round trip less per fused pair.
 * Embedding and LM head, the head reading only each sequence's last
   position in prefill (nanovllm/layers/embed_head.py:56-66).
 * Attention through ``nv4.attention.Attention`` (paged KV cache).
@@ -34,7 +38,8 @@ import torch.nn.functional as F
 from torch import nn
 
 from .attention import Attention
-from .kernels.decoder_ops import qk_norm_rope_store, rmsnorm, silu_mul
+from .kernels.decoder_ops import (qk_norm_rope_store, rmsnorm, rmsnorm_rht_quant_pack, silu_mul,
+                                  silu_mul_rht_quant_pack)
 from .layers.linear_w4a4 import W4A4Linear
 from .utils.context import get_context
 
@@ -125,8 +130,9 @@ class Qwen3Attention(nn.Module):
         self.q_norm = RMSNorm(self.head_dim, eps=rms_norm_eps)
         self.k_norm = RMSNorm(self.head_dim, eps=rms_norm_eps)
 
-    def forward(self, positions, hidden_states):
-        qkv = self.qkv_proj(hidden_states)
+    def forward(self, positions, hidden_states=None, qkv=None):
+        if qkv is None:
+            qkv = self.qkv_proj(hidden_states)
         ctx = get_context()
         # q/k RMSNorm + rotary + KV-cache store in one launch; prefill also
         # needs the rotated keys and the values as tensors.
@@ -153,6 +159,14 @@ class Qwen3MLP(nn.Module):
     def forward(self, x):
         return self.down_proj(silu_mul(self.gate_up_proj(x)))
 
+    def forward_fused(self, x, residual, norm):
+        """W4A4: post-attention add+RMSNorm inside gate_up's quantization,
+        SiLU-mul inside down's; returns (output, residual)."""
+        packed, scale, residual = rmsnorm_rht_quant_pack(x, norm.weight, norm.eps, self.gate_up_proj.signs, residual)
+        gate_up = self.gate_up_proj.forward_quantized(packed, scale)
+        packed, scale = silu_mul_rht_quant_pack(gate_up, self.down_proj.signs)
+        return self.down_proj.forward_quantized(packed, scale), residual
+
 
 class Qwen3DecoderLayer(nn.Module):
     def __init__(self, config, use_w4a4=False) -> None:
@@ -164,8 +178,22 @@ class Qwen3DecoderLayer(nn.Module):
         self.mlp = Qwen3MLP(config.hidden_size, config.intermediate_size, use_w4a4)
         self.input_layernorm = RMSNorm(config.hidden_size, eps=config.rms_norm_eps)
         self.post_attention_layernorm = RMSNorm(config.hidden_size, eps=config.rms_norm_eps)
+        # W4A4 with the 4096-wide hidden state: the norms and SiLU-mul run
+        # inside the projections' activation quantization (one launch each).
+        self.fused = use_w4a4 and config.hidden_size == 4096
 
     def forward(self, positions, hidden_states, residual):
+        if self.fused:
+            attn = self.self_attn
+            norm = self.input_layernorm
+            if residual is None:
+                packed, scale = rmsnorm_rht_quant_pack(hidden_states, norm.weight, norm.eps, attn.qkv_proj.signs)
+                residual = hidden_states
+            else:
+                packed, scale, residual = rmsnorm_rht_quant_pack(hidden_states, norm.weight, norm.eps,
+                                                                 attn.qkv_proj.signs, residual)
+            hidden_states = attn(positions, qkv=attn.qkv_proj.forward_quantized(packed, scale))
+            return self.mlp.forward_fused(hidden_states, residual, self.post_attention_layernorm)
         if residual is None:
             hidden_states, residual = self.input_layernorm(hidden_states), hidden_states
         else:

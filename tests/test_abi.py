@@ -102,7 +102,7 @@ def test_decoder_ops_rejections():
     rms = lib.nv4_rmsnorm
     assert rms(None, None, None, P(A16), P(A16), 4, 4096, 1e-6, None) == _lib.NV4_E_NULL
     assert rms(P(A16), P(A16), None, P(A16), P(A16), 4, 4096, 1e-6, None) == _lib.NV4_E_NULL  # residual pair
-    assert rms(P(A16), None, None, P(A16), P(A16), 4, 4100, 1e-6, None) == _lib.NV4_E_SHAPE   # H % 8
+    assert rms(P(A16), None, None, P(A16), P(A16), 4, 4104, 1e-6, None) == _lib.NV4_E_SHAPE   # H % 16
     assert rms(P(A16), None, None, P(A16), P(A16), 4, 16384, 1e-6, None) == _lib.NV4_E_SHAPE  # H > 8192
     assert rms(P(A16), None, None, P(A16), P(A16), 0, 4096, 1e-6, None) == _lib.NV4_E_SHAPE
     assert rms(P(A16 + 2), None, None, P(A16), P(A16), 4, 4096, 1e-6, None) == _lib.NV4_E_ALIGN
@@ -118,6 +118,18 @@ def test_decoder_ops_rejections():
     assert silu(None, P(A16), 4, 12288, None) == _lib.NV4_E_NULL
     assert silu(P(A16), P(A16), 4, 12, None) == _lib.NV4_E_SHAPE
     assert silu(P(A16 + 8), P(A16), 4, 12288, None) == _lib.NV4_E_ALIGN
+    rq = lib.nv4_rmsnorm_rht_quant_pack
+    def rcall(x=P(A16), ri=None, ro=None, K=4096, M=4, sgn=P(A16)):
+        return rq(x, ri, ro, P(A16), 1e-6, sgn, P(A16), P(A16), M, K, None)
+    assert rcall(x=None) == _lib.NV4_E_NULL
+    assert rcall(ri=P(A16)) == _lib.NV4_E_NULL                   # residual pair
+    assert rcall(K=12288) == _lib.NV4_E_SHAPE
+    assert rcall(M=0) == _lib.NV4_E_SHAPE
+    assert rcall(sgn=P(A16 + 1)) == _lib.NV4_E_ALIGN
+    sq = lib.nv4_silu_mul_rht_quant_pack
+    assert sq(None, P(A16), P(A16), P(A16), 4, 12288, None) == _lib.NV4_E_NULL
+    assert sq(P(A16), P(A16), P(A16), P(A16), 4, 8192, None) == _lib.NV4_E_SHAPE
+    assert sq(P(A16 + 2), P(A16), P(A16), P(A16), 4, 12288, None) == _lib.NV4_E_ALIGN
 
 
 def test_python_wrappers_validate_like_the_reference():

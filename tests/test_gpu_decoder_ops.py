@@ -15,12 +15,19 @@ nanovllm/layers/attention.py:10-40):
   A rotated output y1 = x1 cos - x2 sin inherits a one-ulp change of the
   normalised x1 or x2 without the cancellation shrinking it, so its bound
   adds 2^-7 (|x1| + |x2|).
+
+The fused producer + K1 kernels (``rmsnorm_rht_quant_pack``,
+``silu_mul_rht_quant_pack``) must give exactly the codes and scales of the
+producer kernel followed by ``rht_quant_pack`` (whose parity with the
+oracle is tested elsewhere), and the same residual.
 """
 import pytest
 import torch
 import torch.nn.functional as F
 
-from nv4.kernels.decoder_ops import qk_norm_rope_store, rmsnorm, silu_mul
+from nv4 import rht_quant_pack
+from nv4.kernels.decoder_ops import (qk_norm_rope_store, rmsnorm, rmsnorm_rht_quant_pack, silu_mul,
+                                     silu_mul_rht_quant_pack)
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda:0"
@@ -49,7 +56,7 @@ def ref_rms(x, w, residual=None):
     return y, res
 
 
-@pytest.mark.parametrize("rows,H", [(1, 4096), (7, 4096), (64, 4096), (300, 1024), (3, 8192), (5, 136)])
+@pytest.mark.parametrize("rows,H", [(1, 4096), (7, 4096), (64, 4096), (300, 1024), (3, 8192), (5, 144)])
 @pytest.mark.parametrize("with_residual", [False, True])
 def test_rmsnorm(rows, H, with_residual):
     g = torch.Generator(device=DEV).manual_seed(rows * 31 + H)
@@ -159,3 +166,42 @@ def test_silu_mul_extremes():
     fin = torch.isfinite(ref.float())
     close_bf16(out[fin], ref[fin], "silu extremes", frac=0.05)
     assert torch.equal(out[~fin].float().nan_to_num(0.0), ref[~fin].float().nan_to_num(0.0))
+
+
+@pytest.mark.parametrize("rows", [1, 32, 300])
+@pytest.mark.parametrize("with_residual", [False, True])
+def test_rmsnorm_rht_quant_pack_equals_two_step(rows, with_residual):
+    g = torch.Generator(device=DEV).manual_seed(rows + 77)
+    x = (torch.randn(rows, 4096, generator=g, device=DEV) * 3).to(torch.bfloat16)
+    w = (1 + 0.1 * torch.randn(4096, generator=g, device=DEV)).to(torch.bfloat16)
+    signs = (torch.randint(0, 2, (4096,), generator=g, device=DEV) * 2 - 1).to(torch.int8)
+    res = torch.randn(rows, 4096, generator=g, device=DEV).to(torch.bfloat16) if with_residual else None
+    if with_residual:
+        res2 = res.clone()
+        y, res2 = rmsnorm(x, w, EPS, residual=res2)
+        packed, scale, res = rmsnorm_rht_quant_pack(x, w, EPS, signs, residual=res)
+        assert torch.equal(res, res2)
+    else:
+        y = rmsnorm(x, w, EPS)
+        packed, scale = rmsnorm_rht_quant_pack(x, w, EPS, signs)
+    p2, s2 = k1(y, signs)
+    torch.cuda.synchronize()
+    assert torch.equal(packed, p2) and torch.equal(scale.view(torch.int16), s2.view(torch.int16))
+
+
+def k1(x, signs):
+    M, K = x.shape
+    return rht_quant_pack(x, signs, out_packed=torch.empty((M, K // 2), dtype=torch.int8, device=DEV),
+                          out_scale=torch.empty((M, K // 128), dtype=torch.bfloat16, device=DEV))
+
+
+@pytest.mark.parametrize("K", [4096, 12288])
+@pytest.mark.parametrize("rows", [1, 32, 65])
+def test_silu_mul_rht_quant_pack_equals_two_step(K, rows):
+    g = torch.Generator(device=DEV).manual_seed(rows + K)
+    gu = (torch.randn(rows, 2 * K, generator=g, device=DEV) * 2).to(torch.bfloat16)
+    signs = (torch.randint(0, 2, (K,), generator=g, device=DEV) * 2 - 1).to(torch.int8)
+    packed, scale = silu_mul_rht_quant_pack(gu, signs)
+    p2, s2 = k1(silu_mul(gu), signs)
+    torch.cuda.synchronize()
+    assert torch.equal(packed, p2) and torch.equal(scale.view(torch.int16), s2.view(torch.int16))

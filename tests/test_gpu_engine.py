@@ -4,8 +4,9 @@
   rotary positions from the step's context) reproduces the last-position
   logits of a prefill over the same tokens (flash prefill attention), within
   bf16 rounding.
-* W4A4 decoder: its first qkv projection inside a prefill forward is
-  bit-exact with the oracle chain on the same normalised activations.
+* W4A4 decoder: its first qkv projection inside a prefill forward (input
+  RMSNorm fused into the activation quantization) is bit-exact with the
+  oracle chain on the normalised embeddings.
 * Both: the decode step replayed from the captured HIP graph gives logits
   bit-equal to the eager step (the reference checks the same,
   benchmarks/bench_nano_latency.py:96-107), finite, and a short run of the
@@ -64,23 +65,32 @@ def test_decode_step_matches_prefill_bf16(engines):
 
 
 def test_w4a4_first_projection_matches_oracle(engines):
-    """Capture the qkv projection's input and output inside a real prefill
-    forward of the W4A4 decoder and check the output against the oracle."""
+    """Capture the first layer's qkv projection output inside a real prefill
+    forward of the W4A4 decoder (input RMSNorm fused into the activation
+    quantization) and check it against the oracle chain on the normalised
+    embeddings (nv4 RMSNorm, whose bits the fused kernel reproduces)."""
+    from nv4.kernels.decoder_ops import rmsnorm
     _, eng = engines
     layer = eng.model.model.layers[0]
+    assert layer.fused
     seen = {}
-    h = layer.self_attn.qkv_proj.register_forward_hook(lambda m, i, o: seen.update(x=i[0].clone(), y=o.clone()))
+    h = layer.self_attn.register_forward_pre_hook(lambda m, a, kw: seen.update(qkv=kw["qkv"].clone()),
+                                                  with_kwargs=True)
+    ids = seeded_prompts(1, 70, 1024, seed=9)[0]
     try:
-        eng.prefill(2, seeded_prompts(1, 70, 1024, seed=9)[0], 1.0)
+        eng.prefill(2, ids, 1.0)
     finally:
         h.remove()
+    with torch.inference_mode():
+        emb = eng.model.model.embed_tokens(torch.tensor(ids, device=DEV))
+        y = rmsnorm(emb, layer.input_layernorm.weight, layer.input_layernorm.eps)
     torch.cuda.synchronize()
     m = layer.self_attn.qkv_proj
     assert m.weights_tiled  # the runner's projections read the MFMA-tiled layout
     sd = m.state_dict()  # reference [out, in/2] layout
-    packed, scale = oracle.rht_quant_pack(bf16_bits(seen["x"]), sd["signs"].cpu().numpy())
+    packed, scale = oracle.rht_quant_pack(bf16_bits(y), sd["signs"].cpu().numpy())
     ref = oracle.w4a4_gemm(packed, sd["packed_weight"].cpu().numpy(), scale, bf16_bits(sd["weight_scale"]))
-    assert np.array_equal(bf16_bits(seen["y"]), ref)
+    assert np.array_equal(bf16_bits(seen["qkv"]), ref)
 
 
 @pytest.mark.parametrize("which", ["bf16", "w4a4"])
