@@ -37,6 +37,9 @@
  *                          nanovllm/layers/attention.py:10-40 (caller of the hot path)
  *   nv4_silu_mul        <- SiluAndMul.forward, nanovllm/layers/activation.py:8-11
  *                          (caller of the hot path)
+ *   nv4_gumbel_sample   <- Sampler.forward, nanovllm/layers/sampler.py:5-12
+ *                          (caller of the hot path); nv4_philox4x32_10 is its
+ *                          generator on the host, for known-answer tests
  *   nv4_rmsnorm_rht_quant_pack, nv4_silu_mul_rht_quant_pack <- the producer of
  *                          W4A4Linear's input fused into rht_quant_pack:
  *                          add+RMSNorm (layernorm.py:28-40) before the qkv and
@@ -242,6 +245,23 @@ int nv4_rmsnorm_rht_quant_pack(const void* x, const void* residual_in, void* res
                                void* stream);
 int nv4_silu_mul_rht_quant_pack(const void* gate_up, const int8_t* signs, int8_t* packed, void* scale, int64_t M,
                                 int64_t K, void* stream);
+
+/*
+ * Next-token sampling at per-row temperatures (nanovllm/layers/sampler.py:5-12):
+ * out[b] = argmax_v  l[b,v] / T[b] - log(max(E, 1e-10)),  E = -log U,
+ * which has the distribution of the reference's argmax(softmax(l/T) / E).
+ * U = ((w >> 8) + 0.5) * 2^-24 for word w = v % 4 of the Philox4x32-10 block
+ * with key (seed low, seed high) and counter (v / 4, b, offset low,
+ * offset high).  Ties go to the smallest index.
+ *   logits  [B, V] rows row_stride elements apart (>= V); logits_dtype NV4_BF16
+ *           or NV4_FP32 (element-aligned)
+ *   temperatures fp32 [B] (> 0); out int64 [B]
+ */
+int nv4_gumbel_sample(const void* logits, int64_t row_stride, int logits_dtype, const float* temperatures,
+                      int64_t B, int64_t V, uint64_t seed, uint64_t offset, int64_t* out, void* stream);
+
+/* Philox4x32-10 of one counter block, computed on the host: out = philox(counter[4], key[2]). */
+void nv4_philox4x32_10(const uint32_t* counter, const uint32_t* key, uint32_t* out);
 
 /* Library version string. */
 const char* nv4_version(void);

@@ -7,8 +7,8 @@ forward), then the whole batch decodes together, one token per sequence per
 step, the decode forward replayed from a HIP graph captured for that batch
 size (nanovllm/engine/model_runner.py:211-276).  A step prepares the
 inputs on the host and copies them in (:144-203), runs the model, the LM
-head on each sequence's last hidden state and the Gumbel-max sampler at the
-request temperature (nanovllm/layers/sampler.py:7-12), and returns the
+head on each sequence's last hidden state and the sampler at the request
+temperature (nanovllm/layers/sampler.py:7-12, one HIP launch here), and returns the
 tokens to the host; the decode step time is measured around all of it,
 and decode tokens/s = batch * 1000 / mean step ms over the pure-decode
 steps (bench_nano_latency.py:118).
@@ -28,6 +28,7 @@ import torch
 from .attention import decode_workspace
 from .layers.linear_w4a4 import W4A4Linear
 from .qwen3 import BF16Linear, Qwen3ForCausalLM
+from .sampler import Sampler
 from .utils.context import get_context, reset_context, set_context
 
 
@@ -97,6 +98,7 @@ class Engine:
             max_num_seqs, self.blocks_per_seq)
         self.graphs: dict[int, torch.cuda.CUDAGraph] = {}
         self.graph_vars: dict[str, torch.Tensor] = {}
+        self.sampler = Sampler()
 
     # ------------------------------------------------------------ helpers
     def _slots(self, seq_slot: int, start: int, end: int):
@@ -106,11 +108,8 @@ class Engine:
     def _to_dev(self, values, dtype):
         return torch.tensor(values, dtype=dtype, pin_memory=True).to(self.device, non_blocking=True)
 
-    @staticmethod
-    def sample(logits: torch.Tensor, temperatures: torch.Tensor) -> torch.Tensor:
-        logits = logits.float().div_(temperatures.unsqueeze(dim=1))
-        probs = torch.softmax(logits, dim=-1)
-        return probs.div_(torch.empty_like(probs).exponential_(1).clamp_min_(1e-10)).argmax(dim=-1)
+    def sample(self, logits: torch.Tensor, temperatures: torch.Tensor) -> torch.Tensor:
+        return self.sampler(logits, temperatures)
 
     # -------------------------------------------------------------- steps
     @torch.inference_mode()

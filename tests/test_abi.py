@@ -23,7 +23,7 @@ A16 = 0x10000  # a fake, 16-byte aligned device address: never dereferenced belo
 
 def declared():
     text = HEADER.read_text()
-    return sorted(set(re.findall(r"^(?:int|const char\*)\s+(nv4_\w+)\(", text, re.M)))
+    return sorted(set(re.findall(r"^(?:int|void|const char\*)\s+(nv4_\w+)\(", text, re.M)))
 
 
 def test_every_declared_symbol_is_exported_and_bound():

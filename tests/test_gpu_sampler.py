@@ -1,0 +1,96 @@
+"""GPU tests of the one-launch sampler (``nv4_gumbel_sample``).
+
+The reference samples argmax(softmax(l/T) / Exp(1)) (nanovllm/layers/
+sampler.py:5-12), a draw from softmax(l/T); the kernel draws argmax(l/T -
+log E) from a Philox stream.  Checks:
+* exact stream: for small rows, the kernel's choice equals the argmax
+  recomputed on the host from the same Philox words (host generator pinned by
+  its known answers in test_sampler_host.py);
+* distribution: 8192 rows of the same logits at two temperatures give
+  category frequencies within 5 standard errors of softmax(l/T);
+* real shape (32 x 151936 bf16, strided rows): a dominant logit is chosen;
+* determinism in (seed, offset); the module advances its offset per call.
+"""
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+from nv4 import _lib
+from nv4.sampler import Sampler, gumbel_sample
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda:0"
+
+
+def host_choice(logits_row, temp, row, seed, offset):
+    V = len(logits_row)
+    lib = _lib.load()
+    best, besti = -np.inf, 0
+    for q in range((V + 3) // 4):
+        c = (ctypes.c_uint32 * 4)(q, row, offset & 0xffffffff, offset >> 32)
+        k = (ctypes.c_uint32 * 2)(seed & 0xffffffff, seed >> 32)
+        o = (ctypes.c_uint32 * 4)()
+        lib.nv4_philox4x32_10(c, k, o)
+        for i in range(4):
+            v = 4 * q + i
+            if v >= V:
+                break
+            u = np.float32(((o[i] >> 8) + 0.5) * 2.0 ** -24)
+            e = max(np.float32(-np.log(u)), np.float32(1e-10))
+            s = np.float32(np.float32(logits_row[v]) / np.float32(temp)) - np.float32(np.log(e))
+            if s > best:
+                best, besti = s, v
+    return besti
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_exact_stream_small_rows(dtype):
+    g = torch.Generator().manual_seed(3)
+    B, V = 6, 37
+    logits = torch.randn(B, V, generator=g).to(dtype)
+    temps = torch.tensor([0.5, 0.7, 1.0, 1.3, 2.0, 0.9], dtype=torch.float32)
+    seed, offset = 0x1234_5678_9ABC, 17
+    got = gumbel_sample(logits.to(DEV), temps.to(DEV), seed, offset).cpu().tolist()
+    exp = [host_choice(logits[b].float().numpy(), float(temps[b]), b, seed, offset) for b in range(B)]
+    assert got == exp
+
+
+@pytest.mark.parametrize("temp", [0.6, 1.5])
+def test_distribution_matches_softmax(temp):
+    base = torch.tensor([2.0, 1.0, 0.5, 0.0, -1.0, 3.0, -3.0, 1.5])
+    B = 8192
+    logits = base.repeat(B, 1).to(torch.bfloat16).to(DEV)
+    temps = torch.full((B,), temp, dtype=torch.float32, device=DEV)
+    tok = gumbel_sample(logits, temps, seed=99, offset=5).cpu()
+    freq = torch.bincount(tok, minlength=8).double() / B
+    p = torch.softmax(base.double() / temp, dim=0)
+    se = (p * (1 - p) / B).sqrt()
+    assert ((freq - p).abs() <= 5 * se + 1e-12).all(), (freq, p)
+
+
+def test_real_shape_dominant_logit_strided():
+    B, V = 32, 151936
+    g = torch.Generator(device=DEV).manual_seed(5)
+    wide = torch.randn(B, V + 64, generator=g, device=DEV).to(torch.bfloat16)
+    idx = torch.randint(0, V, (B,), generator=g, device=DEV)
+    wide[torch.arange(B, device=DEV), idx] = 60.0
+    logits = wide[:, :V]
+    temps = torch.full((B,), 0.6, dtype=torch.float32, device=DEV)
+    tok = gumbel_sample(logits, temps, seed=1, offset=0)
+    assert torch.equal(tok, idx)
+
+
+def test_determinism_and_module_offset():
+    B, V = 16, 1000
+    logits = torch.zeros(B, V, dtype=torch.bfloat16, device=DEV)  # uniform: the draw is all randomness
+    temps = torch.ones(B, dtype=torch.float32, device=DEV)
+    a = gumbel_sample(logits, temps, seed=7, offset=3)
+    b = gumbel_sample(logits, temps, seed=7, offset=3)
+    c = gumbel_sample(logits, temps, seed=7, offset=4)
+    assert torch.equal(a, b) and not torch.equal(a, c)
+    s = Sampler(seed=7)
+    s.offset = 3
+    assert torch.equal(s(logits, temps), a) and s.offset == 4
+    assert torch.equal(s(logits, temps), c) and s.offset == 5
