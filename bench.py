@@ -55,7 +55,7 @@ PUBLISHED_GEMM_M32_US = {"qkv": 21.25, "o": 14.97, "gate_up": 79.86, "down": 46.
 PUBLISHED_GEMM_M4096_US = {"qkv": 861.77, "o": 505.62, "gate_up": 3293.68, "down": 1550.64}
 # Published bs32 decode tokens/s of the real Qwen3-8B (one RTX A6000, 32 x 4096
 # prompts, 256 output tokens), benchmarks/README.md:65.
-PUBLISHED_E2E_TOKS = {"bf16": 564.57, "w4a4": 766.71}
+PUBLISHED_E2E_TOKS = {"bf16": 564.57, "w4a4": 766.71, "w4a16": None}
 
 
 def k2_bytes(M, N, K):
@@ -180,16 +180,17 @@ def measured_traffic():
 def e2e_decode(torch, layers, out_tokens):
     """The reference's latency benchmark on the Qwen3-8B-shaped decoder with
     random weights: 32 requests of 4096 seeded token ids, serial prefill, then
-    bs32 decode of ``out_tokens`` tokens (HIP-graph steps), for the W4A4 and
-    the BF16 (hipBLASLt) projections; decode tokens/s = 32 * 1000 / mean step
-    ms over the pure-decode steps (benchmarks/bench_nano_latency.py:32-121)."""
+    bs32 decode of ``out_tokens`` tokens (HIP-graph steps), for the W4A4, the
+    BF16 (hipBLASLt) and the W4A16 (GPTQ, fused q/k/v and gate/up) projections;
+    decode tokens/s = 32 * 1000 / mean step ms over the pure-decode steps
+    (benchmarks/bench_nano_latency.py:32-121)."""
     from nv4.engine import Engine, qwen3_8b_config, run_decode_benchmark, seeded_prompts
     cfg = qwen3_8b_config(layers)
     prompts = seeded_prompts(32, 4096, cfg.vocab_size)
     res, kv = {}, None
-    for which in ("w4a4", "bf16"):
-        eng = Engine(cfg, use_w4a4=(which == "w4a4"), max_num_seqs=32, max_model_len=4096 + out_tokens,
-                     device="cuda:0", seed=1, kv_cache=kv)
+    for which in ("w4a4", "bf16", "w4a16"):
+        eng = Engine(cfg, use_w4a4=(which == "w4a4"), use_w4a16=(which == "w4a16"), max_num_seqs=32,
+                     max_model_len=4096 + out_tokens, device="cuda:0", seed=1, kv_cache=kv)
         kv = eng.kv_cache
         r = run_decode_benchmark(eng, prompts, output_tokens=out_tokens)
         if not (r["graph_equals_eager"] and r["logits_finite"]):
@@ -206,6 +207,7 @@ def e2e_decode(torch, layers, out_tokens):
     del kv
     torch.cuda.empty_cache()
     res["w4a4_over_bf16"] = round(res["w4a4"]["tokens_per_s"] / res["bf16"]["tokens_per_s"], 4)
+    res["w4a16_over_bf16"] = round(res["w4a16"]["tokens_per_s"] / res["bf16"]["tokens_per_s"], 4)
     res["workload"] = (f"Qwen3-8B-shaped decoder ({layers} layers, hidden 4096, intermediate 12288, 32 q / 8 kv "
                        "heads, vocab 151936), random weights; 32 requests x 4096 seeded token ids, serial "
                        f"prefill, bs32 decode of {out_tokens} tokens (HIP graph), KV cache bf16 paged "

@@ -27,7 +27,8 @@ import torch
 
 from .attention import decode_workspace
 from .layers.linear_w4a4 import W4A4Linear
-from .qwen3 import BF16Linear, Qwen3ForCausalLM
+from .layers.linear_w4a16 import W4A16Linear
+from .qwen3 import BF16Linear, Qwen3ForCausalLM, W4A16Qwen3ForCausalLM
 from .sampler import Sampler
 from .utils.context import get_context, reset_context, set_context
 
@@ -46,15 +47,23 @@ def random_init(model: Qwen3ForCausalLM, seed: int) -> None:
     """Random-init weights of the workload: embeddings and LM head ~N(0,
     0.02), norms 1, W4A4 projections with codes uniform in [-8, 7] (random
     bytes), group-128 scales uniform in [0.005, 0.02] and RHT signs +-1, BF16
-    projections ~N(0, 0.02).  W4A4 weights end in the MFMA-tiled order, as
-    after the checkpoint loader."""
+    projections ~N(0, 0.02), GPTQ projections with uniform nibbles and zero
+    points and scales uniform in [0.005, 0.02].  W4A4 weights end in the
+    MFMA-tiled order, as after the checkpoint loader."""
     dev = next(model.parameters()).device
     g = torch.Generator(device=dev).manual_seed(seed)
     for name, p in model.named_parameters():
+        if not p.dtype.is_floating_point or p.dtype == torch.float16:  # GPTQ tensors: below
+            continue
         if name.endswith("norm.weight"):
             p.fill_(1.0)
         else:
             p.copy_(torch.randn(p.shape, generator=g, device=dev, dtype=torch.float32).mul_(0.02))
+    for m in model.modules():
+        if isinstance(m, W4A16Linear):  # uniform nibbles and zero points, scales in [0.005, 0.02]
+            m.qweight.copy_(torch.randint(-2**31, 2**31, m.qweight.shape, generator=g, device=dev, dtype=torch.int64))
+            m.qzeros.copy_(torch.randint(-2**31, 2**31, m.qzeros.shape, generator=g, device=dev, dtype=torch.int64))
+            m.scales.copy_(0.005 + 0.015 * torch.rand(m.scales.shape, generator=g, device=dev))
     for m in model.modules():
         if isinstance(m, W4A4Linear):
             m.packed_weight.copy_(torch.randint(-128, 128, m.packed_weight.shape, generator=g, device=dev,
@@ -68,7 +77,7 @@ def random_init(model: Qwen3ForCausalLM, seed: int) -> None:
 class Engine:
     def __init__(self, hf_config, use_w4a4: bool, max_num_seqs: int, max_model_len: int, block_size: int = 256,
                  device="cuda:0", model: Qwen3ForCausalLM | None = None, kv_cache: torch.Tensor | None = None,
-                 seed: int = 0):
+                 seed: int = 0, use_w4a16: bool = False):
         self.cfg, self.device = hf_config, torch.device(device)
         self.max_num_seqs, self.max_model_len, self.block_size = max_num_seqs, max_model_len, block_size
         self.blocks_per_seq = math.ceil(max_model_len / block_size)
@@ -77,10 +86,12 @@ class Engine:
             torch.set_default_dtype(torch.bfloat16)
             try:
                 with torch.device(self.device):
-                    model = Qwen3ForCausalLM(hf_config, use_w4a4)
+                    model = W4A16Qwen3ForCausalLM(hf_config) if use_w4a16 else Qwen3ForCausalLM(hf_config, use_w4a4)
             finally:
                 torch.set_default_dtype(prev)
             random_init(model, seed)
+            if use_w4a16:
+                model.fuse_projections_()
         self.model = model.eval()
         cfg = hf_config
         head_dim = getattr(cfg, "head_dim", None) or cfg.hidden_size // cfg.num_attention_heads
@@ -234,3 +245,7 @@ def count_w4a4(model) -> int:
 
 def count_bf16(model) -> int:
     return sum(isinstance(m, BF16Linear) for m in model.modules())
+
+
+def count_w4a16(model) -> int:
+    return sum(isinstance(m, W4A16Linear) for m in model.modules())

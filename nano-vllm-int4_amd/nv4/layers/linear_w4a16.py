@@ -47,5 +47,38 @@ class W4A16Linear(nn.Module):
     def forward(self, x):
         shape = x.shape
         x = x.reshape(-1, self.in_features).contiguous()
-        out = dequant_matmul_w4a16(x, self.qweight, self.qzeros, self.scales, self.group_size)
+        # (after fuse_w4a16 the parameters are column views of the fused
+        # tensors; a direct call then reads contiguous copies)
+        out = dequant_matmul_w4a16(x, self.qweight.contiguous(), self.qzeros.contiguous(), self.scales.contiguous(),
+                                   self.group_size)
         return out.reshape(*shape[:-1], self.out_features)
+
+
+@torch.no_grad()
+def fuse_w4a16(linears) -> W4A16Linear:
+    """One GPTQ linear for several that read the same input (q/k/v, gate/up):
+    qweight, qzeros and scales concatenated along N (dim 1), which keeps every
+    column's packing (qzeros packs 8 output channels per int32, so each part's
+    N must be a multiple of 8).  The parts' parameters become views into the
+    fused tensors, so nothing is stored twice and their state-dict entries
+    keep the reference names and values.  The fused forward equals the
+    concatenation of the parts' forwards bit for bit (columns are computed
+    independently)."""
+    K = linears[0].in_features
+    if any(l.in_features != K or l.group_size != 128 or l.out_features % 8 for l in linears):
+        raise ValueError("Fused GPTQ linears need the same input width, group 128 and N % 8 == 0")
+    fused = W4A16Linear.__new__(W4A16Linear)
+    nn.Module.__init__(fused)
+    fused.in_features, fused.group_size = K, 128
+    fused.out_features = sum(l.out_features for l in linears)
+    for name in ("qweight", "qzeros", "scales"):
+        setattr(fused, name, nn.Parameter(torch.cat([getattr(l, name).data for l in linears], dim=1),
+                                          requires_grad=False))
+    off = 0
+    for l in linears:
+        n = l.out_features
+        l.qweight = nn.Parameter(fused.qweight.data[:, off:off + n], requires_grad=False)
+        l.qzeros = nn.Parameter(fused.qzeros.data[:, off // 8:(off + n) // 8], requires_grad=False)
+        l.scales = nn.Parameter(fused.scales.data[:, off:off + n], requires_grad=False)
+        off += n
+    return fused

@@ -6,7 +6,10 @@ nanovllm/models/qwen3.py:14-233 (BF16 and W4A4 variants behind
 loader address the same names:
 
 * ``W4A4Linear`` (RHT + group-128 INT4 activations, grouped INT4 GEMM) for
-  the fused qkv / o / gate_up / down projections when ``use_w4a4``; plain
+  the fused qkv / o / gate_up / down projections when ``use_w4a4``;
+  ``W4A16Linear`` (GPTQ) for separate q/k/v/o/gate/up/down projections when
+  ``use_w4a16`` (``W4A16Qwen3ForCausalLM``, the reference's
+  nanovllm/models/qwen3_w4a16.py:14-252); plain
   BF16 linears (torch ``F.linear``, i.e. hipBLASLt on ROCm) otherwise, with
   the reference's q/k/v and gate/up shard loaders
   (nanovllm/layers/linear.py:54-156, one GPU).
@@ -41,6 +44,7 @@ from .attention import Attention
 from .kernels.decoder_ops import (qk_norm_rope_store, rmsnorm, rmsnorm_rht_quant_pack, silu_mul,
                                   silu_mul_rht_quant_pack)
 from .layers.linear_w4a4 import W4A4Linear
+from .layers.linear_w4a16 import W4A16Linear, fuse_w4a16
 from .utils.context import get_context
 
 
@@ -110,14 +114,21 @@ class BF16Linear(nn.Module):
 
 class Qwen3Attention(nn.Module):
     def __init__(self, hidden_size, num_heads, num_kv_heads, max_position, head_dim=None, rms_norm_eps=1e-6,
-                 rope_theta=1_000_000.0, use_w4a4=False) -> None:
+                 rope_theta=1_000_000.0, use_w4a4=False, use_w4a16=False) -> None:
         super().__init__()
         self.num_heads, self.num_kv_heads = num_heads, num_kv_heads
         self.head_dim = head_dim or hidden_size // num_heads
         self.q_size, self.kv_size = num_heads * self.head_dim, num_kv_heads * self.head_dim
         self.scaling = self.head_dim ** -0.5
         qkv_out = self.q_size + 2 * self.kv_size
-        if use_w4a4:
+        self.use_w4a16 = use_w4a16
+        if use_w4a16:  # separate GPTQ projections, as the reference's W4A16 model (qwen3_w4a16.py:56-74)
+            self.q_proj = W4A16Linear(hidden_size, self.q_size)
+            self.k_proj = W4A16Linear(hidden_size, self.kv_size)
+            self.v_proj = W4A16Linear(hidden_size, self.kv_size)
+            self.o_proj = W4A16Linear(self.q_size, hidden_size)
+            object.__setattr__(self, "qkv_fused", None)  # derived by fuse_projections_(), not in the state dict
+        elif use_w4a4:
             self.qkv_proj = W4A4Linear(hidden_size, qkv_out)
             self.o_proj = W4A4Linear(self.q_size, hidden_size)
         else:
@@ -130,8 +141,17 @@ class Qwen3Attention(nn.Module):
         self.q_norm = RMSNorm(self.head_dim, eps=rms_norm_eps)
         self.k_norm = RMSNorm(self.head_dim, eps=rms_norm_eps)
 
+    def fuse_projections_(self):
+        """W4A16: q/k/v as one N-concatenated GPTQ linear (same bits)."""
+        if self.use_w4a16 and self.qkv_fused is None:
+            object.__setattr__(self, "qkv_fused", fuse_w4a16([self.q_proj, self.k_proj, self.v_proj]))
+
     def forward(self, positions, hidden_states=None, qkv=None):
-        if qkv is None:
+        if qkv is None and self.use_w4a16:
+            h = hidden_states
+            qkv = (self.qkv_fused(h) if self.qkv_fused is not None
+                   else torch.cat([self.q_proj(h), self.k_proj(h), self.v_proj(h)], dim=-1))
+        elif qkv is None:
             qkv = self.qkv_proj(hidden_states)
         ctx = get_context()
         # q/k RMSNorm + rotary + KV-cache store in one launch; prefill also
@@ -146,9 +166,15 @@ class Qwen3Attention(nn.Module):
 
 
 class Qwen3MLP(nn.Module):
-    def __init__(self, hidden_size, intermediate_size, use_w4a4=False) -> None:
+    def __init__(self, hidden_size, intermediate_size, use_w4a4=False, use_w4a16=False) -> None:
         super().__init__()
-        if use_w4a4:
+        self.use_w4a16 = use_w4a16
+        if use_w4a16:  # reference qwen3_w4a16.py:136-160
+            self.gate_proj = W4A16Linear(hidden_size, intermediate_size)
+            self.up_proj = W4A16Linear(hidden_size, intermediate_size)
+            self.down_proj = W4A16Linear(intermediate_size, hidden_size)
+            object.__setattr__(self, "gate_up_fused", None)
+        elif use_w4a4:
             self.gate_up_proj = W4A4Linear(hidden_size, 2 * intermediate_size)
             self.down_proj = W4A4Linear(intermediate_size, hidden_size)
         else:
@@ -156,7 +182,16 @@ class Qwen3MLP(nn.Module):
                                            {0: (0, intermediate_size), 1: (intermediate_size, intermediate_size)})
             self.down_proj = BF16Linear(intermediate_size, hidden_size)
 
+    def fuse_projections_(self):
+        """W4A16: gate/up as one N-concatenated GPTQ linear (same bits)."""
+        if self.use_w4a16 and self.gate_up_fused is None:
+            object.__setattr__(self, "gate_up_fused", fuse_w4a16([self.gate_proj, self.up_proj]))
+
     def forward(self, x):
+        if self.use_w4a16:
+            gate_up = (self.gate_up_fused(x) if self.gate_up_fused is not None
+                       else torch.cat([self.gate_proj(x), self.up_proj(x)], dim=-1))
+            return self.down_proj(silu_mul(gate_up))
         return self.down_proj(silu_mul(self.gate_up_proj(x)))
 
     def forward_fused(self, x, residual, norm):
@@ -169,13 +204,13 @@ class Qwen3MLP(nn.Module):
 
 
 class Qwen3DecoderLayer(nn.Module):
-    def __init__(self, config, use_w4a4=False) -> None:
+    def __init__(self, config, use_w4a4=False, use_w4a16=False) -> None:
         super().__init__()
         self.self_attn = Qwen3Attention(
             config.hidden_size, config.num_attention_heads, config.num_key_value_heads,
             config.max_position_embeddings, getattr(config, "head_dim", None), config.rms_norm_eps,
-            getattr(config, "rope_theta", 1_000_000.0), use_w4a4)
-        self.mlp = Qwen3MLP(config.hidden_size, config.intermediate_size, use_w4a4)
+            getattr(config, "rope_theta", 1_000_000.0), use_w4a4, use_w4a16)
+        self.mlp = Qwen3MLP(config.hidden_size, config.intermediate_size, use_w4a4, use_w4a16)
         self.input_layernorm = RMSNorm(config.hidden_size, eps=config.rms_norm_eps)
         self.post_attention_layernorm = RMSNorm(config.hidden_size, eps=config.rms_norm_eps)
         # W4A4 with the 4096-wide hidden state: the norms and SiLU-mul run
@@ -204,10 +239,11 @@ class Qwen3DecoderLayer(nn.Module):
 
 
 class Qwen3Model(nn.Module):
-    def __init__(self, config, use_w4a4=False) -> None:
+    def __init__(self, config, use_w4a4=False, use_w4a16=False) -> None:
         super().__init__()
         self.embed_tokens = nn.Embedding(config.vocab_size, config.hidden_size)
-        self.layers = nn.ModuleList([Qwen3DecoderLayer(config, use_w4a4) for _ in range(config.num_hidden_layers)])
+        self.layers = nn.ModuleList([Qwen3DecoderLayer(config, use_w4a4, use_w4a16)
+                                     for _ in range(config.num_hidden_layers)])
         self.norm = RMSNorm(config.hidden_size, eps=config.rms_norm_eps)
 
     def forward(self, input_ids, positions):
@@ -224,9 +260,11 @@ class Qwen3ForCausalLM(nn.Module):
         "gate_proj": ("gate_up_proj", 0), "up_proj": ("gate_up_proj", 1),
     }
 
-    def __init__(self, config, use_w4a4=False) -> None:
+    def __init__(self, config, use_w4a4=False, use_w4a16=False) -> None:
         super().__init__()
-        self.model = Qwen3Model(config, use_w4a4)
+        if use_w4a4 and use_w4a16:
+            raise ValueError("W4A16 and W4A4 cannot be enabled together")
+        self.model = Qwen3Model(config, use_w4a4, use_w4a16)
         self.lm_head = nn.Linear(config.hidden_size, config.vocab_size, bias=False)
         if config.tie_word_embeddings:
             self.lm_head.weight = self.model.embed_tokens.weight
@@ -239,3 +277,23 @@ class Qwen3ForCausalLM(nn.Module):
         if ctx.is_prefill and ctx.cu_seqlens_q is not None:
             hidden_states = hidden_states[ctx.cu_seqlens_q[1:] - 1].contiguous()
         return F.linear(hidden_states, self.lm_head.weight)
+
+
+class W4A16Qwen3ForCausalLM(Qwen3ForCausalLM):
+    """The reference's GPTQ model (nanovllm/models/qwen3_w4a16.py:228-252):
+    separate q/k/v and gate/up W4A16 projections under the checkpoint's names
+    (no packed-module mapping, so ``load_model`` copies every GPTQ tensor by
+    name).  ``fuse_projections_()`` (after loading) concatenates q/k/v and
+    gate/up along N into one GPTQ linear each -- one launch instead of three
+    and two, the fused QKV at N = 6144 -- with the parts' parameters kept as
+    views, so the state dict is unchanged and the outputs are the same bits."""
+    packed_modules_mapping = {}
+
+    def __init__(self, config) -> None:
+        super().__init__(config, use_w4a16=True)
+
+    def fuse_projections_(self):
+        for layer in self.model.layers:
+            layer.self_attn.fuse_projections_()
+            layer.mlp.fuse_projections_()
+        return self

@@ -7,7 +7,10 @@
 * W4A4 decoder: its first qkv projection inside a prefill forward (input
   RMSNorm fused into the activation quantization) is bit-exact with the
   oracle chain on the normalised embeddings.
-* Both: the decode step replayed from the captured HIP graph gives logits
+* W4A16 decoder (GPTQ, the reference's use_w4a16 model): the N-fused q/k/v
+  and gate/up projections give the same logits, bit for bit, as the separate
+  projections.
+* All: the decode step replayed from the captured HIP graph gives logits
   bit-equal to the eager step (the reference checks the same,
   benchmarks/bench_nano_latency.py:96-107), finite, and a short run of the
   benchmark loop completes with in-vocabulary tokens.
@@ -37,11 +40,13 @@ def engines():
     c = cfg()
     bf16 = Engine(c, use_w4a4=False, max_num_seqs=4, max_model_len=1024, device=DEV, seed=1)
     w4 = Engine(c, use_w4a4=True, max_num_seqs=4, max_model_len=1024, device=DEV, seed=2, kv_cache=bf16.kv_cache)
-    return bf16, w4
+    w16 = Engine(c, use_w4a4=False, use_w4a16=True, max_num_seqs=4, max_model_len=1024, device=DEV, seed=3,
+                 kv_cache=bf16.kv_cache)
+    return bf16, w4, w16
 
 
 def test_decode_step_matches_prefill_bf16(engines):
-    eng, _ = engines
+    eng = engines[0]
     prompt = seeded_prompts(1, 301, 1024, seed=5)[0]
     temps = torch.full((1,), 1.0, device=DEV)
     with torch.inference_mode():
@@ -70,7 +75,7 @@ def test_w4a4_first_projection_matches_oracle(engines):
     quantization) and check it against the oracle chain on the normalised
     embeddings (nv4 RMSNorm, whose bits the fused kernel reproduces)."""
     from nv4.kernels.decoder_ops import rmsnorm
-    _, eng = engines
+    eng = engines[1]
     layer = eng.model.model.layers[0]
     assert layer.fused
     seen = {}
@@ -93,9 +98,41 @@ def test_w4a4_first_projection_matches_oracle(engines):
     assert np.array_equal(bf16_bits(seen["qkv"]), ref)
 
 
-@pytest.mark.parametrize("which", ["bf16", "w4a4"])
+def test_w4a16_fused_projections_equal_separate(engines):
+    eng = engines[2]
+    ids = seeded_prompts(1, 90, 1024, seed=21)[0]
+
+    def logits():
+        from nv4.utils.context import reset_context, set_context
+        n = len(ids)
+        cu = torch.tensor([0, n], dtype=torch.int32, device=DEV)
+        slots = torch.tensor(eng._slots(3, 0, n), dtype=torch.int32, device=DEV)
+        with torch.inference_mode():
+            set_context(True, cu, cu, n, n, slots, None, None, seqlens_q=(n,))
+            out = eng.model.compute_logits(eng.model(torch.tensor(ids, device=DEV), torch.arange(n, device=DEV)))
+            reset_context()
+        return out.clone()
+
+    layers = eng.model.model.layers
+    assert all(l.self_attn.qkv_fused is not None and l.mlp.gate_up_fused is not None for l in layers)
+    fused = logits()
+    saved = [(l.self_attn.qkv_fused, l.mlp.gate_up_fused) for l in layers]
+    try:
+        for l in layers:
+            object.__setattr__(l.self_attn, "qkv_fused", None)
+            object.__setattr__(l.mlp, "gate_up_fused", None)
+        separate = logits()
+    finally:
+        for l, (q, gu) in zip(layers, saved):
+            object.__setattr__(l.self_attn, "qkv_fused", q)
+            object.__setattr__(l.mlp, "gate_up_fused", gu)
+    torch.cuda.synchronize()
+    assert torch.isfinite(fused).all() and torch.equal(fused, separate)
+
+
+@pytest.mark.parametrize("which", ["bf16", "w4a4", "w4a16"])
 def test_graph_equals_eager_and_benchmark_loop(engines, which):
-    eng = engines[0] if which == "bf16" else engines[1]
+    eng = engines[("bf16", "w4a4", "w4a16").index(which)]
     prompts = seeded_prompts(4, 200, 1024, seed=11)
     res = run_decode_benchmark(eng, prompts, output_tokens=6, temperature=0.6)
     assert res["graph_equals_eager"] and res["logits_finite"]
