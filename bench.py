@@ -66,6 +66,10 @@ def k1_bytes(M, K):
     return 2 * M * K + K + M * K // 2 + M * K // 64
 
 
+def k3_bytes(M, N, K):
+    return 2 * M * K + N * K // 2 + 2 * N * K // 128 + 4 * (K // 128) * (N // 8) + 2 * M * N
+
+
 def parse_args():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -394,9 +398,9 @@ def main():
 def detail_table(torch, nv4, W, dev, R):
     """Per projection at M = 32 and M = 4096: K1 and K2 microseconds (graph
     replays of back-to-back launches, weights rotated past the Infinity
-    Cache), their
-    roofline fractions, and the BF16 hipBLASLt GEMM (torch.mm) on the same
-    shape."""
+    Cache), their roofline fractions, and the BF16 hipBLASLt GEMM (torch.mm)
+    on the same shape; then the W4A16 GPTQ GEMM on the fused QKV at M = 1, 8,
+    32 (fp16 activations, microseconds per call and HBM fraction)."""
     res = {}
     g = torch.Generator(device=dev)
     g.manual_seed(W.BASE_SEED + 2000)
@@ -438,6 +442,25 @@ def detail_table(torch, nv4, W, dev, R):
                 entry["ref_a6000_gemm_us"] = PUBLISHED_GEMM_M4096_US[p]
             res[f"M{M}_{p}"] = entry
             print(f"[detail] M={M} {p}: {entry}", file=sys.stderr, flush=True)
+    # W4A16 GPTQ GEMM on the fused QKV (N = 6144, K = 4096, fp16 activations), decode sizes;
+    # 24 rotating weight sets (315 MB) past the Infinity Cache.
+    for M in (1, 8, 32):
+        N, K = 6144, 4096
+        x = torch.randn(M, K, generator=g, device=dev).to(torch.float16)
+        wsets = []
+        for _ in range(24):
+            qw = torch.randint(-2**31, 2**31, (K // 8, N), generator=g, device=dev, dtype=torch.int64).to(torch.int32)
+            qz = torch.randint(-2**31, 2**31, (K // 128, N // 8), generator=g, device=dev,
+                               dtype=torch.int64).to(torch.int32)
+            sc = (0.005 + 0.015 * torch.rand(K // 128, N, generator=g, device=dev)).to(torch.float16)
+            wsets.append((qw, qz, sc))
+        o16 = torch.empty((M, N), dtype=torch.float16, device=dev)
+        l4 = [lambda w=w: nv4.dequant_matmul_w4a16(x, w[0], w[1], w[2], out=o16) for w in wsets]
+        us4 = graph_launch_us(torch, l4, 20)
+        del wsets
+        entry = {"k3_us": round(us4, 2), "k3_hbm_frac": round(k3_bytes(M, N, K) / (us4 * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
+        res[f"W4A16_M{M}_qkv"] = entry
+        print(f"[detail] W4A16 M={M} qkv: {entry}", file=sys.stderr, flush=True)
     return res
 
 

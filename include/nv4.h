@@ -25,8 +25,10 @@
  *                          MFMA-tiled order (no counterpart in the reference,
  *                          whose kernels read [N,K/2]; W4A4Linear keeps the
  *                          reference layout in its state dict)
- *   nv4_w4a16_gemm      <- nanovllm/layers/linear_w4a16.py:11 tl_dequant_matmul_w4a16
- *                          (called from W4A16Linear.forward :128-148)
+ *   nv4_w4a16_gemm, nv4_w4a16_gemm_ws <- nanovllm/layers/linear_w4a16.py:11
+ *                          tl_dequant_matmul_w4a16 (called from W4A16Linear.forward
+ *                          :128-148; the reference splits K 8 ways with bf16 atomics,
+ *                          the _ws form splits K into 1024-deep fp32 partials)
  *   nv4_paged_decode_attention <- flash_attn_with_kvcache in the decode branch of
  *                          nanovllm/layers/attention.py:72-74 (caller of the hot path)
  *   nv4_rmsnorm         <- RMSNorm.rms_forward / add_rms_forward,
@@ -165,6 +167,19 @@ int nv4_w4a4_linear_tiled(const void* x, const int8_t* signs, const int8_t* w_ti
 int nv4_w4a16_gemm(const void* x, int x_dtype, const int32_t* qweight, const int32_t* qzeros,
                    const void* scales, void* out, int out_dtype,
                    int64_t M, int64_t N, int64_t K, int group, void* stream);
+
+/*
+ * nv4_w4a16_gemm with a caller-provided fp32 workspace, for decode sizes
+ * (M <= 64; larger M runs nv4_w4a16_gemm and ignores the workspace): K is
+ * split into 1024-deep slices, each written as an fp32 partial [S, M, N]
+ * (S = ceil(K/1024)) and then added in slice order and rounded once, so the
+ * result is deterministic (not bit-identical to nv4_w4a16_gemm, whose
+ * summation order differs).  workspace_bytes >= S*M*N*4, 16-byte aligned;
+ * qweight and x 16-byte aligned, scales and out 8-byte aligned.
+ */
+int nv4_w4a16_gemm_ws(const void* x, int x_dtype, const int32_t* qweight, const int32_t* qzeros,
+                      const void* scales, void* out, int out_dtype, float* workspace, int64_t workspace_bytes,
+                      int64_t M, int64_t N, int64_t K, int group, void* stream);
 
 /*
  * Paged decode attention (one new token per sequence; GQA).

@@ -20,6 +20,9 @@
 namespace nv4 {
 namespace {
 
+typedef float v2f __attribute__((ext_vector_type(2)));
+typedef __bf16 v2bf __attribute__((ext_vector_type(2)));
+
 template <bool FP16>
 struct W16Traits;
 template <>
@@ -116,6 +119,208 @@ k3_w4a16(const uint16_t* __restrict__ x, const int32_t* __restrict__ qweight,
     }
 }
 
+// ----------------------------------------------------------------------------
+// Decode-sized kernel (M <= 64) with a deterministic split over K.
+//
+// At decode sizes the 16-column kernel above is bound by load latency (one
+// 4-byte weight load per lane and 32-k step, waited on in turn) and by every
+// workgroup re-reading the whole bf16 activation block.  Here a workgroup
+// owns 64 columns and one 1024-deep K slice (grid: column blocks x slices):
+//  * weights: lane l loads 16 contiguous bytes of a qweight row -- columns
+//    4(l%16) .. +3 of k-octet l/16 -- so a wave reads four 256-byte runs per
+//    32-k step, and all of the slice's loads (8 per lane) are issued up
+//    front; the four words feed four MFMAs whose output columns are
+//    4c + j (j = word);
+//  * activations: the slice's rows (ROWS x 1024 bf16) are copied into LDS in
+//    whole lines once per workgroup and read back as MFMA A operands
+//    (16-byte chunks XOR-swizzled by row);
+//  * dequantization: v = fma(float(q), s, -(z+1) s) -- exactly (q - z - 1) s,
+//    since both products are exact in fp32 -- then one rounding to bf16 (two
+//    values per v_cvt_pk_bf16_f32) or fp16, as the reference rounds the
+//    dequantized weight;
+//  * the four waves take interleaved 32-k steps of the slice; their fp32
+//    tiles are added in wave order in LDS, and the slice's [M, N] fp32 partial
+//    goes to the workspace; a second kernel adds the slices in order and
+//    rounds once (no atomics, same bits on every run).
+// ----------------------------------------------------------------------------
+constexpr int K3_KS = 1024;  // k per slice
+constexpr int K3_NB = 64;    // columns per workgroup
+
+__device__ __forceinline__ int k3_swz(int r, int c) { return r * (K3_KS * 2) + ((c ^ (r & 7)) << 4); }
+
+template <int MB, bool XF16>
+__global__ void __launch_bounds__(256, 1)
+k3_dec(const uint16_t* __restrict__ x, const int32_t* __restrict__ qweight, const int32_t* __restrict__ qzeros,
+       const uint16_t* __restrict__ scales, float* __restrict__ ws, int M, int N, int K) {
+    using TR = W16Traits<XF16>;
+    constexpr int ROWS = MB * 16;
+    __shared__ __align__(16) uint8_t smem[ROWS * K3_KS * 2];  // activation slice, then the wave partials
+    const int t = threadIdx.x, lane = t & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+    const int n0 = blockIdx.x * K3_NB;
+    const int slice = blockIdx.y;
+    const int ks = slice * K3_KS;
+    const int klen = min(K3_KS, K - ks);  // multiple of 128
+    const int steps = klen >> 5;
+    const int c4 = lane & 15, kq = lane >> 4;
+    // Column quad of this lane; quads at or beyond N load the last valid quad (results dropped).
+    const int ncol = min(n0 + 4 * c4, N - 4);
+
+    // ---- weights, zero points and scales of the slice: all loads first.
+    const int nst = (steps + 3 - wave) >> 2;  // steps of this wave (<= 8)
+    v4u wq[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const int st = min(wave + 4 * i, steps - 1);
+        const int64_t row = (int64_t)((ks >> 3) + st * 4 + kq);
+        wq[i] = *reinterpret_cast<const v4u*>(qweight + row * N + ncol);
+    }
+    uint32_t zw[8];
+    uint2 sv[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {  // group of step wave + 4 i is i (4 steps per group)
+        const int g = (ks >> 7) + min(i, (klen >> 7) - 1);
+        zw[i] = (uint32_t)qzeros[(int64_t)g * (N >> 3) + (ncol >> 3)];
+        sv[i] = *reinterpret_cast<const uint2*>(scales + (int64_t)g * N + ncol);
+    }
+    // ---- activation slice into LDS (row r: 128 chunks of 16 bytes).
+    {
+        constexpr int CH = ROWS * (K3_KS / 8);  // 16-byte chunks
+        constexpr int PER = CH / 256;
+        v4u xv[PER];
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+            const int q = t + i * 256;
+            const int r = q >> 7, c = q & 127;
+            const int rr = min(r, M - 1);
+            const int cc = min(c, (klen >> 3) - 1);
+            xv[i] = *reinterpret_cast<const v4u*>(x + (int64_t)rr * K + ks + cc * 8);
+        }
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+            const int q = t + i * 256;
+            *reinterpret_cast<v4u*>(&smem[k3_swz(q >> 7, q & 127)]) = xv[i];
+        }
+    }
+    __syncthreads();
+
+    v4f acc[MB][4];
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[mb][j] = v4f{0.f, 0.f, 0.f, 0.f};
+    const int zsh = 16 * (c4 & 1);  // the quad's 4 zero-point nibbles within its qzeros word
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        if (i < nst) {  // uniform over the wave
+            const int st = wave + 4 * i;
+            float s[4], nzs[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const uint32_t h = ((j < 2 ? sv[i].x : sv[i].y) >> (16 * (j & 1))) & 0xffffu;
+                s[j] = TR::scale_of((uint16_t)h);
+                const float zp1 = (float)(((zw[i] >> (zsh + 4 * j)) & 15u) + 1u);
+                nzs[j] = -(zp1 * s[j]);
+            }
+            typename TR::vec bop[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const uint32_t w = wq[i][j];
+                float v[8];
+#pragma unroll
+                for (int e = 0; e < 8; ++e) v[e] = __builtin_fmaf((float)((w >> (4 * e)) & 15u), s[j], nzs[j]);
+                if constexpr (XF16) {
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) bop[j][e] = (_Float16)v[e];
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 8; e += 2) {
+                        const v2f pr = {v[e], v[e + 1]};
+                        const v2bf b = __builtin_convertvector(pr, v2bf);
+                        bop[j][e] = b[0];
+                        bop[j][e + 1] = b[1];
+                    }
+                }
+            }
+            const int c = st * 4 + kq;  // 16-byte chunk of the k-octet in the slice row
+#pragma unroll
+            for (int mb = 0; mb < MB; ++mb) {
+                const v4u av = *reinterpret_cast<const v4u*>(&smem[k3_swz(mb * 16 + c4, c)]);
+                const typename TR::vec aop = __builtin_bit_cast(typename TR::vec, av);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    if constexpr (XF16)
+                        acc[mb][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(aop, bop[j], acc[mb][j], 0, 0, 0);
+                    else
+                        acc[mb][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(aop, bop[j], acc[mb][j], 0, 0, 0);
+                }
+            }
+        }
+    }
+    __syncthreads();  // the activation slice is dead; its LDS takes the wave partials
+    float* part = reinterpret_cast<float*>(smem);  // [wave][mb][j][256]
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            *reinterpret_cast<v4f*>(&part[((wave * MB + mb) * 4 + j) * 256 + lane * 4]) = acc[mb][j];
+    __syncthreads();
+    // Thread t sums entry e = t of each (mb, j) tile over the waves in order:
+    // MFMA lane e/4, result e%4 -> row 4 (lane/16) + e%4, column 4 (lane%16) + j.
+    const int el = t >> 2, ei = t & 3;
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int o = (mb * 4 + j) * 256 + t;
+            float v = part[o];
+            v = v + part[(MB * 4) * 256 + o];
+            v = v + part[2 * (MB * 4) * 256 + o];
+            v = v + part[3 * (MB * 4) * 256 + o];
+            const int m = mb * 16 + 4 * (el >> 4) + ei, n = n0 + 4 * (el & 15) + j;
+            if (m < M && n < N) ws[((int64_t)slice * M + m) * N + n] = v;
+        }
+}
+
+// out[m, n] = round(sum over slices s in order of ws[s, m, n]).
+template <bool OF16>
+__global__ void __launch_bounds__(256)
+k3_reduce(const float* __restrict__ ws, void* __restrict__ out, int64_t MN, int S) {
+    const int64_t i = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
+    if (i >= MN) return;
+    v4f v = *reinterpret_cast<const v4f*>(ws + i);
+    for (int s = 1; s < S; ++s) {
+        const v4f w = *reinterpret_cast<const v4f*>(ws + (int64_t)s * MN + i);
+        v = v4f{v[0] + w[0], v[1] + w[1], v[2] + w[2], v[3] + w[3]};
+    }
+    uint16_t h[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+        h[k] = OF16 ? __builtin_bit_cast(uint16_t, (_Float16)v[k]) : (uint16_t)f32_to_bf16_rne(v[k]);
+    *reinterpret_cast<uint2*>(static_cast<uint16_t*>(out) + i) =
+        make_uint2((uint32_t)h[0] | ((uint32_t)h[1] << 16), (uint32_t)h[2] | ((uint32_t)h[3] << 16));
+}
+
+template <int MB, bool XF, bool OF>
+hipError_t launch_dec(const void* x, const int32_t* qw, const int32_t* qz, const void* sc, void* out, float* ws,
+                      int M, int N, int K, hipStream_t st) {
+    const int S = (K + K3_KS - 1) / K3_KS;
+    hipLaunchKernelGGL((k3_dec<MB, XF>), dim3((unsigned)((N + K3_NB - 1) / K3_NB), (unsigned)S), dim3(256), 0, st,
+                       static_cast<const uint16_t*>(x), qw, qz, static_cast<const uint16_t*>(sc), ws, M, N, K);
+    const int64_t MN = (int64_t)M * N;  // N % 8 == 0, so MN % 4 == 0
+    hipLaunchKernelGGL((k3_reduce<OF>), dim3((unsigned)((MN / 4 + 255) / 256)), dim3(256), 0, st, ws, out, MN, S);
+    return hipGetLastError();
+}
+
+template <bool XF, bool OF>
+hipError_t dispatch_dec(const void* x, const int32_t* qw, const int32_t* qz, const void* sc, void* out, float* ws,
+                        int M, int N, int K, hipStream_t st) {
+    if (M <= 16) return launch_dec<1, XF, OF>(x, qw, qz, sc, out, ws, M, N, K, st);
+    if (M <= 32) return launch_dec<2, XF, OF>(x, qw, qz, sc, out, ws, M, N, K, st);
+    if (M <= 48) return launch_dec<3, XF, OF>(x, qw, qz, sc, out, ws, M, N, K, st);
+    return launch_dec<4, XF, OF>(x, qw, qz, sc, out, ws, M, N, K, st);
+}
+
 template <int MB, bool XF, bool OF>
 hipError_t launch(const void* x, const int32_t* qw, const int32_t* qz, const void* sc, void* out,
                   int M, int N, int K, hipStream_t st) {
@@ -160,5 +365,33 @@ extern "C" int nv4_w4a16_gemm(const void* x, int x_dtype, const int32_t* qweight
     else
         e = out_dtype == NV4_FP16 ? dispatch<false, true>(x, qweight, qzeros, scales, out, m, n, k, st)
                                   : dispatch<false, false>(x, qweight, qzeros, scales, out, m, n, k, st);
+    return (int)e;
+}
+
+extern "C" int nv4_w4a16_gemm_ws(const void* x, int x_dtype, const int32_t* qweight, const int32_t* qzeros,
+                                 const void* scales, void* out, int out_dtype, float* workspace,
+                                 int64_t workspace_bytes, int64_t M, int64_t N, int64_t K, int group, void* stream) {
+    using namespace nv4;
+    if (M > 64) return nv4_w4a16_gemm(x, x_dtype, qweight, qzeros, scales, out, out_dtype, M, N, K, group, stream);
+    if (!x || !qweight || !qzeros || !scales || !out || !workspace) return NV4_E_NULL;
+    if ((x_dtype != NV4_BF16 && x_dtype != NV4_FP16) || (out_dtype != NV4_BF16 && out_dtype != NV4_FP16))
+        return NV4_E_DTYPE;
+    if (group != 128) return NV4_E_GROUP;
+    if (M < 1 || N < 8 || N % 8 || K < 128 || K % 128 || N > 0x7fffffffLL || K > (1LL << 24)) return NV4_E_SHAPE;
+    const int64_t S = (K + K3_KS - 1) / K3_KS;
+    if (workspace_bytes < S * M * N * 4 || (N + K3_NB - 1) / K3_NB > 0x7fffffffLL || S > 65535) return NV4_E_SHAPE;
+    if (reinterpret_cast<uintptr_t>(x) % 16 || reinterpret_cast<uintptr_t>(qweight) % 16 ||
+        reinterpret_cast<uintptr_t>(qzeros) % 4 || reinterpret_cast<uintptr_t>(scales) % 8 ||
+        reinterpret_cast<uintptr_t>(out) % 8 || reinterpret_cast<uintptr_t>(workspace) % 16)
+        return NV4_E_ALIGN;
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    const int m = (int)M, n = (int)N, k = (int)K;
+    hipError_t e;
+    if (x_dtype == NV4_FP16)
+        e = out_dtype == NV4_FP16 ? dispatch_dec<true, true>(x, qweight, qzeros, scales, out, workspace, m, n, k, st)
+                                  : dispatch_dec<true, false>(x, qweight, qzeros, scales, out, workspace, m, n, k, st);
+    else
+        e = out_dtype == NV4_FP16 ? dispatch_dec<false, true>(x, qweight, qzeros, scales, out, workspace, m, n, k, st)
+                                  : dispatch_dec<false, false>(x, qweight, qzeros, scales, out, workspace, m, n, k, st);
     return (int)e;
 }

@@ -8,6 +8,11 @@ activations, the same bf16 rounding of the dequantized weight.  Unlike the
 reference (split-K 8 with bf16 atomics onto a zeroed output) the HIP kernel
 sums all of K in fp32 and writes each output once, so results do not depend
 on scheduling.  FP16 activations are accepted as well (output fp16).
+
+At decode sizes (M <= 64) the wrapper takes the split-K form
+(``nv4_w4a16_gemm_ws``): 64-column workgroups per 1024-deep K slice writing
+fp32 partials into a workspace from torch's caching allocator, added in slice
+order by a second launch -- still deterministic, and graph-capturable.
 """
 from __future__ import annotations
 
@@ -18,6 +23,7 @@ import torch
 from .. import _lib
 
 _DT = {torch.bfloat16: _lib.BF16, torch.float16: _lib.FP16}
+SLICE_K = 1024  # K per partial of the decode-size split
 
 
 def dequant_matmul_w4a16(x, qweight, qzeros, scales, group_size=128, out=None):
@@ -44,9 +50,18 @@ def dequant_matmul_w4a16(x, qweight, qzeros, scales, group_size=128, out=None):
     lib = _lib.load()
     stream = torch.cuda.current_stream(x.device).cuda_stream
     with torch.cuda.device(x.device):
-        rc = lib.nv4_w4a16_gemm(ctypes.c_void_p(x.data_ptr()), _DT[x.dtype],
-                                ctypes.c_void_p(qweight.data_ptr()), ctypes.c_void_p(qzeros.data_ptr()),
-                                ctypes.c_void_p(scales.data_ptr()), ctypes.c_void_p(out.data_ptr()),
-                                _DT[out.dtype], M, N, K, group_size, ctypes.c_void_p(stream))
+        if M <= 64:
+            S = (K + SLICE_K - 1) // SLICE_K
+            ws = torch.empty((S * M * N,), dtype=torch.float32, device=x.device)
+            rc = lib.nv4_w4a16_gemm_ws(ctypes.c_void_p(x.data_ptr()), _DT[x.dtype],
+                                       ctypes.c_void_p(qweight.data_ptr()), ctypes.c_void_p(qzeros.data_ptr()),
+                                       ctypes.c_void_p(scales.data_ptr()), ctypes.c_void_p(out.data_ptr()),
+                                       _DT[out.dtype], ctypes.c_void_p(ws.data_ptr()), ws.numel() * 4, M, N, K,
+                                       group_size, ctypes.c_void_p(stream))
+        else:
+            rc = lib.nv4_w4a16_gemm(ctypes.c_void_p(x.data_ptr()), _DT[x.dtype],
+                                    ctypes.c_void_p(qweight.data_ptr()), ctypes.c_void_p(qzeros.data_ptr()),
+                                    ctypes.c_void_p(scales.data_ptr()), ctypes.c_void_p(out.data_ptr()),
+                                    _DT[out.dtype], M, N, K, group_size, ctypes.c_void_p(stream))
     _lib.check(rc, "dequant_matmul_w4a16")
     return out
