@@ -6,20 +6,23 @@
 //
 // Decode attention reads the whole KV context of every sequence once per
 // step, so it is bound by HBM bandwidth; the kernel is laid out for streaming:
-//  * pass 1: one workgroup (4 waves) per (sequence, KV head, split of 256
-//    context tokens).  Wave w takes tokens 64w..64w+63 of the split; within a
-//    wave, lane group g (16 lanes) owns tokens 16g..16g+15 in four rounds of
-//    four, and lane j of a group owns head dims 8j..8j+7, so every K and V row
+//  * pass 1: one workgroup (4 waves) per (sequence, KV head, split of
+//    PA_SPLIT context tokens).  Wave w takes a quarter of the split; within a
+//    wave, lane group g (16 lanes) owns PA_SPLIT/16 consecutive tokens, and
+//    lane j of a group owns head dims 8j..8j+7, so every K and V row
 //    of a token (256 contiguous bytes per KV head) is read as one coalesced
 //    piece.  The G query heads that share the KV head stay in registers,
 //    pre-multiplied by scale * log2(e), so the softmax runs in base 2.
-//    Scores are reduced over a group's 16 lanes with DPP, and each group
-//    keeps an online-softmax state (max m, sum l, output o) per head; the
-//    next round's loads are issued before the current round's arithmetic.
+//    A group issues all its K and V loads before any arithmetic (its slot
+//    offsets come from one block-table read when block_size % 16 == 0),
+//    reduces its scores over its 16 lanes with DPP, and keeps one softmax
+//    state (max m, sum l, output o) per head.
 //    The 16 group states of the workgroup are merged through LDS and written
 //    to the split workspace (or, for a single split, normalised into out).
-//  * pass 2: one workgroup per (sequence, query head) merges the splits:
-//    M = max m_s, w_s = 2^(m_s - M), o = sum w_s o_s / sum w_s l_s.
+//  * pass 2: one wave per (sequence, query head) merges the splits: lane s
+//    reads split s's (m, l), M = max m_s, w_s = 2^(m_s - M) (broadcast with
+//    lane reads), o = sum w_s o_s / sum w_s l_s with lane i owning dims 2i,
+//    2i+1 and every split's loads issued before the sums.
 #include "nv4_common.h"
 
 namespace nv4 {
@@ -27,6 +30,7 @@ namespace {
 
 constexpr int PA_D = 128;        // head dim
 constexpr int PA_SPLIT = 256;    // context tokens per pass-1 workgroup
+constexpr int PA_TPG = PA_SPLIT / 16;    // tokens per lane group (16 lane groups per workgroup)
 constexpr int PA_THREADS = 256;  // 4 waves x 64 tokens
 
 constexpr int DPP_QUAD_XOR1 = 0xB1;
@@ -56,7 +60,7 @@ __device__ __forceinline__ void bf16x8_to_f32(const v4u& w, float (&f)[8]) {
     }
 }
 
-template <int G>
+template <int G, bool BLK16>
 __global__ void __launch_bounds__(PA_THREADS)
 pa_split(const uint16_t* __restrict__ q, int64_t q_row, const uint16_t* __restrict__ kc,
          const uint16_t* __restrict__ vc, const int32_t* __restrict__ block_tables, int max_blocks,
@@ -74,6 +78,32 @@ pa_split(const uint16_t* __restrict__ q, int64_t q_row, const uint16_t* __restri
     __shared__ float sm_m[16][G], sm_l[16][G];
     __shared__ float sm_o[16][G][PA_D];
 
+    const int32_t* bt = block_tables + (int64_t)b * max_blocks;
+    const int tok0 = start + (wave * 4 + g) * PA_TPG;  // this group's first token
+    // Element offsets of the group's token rows for this KV head and lane,
+    // clamped into the sequence so every load stays in its own valid slots.
+    // With block_size % 16 == 0 the group's 16 tokens (16-aligned) share one
+    // block: a single block-table read serves them all.
+    int64_t off[PA_TPG];
+    if constexpr (BLK16) {
+        const int c0 = min(tok0, ctx - 1);
+        const int64_t base = ((int64_t)bt[c0 / bs] * bs + c0 % bs) * Hkv + kvh;
+#pragma unroll
+        for (int i = 0; i < PA_TPG; ++i) off[i] = (base + (int64_t)(min(tok0 + i, ctx - 1) - c0) * Hkv) * PA_D + 8 * j;
+    } else {
+#pragma unroll
+        for (int i = 0; i < PA_TPG; ++i) {
+            const int c = min(tok0 + i, ctx - 1);
+            off[i] = (((int64_t)bt[c / bs] * bs + c % bs) * Hkv + kvh) * PA_D + 8 * j;
+        }
+    }
+    // Every K row, then every V row, of the group in flight at once.
+    v4u kb[PA_TPG], vb[PA_TPG];
+#pragma unroll
+    for (int i = 0; i < PA_TPG; ++i) kb[i] = *reinterpret_cast<const v4u*>(kc + off[i]);
+#pragma unroll
+    for (int i = 0; i < PA_TPG; ++i) vb[i] = *reinterpret_cast<const v4u*>(vc + off[i]);
+
     // Query heads kvh*G .. kvh*G+G-1, dims 8j..8j+7, scaled into base 2.
     float qv[G][8];
 #pragma unroll
@@ -84,76 +114,49 @@ pa_split(const uint16_t* __restrict__ q, int64_t q_row, const uint16_t* __restri
 #pragma unroll
         for (int d = 0; d < 8; ++d) qv[h][d] = f[d] * qscale;
     }
-    const int32_t* bt = block_tables + (int64_t)b * max_blocks;
-    const int tok0 = start + wave * 64 + g * 16;  // this group's first token
-    // Element offset of token tt's row for this KV head and lane (clamped
-    // into the sequence so every load stays in its own valid slots).
-    auto row_off = [&](int tt) {
-        const int c = min(tt, ctx - 1);
-        const int64_t slot = (int64_t)bt[c / bs] * bs + c % bs;
-        return (slot * Hkv + kvh) * PA_D + 8 * j;
-    };
 
+    // Scores of the group's tokens (reduced over its 16 lanes), then one
+    // softmax state per head: m = max, l = sum 2^(s - m), o = sum 2^(s - m) v.
+    float sc[PA_TPG][G];
+#pragma unroll
+    for (int i = 0; i < PA_TPG; ++i) {
+        float kf[8];
+        bf16x8_to_f32(kb[i], kf);
+        const bool live = tok0 + i < end;
+#pragma unroll
+        for (int h = 0; h < G; ++h) {
+            float p = 0.0f;
+#pragma unroll
+            for (int d = 0; d < 8; ++d) p = __builtin_fmaf(qv[h][d], kf[d], p);
+            p = row16_sum(p);
+            sc[i][h] = live ? p : -__builtin_inff();
+        }
+    }
     float m[G], l[G], o[G][8];
 #pragma unroll
     for (int h = 0; h < G; ++h) {
-        m[h] = -__builtin_inff();
+        float mx = sc[0][h];
+#pragma unroll
+        for (int i = 1; i < PA_TPG; ++i) mx = fmaxf(mx, sc[i][h]);
+        m[h] = mx;
         l[h] = 0.0f;
 #pragma unroll
         for (int d = 0; d < 8; ++d) o[h][d] = 0.0f;
+        // a group whose tokens are all past the end keeps m = -inf, l = 0, o = 0
+        const bool any = mx != -__builtin_inff();
+#pragma unroll
+        for (int i = 0; i < PA_TPG; ++i) sc[i][h] = any ? __builtin_amdgcn_exp2f(sc[i][h] - mx) : 0.0f;
+#pragma unroll
+        for (int i = 0; i < PA_TPG; ++i) l[h] += sc[i][h];
     }
-
-    v4u kb[2][4], vb[2][4];
-    auto issue = [&](int r, int buf) {
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            const int64_t off = row_off(tok0 + 4 * r + u);
-            kb[buf][u] = *reinterpret_cast<const v4u*>(kc + off);
-            vb[buf][u] = *reinterpret_cast<const v4u*>(vc + off);
-        }
-    };
-    issue(0, 0);
+    for (int i = 0; i < PA_TPG; ++i) {
+        float vf[8];
+        bf16x8_to_f32(vb[i], vf);
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-        const int buf = r & 1;
-        if (r + 1 < 4) issue(r + 1, buf ^ 1);
-        float sc[4][G];
+        for (int h = 0; h < G; ++h)
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            float kf[8];
-            bf16x8_to_f32(kb[buf][u], kf);
-            const bool live = tok0 + 4 * r + u < end;
-#pragma unroll
-            for (int h = 0; h < G; ++h) {
-                float p = 0.0f;
-#pragma unroll
-                for (int d = 0; d < 8; ++d) p = __builtin_fmaf(qv[h][d], kf[d], p);
-                p = row16_sum(p);
-                sc[u][h] = live ? p : -__builtin_inff();
-            }
-        }
-#pragma unroll
-        for (int h = 0; h < G; ++h) {
-            float mx = fmaxf(fmaxf(sc[0][h], sc[1][h]), fmaxf(sc[2][h], sc[3][h]));
-            const float m_new = fmaxf(m[h], mx);
-            // a group whose tokens are all past the end keeps m = -inf: no update
-            const float corr = m_new == -__builtin_inff() ? 1.0f : __builtin_amdgcn_exp2f(m[h] - m_new);
-            float p[4];
-#pragma unroll
-            for (int u = 0; u < 4; ++u)
-                p[u] = m_new == -__builtin_inff() ? 0.0f : __builtin_amdgcn_exp2f(sc[u][h] - m_new);
-            l[h] = l[h] * corr + (p[0] + p[1]) + (p[2] + p[3]);
-            m[h] = m_new;
-#pragma unroll
-            for (int d = 0; d < 8; ++d) o[h][d] *= corr;
-#pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                float vf[8];
-                bf16x8_to_f32(vb[buf][u], vf);
-#pragma unroll
-                for (int d = 0; d < 8; ++d) o[h][d] = __builtin_fmaf(p[u], vf[d], o[h][d]);
-            }
-        }
+            for (int d = 0; d < 8; ++d) o[h][d] = __builtin_fmaf(sc[i][h], vf[d], o[h][d]);
     }
 
     // Merge the 16 group states of the workgroup.
@@ -194,21 +197,60 @@ pa_split(const uint16_t* __restrict__ q, int64_t q_row, const uint16_t* __restri
     }
 }
 
-__global__ void __launch_bounds__(PA_D)
+__global__ void __launch_bounds__(64)
 pa_merge(const int32_t* __restrict__ context_lens, const float* __restrict__ part_o,
          const float* __restrict__ part_ml, uint16_t* __restrict__ out, int Hq, int S, int max_ctx) {
-    const int hq = blockIdx.x, b = blockIdx.y, d = threadIdx.x;
+    const int hq = blockIdx.x, b = blockIdx.y, lane = threadIdx.x;
     const int n = min(S, (min(context_lens[b], max_ctx) + PA_SPLIT - 1) / PA_SPLIT);
     const int64_t base = ((int64_t)b * Hq + hq) * S;
+    float O0 = 0.0f, O1 = 0.0f, L = 0.0f;
+    // Splits in chunks of 64 (one per lane); the running max M rescales
+    // earlier chunks when a later one raises it.
     float M = -__builtin_inff();
-    for (int s = 0; s < n; ++s) M = fmaxf(M, part_ml[(base + s) * 2]);
-    float L = 0.0f, O = 0.0f;
-    for (int s = 0; s < n; ++s) {
-        const float w = __builtin_amdgcn_exp2f(part_ml[(base + s) * 2] - M);
-        L = __builtin_fmaf(w, part_ml[(base + s) * 2 + 1], L);
-        O = __builtin_fmaf(w, part_o[(base + s) * PA_D + d], O);
+    for (int c0 = 0; c0 < n; c0 += 64) {
+        const int sidx = c0 + lane;
+        float ms = -__builtin_inff(), ls = 0.0f;
+        if (sidx < n) {
+            const float2 ml = *reinterpret_cast<const float2*>(part_ml + (base + sidx) * 2);
+            ms = ml.x;
+            ls = ml.y;
+        }
+        float cm = ms;
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) cm = fmaxf(cm, __shfl_xor(cm, off));
+        const float Mn = fmaxf(M, cm);
+        const float corr = M == -__builtin_inff() ? 0.0f : __builtin_amdgcn_exp2f(M - Mn);
+        O0 *= corr;
+        O1 *= corr;
+        L *= corr;
+        M = Mn;
+        const float w = sidx < n ? __builtin_amdgcn_exp2f(ms - M) : 0.0f;
+        float wl = w * ls;
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) wl += __shfl_xor(wl, off);
+        L += wl;
+        const int cnt = min(64, n - c0);
+        constexpr int U = 8;
+        for (int k0 = 0; k0 < cnt; k0 += U) {
+            float2 v[U];
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const int k = min(k0 + u, cnt - 1);
+                v[u] = *reinterpret_cast<const float2*>(part_o + (base + c0 + k) * PA_D + 2 * lane);
+            }
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                if (k0 + u < cnt) {
+                    const float wk = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, w),
+                                                                                         k0 + u));
+                    O0 = __builtin_fmaf(wk, v[u].x, O0);
+                    O1 = __builtin_fmaf(wk, v[u].y, O1);
+                }
+            }
+        }
     }
-    out[((int64_t)b * Hq + hq) * PA_D + d] = (uint16_t)f32_to_bf16_rne(O / L);
+    uint16_t* o = out + ((int64_t)b * Hq + hq) * PA_D + 2 * lane;
+    *reinterpret_cast<uint32_t*>(o) = f32_to_bf16_rne(O0 / L) | (f32_to_bf16_rne(O1 / L) << 16);
 }
 
 template <int G>
@@ -217,12 +259,17 @@ hipError_t pa_launch(const void* q, int64_t q_row, const void* kc, const void* v
                      float qscale, hipStream_t st) {
     float* part_o = ws;
     float* part_ml = ws + (int64_t)B * Hkv * G * S * PA_D;
-    hipLaunchKernelGGL((pa_split<G>), dim3((unsigned)S, (unsigned)Hkv, (unsigned)B), dim3(PA_THREADS), 0, st,
-                       static_cast<const uint16_t*>(q), q_row, static_cast<const uint16_t*>(kc),
-                       static_cast<const uint16_t*>(vc), bt, max_blocks, cl, static_cast<uint16_t*>(out), part_o,
-                       part_ml, Hkv, bs, S, max_ctx, qscale);
+    const dim3 grid((unsigned)S, (unsigned)Hkv, (unsigned)B);
+    if (bs % 16 == 0)
+        hipLaunchKernelGGL((pa_split<G, true>), grid, dim3(PA_THREADS), 0, st, static_cast<const uint16_t*>(q), q_row,
+                           static_cast<const uint16_t*>(kc), static_cast<const uint16_t*>(vc), bt, max_blocks, cl,
+                           static_cast<uint16_t*>(out), part_o, part_ml, Hkv, bs, S, max_ctx, qscale);
+    else
+        hipLaunchKernelGGL((pa_split<G, false>), grid, dim3(PA_THREADS), 0, st, static_cast<const uint16_t*>(q),
+                           q_row, static_cast<const uint16_t*>(kc), static_cast<const uint16_t*>(vc), bt, max_blocks,
+                           cl, static_cast<uint16_t*>(out), part_o, part_ml, Hkv, bs, S, max_ctx, qscale);
     if (S > 1)
-        hipLaunchKernelGGL(pa_merge, dim3((unsigned)(Hkv * G), (unsigned)B), dim3(PA_D), 0, st, cl, part_o, part_ml,
+        hipLaunchKernelGGL(pa_merge, dim3((unsigned)(Hkv * G), (unsigned)B), dim3(64), 0, st, cl, part_o, part_ml,
                            static_cast<uint16_t*>(out), Hkv * G, S, max_ctx);
     return hipGetLastError();
 }
@@ -246,8 +293,8 @@ extern "C" int nv4_paged_decode_attention(const void* q, int64_t q_row_stride, c
     const int64_t S = (max_context + PA_SPLIT - 1) / PA_SPLIT;
     if (workspace_bytes < B * Hq * S * (D + 2) * 4) return NV4_E_SHAPE;
     if (reinterpret_cast<uintptr_t>(q) % 16 || reinterpret_cast<uintptr_t>(k_cache) % 16 ||
-        reinterpret_cast<uintptr_t>(v_cache) % 16 || reinterpret_cast<uintptr_t>(out) % 2 ||
-        reinterpret_cast<uintptr_t>(workspace) % 4 || q_row_stride % 8)
+        reinterpret_cast<uintptr_t>(v_cache) % 16 || reinterpret_cast<uintptr_t>(out) % 4 ||
+        reinterpret_cast<uintptr_t>(workspace) % 8 || q_row_stride % 8)
         return NV4_E_ALIGN;
     const float qscale = scale * 1.4426950408889634f;  // log2(e): softmax in base 2
     hipStream_t st = static_cast<hipStream_t>(stream);

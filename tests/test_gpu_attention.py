@@ -4,8 +4,10 @@ Paged decode attention (``nv4_paged_decode_attention``, the replacement of
 flash_attn_with_kvcache in nanovllm/layers/attention.py:72-74): random bf16
 caches behind shuffled block tables, context lengths at and around the
 256-token split and block boundaries (1, 255, 256, 257, ..., 4352), GQA
-groups 1/2/4, block sizes 256 and 16, and queries read as a strided view of
-a fused qkv tensor; against softmax(scale q.K^T) V computed in fp32.  Bar:
+groups 1/2/4, block sizes 256, 16 (one block-table read per 16 tokens) and
+24 (one read per token), contexts of more than 64 splits (the merge's
+chunked loop), and queries read as a strided view of a fused qkv tensor;
+against softmax(scale q.K^T) V computed in fp32.  Bar:
 |out - ref| <= 1e-2 + 1e-2 |ref| (bf16 output).  Prefill attention (causal
 GQA through the fused flash SDPA kernel) against the same fp32 reference on
 short packed sequences, same bar.
@@ -63,7 +65,7 @@ def check(out, ref, what):
 
 
 @pytest.mark.parametrize("G", [1, 2, 4])
-@pytest.mark.parametrize("bs", [256, 16])
+@pytest.mark.parametrize("bs", [256, 16, 24])
 def test_paged_decode_attention(G, bs):
     Hkv = 8 // G if G < 8 else 1
     Hq = Hkv * G
@@ -87,6 +89,16 @@ def test_paged_decode_attention_qwen3_batch_strided():
     out = paged_decode_attention(q, kc, vc, bt, cl, scale, workspace=ws, max_context=4352)
     torch.cuda.synchronize()
     check(out, reference(q, kc, vc, bt, cl, scale), "qwen3 batch")
+
+
+def test_paged_decode_attention_many_splits():
+    """More than 64 splits of 256 tokens: the merge takes them in chunks of 64."""
+    lens = [64 * 256 + 300, 300, 64 * 256 + 1]
+    q, kc, vc, bt, cl = make_case(3, 32, 8, 256, lens, seed=13)
+    scale = 1 / math.sqrt(128)
+    out = paged_decode_attention(q, kc, vc, bt, cl, scale, max_context=max(lens))
+    torch.cuda.synchronize()
+    check(out, reference(q, kc, vc, bt, cl, scale), "many splits")
 
 
 def test_single_split_writes_output_directly():
