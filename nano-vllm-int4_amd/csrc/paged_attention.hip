@@ -5,20 +5,27 @@
 // context_lens[b] cache slots of the sequence, found through its block table.
 //
 // Decode attention reads the whole KV context of every sequence once per
-// step, so it is bound by HBM bandwidth; the kernel is laid out for streaming:
+// step, so it is bound by HBM bandwidth.  Layout:
 //  * pass 1: one workgroup (4 waves) per (sequence, KV head, split of
-//    PA_SPLIT context tokens).  Wave w takes a quarter of the split; within a
-//    wave, lane group g (16 lanes) owns PA_SPLIT/16 consecutive tokens, and
-//    lane j of a group owns head dims 8j..8j+7, so every K and V row
-//    of a token (256 contiguous bytes per KV head) is read as one coalesced
-//    piece.  The G query heads that share the KV head stay in registers,
-//    pre-multiplied by scale * log2(e), so the softmax runs in base 2.
-//    A group issues all its K and V loads before any arithmetic (its slot
-//    offsets come from one block-table read when block_size % 16 == 0),
-//    reduces its scores over its 16 lanes with DPP, and keeps one softmax
-//    state (max m, sum l, output o) per head.
-//    The 16 group states of the workgroup are merged through LDS and written
-//    to the split workspace (or, for a single split, normalised into out).
+//    PA_SPLIT = 256 context tokens); wave w takes tokens 64w..64w+63 of the
+//    split as two 32-token halves, and issues every K and V load of both
+//    halves (q first) before any arithmetic.  The products run on the matrix
+//    cores (v_mfma_f32_16x16x32_bf16; lane = (k-octet kq, row/column rc)):
+//      - scores S^T[token][head] = K . q^T: A = K rows (lane: token
+//        h0 + 16c + rc, 16-byte chunks kq, kq+4, kq+8, kq+12 -- a 64-byte
+//        piece of the 256-byte row per load), B = q of head rc (zero past the
+//        group's G heads), four 32-dim steps per 16-token tile;
+//      - online softmax in the score layout: lane (kq, rc) holds head rc's
+//        scores for tokens h0 + 16c + 4kq + r, so every exponential is taken
+//        once; the max over the half is shared by the four k-octet rows
+//        (scores in raw units, exponentials in base 2 with scale*log2(e));
+//      - O[head][dim] += P . V: A = P (bf16, as flash attention rounds P for
+//        P.V), B = V: each lane loads 256-byte V rows (chunk rc of its own
+//        score tokens) and an 8x8 transpose of bf16 pairs (v_perm) turns
+//        them into the operand of tile t = dims 8rc + t.
+//    The four wave states (m, l, o per head) are merged through LDS and
+//    written to the split workspace (or, for a single split, normalised
+//    into out).
 //  * pass 2: one wave per (sequence, query head) merges the splits: lane s
 //    reads split s's (m, l), M = max m_s, w_s = 2^(m_s - M) (broadcast with
 //    lane reads), o = sum w_s o_s / sum w_s l_s with lane i owning dims 2i,
@@ -30,35 +37,10 @@ namespace {
 
 constexpr int PA_D = 128;        // head dim
 constexpr int PA_SPLIT = 256;    // context tokens per pass-1 workgroup
-constexpr int PA_TPG = PA_SPLIT / 16;    // tokens per lane group (16 lane groups per workgroup)
 constexpr int PA_THREADS = 256;  // 4 waves x 64 tokens
 
-constexpr int DPP_QUAD_XOR1 = 0xB1;
-constexpr int DPP_QUAD_XOR2 = 0x4E;
-constexpr int DPP_HALF_MIRROR = 0x141;
-constexpr int DPP_MIRROR = 0x140;
-
-template <int CTRL>
-__device__ __forceinline__ float pa_dpp(float v) {
-    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, true));
-}
-
-// Sum over the 16 lanes of a DPP row (every lane gets the sum).
-__device__ __forceinline__ float row16_sum(float v) {
-    v += pa_dpp<DPP_QUAD_XOR1>(v);
-    v += pa_dpp<DPP_QUAD_XOR2>(v);
-    v += pa_dpp<DPP_HALF_MIRROR>(v);
-    v += pa_dpp<DPP_MIRROR>(v);
-    return v;
-}
-
-__device__ __forceinline__ void bf16x8_to_f32(const v4u& w, float (&f)[8]) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        f[2 * i] = __uint_as_float(w[i] << 16);
-        f[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
-    }
-}
+typedef __bf16 v2bf __attribute__((ext_vector_type(2)));
+typedef float v2f __attribute__((ext_vector_type(2)));
 
 template <int G, bool BLK16>
 __global__ void __launch_bounds__(PA_THREADS)
@@ -72,126 +54,200 @@ pa_split(const uint16_t* __restrict__ q, int64_t q_row, const uint16_t* __restri
     const int start = s * PA_SPLIT;
     if (start >= ctx) return;  // nothing of this sequence here; pass 2 skips the split
     const int end = min(start + PA_SPLIT, ctx);
-    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-    const int g = lane >> 4, j = lane & 15;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int kq = lane >> 4, rc = lane & 15;  // MFMA k-octet and row/column of the lane
 
-    __shared__ float sm_m[16][G], sm_l[16][G];
-    __shared__ float sm_o[16][G][PA_D];
+    __shared__ float sm_m[4][G], sm_l[4][G];
+    __shared__ float sm_o[4][G][PA_D];
 
     const int32_t* bt = block_tables + (int64_t)b * max_blocks;
-    const int tok0 = start + (wave * 4 + g) * PA_TPG;  // this group's first token
-    // Element offsets of the group's token rows for this KV head and lane,
-    // clamped into the sequence so every load stays in its own valid slots.
-    // With block_size % 16 == 0 the group's 16 tokens (16-aligned) share one
-    // block: a single block-table read serves them all.
-    int64_t off[PA_TPG];
-    if constexpr (BLK16) {
-        const int c0 = min(tok0, ctx - 1);
-        const int64_t base = ((int64_t)bt[c0 / bs] * bs + c0 % bs) * Hkv + kvh;
+    const uint32_t row = (uint32_t)Hkv * PA_D;  // elements between consecutive slots
+    const uint16_t* kbase = kc + kvh * PA_D + 8 * kq;
+    const uint16_t* vbase = vc + kvh * PA_D + 8 * rc;
+    // First token of half hh (32 tokens) of this wave; a half is two 16-token
+    // runs, 16-aligned.
+    auto half0 = [&](int hh) { return start + 64 * wave + 32 * hh; };
+    // A run of 16 tokens starting at t0 (wave-uniform), clamped into the
+    // sequence: token t0 + d is token t0c + min(d, ctx - 1 - t0c).  With
+    // block_size % 16 == 0 the run lies in one block, whose block-table entry
+    // run_of reads ahead of its use.
+    struct Run {
+        int t0c, blk;
+    };
+    auto run_of = [&](int t0) {
+        Run r;
+        r.t0c = min(t0, ctx - 1);
+        r.blk = BLK16 ? bt[r.t0c / bs] : 0;
+        return r;
+    };
+    auto slot_of = [&](const Run& r, int d) -> uint32_t {
+        const int c = r.t0c + min(d, ctx - 1 - r.t0c);
+        if constexpr (BLK16)
+            return (uint32_t)(r.blk * bs + c % bs);
+        else
+            return (uint32_t)(bt[c / bs] * bs + c % bs);
+    };
+    // Loads of one half.  K, as the A operand of the score MFMA: lane (kq, rc)
+    // holds 16-byte chunks kq, kq+4, kq+8, kq+12 of token h0 + 16c + rc.  V,
+    // as rows: lane (kq, rc) holds chunk rc of tokens h0 + 16c + 4kq + r.
+    auto issue = [&](v4u (&kx)[8], v4u (&vx)[8], const Run& r0, const Run& r1) {
 #pragma unroll
-        for (int i = 0; i < PA_TPG; ++i) off[i] = (base + (int64_t)(min(tok0 + i, ctx - 1) - c0) * Hkv) * PA_D + 8 * j;
-    } else {
+        for (int c = 0; c < 2; ++c) {
+            const Run& r = c ? r1 : r0;
+            const uint16_t* pk = kbase + (uint64_t)slot_of(r, rc) * row;
 #pragma unroll
-        for (int i = 0; i < PA_TPG; ++i) {
-            const int c = min(tok0 + i, ctx - 1);
-            off[i] = (((int64_t)bt[c / bs] * bs + c % bs) * Hkv + kvh) * PA_D + 8 * j;
+            for (int st = 0; st < 4; ++st) kx[4 * c + st] = *reinterpret_cast<const v4u*>(pk + 32 * st);
         }
-    }
-    // Every K row, then every V row, of the group in flight at once.
-    v4u kb[PA_TPG], vb[PA_TPG];
 #pragma unroll
-    for (int i = 0; i < PA_TPG; ++i) kb[i] = *reinterpret_cast<const v4u*>(kc + off[i]);
+        for (int c = 0; c < 2; ++c) {
+            const Run& r = c ? r1 : r0;
 #pragma unroll
-    for (int i = 0; i < PA_TPG; ++i) vb[i] = *reinterpret_cast<const v4u*>(vc + off[i]);
+            for (int i = 0; i < 4; ++i)
+                vx[4 * c + i] = *reinterpret_cast<const v4u*>(vbase + (uint64_t)slot_of(r, 4 * kq + i) * row);
+        }
+    };
 
-    // Query heads kvh*G .. kvh*G+G-1, dims 8j..8j+7, scaled into base 2.
-    float qv[G][8];
+    // B operand of the score MFMA: q of head rc (zero past the group's G
+    // heads), 8 dims per k-octet in the chunk order of the K operand.  Loaded
+    // first and unconditionally (a clamped head, then zeroed), so that the
+    // first half's waits leave the second half's loads in flight.
+    v8bf qb[4];
 #pragma unroll
-    for (int h = 0; h < G; ++h) {
-        const v4u w = *reinterpret_cast<const v4u*>(q + (int64_t)b * q_row + (int64_t)(kvh * G + h) * PA_D + 8 * j);
-        float f[8];
-        bf16x8_to_f32(w, f);
-#pragma unroll
-        for (int d = 0; d < 8; ++d) qv[h][d] = f[d] * qscale;
+    for (int st = 0; st < 4; ++st) {
+        v4u w = *reinterpret_cast<const v4u*>(q + (int64_t)b * q_row + (int64_t)(kvh * G + min(rc, G - 1)) * PA_D +
+                                              8 * (kq + 4 * st));
+        if (rc >= G) w = v4u{0u, 0u, 0u, 0u};
+        qb[st] = __builtin_bit_cast(v8bf, w);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    v4u ka[8], va[8], kb[8], vb[8];
+    {
+        const Run a0 = run_of(half0(0)), a1 = run_of(half0(0) + 16);
+        const Run b0 = run_of(half0(1)), b1 = run_of(half0(1) + 16);
+        issue(ka, va, a0, a1);
+        __builtin_amdgcn_sched_barrier(0);
+        issue(kb, vb, b0, b1);
+        __builtin_amdgcn_sched_barrier(0);
     }
 
-    // Scores of the group's tokens (reduced over its 16 lanes), then one
-    // softmax state per head: m = max, l = sum 2^(s - m), o = sum 2^(s - m) v.
-    float sc[PA_TPG][G];
+    // Softmax state of head rc (the same in the four k-octet rows): running
+    // max m (raw score units), partial sum l over this lane's tokens.  Output
+    // accumulators: tile t holds O[head 4kq + r][dim 8rc + t].
+    float m = -__builtin_inff(), l = 0.0f;
+    v4f acc[8];
 #pragma unroll
-    for (int i = 0; i < PA_TPG; ++i) {
-        float kf[8];
-        bf16x8_to_f32(kb[i], kf);
-        const bool live = tok0 + i < end;
+    for (int t = 0; t < 8; ++t) acc[t] = v4f{0.f, 0.f, 0.f, 0.f};
+
+    auto compute = [&](const v4u (&kx)[8], const v4u (&vx)[8], int h0) {
+        // Scores S[token h0 + 16c + 4kq + r][head rc].
+        v4f sv[2];
+#pragma unroll
+        for (int c = 0; c < 2; ++c) {
+            sv[c] = v4f{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int st = 0; st < 4; ++st)
+                sv[c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8bf, kx[4 * c + st]), qb[st],
+                                                                  sv[c], 0, 0, 0);
+        }
+        float sc[8];
+        float mx = -__builtin_inff();
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const int tk = h0 + 16 * (e >> 2) + 4 * kq + (e & 3);
+            sc[e] = tk < end ? sv[e >> 2][e & 3] : -__builtin_inff();
+            mx = fmaxf(mx, sc[e]);
+        }
+        mx = fmaxf(mx, __shfl_xor(mx, 16));
+        mx = fmaxf(mx, __shfl_xor(mx, 32));
+        const float mn = fmaxf(m, mx);
+        // no live token yet: the state stays m = -inf, l = 0, o = 0
+        const bool any = mn != -__builtin_inff();
+        const float off = any ? -mn * qscale : 0.0f;
+        const float corr = any ? __builtin_amdgcn_exp2f(__builtin_fmaf(m, qscale, off)) : 1.0f;
+        m = mn;
+        float p[8], ls = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            p[e] = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[e], qscale, off));
+            ls += p[e];
+        }
+        l = l * corr + ls;
+        // A operand of the output MFMA: P[head rc][token (kq, e)], bf16
+        // (as flash attention rounds P for its P.V product); zero past G.
+        v4u pw;
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+            const v2bf pp = __builtin_convertvector((v2f){p[2 * w], p[2 * w + 1]}, v2bf);
+            pw[w] = rc < G ? __builtin_bit_cast(uint32_t, pp) : 0u;
+        }
+        const v8bf pa = __builtin_bit_cast(v8bf, pw);
+        // Rescale rows 0..G-1 (heads 0..G-1 sit in the kq = 0 lanes; other
+        // rows are unused) when a head's max moved.
+        float cr[G];
+        bool moved = false;
 #pragma unroll
         for (int h = 0; h < G; ++h) {
-            float p = 0.0f;
-#pragma unroll
-            for (int d = 0; d < 8; ++d) p = __builtin_fmaf(qv[h][d], kf[d], p);
-            p = row16_sum(p);
-            sc[i][h] = live ? p : -__builtin_inff();
+            cr[h] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, corr), h));
+            moved |= cr[h] != 1.0f;
         }
-    }
-    float m[G], l[G], o[G][8];
+        if (moved) {
 #pragma unroll
-    for (int h = 0; h < G; ++h) {
-        float mx = sc[0][h];
+            for (int t = 0; t < 8; ++t)
 #pragma unroll
-        for (int i = 1; i < PA_TPG; ++i) mx = fmaxf(mx, sc[i][h]);
-        m[h] = mx;
-        l[h] = 0.0f;
+                for (int h = 0; h < G; ++h) acc[t][h] *= cr[h];
+        }
+        // B operand of tile t: V[token (kq, e)][dim 8rc + t], e = 0..7, from
+        // this lane's 8 rows (an 8 x 8 transpose of bf16 pairs).
 #pragma unroll
-        for (int d = 0; d < 8; ++d) o[h][d] = 0.0f;
-        // a group whose tokens are all past the end keeps m = -inf, l = 0, o = 0
-        const bool any = mx != -__builtin_inff();
+        for (int t = 0; t < 8; ++t) {
+            const uint32_t sel = (t & 1) ? 0x07060302u : 0x05040100u;
+            v4u bw;
 #pragma unroll
-        for (int i = 0; i < PA_TPG; ++i) sc[i][h] = any ? __builtin_amdgcn_exp2f(sc[i][h] - mx) : 0.0f;
-#pragma unroll
-        for (int i = 0; i < PA_TPG; ++i) l[h] += sc[i][h];
-    }
-#pragma unroll
-    for (int i = 0; i < PA_TPG; ++i) {
-        float vf[8];
-        bf16x8_to_f32(vb[i], vf);
-#pragma unroll
-        for (int h = 0; h < G; ++h)
-#pragma unroll
-            for (int d = 0; d < 8; ++d) o[h][d] = __builtin_fmaf(sc[i][h], vf[d], o[h][d]);
-    }
+            for (int w = 0; w < 4; ++w) bw[w] = __builtin_amdgcn_perm(vx[2 * w + 1][t >> 1], vx[2 * w][t >> 1], sel);
+            acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa, __builtin_bit_cast(v8bf, bw), acc[t], 0, 0, 0);
+        }
+    };
 
-    // Merge the 16 group states of the workgroup.
-    const int gs = wave * 4 + g;
-#pragma unroll
-    for (int h = 0; h < G; ++h) {
-        if (j == 0) {
-            sm_m[gs][h] = m[h];
-            sm_l[gs][h] = l[h];
+    compute(ka, va, half0(0));
+    compute(kb, vb, half0(1));
+
+    // Merge the four wave states of the workgroup.
+    l += __shfl_xor(l, 16);
+    l += __shfl_xor(l, 32);
+    if (kq == 0) {
+        if (rc < G) {
+            sm_m[wave][rc] = m;
+            sm_l[wave][rc] = l;
         }
 #pragma unroll
-        for (int d = 0; d < 8; ++d) sm_o[gs][h][8 * j + d] = o[h][d];
+        for (int h = 0; h < G; ++h) {
+            *reinterpret_cast<v4f*>(&sm_o[wave][h][8 * rc]) = v4f{acc[0][h], acc[1][h], acc[2][h], acc[3][h]};
+            *reinterpret_cast<v4f*>(&sm_o[wave][h][8 * rc + 4]) = v4f{acc[4][h], acc[5][h], acc[6][h], acc[7][h]};
+        }
     }
     __syncthreads();
-    for (int e = t; e < G * PA_D; e += PA_THREADS) {
+    for (int e = threadIdx.x; e < G * PA_D; e += PA_THREADS) {
         const int h = e / PA_D, d = e % PA_D;
         float M = -__builtin_inff();
 #pragma unroll
-        for (int k = 0; k < 16; ++k) M = fmaxf(M, sm_m[k][h]);
-        float L = 0.0f, O = 0.0f;
+        for (int w = 0; w < 4; ++w) M = fmaxf(M, sm_m[w][h]);
+        float Lw = 0.0f, O = 0.0f;
 #pragma unroll
-        for (int k = 0; k < 16; ++k) {
-            const float w = sm_m[k][h] == -__builtin_inff() ? 0.0f : __builtin_amdgcn_exp2f(sm_m[k][h] - M);
-            L = __builtin_fmaf(w, sm_l[k][h], L);
-            O = __builtin_fmaf(w, sm_o[k][h][d], O);
+        for (int w = 0; w < 4; ++w) {
+            const float wt = sm_m[w][h] == -__builtin_inff() ? 0.0f : __builtin_amdgcn_exp2f((sm_m[w][h] - M) * qscale);
+            Lw = __builtin_fmaf(wt, sm_l[w][h], Lw);
+            O = __builtin_fmaf(wt, sm_o[w][h][d], O);
         }
         const int hq = kvh * G + h;
         if (S == 1) {
-            out[((int64_t)b * Hq + hq) * PA_D + d] = (uint16_t)f32_to_bf16_rne(O / L);
+            out[((int64_t)b * Hq + hq) * PA_D + d] = (uint16_t)f32_to_bf16_rne(O / Lw);
         } else {
             const int64_t ps = ((int64_t)b * Hq + hq) * S + s;
             part_o[ps * PA_D + d] = O;
             if (d == 0) {
-                part_ml[ps * 2] = M;
-                part_ml[ps * 2 + 1] = L;
+                part_ml[ps * 2] = M * qscale;  // base-2 units for the merge
+                part_ml[ps * 2 + 1] = Lw;
             }
         }
     }
@@ -285,7 +341,8 @@ extern "C" int nv4_paged_decode_attention(const void* q, int64_t q_row_stride, c
     using namespace nv4;
     if (!q || !k_cache || !v_cache || !block_tables || !context_lens || !out || !workspace) return NV4_E_NULL;
     if (D != PA_D || B < 1 || Hkv < 1 || Hq < 1 || Hq % Hkv || block_size < 1 || max_blocks < 1 ||
-        max_context < 1 || max_context > max_blocks * block_size || B > 65535 || Hkv > 65535 ||
+        max_context < 1 || max_context > max_blocks * block_size || max_context > (1 << 30) || B > 65535 ||
+        Hkv > 65535 ||
         q_row_stride < Hq * D)
         return NV4_E_SHAPE;
     const int64_t G = Hq / Hkv;
