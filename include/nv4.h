@@ -25,10 +25,11 @@
  *                          MFMA-tiled order (no counterpart in the reference,
  *                          whose kernels read [N,K/2]; W4A4Linear keeps the
  *                          reference layout in its state dict)
- *   nv4_w4a16_gemm, nv4_w4a16_gemm_ws <- nanovllm/layers/linear_w4a16.py:11
+ *   nv4_w4a16_gemm, nv4_w4a16_gemm_ws, nv4_w4a16_dequant <- nanovllm/layers/linear_w4a16.py:11
  *                          tl_dequant_matmul_w4a16 (called from W4A16Linear.forward
  *                          :128-148; the reference splits K 8 ways with bf16 atomics,
- *                          the _ws form splits K into 1024-deep fp32 partials)
+ *                          the _ws form splits K into 1024-deep fp32 partials, and
+ *                          prefill-sized M dequantizes once for a library GEMM)
  *   nv4_paged_decode_attention <- flash_attn_with_kvcache in the decode branch of
  *                          nanovllm/layers/attention.py:72-74 (caller of the hot path)
  *   nv4_rmsnorm         <- RMSNorm.rms_forward / add_rms_forward,
@@ -180,6 +181,17 @@ int nv4_w4a16_gemm(const void* x, int x_dtype, const int32_t* qweight, const int
 int nv4_w4a16_gemm_ws(const void* x, int x_dtype, const int32_t* qweight, const int32_t* qzeros,
                       const void* scales, void* out, int out_dtype, float* workspace, int64_t workspace_bytes,
                       int64_t M, int64_t N, int64_t K, int group, void* stream);
+
+/*
+ * Dense dequantization of a GPTQ weight, for prefill-sized M where the
+ * product then runs as a library GEMM x[M,K] @ w[K,N]:
+ *   w[k][n] = cvt(float(q[k][n] - z[k/128][n] - 1) * s),   w row-major [K, N],
+ * with the rounding of nv4_w4a16_gemm: bf16 (w_dtype NV4_BF16) takes the
+ * scale rounded to bf16 first, fp16 takes it as is.  qweight, scales and w
+ * 16-byte aligned; N % 8 == 0, K % 128 == 0, group 128.
+ */
+int nv4_w4a16_dequant(const int32_t* qweight, const int32_t* qzeros, const void* scales, void* w, int w_dtype,
+                      int64_t N, int64_t K, int group, void* stream);
 
 /*
  * Paged decode attention (one new token per sequence; GQA).

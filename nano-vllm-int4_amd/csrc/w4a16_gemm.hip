@@ -339,8 +339,70 @@ hipError_t dispatch(const void* x, const int32_t* qw, const int32_t* qz, const v
     return launch<4, XF, OF>(x, qw, qz, sc, out, M, N, K, st);
 }
 
+// ----------------------------------------------------------------------------
+// Dequantization to a dense [K, N] weight for prefill-sized M (the product
+// then runs as a plain library GEMM).  Thread = one qweight row segment of 8
+// columns (8 words, 32 bytes): it writes the 8 k-rows of those columns, 16
+// bytes per row, with the same per-element rounding as the GEMM kernels:
+// w[k][n] = cvt(float(q - z - 1) * scale).
+// ----------------------------------------------------------------------------
+template <bool F16>
+__global__ void __launch_bounds__(256)
+w4a16_dequant(const int32_t* __restrict__ qweight, const int32_t* __restrict__ qzeros,
+              const uint16_t* __restrict__ scales, uint16_t* __restrict__ w, int N, int K) {
+    using TR = W16Traits<F16>;
+    const int nb = N >> 3;
+    const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (idx >= (int64_t)(K >> 3) * nb) return;
+    const int k8 = (int)(idx / nb), c8 = (int)(idx % nb);
+    const int n0 = c8 * 8, g = k8 >> 4;  // 16 qweight rows per 128-deep group
+    const v4u q0 = *reinterpret_cast<const v4u*>(qweight + (int64_t)k8 * N + n0);
+    const v4u q1 = *reinterpret_cast<const v4u*>(qweight + (int64_t)k8 * N + n0 + 4);
+    const uint32_t zw = (uint32_t)qzeros[(int64_t)g * nb + c8];
+    const v4u sv = *reinterpret_cast<const v4u*>(scales + (int64_t)g * N + n0);
+    const uint32_t qw[8] = {q0[0], q0[1], q0[2], q0[3], q1[0], q1[1], q1[2], q1[3]};
+    float sc[8];
+    int zp1[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        sc[j] = TR::scale_of((uint16_t)(sv[j >> 1] >> (16 * (j & 1))));
+        zp1[j] = (int)((zw >> (4 * j)) & 15u) + 1;
+    }
+#pragma unroll
+    for (int r = 0; r < 8; ++r) {
+        uint32_t h[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) h[j] = TR::cvt((float)((int)((qw[j] >> (4 * r)) & 15u) - zp1[j]) * sc[j]);
+        const v4u o = {h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16), h[6] | (h[7] << 16)};
+        *reinterpret_cast<v4u*>(w + (int64_t)(8 * k8 + r) * N + n0) = o;
+    }
+}
+
 }  // namespace
 }  // namespace nv4
+
+extern "C" int nv4_w4a16_dequant(const int32_t* qweight, const int32_t* qzeros, const void* scales, void* w,
+                                 int w_dtype, int64_t N, int64_t K, int group, void* stream) {
+    using namespace nv4;
+    if (!qweight || !qzeros || !scales || !w) return NV4_E_NULL;
+    if (w_dtype != NV4_BF16 && w_dtype != NV4_FP16) return NV4_E_DTYPE;
+    if (group != 128) return NV4_E_GROUP;
+    if (N < 8 || N % 8 || K < 128 || K % 128 || N > 0x7fffffffLL || K > (1LL << 24)) return NV4_E_SHAPE;
+    const int64_t threads = (K / 8) * (N / 8);
+    if ((threads + 255) / 256 > 0x7fffffffLL) return NV4_E_SHAPE;
+    if (reinterpret_cast<uintptr_t>(qweight) % 16 || reinterpret_cast<uintptr_t>(qzeros) % 4 ||
+        reinterpret_cast<uintptr_t>(scales) % 16 || reinterpret_cast<uintptr_t>(w) % 16)
+        return NV4_E_ALIGN;
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    const dim3 grid((unsigned)((threads + 255) / 256));
+    if (w_dtype == NV4_FP16)
+        hipLaunchKernelGGL((w4a16_dequant<true>), grid, dim3(256), 0, st, qweight, qzeros,
+                           static_cast<const uint16_t*>(scales), static_cast<uint16_t*>(w), (int)N, (int)K);
+    else
+        hipLaunchKernelGGL((w4a16_dequant<false>), grid, dim3(256), 0, st, qweight, qzeros,
+                           static_cast<const uint16_t*>(scales), static_cast<uint16_t*>(w), (int)N, (int)K);
+    return (int)hipGetLastError();
+}
 
 extern "C" int nv4_w4a16_gemm(const void* x, int x_dtype, const int32_t* qweight, const int32_t* qzeros,
                               const void* scales, void* out, int out_dtype,

@@ -38,6 +38,7 @@ SIGNATURES = {
     "nv4_w4a4_untile_weights": ([_P, _P, _I64, _I64, _P], _I),
     "nv4_w4a16_gemm": ([_P, _I, _P, _P, _P, _P, _I, _I64, _I64, _I64, _I, _P], _I),
     "nv4_w4a16_gemm_ws": ([_P, _I, _P, _P, _P, _P, _I, _P, _I64, _I64, _I64, _I64, _I, _P], _I),
+    "nv4_w4a16_dequant": ([_P, _P, _P, _P, _I, _I64, _I64, _I, _P], _I),
     "nv4_paged_decode_attention": ([_P, _I64, _P, _P, _P, _I64, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64,
                                     _I64, ctypes.c_float, _P], _I),
     "nv4_rmsnorm": ([_P, _P, _P, _P, _P, _I64, _I64, ctypes.c_float, _P], _I),

@@ -12,7 +12,10 @@ on scheduling.  FP16 activations are accepted as well (output fp16).
 At decode sizes (M <= 64) the wrapper takes the split-K form
 (``nv4_w4a16_gemm_ws``): 64-column workgroups per 1024-deep K slice writing
 fp32 partials into a workspace from torch's caching allocator, added in slice
-order by a second launch -- still deterministic, and graph-capturable.
+order by a second launch -- still deterministic, and graph-capturable.  At
+prefill sizes (M > 64) the weight is dequantized once into a dense [K, N]
+tensor (``nv4_w4a16_dequant``, the same per-element rounding) and the
+product runs as a library GEMM (torch.mm on hipBLASLt, fp32 accumulation).
 """
 from __future__ import annotations
 
@@ -24,6 +27,31 @@ from .. import _lib
 
 _DT = {torch.bfloat16: _lib.BF16, torch.float16: _lib.FP16}
 SLICE_K = 1024  # K per partial of the decode-size split
+
+
+def dequant_w4a16(qweight, qzeros, scales, dtype=torch.bfloat16, group_size=128):
+    """GPTQ weight -> dense [K, N] in ``dtype`` (bf16 or fp16), rounded as the
+    W4A16 GEMMs round each dequantized weight."""
+    if qweight.dtype != torch.int32 or qzeros.dtype != torch.int32 or scales.dtype != torch.float16:
+        raise TypeError("Expected int32 qweight/qzeros and fp16 scales")
+    if dtype not in _DT or qweight.ndim != 2:
+        raise ValueError("Expected qweight [K/8, N] and a BF16 or FP16 target dtype")
+    K, N = qweight.shape[0] * 8, qweight.shape[1]
+    if group_size != 128 or K % 128 or N % 8:
+        raise ValueError("Require group_size 128, K divisible by 128, N divisible by 8")
+    if tuple(qzeros.shape) != (K // 128, N // 8) or tuple(scales.shape) != (K // 128, N):
+        raise ValueError("Require qzeros [K/128, N/8] and scales [K/128, N]")
+    if any(not t.is_cuda or not t.is_contiguous() or t.device != qweight.device for t in (qweight, qzeros, scales)):
+        raise ValueError("All tensors must be contiguous on one CUDA device")
+    w = torch.empty((K, N), dtype=dtype, device=qweight.device)
+    lib = _lib.load()
+    stream = torch.cuda.current_stream(qweight.device).cuda_stream
+    with torch.cuda.device(qweight.device):
+        rc = lib.nv4_w4a16_dequant(ctypes.c_void_p(qweight.data_ptr()), ctypes.c_void_p(qzeros.data_ptr()),
+                                   ctypes.c_void_p(scales.data_ptr()), ctypes.c_void_p(w.data_ptr()), _DT[dtype],
+                                   N, K, group_size, ctypes.c_void_p(stream))
+    _lib.check(rc, "dequant_w4a16")
+    return w
 
 
 def dequant_matmul_w4a16(x, qweight, qzeros, scales, group_size=128, out=None):
@@ -59,9 +87,15 @@ def dequant_matmul_w4a16(x, qweight, qzeros, scales, group_size=128, out=None):
                                        _DT[out.dtype], ctypes.c_void_p(ws.data_ptr()), ws.numel() * 4, M, N, K,
                                        group_size, ctypes.c_void_p(stream))
         else:
-            rc = lib.nv4_w4a16_gemm(ctypes.c_void_p(x.data_ptr()), _DT[x.dtype],
-                                    ctypes.c_void_p(qweight.data_ptr()), ctypes.c_void_p(qzeros.data_ptr()),
-                                    ctypes.c_void_p(scales.data_ptr()), ctypes.c_void_p(out.data_ptr()),
-                                    _DT[out.dtype], M, N, K, group_size, ctypes.c_void_p(stream))
+            w = torch.empty((K, N), dtype=x.dtype, device=x.device)
+            rc = lib.nv4_w4a16_dequant(ctypes.c_void_p(qweight.data_ptr()), ctypes.c_void_p(qzeros.data_ptr()),
+                                       ctypes.c_void_p(scales.data_ptr()), ctypes.c_void_p(w.data_ptr()),
+                                       _DT[x.dtype], N, K, group_size, ctypes.c_void_p(stream))
+            _lib.check(rc, "dequant_matmul_w4a16")
+            if out.dtype == x.dtype:
+                torch.mm(x, w, out=out)
+            else:
+                out.copy_(torch.mm(x, w))
+            return out
     _lib.check(rc, "dequant_matmul_w4a16")
     return out

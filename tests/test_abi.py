@@ -73,6 +73,14 @@ def test_w4a16_and_linear_rejections():
     assert f(P(A16), 0, P(A16), P(A16), P(A16), P(A16), 0, 4, 64, 4096, 64, None) == _lib.NV4_E_GROUP
     assert f(P(A16), 0, P(A16), P(A16), P(A16), P(A16), 0, 4, 60, 4096, 128, None) == _lib.NV4_E_SHAPE
     assert f(None, 0, *ok[:3], P(A16), 0, 4, 64, 4096, 128, None) == _lib.NV4_E_NULL
+    d = _lib.load().nv4_w4a16_dequant
+    # qweight, qzeros, scales, w, w_dtype, N, K, group
+    assert d(None, P(A16), P(A16), P(A16), 0, 64, 4096, 128, None) == _lib.NV4_E_NULL
+    assert d(P(A16), P(A16), P(A16), P(A16), 2, 64, 4096, 128, None) == _lib.NV4_E_DTYPE   # fp32 target
+    assert d(P(A16), P(A16), P(A16), P(A16), 0, 64, 4096, 64, None) == _lib.NV4_E_GROUP
+    assert d(P(A16), P(A16), P(A16), P(A16), 0, 60, 4096, 128, None) == _lib.NV4_E_SHAPE   # N % 8
+    assert d(P(A16), P(A16), P(A16), P(A16), 0, 64, 4000, 128, None) == _lib.NV4_E_SHAPE   # K % 128
+    assert d(P(A16), P(A16), P(A16 + 8), P(A16), 0, 64, 4096, 128, None) == _lib.NV4_E_ALIGN
     g = _lib.load().nv4_w4a4_linear
     assert g(*([P(A16)] * 7), 4, 64, 2048, None) == _lib.NV4_E_SHAPE
     assert g(None, *([P(A16)] * 6), 4, 64, 4096, None) == _lib.NV4_E_NULL

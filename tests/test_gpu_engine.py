@@ -98,13 +98,18 @@ def test_w4a4_first_projection_matches_oracle(engines):
     assert np.array_equal(bf16_bits(seen["qkv"]), ref)
 
 
-def test_w4a16_fused_projections_equal_separate(engines):
+@pytest.mark.parametrize("n", [48, 90])
+def test_w4a16_fused_projections_equal_separate(engines, n):
+    """Fused q/k/v and gate/up (N-concatenated GPTQ tensors) against the
+    separate projections.  Up to 64 rows the W4A16 GEMM is this library's
+    kernel, whose per-element arithmetic does not depend on N: bit-exact.
+    Above, the product is a library GEMM on the dequantized weight, whose
+    reduction order may change with N: relative RMS difference <= 1e-2."""
     eng = engines[2]
-    ids = seeded_prompts(1, 90, 1024, seed=21)[0]
+    ids = seeded_prompts(1, n, 1024, seed=21)[0]
 
     def logits():
         from nv4.utils.context import reset_context, set_context
-        n = len(ids)
         cu = torch.tensor([0, n], dtype=torch.int32, device=DEV)
         slots = torch.tensor(eng._slots(3, 0, n), dtype=torch.int32, device=DEV)
         with torch.inference_mode():
@@ -127,7 +132,12 @@ def test_w4a16_fused_projections_equal_separate(engines):
             object.__setattr__(l.self_attn, "qkv_fused", q)
             object.__setattr__(l.mlp, "gate_up_fused", gu)
     torch.cuda.synchronize()
-    assert torch.isfinite(fused).all() and torch.equal(fused, separate)
+    assert torch.isfinite(fused).all()
+    if n <= 64:
+        assert torch.equal(fused, separate)
+    else:
+        rel = ((fused.float() - separate.float()).norm() / separate.float().norm()).item()
+        assert rel <= 1e-2, f"relative RMS difference {rel:.3e}"
 
 
 @pytest.mark.parametrize("which", ["bf16", "w4a4", "w4a16"])

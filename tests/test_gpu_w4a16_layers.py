@@ -2,7 +2,9 @@
 
 K3 has no reference test (nanovllm/layers/linear_w4a16.py is exercised by no
 script) and the reference kernel sums split-K partials with BF16 atomics in a
-nondeterministic order, so its exact bits are unpinnable.  The bar here is
+nondeterministic order, so its exact bits are unpinnable.  The dense
+dequantization used for prefill-sized M (nv4_w4a16_dequant) is bit-exact with
+the oracle's rounded dequantized weights.  The GEMM bar here is
 the BF16/FP16 GEMM tolerance: every output within 1e-2 relative of the float64
 product of the activations and the oracle's dequantised weights, measured as
 |out - ref| <= 1e-2 * max(|ref|, rms(ref)) elementwise, plus bit-exact
@@ -19,6 +21,7 @@ import torch
 import oracle
 from conftest import bf16_bits, f16_bits
 from nv4 import W4A4Linear, W4A16Linear, dequant_matmul_w4a16
+from nv4.kernels import dequant_w4a16
 from nv4 import workloads as W
 
 pytestmark = pytest.mark.gpu
@@ -35,7 +38,7 @@ def check_close(out, ref):
 
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
-@pytest.mark.parametrize("M", [1, 8, 32, 33, 64, 100])
+@pytest.mark.parametrize("M", [1, 8, 32, 33, 64, 65, 100, 300])
 def test_k3_w4a16_qkv(M, dtype):
     print(f"[k3] M={M} dtype={dtype}", flush=True)
     case = W.w4a16_case(M, dtype=dtype)
@@ -50,6 +53,19 @@ def test_k3_w4a16_qkv(M, dtype):
     assert out.dtype == dtype and out.shape == (M, 6144)
     check_close(out, ref)
     assert torch.equal(out, out2)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("N,K", [(6144, 4096), (136, 512), (4096, 12288)])
+def test_dense_dequant_bit_exact(N, K, dtype):
+    case = W.w4a16_case(1, N=N, K=K, dtype=dtype)
+    xd = oracle.X_FP16 if dtype == torch.float16 else oracle.X_BF16
+    ref = oracle.w4a16_dequant(case.qweight.numpy(), case.qzeros.numpy(), case.scales.numpy().view(np.uint16),
+                               x_dtype=xd)
+    w = dequant_w4a16(*(t.to(DEV) for t in (case.qweight, case.qzeros, case.scales)), dtype=dtype)
+    torch.cuda.synchronize()
+    assert w.dtype == dtype and tuple(w.shape) == (K, N)
+    assert np.array_equal(w.float().cpu().numpy(), ref.astype(np.float32))
 
 
 @pytest.mark.parametrize("N,K", [(64, 128), (136, 512), (4096, 12288)])
