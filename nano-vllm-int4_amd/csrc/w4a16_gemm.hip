@@ -25,26 +25,92 @@ typedef __bf16 v2bf __attribute__((ext_vector_type(2)));
 
 template <bool FP16>
 struct W16Traits;
+// The eight nibbles of a qweight word as bytes in k order: p0 = q0..q3,
+// p1 = q4..q7 (two byte permutes of the low and high nibbles).
+__device__ __forceinline__ void nibble_bytes(uint32_t w, uint32_t& p0, uint32_t& p1) {
+    const uint32_t lo = w & 0x0F0F0F0Fu, hi = (w >> 4) & 0x0F0F0F0Fu;  // q0 q2 q4 q6 / q1 q3 q5 q7
+    p0 = __builtin_amdgcn_perm(hi, lo, 0x05010400u);
+    p1 = __builtin_amdgcn_perm(hi, lo, 0x07030602u);
+}
+
 template <>
 struct W16Traits<false> {
     typedef v8bf vec;
     typedef __bf16 elem;
+    struct deq {
+        float s, nzs;  // bf16-rounded scale, -(z+1) * s (exact in fp32)
+    };
     __device__ static inline uint16_t cvt(float f) { return (uint16_t)f32_to_bf16_rne(f); }
     __device__ static inline float scale_of(uint16_t s_f16) {
         // fp16 -> fp32 (exact) -> bf16 (rne), as the reference copies fp16
         // scales into a bf16 buffer.
         return bf16_to_f32(f32_to_bf16_rne((float)__builtin_bit_cast(_Float16, s_f16)));
     }
+    __device__ static inline deq prep(uint16_t s_f16, int zp1) {
+        const float s = scale_of(s_f16);
+        return {s, -((float)zp1 * s)};
+    }
+    // bf16 of (q - z - 1) * s for the word's 8 nibbles: fma(q, s, -(z+1) s)
+    // is exact (every term is a small integer times a bf16), then one
+    // rounding per value, two values per v_cvt_pk_bf16_f32.
+    __device__ static inline vec dequant8(uint32_t w, const deq& d) {
+        uint32_t p0, p1;
+        nibble_bytes(w, p0, p1);
+        float v[8];
+        v[0] = __builtin_fmaf((float)(p0 & 0xffu), d.s, d.nzs);
+        v[1] = __builtin_fmaf((float)((p0 >> 8) & 0xffu), d.s, d.nzs);
+        v[2] = __builtin_fmaf((float)((p0 >> 16) & 0xffu), d.s, d.nzs);
+        v[3] = __builtin_fmaf((float)(p0 >> 24), d.s, d.nzs);
+        v[4] = __builtin_fmaf((float)(p1 & 0xffu), d.s, d.nzs);
+        v[5] = __builtin_fmaf((float)((p1 >> 8) & 0xffu), d.s, d.nzs);
+        v[6] = __builtin_fmaf((float)((p1 >> 16) & 0xffu), d.s, d.nzs);
+        v[7] = __builtin_fmaf((float)(p1 >> 24), d.s, d.nzs);
+        vec r;
+#pragma unroll
+        for (int e = 0; e < 8; e += 2) {
+            const v2bf b = __builtin_convertvector((v2f){v[e], v[e + 1]}, v2bf);
+            r[e] = b[0];
+            r[e + 1] = b[1];
+        }
+        return r;
+    }
 };
 template <>
 struct W16Traits<true> {
     typedef v8h vec;
     typedef _Float16 elem;
+    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+    struct deq {
+        h2 s, nmz;  // (s, s) and (-(1024 + z + 1), ...) in fp16
+    };
     __device__ static inline uint16_t cvt(float f) {
         return __builtin_bit_cast(uint16_t, (_Float16)f);
     }
     __device__ static inline float scale_of(uint16_t s_f16) {
         return (float)__builtin_bit_cast(_Float16, s_f16);
+    }
+    __device__ static inline deq prep(uint16_t s_f16, int zp1) {
+        const _Float16 s = __builtin_bit_cast(_Float16, s_f16);
+        const _Float16 m = (_Float16)(-(1024 + zp1));  // exact: an integer below 2048
+        return {h2{s, s}, h2{m, m}};
+    }
+    // fp16 of (q - z - 1) * s for the word's 8 nibbles: each half is built
+    // as the fp16 1024 + q (bit pattern 0x6400 | q), (1024 + q) - (1024 + z
+    // + 1) is exact, and one packed multiply rounds (q - z - 1) * s once.
+    __device__ static inline vec dequant8(uint32_t w, const deq& d) {
+        uint32_t p0, p1;
+        nibble_bytes(w, p0, p1);
+        const uint32_t m = 0x64646464u;
+        const uint32_t h[4] = {__builtin_amdgcn_perm(m, p0, 0x04010400u), __builtin_amdgcn_perm(m, p0, 0x04030402u),
+                               __builtin_amdgcn_perm(m, p1, 0x04010400u), __builtin_amdgcn_perm(m, p1, 0x04030402u)};
+        vec r;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const h2 v = (__builtin_bit_cast(h2, h[e]) + d.nmz) * d.s;
+            r[2 * e] = v[0];
+            r[2 * e + 1] = v[1];
+        }
+        return r;
     }
 };
 
@@ -134,14 +200,16 @@ k3_w4a16(const uint16_t* __restrict__ x, const int32_t* __restrict__ qweight,
 //  * activations: the slice's rows (ROWS x 1024 bf16) are copied into LDS in
 //    whole lines once per workgroup and read back as MFMA A operands
 //    (16-byte chunks XOR-swizzled by row);
-//  * dequantization: v = fma(float(q), s, -(z+1) s) -- exactly (q - z - 1) s,
-//    since both products are exact in fp32 -- then one rounding to bf16 (two
-//    values per v_cvt_pk_bf16_f32) or fp16, as the reference rounds the
-//    dequantized weight;
-//  * the four waves take interleaved 32-k steps of the slice; their fp32
-//    tiles are added in wave order in LDS, and the slice's [M, N] fp32 partial
-//    goes to the workspace; a second kernel adds the slices in order and
-//    rounds once (no atomics, same bits on every run).
+//  * dequantization (W16Traits::dequant8): two byte permutes put a word's
+//    nibbles in k order as bytes; bf16 takes fma(q, s, -(z+1) s) (exact in
+//    fp32) and rounds once per value, fp16 builds each half as 1024 + q
+//    (bit pattern 0x6400 | q) and rounds (q - z - 1) * s once with packed
+//    fp16 arithmetic -- the reference's rounding of the dequantized weight;
+//  * wave w takes the 8 consecutive 32-k steps 8w .. 8w+7 of the slice (two
+//    groups, so two scale/zero preparations per column); the four waves'
+//    fp32 tiles are added in wave order in LDS, and the slice's [M, N] fp32
+//    partial goes to the workspace; a second kernel adds the slices in order
+//    and rounds once (no atomics, same bits on every run).
 // ----------------------------------------------------------------------------
 constexpr int K3_KS = 1024;  // k per slice
 constexpr int K3_NB = 64;    // columns per workgroup
@@ -167,19 +235,21 @@ k3_dec(const uint16_t* __restrict__ x, const int32_t* __restrict__ qweight, cons
     const int ncol = min(n0 + 4 * c4, N - 4);
 
     // ---- weights, zero points and scales of the slice: all loads first.
-    const int nst = (steps + 3 - wave) >> 2;  // steps of this wave (<= 8)
+    // Wave w takes the 8 consecutive 32-k steps 8w .. 8w+7 (groups 2w, 2w+1
+    // of the slice).
+    const int nst = min(8, steps - 8 * wave);  // steps of this wave (may be <= 0)
     v4u wq[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-        const int st = min(wave + 4 * i, steps - 1);
+        const int st = max(0, min(8 * wave + i, steps - 1));
         const int64_t row = (int64_t)((ks >> 3) + st * 4 + kq);
         wq[i] = *reinterpret_cast<const v4u*>(qweight + row * N + ncol);
     }
-    uint32_t zw[8];
-    uint2 sv[8];
+    uint32_t zw[2];
+    uint2 sv[2];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {  // group of step wave + 4 i is i (4 steps per group)
-        const int g = (ks >> 7) + min(i, (klen >> 7) - 1);
+    for (int i = 0; i < 2; ++i) {
+        const int g = (ks >> 7) + max(0, min(2 * wave + i, (klen >> 7) - 1));
         zw[i] = (uint32_t)qzeros[(int64_t)g * (N >> 3) + (ncol >> 3)];
         sv[i] = *reinterpret_cast<const uint2*>(scales + (int64_t)g * N + ncol);
     }
@@ -210,38 +280,23 @@ k3_dec(const uint16_t* __restrict__ x, const int32_t* __restrict__ qweight, cons
 #pragma unroll
         for (int j = 0; j < 4; ++j) acc[mb][j] = v4f{0.f, 0.f, 0.f, 0.f};
     const int zsh = 16 * (c4 & 1);  // the quad's 4 zero-point nibbles within its qzeros word
+    // Per group and column: the scale (as the activation dtype rounds it)
+    // and the zero-point offset.
+    typename TR::deq dq[2][4];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const uint32_t h = ((j < 2 ? sv[i].x : sv[i].y) >> (16 * (j & 1))) & 0xffffu;
+            dq[i][j] = TR::prep((uint16_t)h, (int)((zw[i] >> (zsh + 4 * j)) & 15u) + 1);
+        }
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
         if (i < nst) {  // uniform over the wave
-            const int st = wave + 4 * i;
-            float s[4], nzs[4];
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const uint32_t h = ((j < 2 ? sv[i].x : sv[i].y) >> (16 * (j & 1))) & 0xffffu;
-                s[j] = TR::scale_of((uint16_t)h);
-                const float zp1 = (float)(((zw[i] >> (zsh + 4 * j)) & 15u) + 1u);
-                nzs[j] = -(zp1 * s[j]);
-            }
+            const int st = 8 * wave + i;
             typename TR::vec bop[4];
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const uint32_t w = wq[i][j];
-                float v[8];
-#pragma unroll
-                for (int e = 0; e < 8; ++e) v[e] = __builtin_fmaf((float)((w >> (4 * e)) & 15u), s[j], nzs[j]);
-                if constexpr (XF16) {
-#pragma unroll
-                    for (int e = 0; e < 8; ++e) bop[j][e] = (_Float16)v[e];
-                } else {
-#pragma unroll
-                    for (int e = 0; e < 8; e += 2) {
-                        const v2f pr = {v[e], v[e + 1]};
-                        const v2bf b = __builtin_convertvector(pr, v2bf);
-                        bop[j][e] = b[0];
-                        bop[j][e + 1] = b[1];
-                    }
-                }
-            }
+            for (int j = 0; j < 4; ++j) bop[j] = TR::dequant8(wq[i][j], dq[i >> 2][j]);
             const int c = st * 4 + kq;  // 16-byte chunk of the k-octet in the slice row
 #pragma unroll
             for (int mb = 0; mb < MB; ++mb) {
