@@ -40,7 +40,7 @@
  *                          nanovllm/layers/attention.py:10-40 (caller of the hot path)
  *   nv4_silu_mul        <- SiluAndMul.forward, nanovllm/layers/activation.py:8-11
  *                          (caller of the hot path)
- *   nv4_gumbel_sample   <- Sampler.forward, nanovllm/layers/sampler.py:5-12
+ *   nv4_gumbel_sample, nv4_gumbel_sample_ws <- Sampler.forward, nanovllm/layers/sampler.py:5-12
  *                          (caller of the hot path); nv4_philox4x32_10 is its
  *                          generator on the host, for known-answer tests
  *   nv4_rmsnorm_rht_quant_pack, nv4_silu_mul_rht_quant_pack <- the producer of
@@ -286,6 +286,16 @@ int nv4_silu_mul_rht_quant_pack(const void* gate_up, const int8_t* signs, int8_t
  */
 int nv4_gumbel_sample(const void* logits, int64_t row_stride, int logits_dtype, const float* temperatures,
                       int64_t B, int64_t V, uint64_t seed, uint64_t offset, int64_t* out, void* stream);
+
+/*
+ * nv4_gumbel_sample split over P = nv4_gumbel_sample_chunks(B, V) workgroups
+ * per row (quad-aligned column chunks) plus a merge launch; returns the same
+ * token ids.  workspace: at least 8*B*P bytes, 4-byte aligned; B <= 65535.
+ */
+int64_t nv4_gumbel_sample_chunks(int64_t B, int64_t V);
+int nv4_gumbel_sample_ws(const void* logits, int64_t row_stride, int logits_dtype, const float* temperatures,
+                         int64_t B, int64_t V, uint64_t seed, uint64_t offset, void* workspace,
+                         int64_t workspace_bytes, int64_t* out, void* stream);
 
 /* Philox4x32-10 of one counter block, computed on the host: out = philox(counter[4], key[2]). */
 void nv4_philox4x32_10(const uint32_t* counter, const uint32_t* key, uint32_t* out);

@@ -4,7 +4,8 @@ The reference (nanovllm/layers/sampler.py:5-12) samples
 ``argmax(softmax(logits / T) / clamp(Exp(1), 1e-10))`` -- the Gumbel-max
 form of drawing from softmax(logits / T) -- with seven torch operations over
 the [B, vocab] logits.  ``gumbel_sample`` draws from the same distribution in
-one pass (``nv4_gumbel_sample``): argmax of ``logits / T - log(E)`` with
+one pass over the logits (``nv4_gumbel_sample_ws``: column chunks of every row
+in parallel, then a merge of their maxima): argmax of ``logits / T - log(E)`` with
 E = -log(U) and U from a counter-based Philox4x32-10 stream keyed by
 (seed, offset), so a step's draws are reproducible.  ``Sampler`` keeps the
 reference's module interface and advances the offset once per call.
@@ -20,9 +21,13 @@ from . import _lib
 
 
 def gumbel_sample(logits: torch.Tensor, temperatures: torch.Tensor, seed: int, offset: int,
-                  out: torch.Tensor | None = None) -> torch.Tensor:
+                  out: torch.Tensor | None = None, split: bool = True) -> torch.Tensor:
     """logits [B, V] (bf16 or fp32, rows may be strided), temperatures fp32 [B]
-    -> int64 [B] token ids."""
+    -> int64 [B] token ids.  ``split`` spreads each row over several
+    workgroups (two launches, nv4_gumbel_sample_ws); the tokens are the same
+    as the one-launch form's."""
+    if logits.shape[0] > 65535:
+        split = False
     if logits.ndim != 2 or logits.stride(1) != 1:
         raise ValueError("logits must be [B, V] with unit column stride")
     if logits.dtype == torch.bfloat16:
@@ -40,11 +45,20 @@ def gumbel_sample(logits: torch.Tensor, temperatures: torch.Tensor, seed: int, o
         raise ValueError("All tensors must be on one CUDA device")
     lib = _lib.load()
     stream = torch.cuda.current_stream(logits.device).cuda_stream
+    seed_c, off_c = ctypes.c_uint64(seed & (2**64 - 1)), ctypes.c_uint64(offset & (2**64 - 1))
     with torch.cuda.device(logits.device):
-        rc = lib.nv4_gumbel_sample(ctypes.c_void_p(logits.data_ptr()), logits.stride(0), code,
-                                   ctypes.c_void_p(temperatures.data_ptr()), B, V,
-                                   ctypes.c_uint64(seed & (2**64 - 1)), ctypes.c_uint64(offset & (2**64 - 1)),
-                                   ctypes.c_void_p(out.data_ptr()), ctypes.c_void_p(stream))
+        if split:
+            # each row spread over several workgroups, partials from torch's caching allocator
+            P = lib.nv4_gumbel_sample_chunks(B, V)
+            ws = torch.empty((2 * B * P,), dtype=torch.int32, device=logits.device)
+            rc = lib.nv4_gumbel_sample_ws(ctypes.c_void_p(logits.data_ptr()), logits.stride(0), code,
+                                          ctypes.c_void_p(temperatures.data_ptr()), B, V, seed_c, off_c,
+                                          ctypes.c_void_p(ws.data_ptr()), ws.numel() * 4,
+                                          ctypes.c_void_p(out.data_ptr()), ctypes.c_void_p(stream))
+        else:
+            rc = lib.nv4_gumbel_sample(ctypes.c_void_p(logits.data_ptr()), logits.stride(0), code,
+                                       ctypes.c_void_p(temperatures.data_ptr()), B, V, seed_c, off_c,
+                                       ctypes.c_void_p(out.data_ptr()), ctypes.c_void_p(stream))
     _lib.check(rc, "gumbel_sample")
     return out
 

@@ -23,7 +23,7 @@ A16 = 0x10000  # a fake, 16-byte aligned device address: never dereferenced belo
 
 def declared():
     text = HEADER.read_text()
-    return sorted(set(re.findall(r"^(?:int|void|const char\*)\s+(nv4_\w+)\(", text, re.M)))
+    return sorted(set(re.findall(r"^(?:int|int64_t|void|const char\*)\s+(nv4_\w+)\(", text, re.M)))
 
 
 def test_every_declared_symbol_is_exported_and_bound():
@@ -103,6 +103,20 @@ def test_paged_decode_attention_rejections():
     assert call(ws_bytes=1000) == _lib.NV4_E_SHAPE
     assert call(q_row=100) == _lib.NV4_E_SHAPE
     assert call(q=P(A16 + 4)) == _lib.NV4_E_ALIGN
+
+
+def test_gumbel_split_rejections():
+    lib = _lib.load()
+    assert lib.nv4_gumbel_sample_chunks(32, 151936) == 64     # 2048 workgroups over 32 rows
+    assert lib.nv4_gumbel_sample_chunks(1, 37) == 1
+    f = lib.nv4_gumbel_sample_ws
+    def call(ws=P(A16), ws_bytes=1 << 20, B=32, V=151936, dtype=0, logits=P(A16)):
+        return f(logits, V, dtype, P(A16), B, V, 1, 0, ws, ws_bytes, P(A16), None)
+    assert call(ws=None) == _lib.NV4_E_NULL
+    assert call(ws_bytes=8 * 32 * 64 - 1) == _lib.NV4_E_SHAPE
+    assert call(B=70000) == _lib.NV4_E_SHAPE
+    assert call(dtype=1) == _lib.NV4_E_DTYPE
+    assert call(ws=P(A16 + 2)) == _lib.NV4_E_ALIGN
 
 
 def test_decoder_ops_rejections():

@@ -94,3 +94,18 @@ def test_determinism_and_module_offset():
     s.offset = 3
     assert torch.equal(s(logits, temps), a) and s.offset == 4
     assert torch.equal(s(logits, temps), c) and s.offset == 5
+
+
+@pytest.mark.parametrize("B,V,dtype", [(32, 151936, torch.bfloat16), (3, 37, torch.float32), (5, 4099, torch.bfloat16),
+                                       (1, 200000, torch.float32)])
+def test_split_form_equals_one_launch(B, V, dtype):
+    """The split form (column chunks in parallel, merged) returns exactly the
+    one-launch form's tokens: same Philox draws, same scores, same ties."""
+    g = torch.Generator().manual_seed(B * 1000 + V)
+    logits = (3 * torch.randn(B, V, generator=g)).to(dtype).to(DEV)
+    logits[0, V // 2] = logits[0].max()  # a tie candidate in row 0
+    temps = (0.5 + torch.rand(B, generator=g)).to(DEV)
+    for off in range(4):
+        a = gumbel_sample(logits, temps, seed=11, offset=off, split=True)
+        b = gumbel_sample(logits, temps, seed=11, offset=off, split=False)
+        assert torch.equal(a, b)
