@@ -21,6 +21,7 @@
  *   nv4_w4a4_linear     <- nanovllm/layers/linear_w4a4.py:27-35 W4A4Linear.forward
  *                          (rht_quant_pack + w4a4_grouped_gemm)
  *   nv4_w4a4_gemm_tiled, nv4_w4a4_linear_tiled, nv4_w4a4_tile_weights,
+ *   nv4_w4a4_gemm_f8,
  *   nv4_w4a4_untile_weights <- the same two operators on weights stored in an
  *                          MFMA-tiled order (no counterpart in the reference,
  *                          whose kernels read [N,K/2]; W4A4Linear keeps the
@@ -151,6 +152,20 @@ int nv4_w4a4_gemm_tiled(const int8_t* a, const int8_t* w_tiled, const void* sa, 
 int nv4_w4a4_linear_tiled(const void* x, const int8_t* signs, const int8_t* w_tiled, const void* sw,
                           void* out, int8_t* a_packed, void* a_scale,
                           int64_t M, int64_t N, int64_t K, void* stream);
+
+/*
+ * nv4_w4a4_gemm (w_tiled = 0) / nv4_w4a4_gemm_tiled (w_tiled = 1) for
+ * prefill-sized M on the fp8 matrix cores: the INT4 codes of both operands
+ * are first written as fp8 (e4m3) bytes, one per code, into the caller's
+ * workspace (A [M,K] then W [N,K]; workspace_bytes >= (M + N) * K, 16-byte
+ * aligned), then multiplied with v_mfma_f32_32x32x64_f8f6f4.  Every group dot
+ * is a small integer, exact in fp32, so the results are bit-identical to
+ * nv4_w4a4_gemm.  Same argument rules as nv4_w4a4_gemm; the workspace is
+ * overwritten, and calls sharing one workspace must be stream-ordered.
+ */
+int nv4_w4a4_gemm_f8(const int8_t* a, const int8_t* w, int w_tiled, const void* sa, const void* sw,
+                     int sw_grouped, void* out, int out_fp32, int64_t M, int64_t N, int64_t K,
+                     void* workspace, int64_t workspace_bytes, void* stream);
 
 /*
  * W4A16 GEMM with GPTQ weights (zero-point convention w = (q - z - 1) * s).

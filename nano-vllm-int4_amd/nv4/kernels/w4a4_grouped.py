@@ -9,8 +9,9 @@ form), ``GroupedConfig``/``best_grouped_config`` keep :21-28/:94-101.
 Each output element is, for g in order, ``total = fmaf(float(dot_g),
 sa[m,g]*sw[n,g], total)`` with exact int32 group dots, rounded to bf16 at the
 end (or ``total = fmaf(float(dot_g), sa[m,g], total)``; ``bf16(total*sw[n])``
-for 1-D weight scales).  The HIP kernels (``nv4_w4a4_gemm``) take M at run time:
-nothing is compiled per shape, and there is no split-K and no atomics.
+for 1-D weight scales).  The HIP kernels (``nv4_w4a4_gemm``; for prefill-sized
+M ``nv4_w4a4_gemm_f8``, the same bits on the fp8 matrix cores) take M at run
+time: nothing is compiled per shape, and there is no split-K and no atomics.
 """
 from __future__ import annotations
 
@@ -43,16 +44,37 @@ def _validate_config(cfg: GroupedConfig) -> None:
         raise ValueError("Require positive dimensions, K divisible by 128, N divisible by 8, and whole warps")
 
 
-def _launch(a_packed, w_packed, a_scale, w_scale, out, output_fp32, weight_grouped, weights_tiled=False):
+def use_fp8_path(M, N, K):
+    """Prefill-sized GEMMs run on the fp8 matrix cores (``nv4_w4a4_gemm_f8``):
+    the operand conversion costs about 1.5 (M + N) K bytes of traffic, which
+    pays from M = 1024 on weights larger than 4096 x 4096 and from M = 2048
+    on all of the decoder's projections."""
+    return M >= 2048 or (M >= 1024 and N * K > 4096 * 4096)
+
+
+def _launch(a_packed, w_packed, a_scale, w_scale, out, output_fp32, weight_grouped, weights_tiled=False, fp8=None):
     M, N, K = a_packed.shape[0], w_packed.shape[0], a_packed.shape[1] * 2
+    if fp8 is None:
+        fp8 = use_fp8_path(M, N, K)
     lib = _lib.load()
-    fn = lib.nv4_w4a4_gemm_tiled if weights_tiled else lib.nv4_w4a4_gemm
     stream = torch.cuda.current_stream(a_packed.device).cuda_stream
     with torch.cuda.device(a_packed.device):
-        rc = fn(ctypes.c_void_p(a_packed.data_ptr()), ctypes.c_void_p(w_packed.data_ptr()),
-                ctypes.c_void_p(a_scale.data_ptr()), ctypes.c_void_p(w_scale.data_ptr()),
-                1 if weight_grouped else 0, ctypes.c_void_p(out.data_ptr()),
-                1 if output_fp32 else 0, M, N, K, ctypes.c_void_p(stream))
+        if fp8:
+            # fp8 operand rows for this call (caching allocator: no hipMalloc
+            # once warm); the kernels only read it on this stream.
+            ws = torch.empty((M + N) * K, dtype=torch.uint8, device=a_packed.device)
+            rc = lib.nv4_w4a4_gemm_f8(ctypes.c_void_p(a_packed.data_ptr()), ctypes.c_void_p(w_packed.data_ptr()),
+                                      1 if weights_tiled else 0,
+                                      ctypes.c_void_p(a_scale.data_ptr()), ctypes.c_void_p(w_scale.data_ptr()),
+                                      1 if weight_grouped else 0, ctypes.c_void_p(out.data_ptr()),
+                                      1 if output_fp32 else 0, M, N, K, ctypes.c_void_p(ws.data_ptr()),
+                                      ws.numel(), ctypes.c_void_p(stream))
+        else:
+            fn = lib.nv4_w4a4_gemm_tiled if weights_tiled else lib.nv4_w4a4_gemm
+            rc = fn(ctypes.c_void_p(a_packed.data_ptr()), ctypes.c_void_p(w_packed.data_ptr()),
+                    ctypes.c_void_p(a_scale.data_ptr()), ctypes.c_void_p(w_scale.data_ptr()),
+                    1 if weight_grouped else 0, ctypes.c_void_p(out.data_ptr()),
+                    1 if output_fp32 else 0, M, N, K, ctypes.c_void_p(stream))
     _lib.check(rc, "w4a4_grouped_gemm")
 
 
@@ -84,9 +106,11 @@ def untile_weights(w_tiled):
 
 
 @lru_cache(None)
-def compile_grouped_gemm(M, N, K, cfg=GroupedConfig(), output_fp32=False, weight_grouped=False):
+def compile_grouped_gemm(M, N, K, cfg=GroupedConfig(), output_fp32=False, weight_grouped=False, fp8=None):
     """Return ``kernel(A, W, Sa, Sw, C)`` for exact (M, N, K), as the reference does
-    (its kernel is JIT-specialised on M; this one only checks the shapes)."""
+    (its kernel is JIT-specialised on M; this one only checks the shapes).
+    ``fp8``: force (True) or avoid (False) the fp8 matrix-core path; None
+    chooses by size (``use_fp8_path``)."""
     if min(M, N, K) < 1 or K % GROUP_SIZE or N % 8:
         raise ValueError("Require positive dimensions, K divisible by 128, N divisible by 8, and whole warps")
     _validate_config(cfg)
@@ -101,7 +125,7 @@ def compile_grouped_gemm(M, N, K, cfg=GroupedConfig(), output_fp32=False, weight
         tensors = (a_packed, w_packed, a_scale, w_scale, out)
         if any(not t.is_cuda or not t.is_contiguous() or t.device != a_packed.device for t in tensors):
             raise ValueError("All inputs must be contiguous CUDA tensors on one device")
-        _launch(a_packed, w_packed, a_scale, w_scale, out, output_fp32, weight_grouped)
+        _launch(a_packed, w_packed, a_scale, w_scale, out, output_fp32, weight_grouped, fp8=fp8)
     return kernel
 
 
@@ -112,10 +136,11 @@ def best_grouped_config(M, N, K, weight_grouped=False):
     return GroupedConfig() if M <= 32 else GroupedConfig(64, 128, 2, 128)
 
 
-def w4a4_grouped_gemm(a_packed, w_packed, a_scale, w_scale, out=None, config=None, *, weights_tiled=False):
+def w4a4_grouped_gemm(a_packed, w_packed, a_scale, w_scale, out=None, config=None, *, weights_tiled=False, fp8=None):
     """Packed INT4; BF16 Sa[M,K/128], Sw[N] or Sw[N,K/128], output[M,N].
     ``weights_tiled``: ``w_packed`` holds ``tile_weights`` output (N % 16 == 0);
-    the result is bit-identical."""
+    the result is bit-identical.  ``fp8``: force (True) or avoid (False) the
+    fp8 matrix-core path (same bits); None chooses by size."""
     if a_packed.ndim != 2 or w_packed.ndim != 2 or a_packed.shape[1] != w_packed.shape[1]:
         raise ValueError("Packed inputs must have compatible [M,K/2] and [N,K/2] shapes")
     M, K = a_packed.shape[0], a_packed.shape[1] * 2
@@ -143,5 +168,5 @@ def w4a4_grouped_gemm(a_packed, w_packed, a_scale, w_scale, out=None, config=Non
         _validate_config(config)
     if weights_tiled and N % 16:
         raise ValueError("The tiled weight layout needs N divisible by 16")
-    _launch(a_packed, w_packed, a_scale, w_scale, out, False, weight_grouped, weights_tiled)
+    _launch(a_packed, w_packed, a_scale, w_scale, out, False, weight_grouped, weights_tiled, fp8=fp8)
     return out

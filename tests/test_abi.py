@@ -66,6 +66,27 @@ def test_w4a4_gemm_rejections():
     assert f(*ok, 1, P(A16 + 2), 1, 4, 64, 4096, None) == _lib.NV4_E_ALIGN   # fp32 output
 
 
+def test_w4a4_gemm_f8_rejections():
+    f = _lib.load().nv4_w4a4_gemm_f8
+    a = w = sa = sw = out = P(A16)
+    M, N, K = 256, 64, 4096
+    need = (M + N) * K
+
+    def call(a=a, w=w, tiled=0, sa=sa, sw=sw, out=out, fp32=0, M=M, N=N, K=K, ws=P(A16), nbytes=need):
+        return f(a, w, tiled, sa, sw, 1, out, fp32, M, N, K, ws, nbytes, None)
+
+    assert call(ws=None) == _lib.NV4_E_NULL
+    assert call(a=None) == _lib.NV4_E_NULL
+    assert call(nbytes=need - 1) == _lib.NV4_E_SHAPE                     # workspace too small
+    assert call(N=60) == _lib.NV4_E_SHAPE                                # N % 8
+    assert call(N=40, tiled=1, nbytes=(M + 40) * K) == _lib.NV4_E_SHAPE  # tiled needs N % 16
+    assert call(K=4000) == _lib.NV4_E_SHAPE                              # K % 128
+    assert call(M=0) == _lib.NV4_E_SHAPE
+    assert call(ws=P(A16 + 8)) == _lib.NV4_E_ALIGN
+    assert call(a=P(A16 + 4)) == _lib.NV4_E_ALIGN
+    assert call(out=P(A16 + 2), fp32=1) == _lib.NV4_E_ALIGN
+
+
 def test_w4a16_and_linear_rejections():
     f = _lib.load().nv4_w4a16_gemm
     ok = [P(A16)] * 4
