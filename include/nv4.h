@@ -21,11 +21,13 @@
  *   nv4_w4a4_linear     <- nanovllm/layers/linear_w4a4.py:27-35 W4A4Linear.forward
  *                          (rht_quant_pack + w4a4_grouped_gemm)
  *   nv4_w4a4_gemm_tiled, nv4_w4a4_linear_tiled, nv4_w4a4_tile_weights,
- *   nv4_w4a4_gemm_f8,
  *   nv4_w4a4_untile_weights <- the same two operators on weights stored in an
  *                          MFMA-tiled order (no counterpart in the reference,
  *                          whose kernels read [N,K/2]; W4A4Linear keeps the
  *                          reference layout in its state dict)
+ *   nv4_w4a4_gemm_f8    <- w4a4_grouped_gemm (w4a4_grouped_kernel.py:104) for
+ *                          prefill-sized M: the same operator on the fp8 matrix
+ *                          cores, with a caller workspace for the e4m3 operands
  *   nv4_w4a16_gemm, nv4_w4a16_gemm_ws, nv4_w4a16_dequant <- nanovllm/layers/linear_w4a16.py:11
  *                          tl_dequant_matmul_w4a16 (called from W4A16Linear.forward
  *                          :128-148; the reference splits K 8 ways with bf16 atomics,
