@@ -343,7 +343,10 @@ extern "C" int nv4_w4a4_gemm_f8(const int8_t* a, const int8_t* w, int w_tiled, c
     if (M < 1 || N < 1 || K < 128 || K % 128 || N % 8 || (w_tiled && N % 16)) return NV4_E_SHAPE;
     if (M > 0x7fffffffLL || N > 0x7fffffffLL || K > (1LL << 20)) return NV4_E_SHAPE;
     if (128 * K > 0x7fffffffLL || M * (K / 128) > 0x7fffffffLL || N * (K / 128) > 0x7fffffffLL) return NV4_E_SHAPE;
-    if (((M + 127) / 128) * ((N + 127) / 128) > 0x7fffffffLL) return NV4_E_SHAPE;
+    // Dispatch grids count work-items in 32 bits: the conversion launches one
+    // per 16 packed bytes, the GEMM 256 per output tile.
+    if (((M + 127) / 128) * ((N + F8_BN - 1) / F8_BN) * F8_T > 0xffffffffLL) return NV4_E_SHAPE;
+    if ((M > N ? M : N) * (K / 32) > 0xffffff00LL) return NV4_E_SHAPE;
     if (workspace_bytes < (M + N) * K) return NV4_E_SHAPE;
     if (reinterpret_cast<uintptr_t>(a) % 16 || reinterpret_cast<uintptr_t>(w) % 16 ||
         reinterpret_cast<uintptr_t>(sa) % 2 || reinterpret_cast<uintptr_t>(sw) % 2 ||

@@ -85,6 +85,8 @@ def test_w4a4_gemm_f8_rejections():
     assert call(ws=P(A16 + 8)) == _lib.NV4_E_ALIGN
     assert call(a=P(A16 + 4)) == _lib.NV4_E_ALIGN
     assert call(out=P(A16 + 2), fp32=1) == _lib.NV4_E_ALIGN
+    big = 1 << 27                                                        # M*K/32 beyond a 32-bit grid
+    assert call(M=big, nbytes=(big + N) * K) == _lib.NV4_E_SHAPE
 
 
 def test_w4a16_and_linear_rejections():
