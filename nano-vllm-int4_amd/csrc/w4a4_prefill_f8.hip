@@ -20,10 +20,11 @@
 //
 // Layout as k2_prefill (w4a4_prefill.hip): workgroup = 4 waves, 128 x 128
 // output tile, whole K, two workgroups per CU, XCD-aware tile order; per
-// group the A and W tiles (128 rows x 128 bytes each) and the fp32 scale
-// windows go through a two-stage LDS ring with one barrier per group.  An
-// LDS row holds the group's 128 codes as eight 16-byte chunks, chunk c at
-// c ^ (row % 8).  MFMA 32x32x64: lane l supplies row (A) / column (W) l%32
+// group the A and W tiles (128 rows x 128 bytes each) and the scale windows
+// go through a two-stage LDS ring with one barrier per group.  An LDS row
+// holds the group's 128 codes as eight 16-byte chunks, chunk c at
+// c ^ (row % 8) ^ ((row / 8) % 2): the 16 rows that 16 consecutive lanes read
+// in one LDS cycle of a 16-byte read then cover all 64 banks.  MFMA 32x32x64: lane l supplies row (A) / column (W) l%32
 // and 32 bytes of k -- chunks 4h + 2s, 4h + 2s + 1 of half h = l/32 in
 // k-step s (0..1); A and W read the same chunks, so every product pairs equal
 // k.  Result: lane l holds C[8*(i/4) + 4*(l/32) + i%4][l%32], i = 0..15.
@@ -131,13 +132,13 @@ k2_prefill_f8(const uint8_t* __restrict__ a, const uint8_t* __restrict__ w, cons
     // Direct-to-LDS staging: load i (0..3) of wave w fills the 1 KiB at
     // (4w + i) * 1024 of a tile, lane l the 16 bytes at l * 16: tile row
     // r = 8(4w + i) + l/8 and LDS slot l%8, which holds the row's chunk
-    // (l%8) ^ (r%8).  Rows past the matrix edge repeat the last row (never stored).
+    // (l%8) ^ (r%8) ^ (i%2).  Rows past the matrix edge repeat the last row (never stored).
     const uint8_t* a_t = a + (int64_t)m0 * K;
     const uint8_t* w_t = w + (int64_t)n0 * K;
     uint32_t offa[4], offw[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        const int r = 8 * (4 * wave + i) + (lane >> 3), c = (lane & 7) ^ ((lane >> 3) & 7);
+        const int r = 8 * (4 * wave + i) + (lane >> 3), c = (lane & 7) ^ ((lane >> 3) & 7) ^ (i & 1);
         offa[i] = (uint32_t)(min(r, M - 1 - m0) * K + c * 16);
         offw[i] = (uint32_t)(min(r, N - 1 - n0) * K + c * 16);
     }
@@ -177,12 +178,13 @@ k2_prefill_f8(const uint8_t* __restrict__ a, const uint8_t* __restrict__ w, cons
     // chunks 4*half + 2s and 4*half + 2s + 1 (the block base is a multiple
     // of 32 rows, so the swizzle depends on rc only).
     const int rc = lane & 31, half = lane >> 5;
+    const int rxor = (rc & 7) ^ ((rc >> 3) & 1);
     int oa[2][2], ow[2][2];
 #pragma unroll
     for (int s = 0; s < 2; ++s)
 #pragma unroll
         for (int e = 0; e < 2; ++e) {
-            const int cs = (((4 * half + 2 * s + e) ^ (rc & 7)) << 4) + rc * 128;
+            const int cs = (((4 * half + 2 * s + e) ^ rxor) << 4) + rc * 128;
             oa[s][e] = cs + wm * 64 * 128;
             ow[s][e] = cs + F8_A + wn * 64 * 128;
         }
