@@ -41,9 +41,9 @@
 // An LDS row holds a group's 128 int8 operands as eight 16-byte chunks,
 // chunk u = packed bytes 8u..8u+7 widened (lo nibbles of bytes 0-3, hi
 // nibbles of bytes 0-3, then the same for bytes 4-7), stored at chunk
-// u ^ (row % 8): the eight rows read by eight consecutive lanes fall in
-// distinct bank groups, and so do the chunks eight consecutive staging lanes
-// write.
+// u ^ (row % 8) ^ ((row / 8) % 2): the sixteen rows read by sixteen
+// consecutive lanes fall in distinct bank groups, and so do the chunks eight
+// consecutive staging lanes write.
 //
 // MFMA 32x32x32 i8: lane l supplies row (A) / column (W) l%32 and the
 // k-slots of half h = l/32; k-step s (0..3) reads chunk 4h + s.  A and W use
@@ -69,7 +69,10 @@ constexpr int PF_WSZ = 8 * (PF_BM + PF_BN) * 4;         // 8 groups x (sa[128], 
 constexpr int PF_LDS = PF_WIN + 2 * PF_WSZ;             // 80 KiB: two workgroups fill 160 KiB
 constexpr int PF_GM = 8;                                // M-tiles per column sweep
 
-__device__ __forceinline__ int pf_swz(int r, int u) { return r * 128 + ((u ^ (r & 7)) << 4); }
+// Row r's 16-byte chunk u sits at u ^ (r % 8) ^ ((r / 8) % 2): the 16 rows that
+// 16 consecutive lanes read in one LDS cycle of a 16-byte read cover all 64 banks.
+__device__ __forceinline__ int pf_rxor(int r) { return (r & 7) ^ ((r >> 3) & 1); }
+__device__ __forceinline__ int pf_swz(int r, int u) { return r * 128 + ((u ^ pf_rxor(r)) << 4); }
 
 // Scale magnitudes for which the 2^-8 fold is exact (see the file comment).
 __device__ __forceinline__ bool pf_scale_ok(uint32_t h) {
@@ -187,13 +190,13 @@ __device__ __forceinline__ void pf_body(const int8_t* __restrict__ a, const int8
     };
 
     // Operand reads: lane (rc, half) reads row r = base + rc, chunk 4*half + s
-    // at r*128 + (((4*half + s) ^ (rc & 7)) << 4) (the block base is a
+    // at r*128 + (((4*half + s) ^ pf_rxor(rc)) << 4) (the block base is a
     // multiple of 32 rows, so the swizzle depends on rc only).
     const int rc = lane & 31, half = lane >> 5;
     int oa[4], ow[4];
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
-        const int cs = (((4 * half + s) ^ (rc & 7)) << 4) + rc * 128;
+        const int cs = (((4 * half + s) ^ pf_rxor(rc)) << 4) + rc * 128;
         oa[s] = cs + wm * 64 * 128;
         ow[s] = cs + PF_A + wn * 64 * 128;
     }
