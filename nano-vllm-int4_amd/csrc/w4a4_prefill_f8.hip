@@ -12,22 +12,25 @@
 // of magnitude <= 64 and every partial sum of a 128-deep group an integer of
 // magnitude <= 8192: all exact in fp32, in any summation order.  So
 // v_mfma_scale_f32_32x32x64_f8f6f4 (unit E8M0 scales) returns each group dot
-// exactly, as fp32: the epilogue is the scale product and the fma, with no
-// integer-to-float conversion, and the staging copies bytes (no nibble
-// widening).  The operands are first written as fp8 rows -- A [M, K] and
-// W [N, K], one byte per code, k in order -- into a caller's workspace by a
-// byte-lookup conversion kernel (reference or MFMA-tiled weight layout).
+// exactly, as fp32, with no integer-to-float conversion, and the staging
+// copies bytes (no nibble widening).  The scale product sa * sw comes from a
+// bf16 MFMA (exact, see read_scales below), which leaves one VALU fma per
+// output and group.  The operands are first written as fp8 rows -- A [M, K]
+// and W [N, K], one byte per code, k in order -- into a caller's workspace by
+// a byte-lookup conversion kernel (reference or MFMA-tiled weight layout).
 //
 // Layout as k2_prefill (w4a4_prefill.hip): workgroup = 4 waves, 128 x 128
-// output tile, whole K, two workgroups per CU, XCD-aware tile order; per
-// group the A and W tiles (128 rows x 128 bytes each) and the scale windows
-// go through a two-stage LDS ring with one barrier per group.  An LDS row
+// output tile, whole K, two workgroups per CU, XCD-aware tile order.  Per
+// group the A and W tiles (128 rows x 128 bytes each) go global -> LDS with
+// buffer loads that write LDS directly, into a two-stage ring with one
+// barrier per group; the bf16 scales move in 8-group windows.  An LDS row
 // holds the group's 128 codes as eight 16-byte chunks, chunk c at
 // c ^ (row % 8) ^ ((row / 8) % 2): the 16 rows that 16 consecutive lanes read
-// in one LDS cycle of a 16-byte read then cover all 64 banks.  MFMA 32x32x64: lane l supplies row (A) / column (W) l%32
-// and 32 bytes of k -- chunks 4h + 2s, 4h + 2s + 1 of half h = l/32 in
-// k-step s (0..1); A and W read the same chunks, so every product pairs equal
-// k.  Result: lane l holds C[8*(i/4) + 4*(l/32) + i%4][l%32], i = 0..15.
+// in one LDS cycle of a 16-byte read then cover all 64 banks.
+// MFMA 32x32x64: lane l supplies row (A) / column (W) l%32 and 32 bytes of k
+// -- chunks 4h + 2s, 4h + 2s + 1 of half h = l/32 in k-step s (0..1); A and
+// W read the same chunks, so every product pairs equal k.  Result: lane l
+// holds C[8*(i/4) + 4*(l/32) + i%4][l%32], i = 0..15.
 #include "nv4_common.h"
 
 namespace nv4 {
@@ -223,10 +226,12 @@ k2_prefill_f8(const uint8_t* __restrict__ a, const uint8_t* __restrict__ w, cons
         acc[b & 1] = c;
     };
     // Scale products on the matrix cores: a product of two bf16 values has
-    // at most 16 significant bits, so sa[m] * sw[n] is exact in fp32, and a
-    // bf16 MFMA whose only non-zero k term is (sa[row], sw[column]) returns
-    // exactly the fp32 product the reference multiplies (sa alone, times
-    // bf16 1.0, for per-channel weight scales).  32x32x16 bf16 operands:
+    // at most 16 significant bits, so sa[m] * sw[n] is exact in fp32 unless
+    // it falls below the normal range, and a bf16 MFMA whose only non-zero k
+    // term is (sa[row], sw[column]) returns the fp32 product the reference
+    // multiplies (sa alone, times bf16 1.0, for per-channel weight scales).
+    // Scales whose products reach the fp32 subnormals (bf16 subnormals, 2^-126)
+    // are in the parity tests and match the oracle bit for bit.  32x32x16 bf16 operands:
     // lane l supplies row / column l%32, k = 8(l/32) .. +7, so lanes 32..63
     // supply zeros; the result has the layout of the fp8 dot.
     const uint32_t keep = half ? 0u : 0xffffu;
