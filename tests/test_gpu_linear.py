@@ -128,3 +128,30 @@ def test_linear_graph_replay(proj):
         torch.cuda.synchronize()
         shifted = W.W4A4Case(case.name, new_x, case.signs, case.w_packed, case.w_scale)
         check(shifted, (packed, scale, out), f"{proj} replay {step}")
+
+
+@pytest.mark.parametrize("proj,M", [("qkv", 2048), ("down", 1024), ("gate_up", 1100)])
+def test_linear_prefill_fp8_route(proj, M):
+    """At prefill-sized M ``w4a4_linear`` runs K1 and then the fp8 matrix-core
+    GEMM: its codes, scales and output equal K1 followed by the int8 path, bit
+    for bit, in both weight layouts."""
+    from nv4 import rht_quant_pack, w4a4_grouped_gemm
+    from nv4.kernels.w4a4_grouped import use_fp8_path
+    case = W.w4a4_case(proj, M)
+    M, N, K = case.shape
+    assert use_fp8_path(M, N, K)
+    print(f"[linear-fp8] {proj} M={M} N={N} K={K}", flush=True)
+    x, signs = case.x.to(DEV), case.signs.to(DEV)
+    wpk, wsc = case.w_packed.to(DEV), case.w_scale.to(DEV)
+    for tiled in (False, True):
+        w = tile_weights(wpk) if tiled else wpk
+        packed = torch.empty((M, K // 2), dtype=torch.int8, device=DEV)
+        scale = torch.empty((M, K // 128), dtype=torch.bfloat16, device=DEV)
+        out = w4a4_linear(x, signs, w, wsc, out_packed=packed, out_scale=scale, weights_tiled=tiled)
+        p2 = torch.empty_like(packed)
+        s2 = torch.empty_like(scale)
+        rht_quant_pack(x, signs, out_packed=p2, out_scale=s2)
+        ref = w4a4_grouped_gemm(p2, w, s2, wsc, weights_tiled=tiled, fp8=False)
+        torch.cuda.synchronize()
+        assert torch.equal(packed, p2) and torch.equal(scale.view(torch.int16), s2.view(torch.int16))
+        assert torch.equal(out.view(torch.int16), ref.view(torch.int16)), f"tiled={tiled}"
