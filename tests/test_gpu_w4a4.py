@@ -269,3 +269,48 @@ def test_k2_prefill_tile_orders(M, N, K):
     divisible by the 8 XCDs or not -- so every tile of both orderings is
     written exactly once and lands where it belongs."""
     run_case(M, N, K, 7000 + M + N)
+
+
+@pytest.mark.parametrize("N,K", [(4096, 12288), (6144, 4096), (24576, 4096)])
+def test_k2_decode_back_to_back_repeatable(N, K):
+    """Decode-sized K2 launched back to back over rotating weight sets (the
+    benchmark's pattern, eager and as a replayed graph) gives every call the
+    bits of the same call made alone: no state leaks between launches and no
+    race inside one."""
+    M = 32
+    print(f"[k2-repeat] M={M} N={N} K={K}", flush=True)
+    g = torch.Generator(device=DEV)
+    g.manual_seed(N + K)
+    a = torch.randint(-128, 128, (M, K // 2), generator=g, device=DEV, dtype=torch.int16).to(torch.int8)
+    sa = (0.01 + torch.rand(M, K // 128, generator=g, device=DEV)).to(torch.bfloat16)
+    sets = []
+    for _ in range(3):
+        w = torch.randint(-128, 128, (N, K // 2), generator=g, device=DEV, dtype=torch.int16).to(torch.int8)
+        sw = (0.005 + 0.015 * torch.rand(N, K // 128, generator=g, device=DEV)).to(torch.bfloat16)
+        sets.append((tile_weights(w), sw))
+    refs = []
+    for wt, sw in sets:
+        refs.append(w4a4_grouped_gemm(a, wt, sa, sw, weights_tiled=True))
+        torch.cuda.synchronize()
+    outs = [torch.empty((M, N), dtype=torch.bfloat16, device=DEV) for _ in range(12)]
+    for i, o in enumerate(outs):
+        wt, sw = sets[i % 3]
+        w4a4_grouped_gemm(a, wt, sa, sw, out=o, weights_tiled=True)
+    torch.cuda.synchronize()
+    for i, o in enumerate(outs):
+        assert torch.equal(o.view(torch.int16), refs[i % 3].view(torch.int16)), f"eager call {i}"
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=s):
+        for i, o in enumerate(outs):
+            wt, sw = sets[i % 3]
+            w4a4_grouped_gemm(a, wt, sa, sw, out=o, weights_tiled=True)
+    for rep in range(3):
+        for o in outs:
+            o.zero_()
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        for i, o in enumerate(outs):
+            assert torch.equal(o.view(torch.int16), refs[i % 3].view(torch.int16)), f"replay {rep} call {i}"
