@@ -162,7 +162,7 @@ int nv4_w4a4_linear_tiled(const void* x, const int8_t* signs, const int8_t* w_ti
  * workspace (A [M,K] then W [N,K]; workspace_bytes >= (M + N) * K, 16-byte
  * aligned), then multiplied with v_mfma_f32_32x32x64_f8f6f4.  Every group dot
  * is a small integer, exact in fp32, so the results are bit-identical to
- * nv4_w4a4_gemm.  Same argument rules as nv4_w4a4_gemm, and max(M, N)·K/32
+ * nv4_w4a4_gemm.  Same argument rules as nv4_w4a4_gemm, and (M + N)·K/32
  * below 2^32; the workspace is overwritten, and calls sharing one workspace
  * must be stream-ordered.
  */

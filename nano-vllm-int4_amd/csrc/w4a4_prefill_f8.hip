@@ -73,19 +73,24 @@ __device__ __forceinline__ v4u packed8_to_e4m3(uint32_t d0, uint32_t d1) {
     return r;
 }
 
-// Packed INT4 rows -> fp8 rows.  Thread = one 16-byte unit of the source:
-// reference layout [rows][K/2] (unit u = row * K/32 + c), or the MFMA-tiled
-// weight layout (unit u = (cb*G + g)*64 + l holds packed bytes 64g + 16(l/16)
-// .. +15 of row 16cb + l%16).  Writes 32 fp8 bytes of the row.
-template <bool TILED>
+// Packed INT4 rows -> fp8 rows, both operands in one launch: thread u < ua
+// converts 16-byte unit u of A, the others unit u - ua of W.  A is in the
+// reference layout [M][K/2] (unit u = row * K/32 + c); W in the reference
+// layout or, with W_TILED, the MFMA-tiled one (unit u = (cb*G + g)*64 + l
+// holds packed bytes 64g + 16(l/16) .. +15 of row 16cb + l%16).  Each unit
+// becomes 32 fp8 bytes of its row.
+template <bool W_TILED>
 __global__ void __launch_bounds__(256)
-i4_to_f8_rows(const int8_t* __restrict__ src, uint8_t* __restrict__ dst, int64_t units, int G, int K) {
-    const int64_t u = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    if (u >= units) return;
-    const v4u v = *reinterpret_cast<const v4u*>(src + u * 16);
+i4_to_f8_rows(const int8_t* __restrict__ a, uint8_t* __restrict__ a8, int64_t ua, const int8_t* __restrict__ w,
+              uint8_t* __restrict__ w8, int64_t uw, int G, int K) {
+    int64_t u = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    const bool is_a = u < ua;
+    if (!is_a) u -= ua;
+    if (!is_a && u >= uw) return;
+    const v4u v = *reinterpret_cast<const v4u*>((is_a ? a : w) + u * 16);
     int64_t row;
     int kb;  // first packed byte of the unit within its row
-    if constexpr (TILED) {
+    if (!is_a && W_TILED) {
         const int l = (int)(u & 63);
         const int64_t cg = u >> 6;
         const int g = (int)(cg % G);
@@ -96,7 +101,7 @@ i4_to_f8_rows(const int8_t* __restrict__ src, uint8_t* __restrict__ dst, int64_t
         row = u / per;
         kb = (int)(u % per) * 16;
     }
-    uint8_t* d = dst + row * K + 2 * kb;
+    uint8_t* d = (is_a ? a8 : w8) + row * K + 2 * kb;
     *reinterpret_cast<v4u*>(d) = packed8_to_e4m3(v[0], v[1]);
     *reinterpret_cast<v4u*>(d + 16) = packed8_to_e4m3(v[2], v[3]);
 }
@@ -351,9 +356,9 @@ extern "C" int nv4_w4a4_gemm_f8(const int8_t* a, const int8_t* w, int w_tiled, c
     if (M > 0x7fffffffLL || N > 0x7fffffffLL || K > (1LL << 20)) return NV4_E_SHAPE;
     if (128 * K > 0x7fffffffLL || M * (K / 128) > 0x7fffffffLL || N * (K / 128) > 0x7fffffffLL) return NV4_E_SHAPE;
     // Dispatch grids count work-items in 32 bits: the conversion launches one
-    // per 16 packed bytes, the GEMM 256 per output tile.
+    // per 16 packed bytes of both operands, the GEMM 256 per output tile.
     if (((M + 127) / 128) * ((N + F8_BN - 1) / F8_BN) * F8_T > 0xffffffffLL) return NV4_E_SHAPE;
-    if ((M > N ? M : N) * (K / 32) > 0xffffff00LL) return NV4_E_SHAPE;
+    if ((M + N) * (K / 32) > 0xffffff00LL) return NV4_E_SHAPE;
     if (workspace_bytes < (M + N) * K) return NV4_E_SHAPE;
     if (reinterpret_cast<uintptr_t>(a) % 16 || reinterpret_cast<uintptr_t>(w) % 16 ||
         reinterpret_cast<uintptr_t>(sa) % 2 || reinterpret_cast<uintptr_t>(sw) % 2 ||
@@ -364,14 +369,11 @@ extern "C" int nv4_w4a4_gemm_f8(const int8_t* a, const int8_t* w, int w_tiled, c
     uint8_t* w8 = a8 + M * K;
     const int G = (int)(K / 128);
     const int64_t ua = M * K / 32, uw = N * K / 32;
-    hipLaunchKernelGGL(i4_to_f8_rows<false>, dim3((unsigned)((ua + 255) / 256)), dim3(256), 0, st, a, a8, ua, G,
-                       (int)K);
+    const unsigned cgrid = (unsigned)((ua + uw + 255) / 256);
     if (w_tiled)
-        hipLaunchKernelGGL(i4_to_f8_rows<true>, dim3((unsigned)((uw + 255) / 256)), dim3(256), 0, st, w, w8, uw, G,
-                           (int)K);
+        hipLaunchKernelGGL(i4_to_f8_rows<true>, dim3(cgrid), dim3(256), 0, st, a, a8, ua, w, w8, uw, G, (int)K);
     else
-        hipLaunchKernelGGL(i4_to_f8_rows<false>, dim3((unsigned)((uw + 255) / 256)), dim3(256), 0, st, w, w8, uw,
-                           G, (int)K);
+        hipLaunchKernelGGL(i4_to_f8_rows<false>, dim3(cgrid), dim3(256), 0, st, a, a8, ua, w, w8, uw, G, (int)K);
     const auto* sap = static_cast<const uint16_t*>(sa);
     const auto* swp = static_cast<const uint16_t*>(sw);
     const int m = (int)M, n = (int)N, k = (int)K;
