@@ -45,11 +45,13 @@ def _validate_config(cfg: GroupedConfig) -> None:
 
 
 def use_fp8_path(M, N, K):
-    """Prefill-sized GEMMs run on the fp8 matrix cores (``nv4_w4a4_gemm_f8``):
-    the operand conversion costs about 1.5 (M + N) K bytes of traffic, which
-    pays from M = 1024 on weights larger than 4096 x 4096 and from M = 2048
-    on all of the decoder's projections."""
-    return M >= 2048 or (M >= 1024 and N * K > 4096 * 4096)
+    """Prefill-sized GEMMs run on the fp8 matrix cores (``nv4_w4a4_gemm_f8``).
+    The operand conversion costs about 1.5 (M + N) K bytes of traffic and one
+    launch; measured on the decoder's projections it pays from M = 384 on
+    weights of 4096 x 12288 or more, from M = 768 above 4096 x 4096, and from
+    M = 1024 on all of them."""
+    nk = N * K
+    return M >= 1024 or (M >= 768 and nk > 4096 * 4096) or (M >= 384 and nk >= 4096 * 12288)
 
 
 def _launch(a_packed, w_packed, a_scale, w_scale, out, output_fp32, weight_grouped, weights_tiled=False, fp8=None):
