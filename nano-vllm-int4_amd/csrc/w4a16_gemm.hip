@@ -212,6 +212,7 @@ k3_w4a16(const uint16_t* __restrict__ x, const int32_t* __restrict__ qweight,
 //    and rounds once (no atomics, same bits on every run).
 // ----------------------------------------------------------------------------
 constexpr int K3_KS = 1024;  // k per slice
+constexpr int K3_RSRC_WORD3 = 0x00020000;  // buffer resource word 3 (CDNA): 32-bit data format
 constexpr int K3_NB = 64;    // columns per workgroup
 
 __device__ __forceinline__ int k3_swz(int r, int c) { return r * (K3_KS * 2) + ((c ^ (r & 7)) << 4); }
@@ -234,17 +235,29 @@ k3_dec(const uint16_t* __restrict__ x, const int32_t* __restrict__ qweight, cons
     // Column quad of this lane; quads at or beyond N load the last valid quad (results dropped).
     const int ncol = min(n0 + 4 * c4, N - 4);
 
-    // ---- weights, zero points and scales of the slice: all loads first.
+    // ---- loads, in the order their data is needed (vector loads return in
+    // issue order, so a wait for one load is a wait for every earlier one):
+    // the activation slice, then the slice's zero points and scales, then the
+    // weights, which keep streaming in while the first k-steps run.
+    // Activation slice (row r: 128 chunks of 16 bytes).  Rows at or beyond M
+    // are not loaded: their LDS rows are zero and their results dropped.
+    constexpr int CH = ROWS * (K3_KS / 8);  // 16-byte chunks
+    constexpr int PER = CH / 256;
+    // A buffer resource over the M rows: a load at or past its end returns
+    // zeros without a memory access, so the loads stay unconditional (a load
+    // under a branch makes the compiler wait for it at the join).
+    const __amdgpu_buffer_rsrc_t rx =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(x), (short)0, (int)((uint32_t)M * K * 2u), K3_RSRC_WORD3);
+    v4u xv[PER];
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+        const int q = t + i * 256;
+        const int r = q >> 7, c = q & 127;
+        const int cc = min(c, (klen >> 3) - 1);
+        xv[i] = __builtin_bit_cast(v4u, __builtin_amdgcn_raw_buffer_load_b128(rx, (int)(((uint32_t)r * K + ks + cc * 8) * 2u), 0, 0));
+    }
     // Wave w takes the 8 consecutive 32-k steps 8w .. 8w+7 (groups 2w, 2w+1
     // of the slice).
-    const int nst = min(8, steps - 8 * wave);  // steps of this wave (may be <= 0)
-    v4u wq[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        const int st = max(0, min(8 * wave + i, steps - 1));
-        const int64_t row = (int64_t)((ks >> 3) + st * 4 + kq);
-        wq[i] = *reinterpret_cast<const v4u*>(qweight + row * N + ncol);
-    }
     uint32_t zw[2];
     uint2 sv[2];
 #pragma unroll
@@ -253,24 +266,18 @@ k3_dec(const uint16_t* __restrict__ x, const int32_t* __restrict__ qweight, cons
         zw[i] = (uint32_t)qzeros[(int64_t)g * (N >> 3) + (ncol >> 3)];
         sv[i] = *reinterpret_cast<const uint2*>(scales + (int64_t)g * N + ncol);
     }
-    // ---- activation slice into LDS (row r: 128 chunks of 16 bytes).
-    {
-        constexpr int CH = ROWS * (K3_KS / 8);  // 16-byte chunks
-        constexpr int PER = CH / 256;
-        v4u xv[PER];
+    const int nst = min(8, steps - 8 * wave);  // steps of this wave (may be <= 0)
+    v4u wq[8];
 #pragma unroll
-        for (int i = 0; i < PER; ++i) {
-            const int q = t + i * 256;
-            const int r = q >> 7, c = q & 127;
-            const int rr = min(r, M - 1);
-            const int cc = min(c, (klen >> 3) - 1);
-            xv[i] = *reinterpret_cast<const v4u*>(x + (int64_t)rr * K + ks + cc * 8);
-        }
+    for (int i = 0; i < 8; ++i) {
+        const int st = max(0, min(8 * wave + i, steps - 1));
+        const int64_t row = (int64_t)((ks >> 3) + st * 4 + kq);
+        wq[i] = *reinterpret_cast<const v4u*>(qweight + row * N + ncol);
+    }
 #pragma unroll
-        for (int i = 0; i < PER; ++i) {
-            const int q = t + i * 256;
-            *reinterpret_cast<v4u*>(&smem[k3_swz(q >> 7, q & 127)]) = xv[i];
-        }
+    for (int i = 0; i < PER; ++i) {
+        const int q = t + i * 256;
+        *reinterpret_cast<v4u*>(&smem[k3_swz(q >> 7, q & 127)]) = xv[i];
     }
     __syncthreads();
 
@@ -290,27 +297,36 @@ k3_dec(const uint16_t* __restrict__ x, const int32_t* __restrict__ qweight, cons
             const uint32_t h = ((j < 2 ? sv[i].x : sv[i].y) >> (16 * (j & 1))) & 0xffffu;
             dq[i][j] = TR::prep((uint16_t)h, (int)((zw[i] >> (zsh + 4 * j)) & 15u) + 1);
         }
+    auto kstep = [&](int i) {
+        const int st = 8 * wave + i;
+        typename TR::vec bop[4];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        if (i < nst) {  // uniform over the wave
-            const int st = 8 * wave + i;
-            typename TR::vec bop[4];
+        for (int j = 0; j < 4; ++j) bop[j] = TR::dequant8(wq[i][j], dq[i >> 2][j]);
+        const int c = st * 4 + kq;  // 16-byte chunk of the k-octet in the slice row
 #pragma unroll
-            for (int j = 0; j < 4; ++j) bop[j] = TR::dequant8(wq[i][j], dq[i >> 2][j]);
-            const int c = st * 4 + kq;  // 16-byte chunk of the k-octet in the slice row
+        for (int mb = 0; mb < MB; ++mb) {
+            const v4u av = *reinterpret_cast<const v4u*>(&smem[k3_swz(mb * 16 + c4, c)]);
+            const typename TR::vec aop = __builtin_bit_cast(typename TR::vec, av);
 #pragma unroll
-            for (int mb = 0; mb < MB; ++mb) {
-                const v4u av = *reinterpret_cast<const v4u*>(&smem[k3_swz(mb * 16 + c4, c)]);
-                const typename TR::vec aop = __builtin_bit_cast(typename TR::vec, av);
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    if constexpr (XF16)
-                        acc[mb][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(aop, bop[j], acc[mb][j], 0, 0, 0);
-                    else
-                        acc[mb][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(aop, bop[j], acc[mb][j], 0, 0, 0);
-                }
+            for (int j = 0; j < 4; ++j) {
+                if constexpr (XF16)
+                    acc[mb][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(aop, bop[j], acc[mb][j], 0, 0, 0);
+                else
+                    acc[mb][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(aop, bop[j], acc[mb][j], 0, 0, 0);
             }
         }
+    };
+    // A full slice gives every wave all 8 steps: that loop has no branch, so
+    // the weight loads stay where they were issued and each step waits only
+    // for its own (a load used only under a branch is moved into it and
+    // waited for there in full).
+    if (nst == 8) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) kstep(i);
+    } else {
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+            if (i < nst) kstep(i);  // uniform over the wave
     }
     __syncthreads();  // the activation slice is dead; its LDS takes the wave partials
     float* part = reinterpret_cast<float*>(smem);  // [wave][mb][j][256]
