@@ -74,9 +74,14 @@ __device__ __forceinline__ void load_bf16x16(const uint16_t* __restrict__ xp, fl
     }
 }
 
-// a[i] *= sign[i] for 16 contiguous int8 signs (exact).
-__device__ __forceinline__ void apply_signs16(const int8_t* __restrict__ sp, float (&a)[16]) {
-    const v4u sv = *reinterpret_cast<const v4u*>(sp);
+// a[i] *= sign[i] for 16 contiguous int8 signs sv (exact).  The signs are
+// loaded before the row's values: vector loads complete in issue order, so
+// the wait for the values then covers them too (loaded after the values,
+// they would cost a second round trip to memory).
+__device__ __forceinline__ v4u load_signs16(const int8_t* __restrict__ sp) {
+    return *reinterpret_cast<const v4u*>(sp);
+}
+__device__ __forceinline__ void apply_signs16(const v4u sv, float (&a)[16]) {
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
         const int sg = (int)(int8_t)((sv[i >> 2] >> (8 * (i & 3))) & 0xffu);
@@ -207,8 +212,9 @@ __device__ __forceinline__ void k1_row12288(Prologue&& prologue, const int8_t* _
     const int t = threadIdx.x, w = t >> 6, l = t & 63;
     if (w < 12) {
         float a[16];
+        const v4u sv = load_signs16(signs + w * 1024 + 16 * l);
         prologue(w * 1024 + 16 * l, a);
-        apply_signs16(signs + w * 1024 + 16 * l, a);
+        apply_signs16(sv, a);
         float* blk = buf + w * 1024;
         chunk1024_bits0_9(a, blk, l);
 #pragma unroll
@@ -250,8 +256,9 @@ __device__ __forceinline__ void k1_row4096(Prologue&& prologue, const int8_t* __
                                            float* __restrict__ buf) {
     const int t = threadIdx.x, w = t >> 6, l = t & 63;
     float a[16];
+    const v4u sv = load_signs16(signs + w * 1024 + 16 * l);
     prologue(w * 1024 + 16 * l, a);
-    apply_signs16(signs + w * 1024 + 16 * l, a);
+    apply_signs16(sv, a);
     float* blk = buf + w * 1024;
     reg_butterflies(a);
 #pragma unroll

@@ -71,17 +71,20 @@ __device__ __forceinline__ float rms_rsqrt256(float ss, float* red, int H, float
     return rsqrtf(tot / (float)H + eps);
 }
 
-// y = bf16(bf16(h * r) * w) for 16 contiguous values, as fp32.
-__device__ __forceinline__ void rms_apply16(const float (&h)[16], float r, const uint16_t* __restrict__ w,
+// y = bf16(bf16(h * r) * w) for 16 contiguous values, as fp32 (w0, w1: the
+// 16 bf16 weights, loaded by the caller ahead of the row).
+__device__ __forceinline__ void rms_apply16(const float (&h)[16], float r, const v4u w0, const v4u w1,
                                             float (&y)[16]) {
-    const v4u w0 = *reinterpret_cast<const v4u*>(w);
-    const v4u w1 = *reinterpret_cast<const v4u*>(w + 8);
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
         const uint32_t ww = i < 8 ? w0[(i & 7) >> 1] : w1[(i & 7) >> 1];
         const float wf = bf16_to_f32((ww >> (16 * (i & 1))) & 0xffffu);
         y[i] = round_bf16(round_bf16(h[i] * r) * wf);
     }
+}
+__device__ __forceinline__ void rms_apply16(const float (&h)[16], float r, const uint16_t* __restrict__ w,
+                                            float (&y)[16]) {
+    rms_apply16(h, r, *reinterpret_cast<const v4u*>(w), *reinterpret_cast<const v4u*>(w + 8), y);
 }
 
 __device__ __forceinline__ float silu_mul1(float g, float u) { return round_bf16(round_bf16(g / (1.0f + expf(-g))) * u); }

@@ -46,11 +46,14 @@ k1_k4096_rmsnorm(const uint16_t* x, const uint16_t* res_in, uint16_t* res_out, c
     const int64_t off = (int64_t)blockIdx.x * 4096;
     k1_row4096(
         [&](int c0, float (&v)[16]) {
+            // The norm weights are loaded ahead of the row (one round trip).
+            const v4u w0 = *reinterpret_cast<const v4u*>(nw + c0);
+            const v4u w1 = *reinterpret_cast<const v4u*>(nw + c0 + 8);
             float h[16], ss = 0.0f;
             rms_load16<RESID>(x + off + c0, RESID ? res_in + off + c0 : nullptr,
                               RESID ? res_out + off + c0 : nullptr, h, ss);
             const float r = rms_rsqrt256(ss, red, 4096, eps);
-            rms_apply16(h, r, nw + c0, v);
+            rms_apply16(h, r, w0, w1, v);
         },
         signs, packed + (int64_t)blockIdx.x * 2048, scale + (int64_t)blockIdx.x * 32, buf);
 }
