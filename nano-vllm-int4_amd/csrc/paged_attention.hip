@@ -253,12 +253,49 @@ pa_split(const uint16_t* __restrict__ q, int64_t q_row, const uint16_t* __restri
     }
 }
 
+// Split merge, one wave per (sequence, query head).  SMAX > 0 (S <= SMAX
+// <= 64 splits): the split maxima and every partial row are loaded with the
+// context length, in one round trip to memory (rows past S repeat row S-1
+// and are not used), then merged with the operation sequence of the general
+// form below for a single chunk, so the result has the same bits.  SMAX = 0:
+// any S, in chunks of 64 splits.
+template <int SMAX>
 __global__ void __launch_bounds__(64)
 pa_merge(const int32_t* __restrict__ context_lens, const float* __restrict__ part_o,
          const float* __restrict__ part_ml, uint16_t* __restrict__ out, int Hq, int S, int max_ctx) {
     const int hq = blockIdx.x, b = blockIdx.y, lane = threadIdx.x;
-    const int n = min(S, (min(context_lens[b], max_ctx) + PA_SPLIT - 1) / PA_SPLIT);
     const int64_t base = ((int64_t)b * Hq + hq) * S;
+    if constexpr (SMAX > 0) {
+        const int clen = context_lens[b];
+        const float2 ml = *reinterpret_cast<const float2*>(part_ml + (base + min(lane, S - 1)) * 2);
+        float2 v[SMAX];
+#pragma unroll
+        for (int u = 0; u < SMAX; ++u)
+            v[u] = *reinterpret_cast<const float2*>(part_o + (base + min(u, S - 1)) * PA_D + 2 * lane);
+        const int n = min(S, (min(clen, max_ctx) + PA_SPLIT - 1) / PA_SPLIT);
+        const float ms = lane < n ? ml.x : -__builtin_inff(), ls = lane < n ? ml.y : 0.0f;
+        float M = ms;
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) M = fmaxf(M, __shfl_xor(M, off));
+        const float w = lane < n ? __builtin_amdgcn_exp2f(ms - M) : 0.0f;
+        float L = w * ls;
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) L += __shfl_xor(L, off);
+        L = 0.0f + L;
+        float O0 = 0.0f, O1 = 0.0f;
+#pragma unroll
+        for (int u = 0; u < SMAX; ++u) {
+            if (u < n) {
+                const float wk = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, w), u));
+                O0 = __builtin_fmaf(wk, v[u].x, O0);
+                O1 = __builtin_fmaf(wk, v[u].y, O1);
+            }
+        }
+        uint16_t* o = out + ((int64_t)b * Hq + hq) * PA_D + 2 * lane;
+        *reinterpret_cast<uint32_t*>(o) = f32_to_bf16_rne(O0 / L) | (f32_to_bf16_rne(O1 / L) << 16);
+        return;
+    }
+    const int n = min(S, (min(context_lens[b], max_ctx) + PA_SPLIT - 1) / PA_SPLIT);
     float O0 = 0.0f, O1 = 0.0f, L = 0.0f;
     // Splits in chunks of 64 (one per lane); the running max M rescales
     // earlier chunks when a later one raises it.
@@ -324,9 +361,22 @@ hipError_t pa_launch(const void* q, int64_t q_row, const void* kc, const void* v
         hipLaunchKernelGGL((pa_split<G, false>), grid, dim3(PA_THREADS), 0, st, static_cast<const uint16_t*>(q),
                            q_row, static_cast<const uint16_t*>(kc), static_cast<const uint16_t*>(vc), bt, max_blocks,
                            cl, static_cast<uint16_t*>(out), part_o, part_ml, Hkv, bs, S, max_ctx, qscale);
-    if (S > 1)
-        hipLaunchKernelGGL(pa_merge, dim3((unsigned)(Hkv * G), (unsigned)B), dim3(64), 0, st, cl, part_o, part_ml,
-                           static_cast<uint16_t*>(out), Hkv * G, S, max_ctx);
+    if (S > 1) {
+        const dim3 mg((unsigned)(Hkv * G), (unsigned)B);
+        auto* o16 = static_cast<uint16_t*>(out);
+        if (S <= 8)
+            hipLaunchKernelGGL(pa_merge<8>, mg, dim3(64), 0, st, cl, part_o, part_ml, o16, Hkv * G, S, max_ctx);
+        else if (S <= 16)
+            hipLaunchKernelGGL(pa_merge<16>, mg, dim3(64), 0, st, cl, part_o, part_ml, o16, Hkv * G, S, max_ctx);
+        else if (S <= 24)
+            hipLaunchKernelGGL(pa_merge<24>, mg, dim3(64), 0, st, cl, part_o, part_ml, o16, Hkv * G, S, max_ctx);
+        else if (S <= 32)
+            hipLaunchKernelGGL(pa_merge<32>, mg, dim3(64), 0, st, cl, part_o, part_ml, o16, Hkv * G, S, max_ctx);
+        else if (S <= 64)
+            hipLaunchKernelGGL(pa_merge<64>, mg, dim3(64), 0, st, cl, part_o, part_ml, o16, Hkv * G, S, max_ctx);
+        else
+            hipLaunchKernelGGL(pa_merge<0>, mg, dim3(64), 0, st, cl, part_o, part_ml, o16, Hkv * G, S, max_ctx);
+    }
     return hipGetLastError();
 }
 

@@ -6,7 +6,8 @@ caches behind shuffled block tables, context lengths at and around the
 256-token split and block boundaries (1, 255, 256, 257, ..., 4352), GQA
 groups 1/2/4, block sizes 256, 16 (one block-table read per 16 tokens) and
 24 (one read per token), contexts of more than 64 splits (the merge's
-chunked loop), and queries read as a strided view of a fused qkv tensor;
+chunked loop), every compile-time split count of the merge (bit-equal to the
+chunked form), and queries read as a strided view of a fused qkv tensor;
 against softmax(scale q.K^T) V computed in fp32.  Bar:
 |out - ref| <= 1e-2 + 1e-2 |ref| (bf16 output).  Prefill attention (causal
 GQA through the fused flash SDPA kernel) against the same fp32 reference on
@@ -99,6 +100,25 @@ def test_paged_decode_attention_many_splits():
     out = paged_decode_attention(q, kc, vc, bt, cl, scale, max_context=max(lens))
     torch.cuda.synchronize()
     check(out, reference(q, kc, vc, bt, cl, scale), "many splits")
+
+
+@pytest.mark.parametrize("max_ctx", [512, 2304, 4352, 8000, 12000])
+def test_merge_split_counts_equal_chunked_form(max_ctx):
+    """Each compile-time split count of the merge (S up to 8, 16, 24, 32, 64:
+    every load in one round trip) gives the bits of the chunked general form,
+    which a block table widened to 65 splits selects for the same contexts."""
+    lens = [max_ctx, 1, 257, max_ctx - 255, (2 * max_ctx) // 3]
+    q, kc, vc, bt, cl = make_case(len(lens), 32, 8, 256, lens, seed=max_ctx)
+    scale = 1 / math.sqrt(128)
+    wide = 65 * 256
+    pad = torch.zeros(bt.shape[0], wide // 256 - bt.shape[1], dtype=torch.int32, device=DEV)  # never read
+    bt_wide = torch.cat([bt, pad], 1).contiguous()
+    print(f"[attn] merge max_ctx={max_ctx} splits={(max_ctx + 255) // 256}", flush=True)
+    out = paged_decode_attention(q, kc, vc, bt, cl, scale, max_context=max_ctx)
+    out_chunked = paged_decode_attention(q, kc, vc, bt_wide, cl, scale, max_context=wide)
+    torch.cuda.synchronize()
+    check(out, reference(q, kc, vc, bt, cl, scale), f"max_ctx={max_ctx}")
+    assert torch.equal(out, out_chunked)
 
 
 def test_single_split_writes_output_directly():
