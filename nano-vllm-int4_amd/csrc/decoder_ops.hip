@@ -82,31 +82,36 @@ qk_norm_rope_store(const uint16_t* __restrict__ qkv, int64_t qkv_row, int T, int
     const int h = (int)(item % heads);
     const int l = threadIdx.x & 63;
     const uint16_t* src = qkv + tok * qkv_row + (int64_t)h * 128;
-    float x1 = bf16_to_f32(src[l]), x2 = bf16_to_f32(src[l + 64]);
-    if (h >= Hq + Hkv) {  // value head: copy to its slot (and v_out)
-        const int kvh = h - Hq - Hkv;
-        const int64_t slot = slots[tok];
-        if (slot >= 0 && slot < num_slots) {
-            uint16_t* dst = v_cache + (slot * Hkv + kvh) * 128;
-            dst[l] = src[l];
-            dst[l + 64] = src[l + 64];
-        }
-        if (v_out) {
-            v_out[(tok * Hkv + kvh) * 128 + l] = src[l];
-            v_out[(tok * Hkv + kvh) * 128 + l + 64] = src[l + 64];
-        }
-        return;
-    }
+    // Every load that depends on no other load goes out first, so the wave
+    // waits on memory twice (these, then the cos/sin row of the position)
+    // instead of once per operand.
     const bool is_q = h < Hq;
     const uint16_t* wt = is_q ? qw : kw;
-    const float var = wave_sum(x1 * x1 + x2 * x2) / 128.0f;
-    const float r = rsqrtf(var + eps);
-    x1 = round_bf16(round_bf16(x1 * r) * bf16_to_f32(wt[l]));
-    x2 = round_bf16(round_bf16(x2 * r) * bf16_to_f32(wt[l + 64]));
     int64_t pos = positions[tok];
+    const int64_t slot = slots[tok];
+    const uint16_t xb1 = src[l], xb2 = src[l + 64];
+    const uint16_t wb1 = wt[l], wb2 = wt[l + 64];
     if (pos < 0 || pos >= max_position) pos = 0;  // out-of-table positions: never read outside the table
     const float* cs = cos_sin + pos * 128;
     const float c = cs[l], s = cs[64 + l];
+    float x1 = bf16_to_f32(xb1), x2 = bf16_to_f32(xb2);
+    if (h >= Hq + Hkv) {  // value head: copy to its slot (and v_out)
+        const int kvh = h - Hq - Hkv;
+        if (slot >= 0 && slot < num_slots) {
+            uint16_t* dst = v_cache + (slot * Hkv + kvh) * 128;
+            dst[l] = xb1;
+            dst[l + 64] = xb2;
+        }
+        if (v_out) {
+            v_out[(tok * Hkv + kvh) * 128 + l] = xb1;
+            v_out[(tok * Hkv + kvh) * 128 + l + 64] = xb2;
+        }
+        return;
+    }
+    const float var = wave_sum(x1 * x1 + x2 * x2) / 128.0f;
+    const float r = rsqrtf(var + eps);
+    x1 = round_bf16(round_bf16(x1 * r) * bf16_to_f32(wb1));
+    x2 = round_bf16(round_bf16(x2 * r) * bf16_to_f32(wb2));
     const float a = x1 * c, b = x2 * s, d = x2 * c, e = x1 * s;
     const uint16_t y1 = (uint16_t)f32_to_bf16_rne(a - b);
     const uint16_t y2 = (uint16_t)f32_to_bf16_rne(d + e);
@@ -116,7 +121,6 @@ qk_norm_rope_store(const uint16_t* __restrict__ qkv, int64_t qkv_row, int T, int
         dst[l + 64] = y2;
     } else {
         const int kvh = h - Hq;
-        const int64_t slot = slots[tok];
         if (slot >= 0 && slot < num_slots) {
             uint16_t* dst = k_cache + (slot * Hkv + kvh) * 128;
             dst[l] = y1;
