@@ -219,7 +219,8 @@ int nv4_w4a16_dequant(const int32_t* qweight, const int32_t* qzeros, const void*
  *   k/v_cache     bf16 [num_blocks, block_size, Hkv, 128]
  *   block_tables  int32 [B, max_blocks]: the first ceil(context_lens[b]/block_size)
  *                 entries of row b are valid block indices
- *   context_lens  int32 [B], 1 <= context_lens[b] <= max_context
+ *   context_lens  int32 [B], context_lens[b] <= max_context; a row with
+ *                 context_lens[b] <= 0 (empty context) gets an output of zeros
  *   out           bf16 [B, Hq, 128] (contiguous)
  *   workspace     fp32 scratch of at least B*Hq*S*(128+2)*4 bytes, S = ceil(max_context/256)
  * Hq / Hkv in {1, 2, 4}; softmax(scale * q.K^T) V with fp32 arithmetic.

@@ -82,9 +82,11 @@ qk_norm_rope_store(const uint16_t* __restrict__ qkv, int64_t qkv_row, int T, int
     const int h = (int)(item % heads);
     const int l = threadIdx.x & 63;
     const uint16_t* src = qkv + tok * qkv_row + (int64_t)h * 128;
-    // Every load that depends on no other load goes out first, so the wave
-    // waits on memory twice (these, then the cos/sin row of the position)
-    // instead of once per operand.
+    // Every load that depends on no other load is written first.  The
+    // compiler still moves the position and norm-weight loads into the
+    // query/key path, so the wave waits on memory three times (the head
+    // values and slot, the position with the norm weights, then the cos/sin
+    // row of the position) instead of once per operand.
     const bool is_q = h < Hq;
     const uint16_t* wt = is_q ? qw : kw;
     int64_t pos = positions[tok];

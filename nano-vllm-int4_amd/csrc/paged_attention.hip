@@ -52,7 +52,15 @@ pa_split(const uint16_t* __restrict__ q, int64_t q_row, const uint16_t* __restri
     const int Hq = Hkv * G;
     const int ctx = min(context_lens[b], max_ctx);  // never past the block table's row
     const int start = s * PA_SPLIT;
-    if (start >= ctx) return;  // nothing of this sequence here; pass 2 skips the split
+    if (start >= ctx) {
+        // Nothing of this sequence here; pass 2 skips the split.  An empty
+        // context (ctx <= 0) with a single split has no pass 2: its output
+        // is defined as zeros.
+        if (S == 1)
+            for (int e = threadIdx.x; e < G * PA_D; e += PA_THREADS)
+                out[((int64_t)b * Hq + kvh * G + e / PA_D) * PA_D + e % PA_D] = 0;
+        return;
+    }
     const int end = min(start + PA_SPLIT, ctx);
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -292,7 +300,8 @@ pa_merge(const int32_t* __restrict__ context_lens, const float* __restrict__ par
             }
         }
         uint16_t* o = out + ((int64_t)b * Hq + hq) * PA_D + 2 * lane;
-        *reinterpret_cast<uint32_t*>(o) = f32_to_bf16_rne(O0 / L) | (f32_to_bf16_rne(O1 / L) << 16);
+        // n == 0 (an empty context): L == 0 and the output is zeros.
+        *reinterpret_cast<uint32_t*>(o) = n > 0 ? f32_to_bf16_rne(O0 / L) | (f32_to_bf16_rne(O1 / L) << 16) : 0u;
         return;
     }
     const int n = min(S, (min(context_lens[b], max_ctx) + PA_SPLIT - 1) / PA_SPLIT);
@@ -343,7 +352,7 @@ pa_merge(const int32_t* __restrict__ context_lens, const float* __restrict__ par
         }
     }
     uint16_t* o = out + ((int64_t)b * Hq + hq) * PA_D + 2 * lane;
-    *reinterpret_cast<uint32_t*>(o) = f32_to_bf16_rne(O0 / L) | (f32_to_bf16_rne(O1 / L) << 16);
+    *reinterpret_cast<uint32_t*>(o) = n > 0 ? f32_to_bf16_rne(O0 / L) | (f32_to_bf16_rne(O1 / L) << 16) : 0u;
 }
 
 template <int G>

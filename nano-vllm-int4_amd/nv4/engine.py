@@ -116,6 +116,17 @@ class Engine:
         base = seq_slot * self.blocks_per_seq * self.block_size
         return list(range(base + start, base + end))
 
+    def _check_fits(self, seq_slots, lengths) -> None:
+        """Every sequence slot must exist and every length fit the slot's run
+        of blocks: a longer sequence would write its keys and values into the
+        next slot's blocks and attend to a truncated context.  Host lists
+        only, so the check costs no device synchronisation."""
+        for s, n in zip(seq_slots, lengths):
+            if not 0 <= s < self.max_num_seqs:
+                raise ValueError(f"sequence slot {s} outside [0, {self.max_num_seqs})")
+            if not 1 <= n <= self.max_model_len:
+                raise ValueError(f"sequence length {n} outside [1, max_model_len={self.max_model_len}]")
+
     def _to_dev(self, values, dtype):
         return torch.tensor(values, dtype=dtype, pin_memory=True).to(self.device, non_blocking=True)
 
@@ -126,6 +137,7 @@ class Engine:
     @torch.inference_mode()
     def prefill(self, seq_slot: int, token_ids: list[int], temperature: float) -> int:
         n = len(token_ids)
+        self._check_fits([seq_slot], [n])
         input_ids = self._to_dev(token_ids, torch.int64)
         positions = self._to_dev(list(range(n)), torch.int64)
         cu = self._to_dev([0, n], torch.int32)
@@ -138,6 +150,9 @@ class Engine:
 
     def _set_decode_inputs(self, seq_slots, last_tokens, lengths):
         bs = len(seq_slots)
+        if len(last_tokens) != bs or len(lengths) != bs or bs < 1:
+            raise ValueError("decode needs one last token and one length per sequence slot")
+        self._check_fits(seq_slots, lengths)
         input_ids = self._to_dev(last_tokens, torch.int64)
         positions = self._to_dev([n - 1 for n in lengths], torch.int64)
         context_lens = self._to_dev(lengths, torch.int32)

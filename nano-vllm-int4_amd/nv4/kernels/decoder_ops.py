@@ -72,6 +72,9 @@ def qk_norm_rope_store(qkv, num_heads, num_kv_heads, q_norm_w, k_norm_w, cos_sin
         raise TypeError("cos_sin must be a contiguous FP32 [max_position, 128] table")
     if positions.dtype != torch.int64 or tuple(positions.shape) != (T,):
         raise TypeError("positions must be int64 [T]")
+    for w in (q_norm_w, k_norm_w):
+        if w.dtype != torch.bfloat16 or tuple(w.shape) != (D,) or not w.is_contiguous():
+            raise TypeError("q/k norm weights must be contiguous BF16 [128]")
     max_position = cos_sin.numel() // D
     dev = qkv.device
     q = torch.empty((T, num_heads, D), dtype=torch.bfloat16, device=dev)

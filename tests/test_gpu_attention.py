@@ -11,7 +11,8 @@ chunked form), and queries read as a strided view of a fused qkv tensor;
 against softmax(scale q.K^T) V computed in fp32.  Bar:
 |out - ref| <= 1e-2 + 1e-2 |ref| (bf16 output).  Prefill attention (causal
 GQA through the fused flash SDPA kernel) against the same fp32 reference on
-short packed sequences, same bar.
+packed sequences up to the 4096-token prompt of the end-to-end workload,
+same bar.  Rows with an empty context give zeros.
 """
 import math
 
@@ -129,9 +130,28 @@ def test_single_split_writes_output_directly():
     check(out, reference(q, kc, vc, bt, cl, 0.1), "one split")
 
 
-def test_prefill_attention_flash():
+@pytest.mark.parametrize("max_ctx", [256, 4352])
+def test_empty_context_rows_are_zero(max_ctx):
+    """A row whose context length is 0 (or negative) has nothing to attend
+    to: its output is defined as zeros, with one split (no merge pass) and
+    with several; the other rows are unaffected."""
+    lens = [100, 0, 257, 1]
+    q, kc, vc, bt, cl = make_case(4, 32, 8, 256, lens, seed=max_ctx + 1)
+    if max_ctx == 256:
+        lens[2], cl[2] = 256, 256
+    cl[3] = -5
+    out = torch.full((4, 32, 128), float("nan"), dtype=torch.bfloat16, device=DEV)
+    bt = torch.cat([bt, torch.zeros(4, max(0, max_ctx // 256 - bt.shape[1]), dtype=torch.int32, device=DEV)], 1)
+    paged_decode_attention(q, kc, vc, bt.contiguous(), cl, 0.1, out=out, max_context=max_ctx)
+    torch.cuda.synchronize()
+    assert torch.equal(out[1], torch.zeros_like(out[1])) and torch.equal(out[3], torch.zeros_like(out[3]))
+    live = [0, 2]
+    check(out[live], reference(q[live], kc, vc, bt[live], cl[live], 0.1), f"live rows max_ctx={max_ctx}")
+
+
+@pytest.mark.parametrize("lens", [[1, 17, 300], [4096, 33]])
+def test_prefill_attention_flash(lens):
     g = torch.Generator(device=DEV).manual_seed(3)
-    lens = [1, 17, 300]
     T = sum(lens)
     q = torch.randn(T, 32, 128, generator=g, device=DEV).to(torch.bfloat16)
     k = torch.randn(T, 8, 128, generator=g, device=DEV).to(torch.bfloat16)

@@ -146,6 +146,36 @@ def test_qk_norm_rope_store(T, Hq, Hkv):
     assert torch.equal(q2, q) and torch.equal(kc2, kc) and torch.equal(vc2, vc)
 
 
+def test_qk_norm_rope_store_out_of_table_positions_read_row_zero():
+    """Positions outside [0, max_position) are documented to rotate with row
+    0 of the table (cos 1, sin 0: no rotation) instead of reading past it;
+    callers keep positions inside the table."""
+    g = torch.Generator(device=DEV).manual_seed(77)
+    Hq, Hkv, T = 8, 2, 4
+    qkv = (torch.randn(T, (Hq + 2 * Hkv) * 128, generator=g, device=DEV) * 2).to(torch.bfloat16)
+    qw = (1 + 0.2 * torch.randn(128, generator=g, device=DEV)).to(torch.bfloat16)
+    kw = (1 + 0.2 * torch.randn(128, generator=g, device=DEV)).to(torch.bfloat16)
+    table = rope_table(64)
+    bad = torch.tensor([64, 1000, -1, 2**40], dtype=torch.int64, device=DEV)
+    zero = torch.zeros(T, dtype=torch.int64, device=DEV)
+    q_bad, k_bad, v_bad = qk_norm_rope_store(qkv, Hq, Hkv, qw, kw, table, bad, EPS, return_kv=True)
+    q_0, k_0, v_0 = qk_norm_rope_store(qkv, Hq, Hkv, qw, kw, table, zero, EPS, return_kv=True)
+    assert torch.equal(q_bad, q_0) and torch.equal(k_bad, k_0) and torch.equal(v_bad, v_0)
+
+
+def test_qk_norm_rope_store_rejects_bad_norm_weights():
+    qkv = torch.zeros(2, (4 + 2) * 128, dtype=torch.bfloat16, device=DEV)
+    table = rope_table(16)
+    pos = torch.zeros(2, dtype=torch.int64, device=DEV)
+    good = torch.ones(128, dtype=torch.bfloat16, device=DEV)
+    for bad in (torch.ones(128, dtype=torch.float32, device=DEV), torch.ones(64, dtype=torch.bfloat16, device=DEV),
+                torch.ones(256, dtype=torch.bfloat16, device=DEV)[::2]):
+        with pytest.raises(TypeError):
+            qk_norm_rope_store(qkv, 4, 1, bad, good, table, pos, EPS)
+        with pytest.raises(TypeError):
+            qk_norm_rope_store(qkv, 4, 1, good, bad, table, pos, EPS)
+
+
 @pytest.mark.parametrize("rows,I", [(1, 12288), (32, 12288), (70, 12288), (3, 8)])
 def test_silu_mul(rows, I):
     g = torch.Generator(device=DEV).manual_seed(rows + I)
