@@ -44,6 +44,17 @@ class W4A4Linear(nn.Module):
             self.weights_tiled = True
         return self
 
+    @torch.no_grad()
+    def assign_quantized_(self, packed: torch.Tensor, scale: torch.Tensor, signs: torch.Tensor) -> "W4A4Linear":
+        """Install checkpoint tensors in the reference layout (packed int8
+        [out, in/2], bf16 scales [out, in/128], int8 signs [in]) onto this
+        module's device; on a GPU the weights are then tiled in place."""
+        self.packed_weight.copy_(packed)
+        self.weight_scale.copy_(scale)
+        self.signs.copy_(signs)
+        self.weights_tiled = False
+        return self.tile_weights_()
+
     def _save_to_state_dict(self, destination, prefix, keep_vars):
         super()._save_to_state_dict(destination, prefix, keep_vars)
         if self.weights_tiled:

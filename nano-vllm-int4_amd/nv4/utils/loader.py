@@ -35,22 +35,41 @@ def resolve_model_path(path: str) -> str:
     return snapshot_download(repo_id=path, local_files_only=True)
 
 
-def load_model(model: nn.Module, path: str):
-    path = resolve_model_path(path)
-    packed_modules_mapping = getattr(model, "packed_modules_mapping", {})
-    for file in sorted(glob(os.path.join(path, "*.safetensors"))):
-        with safe_open(file, "pt", "cpu") as f:
-            for weight_name in f.keys():
-                if weight_name.endswith(".g_idx"):
-                    continue
-                for k, (v, shard_id) in packed_modules_mapping.items():
-                    if k in weight_name:
-                        param = model.get_parameter(weight_name.replace(k, v))
-                        param.weight_loader(param, f.get_tensor(weight_name), shard_id)
-                        break
-                else:
-                    param = model.get_parameter(weight_name)
-                    getattr(param, "weight_loader", default_weight_loader)(param, f.get_tensor(weight_name))
+def _destination(weight_name: str, mapping: dict):
+    """(parameter name, shard id) a checkpoint tensor is loaded into: the
+    first ``packed_modules_mapping`` key contained in the name routes it to
+    the fused parameter with that key's shard id; any other tensor goes to
+    the parameter of its own name (shard id None)."""
+    key = next((k for k in mapping if k in weight_name), None)
+    if key is None:
+        return weight_name, None
+    fused, shard_id = mapping[key]
+    return weight_name.replace(key, fused), shard_id
+
+
+def checkpoint_tensors(root: str):
+    """(name, CPU tensor) for every tensor of every ``*.safetensors`` file
+    under ``root``, file by file in name order; GPTQ ``g_idx`` tensors
+    (static groups: always k // 128) are not yielded."""
+    for path in sorted(glob(os.path.join(root, "*.safetensors"))):
+        with safe_open(path, "pt", "cpu") as f:
+            for name in f.keys():
+                if not name.endswith(".g_idx"):
+                    yield name, f.get_tensor(name)
+
+
+def load_model(model: nn.Module, path: str) -> None:
+    """Copy every checkpoint tensor into ``model``: fused q/k/v and gate/up
+    parameters through their ``weight_loader`` with the shard id, the rest
+    through theirs (or a plain copy)."""
+    mapping = getattr(model, "packed_modules_mapping", {})
+    for name, tensor in checkpoint_tensors(resolve_model_path(path)):
+        target, shard_id = _destination(name, mapping)
+        param = model.get_parameter(target)
+        if shard_id is None:
+            getattr(param, "weight_loader", default_weight_loader)(param, tensor)
+        else:
+            param.weight_loader(param, tensor, shard_id)
 
 
 def load_w4a16_model(model: nn.Module, path: str) -> nn.Module:

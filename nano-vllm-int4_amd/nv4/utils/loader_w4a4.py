@@ -46,87 +46,134 @@ GROUPS = (
     ("mlp", "gate_up_proj", ("gate_proj", "up_proj"), "gate_up"),
     ("mlp", "down_proj", ("down_proj",), "down"),
 )
+# Quantization settings the kernels implement, as the manifest must state
+# them (``is`` comparison for the booleans the format requires literally).
+_CONTRACT = (
+    ("group_size", lambda v: v == 128),
+    ("static_groups", bool),
+    ("runtime_column_permutation", lambda v: v is False),
+    ("evaluation_activation_group_size", lambda v: v == 128),
+    ("evaluation_activation_clipping", lambda v: v == 0.9),
+    ("layout_version", lambda v: v == LAYOUT_VERSION),
+)
 
 
-def sha256(path) -> str:
-    digest = hashlib.sha256()
-    with Path(path).open("rb") as handle:
-        for chunk in iter(lambda: handle.read(8 * 1024**2), b""):
-            digest.update(chunk)
-    return digest.hexdigest()
+def sha256(path, block: int = 1 << 24) -> str:
+    """Hex SHA-256 of a file, read in ``block``-byte pieces into one buffer."""
+    digest, buf = hashlib.sha256(), bytearray(block)
+    view = memoryview(buf)
+    with open(path, "rb", buffering=0) as f:
+        while True:
+            n = f.readinto(view)
+            if not n:
+                return digest.hexdigest()
+            digest.update(view[:n])
 
 
-def _check_contract(manifest: dict) -> dict:
-    cfg = manifest.get("config", {})
-    if manifest.get("format") != FORMAT or not manifest.get("complete"):
-        raise ValueError("Incomplete or unsupported W4A4 checkpoint")
-    if (cfg.get("group_size") != 128 or not cfg.get("static_groups")
-            or cfg.get("runtime_column_permutation") is not False
-            or cfg.get("evaluation_activation_group_size") != 128
-            or cfg.get("evaluation_activation_clipping") != 0.9
-            or cfg.get("layout_version") != LAYOUT_VERSION):
-        raise ValueError("Checkpoint quantization contract differs from the native kernel")
-    return cfg
+class Manifest:
+    """``manifest.json`` of a checkpoint directory, checked against the
+    format on construction; the other checks run when their inputs are
+    known (base directory, model depth, shard files)."""
+
+    def __init__(self, checkpoint: Path):
+        self.root = checkpoint
+        self.data = json.loads((checkpoint / "manifest.json").read_text())
+        if self.data.get("format") != FORMAT or not self.data.get("complete"):
+            raise ValueError("Incomplete or unsupported W4A4 checkpoint")
+        self.config = self.data.get("config", {})
+        if not all(ok(self.config.get(key)) for key, ok in _CONTRACT):
+            raise ValueError("Checkpoint quantization contract differs from the native kernel")
+
+    def require_base(self, base: Path) -> None:
+        if sha256(base / "config.json") != self.config.get("model_config_sha256"):
+            raise ValueError("Base model config does not match the calibrated checkpoint")
+
+    def require_depth(self, num_layers: int) -> None:
+        if sorted(self.data.get("layers", {})) != sorted(map(str, range(num_layers))):
+            raise ValueError("Checkpoint layer set does not match the model")
+
+    def shard(self, index: int) -> Path:
+        """The verified shard file of layer ``index``: inside the checkpoint
+        directory and hashing to its manifest entry."""
+        entry = self.data["layers"][str(index)]
+        path = (self.root / entry["file"]).resolve()
+        if not path.is_relative_to(self.root) or sha256(path) != entry["sha256"]:
+            raise ValueError(f"Invalid checkpoint shard: layer {index}")
+        return path
+
+
+def _load_base_parameters(model, base: Path) -> None:
+    """Copy the BF16 parameters of the quantized model (embeddings, norms,
+    LM head) from the base directory; the base files' projection weights
+    are never read (their names match no parameter).  The first shard that
+    holds a name supplies it."""
+    params = dict(model.named_parameters())
+    found: set[str] = set()
+    for path in sorted(base.glob("*.safetensors")):
+        with safe_open(str(path), framework="pt", device="cpu") as f:
+            for name in sorted((set(f.keys()) & params.keys()) - found):
+                tensor, param = f.get_tensor(name), params[name]
+                if (tensor.dtype, param.dtype) != (torch.bfloat16, torch.bfloat16):
+                    raise ValueError(f"Expected BF16 base parameter: {name}")
+                getattr(param, "weight_loader", default_weight_loader)(param, tensor)
+                found.add(name)
+    if found != params.keys():
+        raise ValueError(f"Missing base parameters: {sorted(params.keys() - found)}")
+
+
+def _checked_signs(tensor, module: W4A4Linear, where: str):
+    ok = tensor.dtype == torch.int8 and tuple(tensor.shape) == (module.in_features,)
+    if not ok or bool(((tensor != 1) & (tensor != -1)).any()):
+        raise ValueError(f"Invalid RHT signs at layer {where}")
+    return tensor
+
+
+def _checked_weights(codes, scales, module: W4A4Linear, where: str):
+    """Concatenate the source projections along N and check the result
+    against the fused module's buffers."""
+    codes, scales = torch.cat(codes), torch.cat(scales)
+    shapes_ok = (codes.dtype == torch.int8 and codes.shape == module.packed_weight.shape
+                 and scales.dtype == torch.bfloat16 and scales.shape == module.weight_scale.shape)
+    if not shapes_ok or not bool((torch.isfinite(scales) & (scales > 0)).all()):
+        raise ValueError(f"Invalid weight/scale at layer {where}")
+    return codes, scales
+
+
+def _load_layer(index: int, layer, shard: Path) -> int:
+    """Fill the four fused W4A4 modules of one decoder layer from its shard;
+    returns the number of source projections read."""
+    read = 0
+    with safe_open(str(shard), framework="pt", device="cpu") as f:
+        for parent, target, sources, sign_key in GROUPS:
+            module = getattr(getattr(layer, parent), target)
+            where = f"{index}/{target}"
+            if not isinstance(module, W4A4Linear):
+                raise TypeError(f"Expected W4A4Linear at layer {where}")
+            signs = _checked_signs(f.get_tensor(f"signs.{sign_key}"), module, where)
+            codes, scales = _checked_weights([f.get_tensor(f"{parent}.{s}.packed") for s in sources],
+                                             [f.get_tensor(f"{parent}.{s}.scale") for s in sources], module, where)
+            module.assign_quantized_(codes, scales, signs)
+            read += len(sources)
+    return read
 
 
 @torch.no_grad()
-def load_w4a4_model(model, model_path, checkpoint_path):
+def load_w4a4_model(model, model_path, checkpoint_path) -> dict:
+    """Load a calibrated W4A4 checkpoint into a ``Qwen3ForCausalLM`` built
+    with ``use_w4a4``: the manifest is checked against the kernels'
+    quantization contract and the base model's ``config.json``, the BF16
+    parameters come from the base directory, and each layer's projections
+    from its verified shard (already in the MFMA-tiled order on a GPU
+    model).  Returns the quantization summary the runner reports."""
     base = Path(resolve_model_path(str(model_path)))
-    checkpoint = Path(checkpoint_path).resolve()
-    manifest = json.loads((checkpoint / "manifest.json").read_text())
-    cfg = _check_contract(manifest)
-    if sha256(base / "config.json") != cfg.get("model_config_sha256"):
-        raise ValueError("Base model config does not match the calibrated checkpoint")
+    manifest = Manifest(Path(checkpoint_path).resolve())
+    manifest.require_base(base)
     layers = model.model.layers
-    if set(manifest.get("layers", {})) != {str(i) for i in range(len(layers))}:
-        raise ValueError("Checkpoint layer set does not match the model")
-
-    # Only embeddings, head and norms are parameters of the quantized model;
-    # the base files' projection weights are skipped unread.
-    remaining = dict(model.named_parameters())
-    for shard in sorted(base.glob("*.safetensors")):
-        with safe_open(str(shard), framework="pt", device="cpu") as handle:
-            for name in handle.keys():
-                if name in remaining:
-                    param = remaining.pop(name)
-                    value = handle.get_tensor(name)
-                    if value.dtype != torch.bfloat16 or param.dtype != torch.bfloat16:
-                        raise ValueError(f"Expected BF16 base parameter: {name}")
-                    getattr(param, "weight_loader", default_weight_loader)(param, value)
-    if remaining:
-        raise ValueError(f"Missing base parameters: {sorted(remaining)}")
-
-    count = 0
-    for index, layer in enumerate(layers):
-        entry = manifest["layers"][str(index)]
-        shard = (checkpoint / entry["file"]).resolve()
-        if not shard.is_relative_to(checkpoint) or sha256(shard) != entry["sha256"]:
-            raise ValueError(f"Invalid checkpoint shard: layer {index}")
-        with safe_open(str(shard), framework="pt", device="cpu") as handle:
-            for parent, target, sources, sign_name in GROUPS:
-                module = getattr(getattr(layer, parent), target)
-                if not isinstance(module, W4A4Linear):
-                    raise TypeError(f"Expected W4A4Linear at layer {index}/{target}")
-                signs = handle.get_tensor(f"signs.{sign_name}")
-                if (signs.dtype != torch.int8 or signs.shape != module.signs.shape
-                        or not torch.all((signs == 1) | (signs == -1))):
-                    raise ValueError(f"Invalid RHT signs at layer {index}/{target}")
-                packed = torch.cat([handle.get_tensor(f"{parent}.{name}.packed") for name in sources])
-                scale = torch.cat([handle.get_tensor(f"{parent}.{name}.scale") for name in sources])
-                if (packed.dtype != torch.int8 or packed.shape != module.packed_weight.shape
-                        or scale.dtype != torch.bfloat16 or scale.shape != module.weight_scale.shape
-                        or not torch.isfinite(scale).all() or not torch.all(scale > 0)):
-                    raise ValueError(f"Invalid weight/scale at layer {index}/{target}")
-                module.packed_weight.copy_(packed)
-                module.weight_scale.copy_(scale)
-                module.signs.copy_(signs)
-                module.weights_tiled = False  # the buffer now holds the reference layout
-                count += len(sources)
-    for module in model.modules():  # decode-kernel weight order (GPU modules; bit-identical results)
-        if isinstance(module, W4A4Linear):
-            module.tile_weights_()
-    return {"format": FORMAT, "projections": count, "native_linear_modules": len(layers) * 4,
-            "checkpoint_manifest_sha256": sha256(checkpoint / "manifest.json"),
+    manifest.require_depth(len(layers))
+    _load_base_parameters(model, base)
+    projections = sum(_load_layer(i, layer, manifest.shard(i)) for i, layer in enumerate(layers))
+    return {"format": FORMAT, "projections": projections, "native_linear_modules": 4 * len(layers),
+            "checkpoint_manifest_sha256": sha256(manifest.root / "manifest.json"),
             "weight_group_size": 128, "activation_group_size": 128, "activation_clipping": 0.9,
             "scale_dtype": "bfloat16", "split_k": False}
 
