@@ -69,6 +69,7 @@ extern "C" {
 #define NV4_E_LAYOUT (-4)    /* unknown rotation layout */
 #define NV4_E_DTYPE (-5)     /* unknown dtype code */
 #define NV4_E_GROUP (-6)     /* unsupported quantization group size */
+#define NV4_E_SCRATCH (-7)   /* needs more device scratch than the allocation-free entry point has */
 
 /* Rotation layouts for nv4_rht_quant_pack. */
 #define NV4_LAYOUT_REFERENCE 0 /* "row_DH_paley12_kron_sylvester_v1": full-width
@@ -230,6 +231,29 @@ int nv4_paged_decode_attention(const void* q, int64_t q_row_stride, const void* 
                                void* out, float* workspace, int64_t workspace_bytes, int64_t B, int64_t Hq,
                                int64_t Hkv, int64_t D, int64_t block_size, int64_t max_context, float scale,
                                void* stream);
+
+/*
+ * nv4_paged_decode_attention without a workspace argument.  No counterpart in
+ * the reference: it is for callers that cannot allocate device memory (code
+ * under HIP-graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  The split partials go to a device array of the library,
+ * NV4_PA_SCRATCH_BYTES (16 MiB) per GPU, held from the first call on that GPU
+ * until the process ends; nothing is allocated or freed by the call.  A call
+ * needing more than that (B*Hq*S*(128+2)*4 bytes with S =
+ * ceil(max_context/256) > 1) returns NV4_E_SCRATCH before launching anything.
+ * Every call on one GPU shares that GPU's array: calls that overlap in time on
+ * one GPU (different streams without ordering between them) race on it and
+ * must not be issued.  Same arguments, rules and results (bit for bit) as
+ * nv4_paged_decode_attention.  The first call on a device looks up the array's
+ * address (hipGetSymbolAddress) with that device current; make it outside
+ * graph capture.
+ */
+#define NV4_PA_SCRATCH_BYTES (16ll << 20)
+int nv4_paged_decode_attention_noalloc(const void* q, int64_t q_row_stride, const void* k_cache,
+                                       const void* v_cache, const int32_t* block_tables, int64_t max_blocks,
+                                       const int32_t* context_lens, void* out, int64_t B, int64_t Hq, int64_t Hkv,
+                                       int64_t D, int64_t block_size, int64_t max_context, float scale,
+                                       void* stream);
 
 /*
  * RMSNorm over rows of H bf16 values (nanovllm/layers/layernorm.py:16-50):

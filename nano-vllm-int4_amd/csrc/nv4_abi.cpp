@@ -12,6 +12,7 @@ extern "C" const char* nv4_strerror(int code) {
         case NV4_E_LAYOUT: return "unknown rotation layout";
         case NV4_E_DTYPE: return "unknown dtype code";
         case NV4_E_GROUP: return "unsupported group size";
+        case NV4_E_SCRATCH: return "needs more device scratch than the allocation-free entry point has";
         default: return code > 0 ? "hip error" : "unknown error";
     }
 }

@@ -32,6 +32,8 @@
 //    2i+1 and every split's loads issued before the sums.
 #include "nv4_common.h"
 
+#include <mutex>
+
 namespace nv4 {
 namespace {
 
@@ -392,35 +394,111 @@ hipError_t pa_launch(const void* q, int64_t q_row, const void* kc, const void* v
 }  // namespace
 }  // namespace nv4
 
+// Device scratch of the allocation-free entry point
+// (nv4_paged_decode_attention_noalloc): the split partials live here instead
+// of in a caller's workspace.  Each device holds its own copy for the life of
+// the process; its address on a device comes from hipGetSymbolAddress (the
+// name itself is a host-side stand-in that must never reach a kernel).
+static __device__ __align__(256) float scratch[NV4_PA_SCRATCH_BYTES / sizeof(float)];
+
+namespace nv4 {
+namespace {
+
+// Argument rules shared by both entry points; on success *splits is S.
+int pa_check(const void* q, int64_t q_row_stride, const void* k_cache, const void* v_cache,
+             const int32_t* block_tables, int64_t max_blocks, const int32_t* context_lens, const void* out,
+             int64_t B, int64_t Hq, int64_t Hkv, int64_t D, int64_t block_size, int64_t max_context,
+             int64_t* splits) {
+    if (!q || !k_cache || !v_cache || !block_tables || !context_lens || !out) return NV4_E_NULL;
+    if (D != PA_D || B < 1 || Hkv < 1 || Hq < 1 || Hq % Hkv || block_size < 1 || max_blocks < 1 ||
+        max_context < 1 || max_context > max_blocks * block_size || max_context > (1 << 30) || B > 65535 ||
+        Hkv > 65535 || q_row_stride < Hq * D)
+        return NV4_E_SHAPE;
+    const int64_t G = Hq / Hkv;
+    if (G != 1 && G != 2 && G != 4) return NV4_E_SHAPE;  // the merge keeps 16 x G x 128 fp32 in LDS
+    if (reinterpret_cast<uintptr_t>(q) % 16 || reinterpret_cast<uintptr_t>(k_cache) % 16 ||
+        reinterpret_cast<uintptr_t>(v_cache) % 16 || reinterpret_cast<uintptr_t>(out) % 4 || q_row_stride % 8)
+        return NV4_E_ALIGN;
+    *splits = (max_context + PA_SPLIT - 1) / PA_SPLIT;
+    return NV4_OK;
+}
+
+int pa_run(const void* q, int64_t q_row_stride, const void* k_cache, const void* v_cache,
+           const int32_t* block_tables, int64_t max_blocks, const int32_t* context_lens, void* out, float* ws,
+           int64_t B, int64_t Hq, int64_t Hkv, int64_t block_size, int64_t max_context, int64_t S, float scale,
+           void* stream) {
+    const float qscale = scale * 1.4426950408889634f;  // log2(e): softmax in base 2
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    const int b = (int)B, hkv = (int)Hkv, bs = (int)block_size, s = (int)S, mb = (int)max_blocks;
+    switch (Hq / Hkv) {
+        case 1: return (int)pa_launch<1>(q, q_row_stride, k_cache, v_cache, block_tables, mb, context_lens, out, ws,
+                                         b, hkv, bs, s, (int)max_context, qscale, st);
+        case 2: return (int)pa_launch<2>(q, q_row_stride, k_cache, v_cache, block_tables, mb, context_lens, out, ws,
+                                         b, hkv, bs, s, (int)max_context, qscale, st);
+        default: return (int)pa_launch<4>(q, q_row_stride, k_cache, v_cache, block_tables, mb, context_lens, out,
+                                          ws, b, hkv, bs, s, (int)max_context, qscale, st);
+    }
+}
+
+// Device address of `scratch` on the current device, looked up once per
+// device (with that device current) and kept.
+constexpr int PA_MAX_DEVICES = 64;
+std::mutex g_scratch_mu;
+float* g_scratch_ptr[PA_MAX_DEVICES] = {};
+
+int scratch_on_current_device(float** ptr) {
+    int dev = -1;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return (int)e;
+    if (dev < 0 || dev >= PA_MAX_DEVICES) return NV4_E_SHAPE;
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void* p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return (int)e;
+        if (!p) return NV4_E_NULL;
+        g_scratch_ptr[dev] = static_cast<float*>(p);
+    }
+    *ptr = g_scratch_ptr[dev];
+    return NV4_OK;
+}
+
+}  // namespace
+}  // namespace nv4
+
 extern "C" int nv4_paged_decode_attention(const void* q, int64_t q_row_stride, const void* k_cache,
                                           const void* v_cache, const int32_t* block_tables, int64_t max_blocks,
                                           const int32_t* context_lens, void* out, float* workspace,
                                           int64_t workspace_bytes, int64_t B, int64_t Hq, int64_t Hkv, int64_t D,
                                           int64_t block_size, int64_t max_context, float scale, void* stream) {
     using namespace nv4;
-    if (!q || !k_cache || !v_cache || !block_tables || !context_lens || !out || !workspace) return NV4_E_NULL;
-    if (D != PA_D || B < 1 || Hkv < 1 || Hq < 1 || Hq % Hkv || block_size < 1 || max_blocks < 1 ||
-        max_context < 1 || max_context > max_blocks * block_size || max_context > (1 << 30) || B > 65535 ||
-        Hkv > 65535 ||
-        q_row_stride < Hq * D)
-        return NV4_E_SHAPE;
-    const int64_t G = Hq / Hkv;
-    if (G != 1 && G != 2 && G != 4) return NV4_E_SHAPE;  // the merge keeps 16 x G x 128 fp32 in LDS
-    const int64_t S = (max_context + PA_SPLIT - 1) / PA_SPLIT;
+    int64_t S = 0;
+    const int rc = pa_check(q, q_row_stride, k_cache, v_cache, block_tables, max_blocks, context_lens, out, B, Hq,
+                            Hkv, D, block_size, max_context, &S);
+    if (rc != NV4_OK) return rc;
+    if (!workspace) return NV4_E_NULL;
     if (workspace_bytes < B * Hq * S * (D + 2) * 4) return NV4_E_SHAPE;
-    if (reinterpret_cast<uintptr_t>(q) % 16 || reinterpret_cast<uintptr_t>(k_cache) % 16 ||
-        reinterpret_cast<uintptr_t>(v_cache) % 16 || reinterpret_cast<uintptr_t>(out) % 4 ||
-        reinterpret_cast<uintptr_t>(workspace) % 8 || q_row_stride % 8)
-        return NV4_E_ALIGN;
-    const float qscale = scale * 1.4426950408889634f;  // log2(e): softmax in base 2
-    hipStream_t st = static_cast<hipStream_t>(stream);
-    const int b = (int)B, hkv = (int)Hkv, bs = (int)block_size, s = (int)S, mb = (int)max_blocks;
-    switch (G) {
-        case 1: return (int)pa_launch<1>(q, q_row_stride, k_cache, v_cache, block_tables, mb, context_lens, out,
-                                         workspace, b, hkv, bs, s, (int)max_context, qscale, st);
-        case 2: return (int)pa_launch<2>(q, q_row_stride, k_cache, v_cache, block_tables, mb, context_lens, out,
-                                         workspace, b, hkv, bs, s, (int)max_context, qscale, st);
-        default: return (int)pa_launch<4>(q, q_row_stride, k_cache, v_cache, block_tables, mb, context_lens, out,
-                                          workspace, b, hkv, bs, s, (int)max_context, qscale, st);
-    }
+    if (reinterpret_cast<uintptr_t>(workspace) % 8) return NV4_E_ALIGN;
+    return pa_run(q, q_row_stride, k_cache, v_cache, block_tables, max_blocks, context_lens, out, workspace, B, Hq,
+                  Hkv, block_size, max_context, S, scale, stream);
+}
+
+extern "C" int nv4_paged_decode_attention_noalloc(const void* q, int64_t q_row_stride, const void* k_cache,
+                                                  const void* v_cache, const int32_t* block_tables,
+                                                  int64_t max_blocks, const int32_t* context_lens, void* out,
+                                                  int64_t B, int64_t Hq, int64_t Hkv, int64_t D, int64_t block_size,
+                                                  int64_t max_context, float scale, void* stream) {
+    using namespace nv4;
+    int64_t S = 0;
+    int rc = pa_check(q, q_row_stride, k_cache, v_cache, block_tables, max_blocks, context_lens, out, B, Hq, Hkv, D,
+                      block_size, max_context, &S);
+    if (rc != NV4_OK) return rc;
+    // Only the split partials (S > 1) use the scratch; their size is checked
+    // before anything is launched.
+    if (S > 1 && B * Hq * S * (D + 2) * 4 > NV4_PA_SCRATCH_BYTES) return NV4_E_SCRATCH;
+    float* ws = nullptr;
+    rc = scratch_on_current_device(&ws);
+    if (rc != NV4_OK) return rc;
+    return pa_run(q, q_row_stride, k_cache, v_cache, block_tables, max_blocks, context_lens, out, ws, B, Hq, Hkv,
+                  block_size, max_context, S, scale, stream);
 }

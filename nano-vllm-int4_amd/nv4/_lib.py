@@ -21,6 +21,8 @@ NV4_E_ALIGN = -3
 NV4_E_LAYOUT = -4
 NV4_E_DTYPE = -5
 NV4_E_GROUP = -6
+NV4_E_SCRATCH = -7
+PA_SCRATCH_BYTES = 16 << 20  # device scratch of nv4_paged_decode_attention_noalloc
 
 LAYOUT_REFERENCE = 0
 LAYOUT_BLOCK128 = 1
@@ -42,6 +44,8 @@ SIGNATURES = {
     "nv4_w4a16_dequant": ([_P, _P, _P, _P, _I, _I64, _I64, _I, _P], _I),
     "nv4_paged_decode_attention": ([_P, _I64, _P, _P, _P, _I64, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64,
                                     _I64, ctypes.c_float, _P], _I),
+    "nv4_paged_decode_attention_noalloc": ([_P, _I64, _P, _P, _P, _I64, _P, _P, _I64, _I64, _I64, _I64, _I64,
+                                            _I64, ctypes.c_float, _P], _I),
     "nv4_rmsnorm": ([_P, _P, _P, _P, _P, _I64, _I64, ctypes.c_float, _P], _I),
     "nv4_qk_norm_rope_store": ([_P, _I64, _I64, _I64, _I64, _P, _P, _P, _I64, _P, _P, _I64, _P, _P, _P, _P, _P,
                                 ctypes.c_float, _P], _I),
