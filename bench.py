@@ -20,8 +20,9 @@ Timing rules:
   between HIP events on the stream it runs on; its algorithmic bytes
   (M*K/2 + M*K/64 + N*K/2 + N*K/64 + 2*M*N per launch) over that time give
   the roofline fraction against the 8 TB/s HBM peak.
-* The CPU baseline is the repository's C oracle (the same chain), timed on
-  this host's cores on a bounded number of steps.
+* The CPU baseline is the repository's C oracle (the same chain, and one
+  entry per workload configuration), timed on this host's cores on a
+  bounded number of steps.
 * ``e2e_decode``: the decoder around the hot path, end to end -- the
   reference's latency benchmark (32 x 4096-token prompts, serial prefill,
   bs32 decode of 256 tokens with HIP-graph steps) on the Qwen3-8B-shaped
@@ -83,6 +84,9 @@ def parse_args():
     ap.add_argument("--no-e2e", action="store_true", help="skip the end-to-end bs32 decode of the decoder")
     ap.add_argument("--e2e-layers", type=int, default=36, help="decoder layers of the end-to-end model")
     ap.add_argument("--e2e-tokens", type=int, default=256, help="output tokens per request (end to end)")
+    ap.add_argument("--pmc-prefill", action="store_true",
+                    help="for rocprofv3 --pmc: three launches of the fp8 prefill GEMM at gate_up M=4096 "
+                         "(after its operand conversion) and three 256 MiB device copies, then exit")
     ap.add_argument("--pmc-pass", action="store_true",
                     help="for rocprofv3 --pmc: eager decode GEMM launches (3 rounds over the rotating sets) "
                          "and three plain 256 MiB device copies as the counter calibration, then exit")
@@ -168,16 +172,82 @@ def pmc_pass(torch, linear, R):
     print(f"pmc pass done: {3 * R * len(PROJECTIONS)} linear launches, 3 copies of {COPY_BYTES} bytes", flush=True)
 
 
+DECODE_GEMM_SOURCES = ("nano-vllm-int4_amd/csrc/w4a4_gemm.hip", "nano-vllm-int4_amd/csrc/nv4_common.h")
+
+
+def decode_gemm_source_sha():
+    """SHA-256 over the sources of the decode GEMM kernels (the recorded
+    counter traffic belongs to exactly these)."""
+    import hashlib
+    h = hashlib.sha256()
+    for rel in DECODE_GEMM_SOURCES:
+        h.update((ROOT / rel).read_bytes())
+    return h.hexdigest()
+
+
+def pmc_prefill(torch, W, dev):
+    """Kernels for a hardware-counter run of the prefill GEMM: the W4A4
+    grouped GEMM at gate_up M=4096 (K1 codes of seeded activations, MFMA-tiled
+    weights), three launches on the fp8 path (each: the operand conversion
+    kernel, then k2_prefill_f8), then three copies of COPY_BYTES for the
+    FETCH_SIZE / WRITE_SIZE calibration."""
+    import nv4
+    M, (N, K) = 4096, W.PROJECTIONS["gate_up"]
+    g = torch.Generator(device=dev)
+    g.manual_seed(W.BASE_SEED + 3000)
+    x = torch.randn(M, K, generator=g, device=dev).to(torch.bfloat16)
+    sg = torch.randint(0, 2, (K,), generator=g, device=dev, dtype=torch.int8) * 2 - 1
+    wp = nv4.tile_weights(torch.randint(-128, 128, (N, K // 2), generator=g, device=dev,
+                                        dtype=torch.int16).to(torch.int8))
+    sw = (0.005 + 0.015 * torch.rand(N, K // 128, generator=g, device=dev)).to(torch.bfloat16)
+    pk = torch.empty((M, K // 2), dtype=torch.int8, device=dev)
+    sc = torch.empty((M, K // 128), dtype=torch.bfloat16, device=dev)
+    nv4.rht_quant_pack(x, sg, out_packed=pk, out_scale=sc)
+    out = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+    for _ in range(3):
+        nv4.w4a4_grouped_gemm(pk, wp, sc, sw, out=out, weights_tiled=True, fp8=True)
+    src = torch.empty(COPY_BYTES, dtype=torch.uint8, device=dev)
+    dst = torch.empty_like(src)
+    src.fill_(1)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print("pmc prefill pass done: 3 fp8 prefill GEMMs at gate_up M=4096, 3 copies of "
+          f"{COPY_BYTES} bytes", flush=True)
+
+
 def measured_traffic():
     """HBM bytes per decode-GEMM launch from the committed counter summary
     (two rocprofv3 --pmc passes, FETCH_SIZE and WRITE_SIZE, scaled by the
-    copy calibration), or None when the summary is absent."""
+    copy calibration).  The summary records the hash of the kernel sources it
+    was measured on; when those sources have changed since, the figure is
+    stale and is reported as None with the reason."""
     path = ROOT / "profiles" / "decode_gemm_m32_traffic.json"
     try:
         with open(path) as f:
-            return json.load(f)
+            rec = json.load(f)
     except (OSError, ValueError):
-        return None
+        return {"bytes_per_launch": None, "source": "no counter summary committed"}
+    if rec.get("kernel_source_sha256") != decode_gemm_source_sha():
+        return {"bytes_per_launch": None,
+                "source": f"{path.name} was measured on other kernel sources (stale): re-run the --pmc passes"}
+    return rec
+
+
+def k2_medians(torch, gemm, R, rounds=9, replays=20):
+    """Per projection, the median over ``rounds`` rounds of the decode GEMM's
+    microseconds per launch (a graph of back-to-back launches over the R
+    rotating weight sets, replayed between HIP events), the projections in a
+    freshly shuffled order every round."""
+    import random
+    rng = random.Random(20261108)
+    samples = {p: [] for p in PROJECTIONS}
+    order = list(PROJECTIONS)
+    for _ in range(rounds):
+        rng.shuffle(order)
+        for p in order:
+            samples[p].append(graph_launch_us(torch, [lambda l=l, p=p: gemm(l, p) for l in range(R)], replays))
+    return {p: statistics.median(v) for p, v in samples.items()}
 
 
 # -------------------------------------------------------------- end to end
@@ -220,50 +290,95 @@ def e2e_decode(torch, layers, out_tokens):
 
 
 # ---------------------------------------------------------------- CPU leg
+def cpu_threads():
+    """Host threads for the CPU baseline: every core this process may run on
+    (its affinity set), bounded by OMP_NUM_THREADS when the host sets it (the
+    GPU box gives a job a 16-core share and says so there)."""
+    n = len(os.sched_getaffinity(0))
+    cap = os.environ.get("OMP_NUM_THREADS", "")
+    return min(n, int(cap)) if cap.isdigit() and int(cap) > 0 else n, n
+
+
+def cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def _median_time(fn, warmups=2, min_runs=5, seconds=2.0, max_runs=200):
+    for _ in range(warmups):
+        fn()
+    times = []
+    start = time.perf_counter()
+    while len(times) < min_runs or (time.perf_counter() - start < seconds and len(times) < max_runs):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    return statistics.median(times), len(times)
+
+
 def cpu_baseline(M, seconds):
+    """The oracle (the repository's C restatement of the reference's numerics,
+    OpenMP over rows) on this host's cores, on the same seeded workloads:
+    the bench step (the W4A4 chain of the four projections at M), and one
+    entry per workload configuration -- o_proj chain at M = 32, the W4A16
+    fused-QKV GEMM at M = 1 / 8 / 32, gate_up and down at M = 4096 (a
+    64-row sample, scaled by 4096 / 64: rows are independent in both K1 and
+    K2) and down at M = 32.  Medians of >= 5 runs after 2 warm-ups."""
     import numpy as np
     import torch
 
     import oracle
     from nv4 import workloads as W
 
-    threads = min(16, len(os.sched_getaffinity(0)))
+    threads, affinity = cpu_threads()
     torch.set_num_threads(threads)
 
     def bits(t):
         return t.contiguous().view(torch.int16).numpy().view(np.uint16)
-    cases = []
-    for p in PROJECTIONS:
-        c = W.w4a4_case(p, M)
-        cases.append((bits(c.x), c.signs.numpy(), c.w_packed.numpy(), bits(c.w_scale)))
 
-    def step():
-        for x, s, wp, sw in cases:
-            pk, sc = oracle.rht_quant_pack(x, s, threads=threads)
-            oracle.w4a4_gemm(pk, wp, sc, sw, threads=threads)
-    for _ in range(2):
-        step()
-    times = []
-    t_start = time.perf_counter()
-    while len(times) < 5 or (time.perf_counter() - t_start < seconds and len(times) < 200):
-        t0 = time.perf_counter()
-        step()
-        times.append(time.perf_counter() - t0)
-    model = "unknown"
-    try:
-        with open("/proc/cpuinfo") as f:
-            for line in f:
-                if line.startswith("model name"):
-                    model = line.split(":", 1)[1].strip()
-                    break
-    except OSError:
-        pass
-    med = statistics.median(times)
-    return {
+    def chain_fn(projections, rows):
+        cases = []
+        for p in projections:
+            c = W.w4a4_case(p, rows)
+            cases.append((bits(c.x), c.signs.numpy(), c.w_packed.numpy(), bits(c.w_scale)))
+
+        def run():
+            for x, sg, wp, sw in cases:
+                pk, sc = oracle.rht_quant_pack(x, sg, threads=threads)
+                oracle.w4a4_gemm(pk, wp, sc, sw, threads=threads)
+        return run
+
+    model = cpu_model()
+    med, n = _median_time(chain_fn(PROJECTIONS, M), seconds=seconds)
+    entry = {
         "value": round(med * 1e6, 1), "unit": "us/step", "cores": threads, "kind": "port",
-        "sample": (f"{len(times)} steps (after 2 warm-ups) of the oracle's W4A4 chain, M={M}, "
-                   f"qkv/o/gate_up/down, median; {threads} OpenMP threads on {model}"),
+        "sample": (f"{n} steps (after 2 warm-ups) of the oracle's W4A4 chain, M={M}, qkv/o/gate_up/down, "
+                   f"median; {threads} OpenMP threads (affinity {affinity}) on {model}"),
+        "cpu_model": model, "affinity_cores": affinity,
     }
+    configs = {}
+    med, n = _median_time(chain_fn(["o"], 32), seconds=1.0)
+    configs["config0_o_chain_M32"] = {"value_us": round(med * 1e6, 1), "runs": n}
+    for m16 in (1, 8, 32):
+        c = W.w4a16_case(m16)
+        args = (bits(c.x), c.qweight.numpy(), c.qzeros.numpy(), c.scales.numpy().view(np.uint16))
+        med, n = _median_time(lambda a=args: oracle.w4a16_gemm(*a, x_dtype=oracle.X_FP16, threads=threads),
+                              seconds=1.0)
+        configs[f"config1_w4a16_qkv_M{m16}"] = {"value_us": round(med * 1e6, 1), "runs": n}
+    for proj, key in (("gate_up", "config2_gate_up_M4096"), ("down", "config3_down_M4096")):
+        med, n = _median_time(chain_fn([proj], 64), seconds=2.0)
+        configs[key] = {"value_us": round(med * 1e6 * 4096 / 64, 1), "runs": n,
+                        "sample": "64 of 4096 rows (K1 + K2), scaled x64"}
+    med, n = _median_time(chain_fn(["down"], 32), seconds=1.0)
+    configs["config3_down_chain_M32"] = {"value_us": round(med * 1e6, 1), "runs": n}
+    entry["configs"] = configs
+    return entry
 
 
 # -------------------------------------------------------------------- main
@@ -282,6 +397,9 @@ def main():
     nv4._lib.load()  # raises if the HIP library is missing: there is no fallback
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    if args.pmc_prefill:
+        pmc_prefill(torch, W, dev)
+        return
     M, R = args.m, max(1, args.rotate)
     acts, sets = make_layer_sets(torch, W, M, R, dev)
     pk = {p: torch.empty((M, W.PROJECTIONS[p][1] // 2), dtype=torch.int8, device=dev) for p in PROJECTIONS}
@@ -302,6 +420,7 @@ def main():
     if args.pmc_pass:
         pmc_pass(torch, linear, R)
         return
+
 
     # Eager reference outputs of set 0, then one graph per weight set.
     step(0)
@@ -340,8 +459,7 @@ def main():
     # Dominant kernel: the decode GEMM, timed per projection over the rotating
     # weight sets (equal launch counts per projection, so the mean of the
     # per-projection averages is the kernel's average launch).
-    k2_us = {p: graph_launch_us(torch, [lambda l=l, p=p: gemm(l, p) for l in range(R)], replays=40)
-             for p in PROJECTIONS}
+    k2_us = k2_medians(torch, gemm, R, rounds=9, replays=20)
     avg_launch_us = statistics.mean(k2_us.values())
     avg_bytes = statistics.mean(k2_bytes(M, *W.PROJECTIONS[p]) for p in PROJECTIONS)
     achieved = avg_bytes / (avg_launch_us * 1e-6) / 1e9       # GB/s
@@ -378,8 +496,9 @@ def main():
             "traffic_source": (traffic or {}).get("source"),
             "avg_launch_us": round(avg_launch_us, 3), "algorithmic_bytes_per_launch": int(avg_bytes),
             "per_projection_us": {p: round(v, 3) for p, v in k2_us.items()},
-            "timing": (f"HIP events around 40 replays of a graph of {R} back-to-back launches per "
-                       "projection (one per weight set)"),
+            "timing": (f"median over 9 rounds (projections in shuffled order each round) of HIP events "
+                       f"around 20 replays of a graph of {R} back-to-back launches per projection (one per "
+                       "weight set)"),
         },
     }
 
