@@ -45,6 +45,8 @@ def lib():
         sigs = {
             "orc_rht_rows": [P, P, P, I64, I64, I, I],
             "orc_quantize_rows": [P, P, P, I64, I64, I64, I],
+            "orc_weight_quantize": [P, P, P, I64, I64, I64, ctypes.c_float, I, I],
+            "orc_weight_dequantize": [P, P, P, I64, I64, I64],
             "orc_pack_int4": [P, P, I64],
             "orc_unpack_int4": [P, P, I64],
             "orc_rht_quant_pack": [P, P, P, P, I64, I64, I, I],
@@ -177,6 +179,65 @@ def rht_quant_pack(x_bf16: np.ndarray, signs: np.ndarray, layout: int = LAYOUT_R
     _check(lib().orc_rht_quant_pack(_ptr(x), _ptr(s), _ptr(packed), _ptr(scales), M, K, layout, threads),
            "rht_quant_pack")
     return packed, scales
+
+
+# ------------------------------------------------------- weight quantization
+DIVISION_CPU, DIVISION_CUDA = 0, 1
+
+
+def weight_quantize(w, group: int = 128, clip: float = 1.0, division: int = DIVISION_CUDA,
+                    threads: int = 0):
+    """Round-to-nearest grouped quantizer of fp32 rows ``w`` [N,K].
+
+    ``grouped_quantize(w, group, clip)`` (benchmarks/kernel_bench_common.py:
+    36-42) and, at clip 1, ``quantize_groups`` (benchmarks/rht_gptq_grouped.py:
+    27-34; K need not be a multiple of ``group``) and ``quantize_rows``
+    (benchmarks/rht_reference.py:70-77, group = K).  ``division`` names the
+    device the reference ran the expression on: DIVISION_CUDA multiplies by
+    RN(1/7), DIVISION_CPU divides by 7.  Returns (int8 codes [N,K], bf16 scale
+    bits [N, ceil(K/group)]).
+    """
+    x = np.ascontiguousarray(w, dtype=np.float32)
+    N, K = x.shape
+    G = -(-K // group)
+    codes = np.empty((N, K), dtype=np.int8)
+    scales = np.empty((N, G), dtype=np.uint16)
+    _check(lib().orc_weight_quantize(_ptr(x), _ptr(codes), _ptr(scales), N, K, group, ctypes.c_float(clip),
+                                     division, threads), "weight_quantize")
+    return codes, scales
+
+
+def weight_dequantize(codes, scales_bf16, group: int = 128) -> np.ndarray:
+    """codes [N,K] x bf16 scale bits [N,ceil(K/group)] -> exact fp32 [N,K]
+    (benchmarks/rht_gptq_grouped.py:37-39)."""
+    c = np.ascontiguousarray(codes, dtype=np.int8)
+    s = np.ascontiguousarray(scales_bf16, dtype=np.uint16)
+    N, K = c.shape
+    if s.shape != (N, -(-K // group)):
+        raise ValueError("scale shape does not match codes and group")
+    out = np.empty((N, K), dtype=np.float32)
+    _check(lib().orc_weight_dequantize(_ptr(c), _ptr(s), _ptr(out), N, K, group), "weight_dequantize")
+    return out
+
+
+def error_stats(actual, reference) -> dict:
+    """Error summary of ``actual`` against ``reference``
+    (benchmarks/rht_reference.py:99-108).  As there, both are taken to fp32,
+    the difference and the squares are fp32 operations, and the squares are
+    summed in float64; the cosine's dot product is float64.  Returns relative
+    RMSE sqrt(sse/energy), max |d|, cosine, sse, reference energy and element
+    count, with denominators floored at 1e-30.  The float64 sums run in numpy's
+    pairwise order, so their last bits may differ from torch's reduction."""
+    a = np.ascontiguousarray(actual, dtype=np.float32).ravel()
+    r = np.ascontiguousarray(reference, dtype=np.float32).ravel()
+    d = a - r
+    sse = float(np.sum((d * d).astype(np.float64)))
+    energy = float(np.sum((r * r).astype(np.float64)))
+    own = float(np.sum((a * a).astype(np.float64)))
+    cosine = float(a.astype(np.float64) @ r.astype(np.float64)) / max(np.sqrt(own * energy), 1e-30)
+    return {"relative_rmse": float(np.sqrt(sse / max(energy, 1e-30))),
+            "max_abs": float(np.max(np.abs(d))) if d.size else 0.0,
+            "cosine": cosine, "sse": sse, "reference_energy": energy, "elements": int(d.size)}
 
 
 # ------------------------------------------------------------------- K2 path

@@ -22,6 +22,14 @@
  *   orc_quantize_rows   the reference known-answer list (ties, clip-7/0.9,
  *                       BF16-scale-before-codes boundary, zero and 1e-40
  *                       groups), brute force over all codes of a group.
+ *   orc_weight_quantize equals orc_quantize_rows at clip 0.9 with the CUDA
+ *                       division; the reference self-test's zero row; exact
+ *                       dyadic groups (codes recovered, zero error); every code
+ *                       a nearest grid point of its bf16 scale; the scale
+ *                       within half a bf16 ulp of mx*clip/7; torch's own CPU
+ *                       evaluation of the reference expression for the CPU
+ *                       division; ragged last group; two planted mistakes.
+ *   orc_weight_dequantize exact products against float64.
  *   orc_pack_int4       the reference packed-byte vector 98 ba dc fe 10 32 54 76.
  *   orc_w4a4_gemm       brute-force integer dots with exact-rational FMA
  *                       replay, constant-dyadic-scale reductions, float64
@@ -257,6 +265,72 @@ int orc_quantize_rows(const float* r, int8_t* codes, uint16_t* scales,
             quantize_group(r + m * K + g * group, codes + m * K + g * group,
                            scales + m * (K / group) + g, group);
     (void)threads;
+    return ORC_OK;
+}
+
+/* Round-to-nearest weight quantizer with static groups along K (RTN-G128).
+ * benchmarks/rht_gptq_grouped.py:27-34 (quantize_groups: each K-slice of
+ * `group` columns, the last one possibly shorter, through
+ * benchmarks/rht_reference.py:70-77 quantize_rows) and
+ * benchmarks/kernel_bench_common.py:36-42 (grouped_quantize with a clip):
+ *   mx = max|w| over the group; t = RN(mx * clip) then t / 7;
+ *   scale = mx == 0 ? 1 : bf16(max(t, 2^-126));
+ *   q = clamp(rint_even(w / fp32(scale)), -7, 7), IEEE division.
+ * The reference evaluates these lines with torch, whose `tensor / 7` is an
+ * IEEE division on the CPU but RN(t * RN(1/7)) on a CUDA device (division by
+ * a host scalar becomes a multiplication by its fp32 reciprocal), so the
+ * device the reference ran on is an argument: reciprocal = 0 for CPU tensors,
+ * 1 for CUDA tensors.  quantize_rows is clip = 1 (RN(mx * 1) = mx) and
+ * group = K.  w fp32 [N,K] -> codes int8 [N,K], scales bf16 [N,ceil(K/group)]. */
+int orc_weight_quantize(const float* w, int8_t* codes, uint16_t* scales, int64_t N, int64_t K,
+                        int64_t group, float clip, int reciprocal, int threads) {
+    if (!w || !codes || !scales || N < 0 || K < 1 || group < 1 || !(clip > 0.0f)) return ORC_EINVAL;
+    const int64_t G = (K + group - 1) / group;
+#ifdef _OPENMP
+    if (threads > 0) omp_set_num_threads(threads);
+#pragma omp parallel for schedule(static)
+#endif
+    for (int64_t n = 0; n < N; ++n) {
+        for (int64_t g = 0; g < G; ++g) {
+            const int64_t k0 = g * group, len = (k0 + group <= K) ? group : K - k0;
+            const float* r = w + n * K + k0;
+            float mx = 0.0f;
+            for (int64_t i = 0; i < len; ++i) { float v = fabsf(r[i]); if (v > mx) mx = v; }
+            uint16_t sb;
+            if (mx == 0.0f) {
+                sb = f32_to_bf16(1.0f);
+            } else {
+                float t = mx * clip;
+                t = reciprocal ? t * c_inv7() : t / 7.0f;
+                if (g_mutation == 6) t = reciprocal ? t / 7.0f : t * c_inv7();   /* the other device's division */
+                if (t < c_tiny()) t = c_tiny();
+                sb = f32_to_bf16(t);
+            }
+            const float s = bf16_to_f32(sb);
+            for (int64_t i = 0; i < len; ++i) {
+                float v = rintf(r[i] / s);
+                if (g_mutation == 7) v = truncf(r[i] / s);                     /* toward zero */
+                if (v > 7.0f) v = 7.0f;
+                if (v < -7.0f) v = -7.0f;
+                codes[n * K + k0 + i] = (int8_t)v;
+            }
+            scales[n * G + g] = sb;
+        }
+    }
+    (void)threads;
+    return ORC_OK;
+}
+
+/* codes [N,K] x bf16 scales [N,ceil(K/group)] -> fp32 [N,K]: the product of a
+ * code in [-8,7] and a bf16 value is exact in fp32
+ * (benchmarks/rht_gptq_grouped.py:37-39). */
+int orc_weight_dequantize(const int8_t* codes, const uint16_t* scales, float* out, int64_t N, int64_t K,
+                          int64_t group) {
+    if (!codes || !scales || !out || N < 0 || K < 1 || group < 1) return ORC_EINVAL;
+    const int64_t G = (K + group - 1) / group;
+    for (int64_t n = 0; n < N; ++n)
+        for (int64_t k = 0; k < K; ++k)
+            out[n * K + k] = (float)codes[n * K + k] * bf16_to_f32(scales[n * G + k / group]);
     return ORC_OK;
 }
 

@@ -216,6 +216,52 @@ def test_k2_chain_qwen3_shapes_m4096_sampled(proj, tiled, fp8):
     assert_bits_equal(bf16_bits(out)[rows], o_ref, f"{proj} M=4096 sampled rows")
 
 
+def rtn_inputs(M, N, K, seed):
+    """Operands as the reference's kernel benchmarks make them
+    (benchmarks/tune_w4a4_aw_grouped.py:41-49): bf16 x ~ N(0,1) and
+    w ~ N(0,1)/sqrt(K), a zero row in each (x's kept when M = 1), activations quantized at clip 0.9
+    and weights round-to-nearest at clip 1 in groups of 128 (the oracle's
+    restatement of grouped_quantize, CUDA division)."""
+    rng = np.random.default_rng(seed)
+    x = oracle.bf16_to_f32(oracle.f32_to_bf16(rng.standard_normal((M, K)).astype(np.float32)))
+    w = oracle.bf16_to_f32(oracle.f32_to_bf16((rng.standard_normal((N, K)) / np.sqrt(K)).astype(np.float32)))
+    if M > 1:
+        x[0] = 0
+    w[0] = 0
+    qa, sa = oracle.weight_quantize(x, 128, 0.9, oracle.DIVISION_CUDA)
+    qw, sw = oracle.weight_quantize(w, 128, 1.0, oracle.DIVISION_CUDA)
+    return x, w, oracle.pack_int4(qa), oracle.pack_int4(qw), sa, sw
+
+
+@pytest.mark.parametrize("M,N,K", [(1, 6144, 4096), (32, 4096, 12288), (32, 24576, 4096), (600, 528, 4096),
+                                   (2048, 1040, 4096)])
+def test_k2_rtn_quantized_weights(M, N, K):
+    """Realistic per-group weight scales (RTN-G128 of Gaussian weights) through
+    the size-chosen kernel, reference and tiled layouts: bit-exact against the
+    oracle in bf16; the fp32 output within 2e-6 relative RMSE of the float64
+    grouped sum (verify_w4a4_aw_grouped.py:75-76); the W4A4 product within the
+    expected INT4 error of the unquantized x @ w.T."""
+    print(f"[k2-rtn] M={M} N={N} K={K}", flush=True)
+    x, wf, ap, wp, sa, sw = rtn_inputs(M, N, K, M * 3 + N + K)
+    exp = oracle.w4a4_gemm(ap, wp, sa, sw)
+    a, w, s_a, s_w = to_dev(ap, wp, sa, sw)
+    out = w4a4_grouped_gemm(a, w, s_a, s_w)
+    out_t = w4a4_grouped_gemm(a, tile_weights(w), s_a, s_w, weights_tiled=True)
+    out32 = torch.full((M, N), float("nan"), device=DEV, dtype=torch.float32)
+    compile_grouped_gemm(M, N, K, output_fp32=True, weight_grouped=True)(a, w, s_a, s_w, out32)
+    torch.cuda.synchronize()
+    assert_bits_equal(bf16_bits(out), exp, "bf16 output")
+    assert_bits_equal(bf16_bits(out_t), exp, "bf16 output, tiled weights")
+    dots = oracle.w4a4_group_dots(ap, wp).astype(np.float64)
+    precise = np.einsum("mng,mg,ng->mn", dots, oracle.bf16_to_f32(sa).astype(np.float64),
+                        oracle.bf16_to_f32(sw).astype(np.float64))
+    got32 = out32.cpu().numpy().astype(np.float64)
+    rrmse = np.sqrt(np.mean((got32 - precise) ** 2) / max(np.mean(precise ** 2), 1e-20))
+    assert rrmse < 2e-6, rrmse
+    st = oracle.error_stats(oracle.bf16_to_f32(bf16_bits(out)), (x.astype(np.float64) @ wf.T.astype(np.float64)))
+    assert st["relative_rmse"] < 0.25 and st["cosine"] > 0.97, st
+
+
 def extreme_scales(rng, rows, G, frac=0.05):
     """bf16 scale bits: ordinary values with a sprinkling of tiny normals
     (2^-126), bf16 subnormals (2^-133), huge values (2^70) and zeros, so the
