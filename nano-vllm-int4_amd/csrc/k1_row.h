@@ -16,16 +16,19 @@
 // Mapping to the hardware.  A 1024-point chunk is one wave: lane l loads the
 // 16 contiguous columns 16l..16l+15, so butterfly bits 0-3 are register
 // bits.  A wave-local LDS transpose (no workgroup barrier) then puts bits 4-7
-// in registers, with bits 0-3 and 8-9 on the lane index; bits 8-9 sit on
-// lane bits 0-1 and are finished with DPP quad permutes.  K = 4096 spans
+// in registers, with bits 0-3 and 8-9 on the lane index.  K = 4096 spans
 // four waves: one workgroup transpose brings bits 8-11 into registers.
-// K = 12288 needs all 12 chunks of a column for the H12 stage: one thread
-// per column reads them from LDS.  Quantization reads 16 contiguous values
-// per thread (8 adjacent lanes hold one 128-group).
+// K = 12288 finishes bits 8-9 (lane bits 0-1) with DPP quad permutes, and
+// needs all 12 chunks of a column for the H12 stage: one thread per column
+// reads them from LDS.  Quantization reads 16 contiguous values per thread
+// (8 adjacent lanes hold one 128-group).
 //
-// LDS layout: each 1024-column chunk is stored XOR-swizzled (swz below) so
-// that the contiguous, transposed, per-column and per-unit access patterns
-// are all free of bank conflicts on 32 or 64 banks.
+// LDS layout: column c of a 1024-column chunk sits at lds_pos(c) = c +
+// (c >> 4) + 8 (c >> 9) in the chunk's block of K1_BLOCK floats.  Every
+// access pattern above is then one base register per thread plus constant
+// offsets (no per-access address arithmetic), and the 32 lanes a half-wave
+// serves hit 32 distinct banks (the cross-wave transpose of K = 4096 has one
+// two-way pair).
 #pragma once
 
 #include "nv4_common.h"
@@ -33,11 +36,15 @@
 namespace nv4 {
 namespace {
 
-__device__ __forceinline__ int swz(int c) { return c ^ ((c >> 4) & 0x3F) ^ ((c >> 6) & 8); }
+constexpr int K1_BLOCK = 1096;  // > lds_pos(1023) = 1094
+__host__ __device__ constexpr int lds_pos(int c) { return c + (c >> 4) + 8 * (c >> 9); }
 
 // Column of chunk-local index held by lane l in register r after the
 // wave-local transpose: bits 0-3 = l >> 2, bits 4-7 = r, bits 8-9 = l & 3.
 __device__ __forceinline__ int col_t(int l, int r) { return (l >> 2) | (r << 4) | ((l & 3) << 8); }
+// lds_pos(16 l + r) = unit_base(l) + r; lds_pos(col_t(l, r)) = tr_base(l) + 17 r.
+__device__ __forceinline__ int unit_base(int l) { return 17 * l + 8 * (l >> 5); }
+__device__ __forceinline__ int tr_base(int l) { return (l >> 2) + 272 * (l & 3) + 8 * ((l & 3) >> 1); }
 
 __host__ __device__ constexpr bool paley_positive(int s, int d) {
     if (s == 0 || d == 0) return true;
@@ -103,44 +110,42 @@ __device__ __forceinline__ void reg_butterflies(float (&a)[N]) {
             }
 }
 
-// Butterfly across lanes l and l ^ (1 << LB) (LB = 0 or 1): the lower lane
-// keeps lo + hi, the upper lo - hi; fma(v, -1, t) rounds t - v once.
-template <int LB>
-__device__ __forceinline__ void lane_butterflies(float (&a)[16], int l) {
+// Butterfly across lanes l and l ^ (1 << LB) (LB = 0 or 1) in one fma per
+// value, v = RN(partner * sg + v) with sg = -1 on the upper lane: the lower
+// lane gets lo + hi, the upper hi - lo = -(lo - hi) (RN is symmetric).  So
+// after the stages on bits 0 and 1 the lane holds its value times
+// lane_flip(l) = (-1)^(bit 0 + bit 1 of l); the flip of the partners is the
+// same at bit 1, and the caller's normalisation multiplies it out exactly.
+template <int LB, int N>
+__device__ __forceinline__ void lane_butterflies(float (&a)[N], int l) {
     const float sg = (l >> LB) & 1 ? -1.0f : 1.0f;
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-        const float other = dpp<LB == 0 ? DPP_QUAD_XOR1 : DPP_QUAD_XOR2>(a[r]);
-        a[r] = __builtin_fmaf(a[r], sg, other);
-    }
+    for (int r = 0; r < N; ++r) a[r] = __builtin_fmaf(dpp<LB == 0 ? DPP_QUAD_XOR1 : DPP_QUAD_XOR2>(a[r]), sg, a[r]);
 }
+__device__ __forceinline__ float lane_flip(int l) { return ((l ^ (l >> 1)) & 1) ? -1.0f : 1.0f; }
 
-// Max over the 8 adjacent lanes that hold one 128-group.
-__device__ __forceinline__ float group8_max(float m) {
-    m = fmaxf(m, dpp<DPP_QUAD_XOR1>(m));
-    m = fmaxf(m, dpp<DPP_QUAD_XOR2>(m));
-    return fmaxf(m, dpp<DPP_HALF_MIRROR>(m));
-}
-
-// Quantize 16 contiguous values (one eighth of a 128-group; the group's 8
-// lanes must be active together), write 8 packed bytes and, from the group's
-// first lane, the bf16 scale.
+// Quantization of N contiguous values per lane, the 128-group spread over
+// 128/N adjacent lanes that must be active together (QLANES = 128 / N).
 //
-// Codes: q = clamp(rint(v / s)) with the IEEE quotient.  Fast path: p =
-// v * rcp(s) with v_rcp_f32 (<= 1 ulp), so |p - v/s| <= 1.5 * 2^-23 * |v/s|
-// < 2^-20 (|v/s| < 8 because s >= ~0.128 * max|v|).  If |p - rint(p)| <
-// 0.5 - 2^-18, then v/s, and its rounded quotient (within 2^-22), lie
-// strictly inside the same unit interval around rint(p), so rint of the IEEE
-// quotient equals rint(p).  A lane whose values fail the test (near a
-// half-integer, or s outside [2^-126, 2^100]) recomputes them with the IEEE
-// division.  Nibbles are assembled exactly in fp32: sum (q_i + 8) * 16^i over
-// four values is an integer below 2^16, and (q + 8) ^ 8 == q & 15.
-__device__ __forceinline__ void quantize16_store(const float (&v)[16], int8_t* __restrict__ dst8,
-                                                 uint16_t* __restrict__ scale_dst, bool leader) {
+// Codes: q = clamp(rint(v / s)) with the IEEE quotient, computed as
+// q + 8 = rint(p) for p = fma(v, rcp(s), 8): v_rcp_f32 is within 1 ulp, so
+// |v * rcp(s) - v/s| <= 2^-23 |v/s| < 2^-20 (|v/s| < 8 because s >= ~0.128 *
+// max|v|), the fma adds at most ulp(16)/2 = 2^-20, and the IEEE quotient is
+// within 2^-21 of v/s: p lies within 2^-18 of v/s + 8 and of RN(v/s) + 8.
+// If every |p - rint(p)| of the lane is below 0.5 - 2^-18, each of those
+// lies strictly inside the unit interval around rint(p), so rint(RN(v/s)) + 8
+// = rint(p).  A lane that fails the test (a value near a half-integer, or s
+// outside [2^-126, 2^100]) recomputes its values with the IEEE division.
+// Nibbles are assembled exactly in fp32: sum (q_i + 8) * 16^i over four
+// values is an integer below 2^16, and (q + 8) ^ 8 == q & 15.
+template <int N>
+__device__ __forceinline__ uint32_t group_scale_bits(const float (&v)[N], float& s) {
     float mx = 0.0f;
 #pragma unroll
-    for (int i = 0; i < 16; ++i) mx = fmaxf(mx, fabsf(v[i]));
-    mx = group8_max(mx);
+    for (int i = 0; i < N; i += 2) mx = fmaxf(mx, fmaxf(fabsf(v[i]), fabsf(v[i + 1])));
+    mx = fmaxf(mx, dpp<DPP_QUAD_XOR1>(mx));
+    if constexpr (N <= 32) mx = fmaxf(mx, dpp<DPP_QUAD_XOR2>(mx));
+    if constexpr (N == 16) mx = fmaxf(mx, dpp<DPP_HALF_MIRROR>(mx));
     uint32_t sb;
     if (mx == 0.0f) {
         sb = 0x3F80u;  // 1.0
@@ -150,44 +155,65 @@ __device__ __forceinline__ void quantize16_store(const float (&v)[16], int8_t* _
         t = fmaxf(t, 0x1p-126f);
         sb = f32_to_bf16_rne(t);
     }
-    const float s = bf16_to_f32(sb);
+    s = bf16_to_f32(sb);
+    return sb;
+}
+
+// Packed bytes of N codes: word k holds codes 8k..8k+7, low nibble first.
+template <int N>
+__device__ __forceinline__ void codes_pack(const float (&v)[N], float s, uint32_t (&words)[N / 8]) {
     const float y = __builtin_amdgcn_rcpf(s);
-    bool exact = s <= 0x1p100f;
-    float q[16];
+    float q[N], dev = 0.0f;
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-        const float p = v[i] * y;
-        q[i] = __builtin_rintf(p);
-        exact = exact & (fabsf(p - q[i]) < 0x1.ffffp-2f);
+    for (int i = 0; i < N; i += 2) {
+        const float p0 = __builtin_fmaf(v[i], y, 8.0f), p1 = __builtin_fmaf(v[i + 1], y, 8.0f);
+        q[i] = __builtin_rintf(p0);
+        q[i + 1] = __builtin_rintf(p1);
+        dev = fmaxf(dev, fmaxf(fabsf(p0 - q[i]), fabsf(p1 - q[i + 1])));
     }
-    if (!exact) {
+    if (!(dev < 0x1.ffffp-2f && s <= 0x1p100f)) {
 #pragma unroll
-        for (int i = 0; i < 16; ++i) q[i] = __builtin_rintf(v[i] / s);
+        for (int i = 0; i < N; ++i) q[i] = __builtin_rintf(v[i] / s) + 8.0f;
     }
-    uint32_t half[4];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        float h = __builtin_amdgcn_fmed3f(q[4 * j + 3], -7.0f, 7.0f);
+    for (int k = 0; k < N / 8; ++k) {
+        uint32_t half[2];
 #pragma unroll
-        for (int i = 2; i >= 0; --i) h = __builtin_fmaf(h, 16.0f, __builtin_amdgcn_fmed3f(q[4 * j + i], -7.0f, 7.0f));
-        half[j] = (uint32_t)(h + 34952.0f);  // + 8 * (1 + 16 + 256 + 4096)
+        for (int j = 0; j < 2; ++j) {
+            const int b = 8 * k + 4 * j;
+            float h = __builtin_amdgcn_fmed3f(q[b + 3], 1.0f, 15.0f);
+#pragma unroll
+            for (int i = 2; i >= 0; --i) h = __builtin_fmaf(h, 16.0f, __builtin_amdgcn_fmed3f(q[b + i], 1.0f, 15.0f));
+            half[j] = (uint32_t)h;
+        }
+        words[k] = (half[0] | (half[1] << 16)) ^ 0x88888888u;
     }
-    const uint32_t w0 = (half[0] | (half[1] << 16)) ^ 0x88888888u;
-    const uint32_t w1 = (half[2] | (half[3] << 16)) ^ 0x88888888u;
-    *reinterpret_cast<uint2*>(dst8) = make_uint2(w0, w1);
+}
+
+// 16 values per lane, 8 lanes per group: 8 packed bytes and, from the
+// group's first lane, the bf16 scale.
+__device__ __forceinline__ void quantize16_store(const float (&v)[16], int8_t* __restrict__ dst8,
+                                                 uint16_t* __restrict__ scale_dst, bool leader) {
+    float s;
+    const uint32_t sb = group_scale_bits(v, s);
+    uint32_t w[2];
+    codes_pack(v, s, w);
+    *reinterpret_cast<uint2*>(dst8) = make_uint2(w[0], w[1]);
     if (leader) *scale_dst = (uint16_t)sb;
 }
 
 // Butterfly bits 0-9 of the 1024-point chunk whose LDS block is blk, by one
 // wave (lane l, columns 16l..16l+15 in a).  On return a holds columns
-// col_t(l, r), and blk is free for the caller.
+// col_t(l, r) times lane_flip(l), and blk is free for the caller.
 __device__ __forceinline__ void chunk1024_bits0_9(float (&a)[16], float* __restrict__ blk, int l) {
     reg_butterflies(a);
+    float* pu = blk + unit_base(l);
 #pragma unroll
-    for (int r = 0; r < 16; ++r) blk[swz(16 * l + r)] = a[r];
+    for (int r = 0; r < 16; ++r) pu[r] = a[r];
     wave_lds_sync();
+    const float* pt = blk + tr_base(l);
 #pragma unroll
-    for (int r = 0; r < 16; ++r) a[r] = blk[swz(col_t(l, r))];
+    for (int r = 0; r < 16; ++r) a[r] = pt[17 * r];
     reg_butterflies(a);
     lane_butterflies<0>(a, l);
     lane_butterflies<1>(a, l);
@@ -197,90 +223,101 @@ __device__ __forceinline__ void chunk1024_bits0_9(float (&a)[16], float* __restr
 // butterflies of one chunk each, then every thread runs the H12 stage of one
 // column, and threads 0-767 quantize one 16-column unit each.
 constexpr int K12_THREADS = 1024;
-constexpr int K12_LDS = 12 * 1024;
+constexpr int K12_LDS = 12 * K1_BLOCK;
 
-//
 // The row's values come from a prologue: prologue(col0, v) fills v[0..15]
 // with the fp32 values of columns col0..col0+15 (bf16 x, or the output of a
 // fused RMSNorm / SiLU-mul rounded to bf16); they are multiplied by the
-// signs here.  Threads 0-767 (waves 0-11) call it once each, with
-// col0 = 16 t.
+// signs sv here (the caller loads them, ahead of the row: k1_signs12288).
+// Threads 0-767 (waves 0-11) call it once each, with col0 = 16 t.
+__device__ __forceinline__ v4u k1_signs12288(const int8_t* __restrict__ signs) {
+    const int w = min((int)threadIdx.x >> 6, 11), l = threadIdx.x & 63;
+    return load_signs16(signs + w * 1024 + 16 * l);
+}
+
 template <class Prologue>
-__device__ __forceinline__ void k1_row12288(Prologue&& prologue, const int8_t* __restrict__ signs,
-                                            int8_t* __restrict__ prow, uint16_t* __restrict__ srow,
-                                            float* __restrict__ buf) {
+__device__ __forceinline__ void k1_row12288(Prologue&& prologue, const v4u sv, int8_t* __restrict__ prow,
+                                            uint16_t* __restrict__ srow, float* __restrict__ buf) {
     const int t = threadIdx.x, w = t >> 6, l = t & 63;
     if (w < 12) {
         float a[16];
-        const v4u sv = load_signs16(signs + w * 1024 + 16 * l);
         prologue(w * 1024 + 16 * l, a);
         apply_signs16(sv, a);
-        float* blk = buf + w * 1024;
+        float* blk = buf + w * K1_BLOCK;
         chunk1024_bits0_9(a, blk, l);
+        float* pt = blk + tr_base(l);
+        const float norm = lane_flip(l) * 0x1p-5f;
 #pragma unroll
-        for (int r = 0; r < 16; ++r) blk[swz(col_t(l, r))] = a[r] * 0x1p-5f;
+        for (int r = 0; r < 16; ++r) pt[17 * r] = a[r] * norm;
     }
     __syncthreads();
     {
-        const int c = swz(t);
+        float* pc = buf + lds_pos(t);
         float v[12];
 #pragma unroll
-        for (int s = 0; s < 12; ++s) v[s] = buf[s * 1024 + c];
+        for (int s = 0; s < 12; ++s) v[s] = pc[s * K1_BLOCK];
         const float inv12 = 0x1.279a74p-2f;  // RN(1/sqrt 12)
 #pragma unroll
         for (int d = 0; d < 12; ++d) {
             float acc = v[0];
 #pragma unroll
             for (int s = 1; s < 12; ++s) acc = paley_positive(s, d) ? acc + v[s] : acc - v[s];
-            buf[d * 1024 + c] = acc * inv12;
+            pc[d * K1_BLOCK] = acc * inv12;
         }
     }
     __syncthreads();
     if (w < 12) {
+        const float* pu = buf + w * K1_BLOCK + unit_base(l);
         float v[16];
 #pragma unroll
-        for (int i = 0; i < 16; ++i) v[i] = buf[w * 1024 + swz(16 * l + i)];
+        for (int i = 0; i < 16; ++i) v[i] = pu[i];
         quantize16_store(v, prow + 8 * t, srow + (t >> 3), (t & 7) == 0);
     }
 }
 
-// K = 4096 (one 4096-point chunk) by 256 threads: each wave runs bits 0-9 of
+// K = 4096 (one 4096-point chunk) by 256 threads: each wave runs bits 0-7 of
 // its 1024-column quarter, one workgroup transpose brings bits 8-11 into
-// registers (thread t: columns t | r << 8).  Every thread calls the
-// prologue once, with col0 = 16 t.
-constexpr int K4_LDS = 4 * 1024;
+// registers (thread t: columns t + 256 r), a second one the contiguous
+// units back for quantization.  Every thread calls the prologue once, with
+// col0 = 16 t; sv are its 16 signs (k1_signs4096).
+constexpr int K4_THREADS = 256;
+constexpr int K4_LDS = 4 * K1_BLOCK;
+
+__device__ __forceinline__ v4u k1_signs4096(const int8_t* __restrict__ signs) {
+    return load_signs16(signs + 16 * threadIdx.x);
+}
 
 template <class Prologue>
-__device__ __forceinline__ void k1_row4096(Prologue&& prologue, const int8_t* __restrict__ signs,
-                                           int8_t* __restrict__ prow, uint16_t* __restrict__ srow,
-                                           float* __restrict__ buf) {
+__device__ __forceinline__ void k1_row4096(Prologue&& prologue, const v4u sv, int8_t* __restrict__ prow,
+                                           uint16_t* __restrict__ srow, float* __restrict__ buf) {
     const int t = threadIdx.x, w = t >> 6, l = t & 63;
     float a[16];
-    const v4u sv = load_signs16(signs + w * 1024 + 16 * l);
-    prologue(w * 1024 + 16 * l, a);
+    prologue(16 * t, a);
     apply_signs16(sv, a);
-    float* blk = buf + w * 1024;
     reg_butterflies(a);
+    float* pu = buf + w * K1_BLOCK + unit_base(l);
 #pragma unroll
-    for (int r = 0; r < 16; ++r) blk[swz(16 * l + r)] = a[r];
+    for (int r = 0; r < 16; ++r) pu[r] = a[r];
     wave_lds_sync();
+    float* pt = buf + w * K1_BLOCK + tr_base(l);
 #pragma unroll
-    for (int r = 0; r < 16; ++r) a[r] = blk[swz(col_t(l, r))];
+    for (int r = 0; r < 16; ++r) a[r] = pt[17 * r];
     reg_butterflies(a);
 #pragma unroll
-    for (int r = 0; r < 16; ++r) blk[swz(col_t(l, r))] = a[r];
+    for (int r = 0; r < 16; ++r) pt[17 * r] = a[r];
     __syncthreads();
-    // register r: bits 0-1 -> column bits 8-9, bits 2-3 -> column bits 10-11.
+    // Register r holds column t + 256 r: chunk r >> 2, chunk column
+    // 256 (r & 3) + t, at lds_pos = t + (t >> 4) + 272 (r & 3) + 8 ((r & 3) >> 1).
+    float* pc = buf + t + (t >> 4);
 #pragma unroll
-    for (int r = 0; r < 16; ++r) a[r] = buf[(r >> 2) * 1024 + swz(t | ((r & 3) << 8))];
+    for (int r = 0; r < 16; ++r) a[r] = pc[(r >> 2) * K1_BLOCK + 272 * (r & 3) + 8 * ((r & 3) >> 1)];
     reg_butterflies(a);
 #pragma unroll
-    for (int r = 0; r < 16; ++r) buf[(r >> 2) * 1024 + swz(t | ((r & 3) << 8))] = a[r] * 0x1p-6f;
+    for (int r = 0; r < 16; ++r) pc[(r >> 2) * K1_BLOCK + 272 * (r & 3) + 8 * ((r & 3) >> 1)] = a[r] * 0x1p-6f;
     __syncthreads();
-    float v[16];
 #pragma unroll
-    for (int i = 0; i < 16; ++i) v[i] = buf[w * 1024 + swz(16 * l + i)];
-    quantize16_store(v, prow + 8 * t, srow + (t >> 3), (t & 7) == 0);
+    for (int i = 0; i < 16; ++i) a[i] = pu[i];
+    quantize16_store(a, prow + 8 * t, srow + (t >> 3), (t & 7) == 0);
 }
 
 }  // namespace

@@ -25,18 +25,12 @@ __device__ __forceinline__ float wave_sum(float v) {
 
 __device__ __forceinline__ float round_bf16(float f) { return bf16_to_f32(f32_to_bf16_rne(f)); }
 
-// h = float(x) (+ float(res)) for 16 contiguous values; with a residual the
-// rounded sum goes to res_out.  Accumulates the sum of squares into ss.
+// h = float(x) (+ float(res)) for 16 contiguous values given as bf16 pairs
+// (x0, x1; r0, r1); with a residual the rounded sum goes to res_out.
+// Accumulates the sum of squares into ss.
 template <bool RESID>
-__device__ __forceinline__ void rms_load16(const uint16_t* __restrict__ x, const uint16_t* res, uint16_t* res_out,
-                                           float (&h)[16], float& ss) {
-    const v4u x0 = *reinterpret_cast<const v4u*>(x);
-    const v4u x1 = *reinterpret_cast<const v4u*>(x + 8);
-    v4u r0 = {0u, 0u, 0u, 0u}, r1 = r0;
-    if constexpr (RESID) {
-        r0 = *reinterpret_cast<const v4u*>(res);
-        r1 = *reinterpret_cast<const v4u*>(res + 8);
-    }
+__device__ __forceinline__ void rms_h16(const v4u x0, const v4u x1, const v4u r0, const v4u r1, uint16_t* res_out,
+                                        float (&h)[16], float& ss) {
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
         const uint32_t xw = i < 8 ? x0[(i & 7) >> 1] : x1[(i & 7) >> 1];
@@ -58,6 +52,20 @@ __device__ __forceinline__ void rms_load16(const uint16_t* __restrict__ x, const
         *reinterpret_cast<v4u*>(res_out) = o0;
         *reinterpret_cast<v4u*>(res_out + 8) = o1;
     }
+}
+
+// rms_h16 on 16 contiguous values loaded from x (and res).
+template <bool RESID>
+__device__ __forceinline__ void rms_load16(const uint16_t* __restrict__ x, const uint16_t* res, uint16_t* res_out,
+                                           float (&h)[16], float& ss) {
+    const v4u x0 = *reinterpret_cast<const v4u*>(x);
+    const v4u x1 = *reinterpret_cast<const v4u*>(x + 8);
+    v4u r0 = {0u, 0u, 0u, 0u}, r1 = r0;
+    if constexpr (RESID) {
+        r0 = *reinterpret_cast<const v4u*>(res);
+        r1 = *reinterpret_cast<const v4u*>(res + 8);
+    }
+    rms_h16<RESID>(x0, x1, r0, r1, res_out, h, ss);
 }
 
 // Workgroup (256 threads) reduction of the per-thread sums of squares and
@@ -89,14 +97,10 @@ __device__ __forceinline__ void rms_apply16(const float (&h)[16], float r, const
 
 __device__ __forceinline__ float silu_mul1(float g, float u) { return round_bf16(round_bf16(g / (1.0f + expf(-g))) * u); }
 
-// y = silu(g) * u (bf16 rounding points above) for 16 contiguous values.
-__device__ __forceinline__ void silu_mul16(const uint16_t* __restrict__ g, const uint16_t* __restrict__ u,
-                                           float (&y)[16]) {
+// y = silu(g) * u (bf16 rounding points above) for 16 contiguous values
+// given as bf16 pairs (g0, g1; u0, u1).
+__device__ __forceinline__ void silu_mul16(const v4u g0, const v4u g1, const v4u u0, const v4u u1, float (&y)[16]) {
     float gf[16], uf[16];
-    const v4u g0 = *reinterpret_cast<const v4u*>(g);
-    const v4u g1 = *reinterpret_cast<const v4u*>(g + 8);
-    const v4u u0 = *reinterpret_cast<const v4u*>(u);
-    const v4u u1 = *reinterpret_cast<const v4u*>(u + 8);
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
         const uint32_t gw = i < 8 ? g0[(i & 7) >> 1] : g1[(i & 7) >> 1];
@@ -106,6 +110,12 @@ __device__ __forceinline__ void silu_mul16(const uint16_t* __restrict__ g, const
     }
 #pragma unroll
     for (int i = 0; i < 16; ++i) y[i] = silu_mul1(gf[i], uf[i]);
+}
+
+__device__ __forceinline__ void silu_mul16(const uint16_t* __restrict__ g, const uint16_t* __restrict__ u,
+                                           float (&y)[16]) {
+    silu_mul16(*reinterpret_cast<const v4u*>(g), *reinterpret_cast<const v4u*>(g + 8),
+               *reinterpret_cast<const v4u*>(u), *reinterpret_cast<const v4u*>(u + 8), y);
 }
 
 }  // namespace

@@ -11,71 +11,140 @@
 namespace nv4 {
 namespace {
 
-// K = 12288: one workgroup of 1024 threads per row.
-__global__ void __launch_bounds__(K12_THREADS)
-k1_k12288(const uint16_t* __restrict__ x, const int8_t* __restrict__ signs,
-          int8_t* __restrict__ packed, uint16_t* __restrict__ scale) {
-    __shared__ float buf[K12_LDS];
-    const int64_t row = blockIdx.x;
-    const uint16_t* xr = x + row * 12288;
-    k1_row12288([&](int c0, float (&v)[16]) { load_bf16x16(xr + c0, v); }, signs, packed + row * 6144,
-                scale + row * 96, buf);
-}
+// Row sources: load(row, c0, raw) issues the loads of one thread's 16
+// columns c0..c0+15 of a row; values(raw, row, c0, v) turns them into the
+// fp32 values the transform takes: the bf16 input itself, or the output of
+// the fused producer rounded to bf16 as the separate op would store it.
+struct RowX {  // bf16 rows of width K
+    const uint16_t* __restrict__ x;
+    int K;
+    struct Raw { v4u a, b; };
+    __device__ __forceinline__ void load(int64_t row, int c0, Raw& r) const {
+        const uint16_t* p = x + row * K + c0;
+        r.a = *reinterpret_cast<const v4u*>(p);
+        r.b = *reinterpret_cast<const v4u*>(p + 8);
+    }
+    __device__ __forceinline__ void values(const Raw& r, int64_t, int, float (&v)[16]) const {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const uint32_t xw = i < 8 ? r.a[(i & 7) >> 1] : r.b[(i & 7) >> 1];
+            v[i] = bf16_to_f32((xw >> (16 * (i & 1))) & 0xffffu);
+        }
+    }
+};
 
-// K = 4096: one workgroup of 256 threads per row.
-__global__ void __launch_bounds__(256)
-k1_k4096(const uint16_t* __restrict__ x, const int8_t* __restrict__ signs,
-         int8_t* __restrict__ packed, uint16_t* __restrict__ scale) {
-    __shared__ float buf[K4_LDS];
+struct RowSilu {  // SiLU(gate) * up of [M, 2K] gate/up rows
+    const uint16_t* __restrict__ gu;
+    int K;
+    struct Raw { v4u g0, g1, u0, u1; };
+    __device__ __forceinline__ void load(int64_t row, int c0, Raw& r) const {
+        const uint16_t* g = gu + row * 2 * K + c0;
+        r.g0 = *reinterpret_cast<const v4u*>(g);
+        r.g1 = *reinterpret_cast<const v4u*>(g + 8);
+        r.u0 = *reinterpret_cast<const v4u*>(g + K);
+        r.u1 = *reinterpret_cast<const v4u*>(g + K + 8);
+    }
+    __device__ __forceinline__ void values(const Raw& r, int64_t, int, float (&v)[16]) const {
+        silu_mul16(r.g0, r.g1, r.u0, r.u1, v);
+    }
+};
+
+// add + RMSNorm of 4096-wide rows (K4_THREADS = 256 threads; thread t's unit
+// is columns 16t..16t+15, the unit nv4_rmsnorm's thread t owns, so the sum
+// of squares runs in nv4_rmsnorm's order).  The caller sets the thread's
+// norm weights w0/w1 (loaded ahead of the row) and red (4 floats of LDS).
+template <bool RESID>
+struct RowRms {
+    const uint16_t* x;
+    const uint16_t* res_in;
+    uint16_t* res_out;
+    float eps;
+    v4u w0, w1;
+    float* red;
+    struct Raw { v4u x0, x1, r0, r1; };
+    __device__ __forceinline__ void load(int64_t row, int c0, Raw& r) const {
+        const int64_t off = row * 4096 + c0;
+        r.x0 = *reinterpret_cast<const v4u*>(x + off);
+        r.x1 = *reinterpret_cast<const v4u*>(x + off + 8);
+        r.r0 = RESID ? *reinterpret_cast<const v4u*>(res_in + off) : v4u{0u, 0u, 0u, 0u};
+        r.r1 = RESID ? *reinterpret_cast<const v4u*>(res_in + off + 8) : v4u{0u, 0u, 0u, 0u};
+    }
+    __device__ __forceinline__ void values(const Raw& r, int64_t row, int c0, float (&v)[16]) const {
+        float h[16], ss = 0.0f;
+        rms_h16<RESID>(r.x0, r.x1, r.r0, r.r1, RESID ? res_out + row * 4096 + c0 : nullptr, h, ss);
+        rms_apply16(h, rms_rsqrt256(ss, red, 4096, eps), w0, w1, v);
+    }
+};
+
+// K = 4096: one workgroup of K4_THREADS threads per row.
+template <class Src>
+__device__ __forceinline__ void k1_k4096_body(const Src& src, const int8_t* __restrict__ signs,
+                                              int8_t* __restrict__ packed, uint16_t* __restrict__ scale,
+                                              float* buf) {
+    const v4u sv = k1_signs4096(signs);
     const int64_t row = blockIdx.x;
-    const uint16_t* xr = x + row * 4096;
-    k1_row4096([&](int c0, float (&v)[16]) { load_bf16x16(xr + c0, v); }, signs, packed + row * 2048,
+    const int c0 = 16 * threadIdx.x;
+    typename Src::Raw raw;
+    src.load(row, c0, raw);
+    k1_row4096([&](int, float (&v)[16]) { src.values(raw, row, c0, v); }, sv, packed + row * 2048,
                scale + row * 32, buf);
 }
 
-// K = 4096 behind add+RMSNorm (same bits as nv4_rmsnorm followed by K1):
-// thread t's prologue unit is columns 16t..16t+15, the unit nv4_rmsnorm's
-// thread t owns for a 4096-wide row.
+template <class Src>
+__global__ void __launch_bounds__(K4_THREADS)
+k1_k4096(Src src, const int8_t* __restrict__ signs, int8_t* __restrict__ packed, uint16_t* __restrict__ scale) {
+    __shared__ float buf[K4_LDS];
+    k1_k4096_body(src, signs, packed, scale, buf);
+}
+
+// add + RMSNorm in front: the norm weights are loaded ahead of the row.
 template <bool RESID>
-__global__ void __launch_bounds__(256)
-k1_k4096_rmsnorm(const uint16_t* x, const uint16_t* res_in, uint16_t* res_out, const uint16_t* __restrict__ nw,
-                 float eps, const int8_t* __restrict__ signs, int8_t* __restrict__ packed,
-                 uint16_t* __restrict__ scale) {
+__global__ void __launch_bounds__(K4_THREADS)
+k1_k4096_rms(RowRms<RESID> src, const uint16_t* __restrict__ nw, const int8_t* __restrict__ signs,
+             int8_t* __restrict__ packed, uint16_t* __restrict__ scale) {
     __shared__ float buf[K4_LDS];
     __shared__ float red[4];
-    const int64_t off = (int64_t)blockIdx.x * 4096;
-    k1_row4096(
-        [&](int c0, float (&v)[16]) {
-            // The norm weights are loaded ahead of the row (one round trip).
-            const v4u w0 = *reinterpret_cast<const v4u*>(nw + c0);
-            const v4u w1 = *reinterpret_cast<const v4u*>(nw + c0 + 8);
-            float h[16], ss = 0.0f;
-            rms_load16<RESID>(x + off + c0, RESID ? res_in + off + c0 : nullptr,
-                              RESID ? res_out + off + c0 : nullptr, h, ss);
-            const float r = rms_rsqrt256(ss, red, 4096, eps);
-            rms_apply16(h, r, w0, w1, v);
-        },
-        signs, packed + (int64_t)blockIdx.x * 2048, scale + (int64_t)blockIdx.x * 32, buf);
+    src.w0 = *reinterpret_cast<const v4u*>(nw + 16 * threadIdx.x);
+    src.w1 = *reinterpret_cast<const v4u*>(nw + 16 * threadIdx.x + 8);
+    src.red = red;
+    k1_k4096_body(src, signs, packed, scale, buf);
 }
 
-// K1 behind SiLU-and-mul of a [M, 2K] gate/up row (same bits as nv4_silu_mul
-// followed by K1).
-__global__ void __launch_bounds__(256)
-k1_k4096_silu(const uint16_t* __restrict__ gu, const int8_t* __restrict__ signs, int8_t* __restrict__ packed,
-              uint16_t* __restrict__ scale) {
-    __shared__ float buf[K4_LDS];
-    const uint16_t* g = gu + (int64_t)blockIdx.x * 8192;
-    k1_row4096([&](int c0, float (&v)[16]) { silu_mul16(g + c0, g + 4096 + c0, v); }, signs,
-               packed + (int64_t)blockIdx.x * 2048, scale + (int64_t)blockIdx.x * 32, buf);
-}
-
+// K = 12288: one workgroup of 1024 threads per row.  Waves 12-15 hold no
+// columns in the butterfly phases (they join the H12 stage); their loads
+// repeat the row's last 16 columns, so that every load is unconditional.
+template <class Src>
 __global__ void __launch_bounds__(K12_THREADS)
-k1_k12288_silu(const uint16_t* __restrict__ gu, const int8_t* __restrict__ signs, int8_t* __restrict__ packed,
-               uint16_t* __restrict__ scale) {
+k1_k12288(Src src, const int8_t* __restrict__ signs, int8_t* __restrict__ packed, uint16_t* __restrict__ scale) {
     __shared__ float buf[K12_LDS];
-    const uint16_t* g = gu + (int64_t)blockIdx.x * 24576;
-    k1_row12288([&](int c0, float (&v)[16]) { silu_mul16(g + c0, g + 12288 + c0, v); }, signs,
-                packed + (int64_t)blockIdx.x * 6144, scale + (int64_t)blockIdx.x * 96, buf);
+    const v4u sv = k1_signs12288(signs);
+    const int64_t row = blockIdx.x;
+    const int c0 = 16 * min((int)threadIdx.x, 767);
+    typename Src::Raw raw;
+    src.load(row, c0, raw);
+    k1_row12288([&](int, float (&v)[16]) { src.values(raw, row, c0, v); }, sv, packed + row * 6144,
+                scale + row * 96, buf);
+}
+
+template <class Src>
+hipError_t launch_k4096(const Src& src, const int8_t* signs, int8_t* packed, uint16_t* scale, int M, hipStream_t st) {
+    hipLaunchKernelGGL((k1_k4096<Src>), dim3((unsigned)M), dim3(K4_THREADS), 0, st, src, signs, packed, scale);
+    return hipGetLastError();
+}
+
+template <class Src>
+hipError_t launch_k12288(const Src& src, const int8_t* signs, int8_t* packed, uint16_t* scale, int M,
+                         hipStream_t st) {
+    hipLaunchKernelGGL((k1_k12288<Src>), dim3((unsigned)M), dim3(K12_THREADS), 0, st, src, signs, packed, scale);
+    return hipGetLastError();
+}
+
+template <bool RESID>
+hipError_t launch_rms4096(const RowRms<RESID>& src, const uint16_t* nw, const int8_t* signs, int8_t* packed,
+                          uint16_t* scale, int M, hipStream_t st) {
+    hipLaunchKernelGGL((k1_k4096_rms<RESID>), dim3((unsigned)M), dim3(K4_THREADS), 0, st, src, nw, signs, packed,
+                       scale);
+    return hipGetLastError();
 }
 
 // block128 layout: every aligned 128-block gets its own 128-point Sylvester
@@ -143,14 +212,8 @@ extern "C" int nv4_rht_quant_pack(const void* x, const int8_t* signs, int8_t* pa
     if (layout == NV4_LAYOUT_REFERENCE) {
         const auto* xp = static_cast<const uint16_t*>(x);
         auto* sp = static_cast<uint16_t*>(scale);
-        if (K == 4096) {
-            hipLaunchKernelGGL(k1_k4096, dim3((unsigned)M), dim3(256), 0, st, xp, signs, packed, sp);
-            return (int)hipGetLastError();
-        }
-        if (K == 12288) {
-            hipLaunchKernelGGL(k1_k12288, dim3((unsigned)M), dim3(K12_THREADS), 0, st, xp, signs, packed, sp);
-            return (int)hipGetLastError();
-        }
+        if (K == 4096) return (int)launch_k4096(RowX{xp, 4096}, signs, packed, sp, (int)M, st);
+        if (K == 12288) return (int)launch_k12288(RowX{xp, 12288}, signs, packed, sp, (int)M, st);
         return NV4_E_SHAPE;
     }
     if (layout == NV4_LAYOUT_BLOCK128) {
@@ -181,14 +244,13 @@ extern "C" int nv4_rmsnorm_rht_quant_pack(const void* x, const void* residual_in
     const auto* xp = static_cast<const uint16_t*>(x);
     const auto* wp = static_cast<const uint16_t*>(norm_weight);
     auto* sp = static_cast<uint16_t*>(scale);
-    if (residual_in)
-        hipLaunchKernelGGL(k1_k4096_rmsnorm<true>, dim3((unsigned)M), dim3(256), 0, st, xp,
-                           static_cast<const uint16_t*>(residual_in), static_cast<uint16_t*>(residual_out), wp, eps,
-                           signs, packed, sp);
-    else
-        hipLaunchKernelGGL(k1_k4096_rmsnorm<false>, dim3((unsigned)M), dim3(256), 0, st, xp, nullptr, nullptr, wp,
-                           eps, signs, packed, sp);
-    return (int)hipGetLastError();
+    if (residual_in) {
+        RowRms<true> src{xp, static_cast<const uint16_t*>(residual_in), static_cast<uint16_t*>(residual_out), eps,
+                         {}, {}, nullptr};
+        return (int)launch_rms4096(src, wp, signs, packed, sp, (int)M, st);
+    }
+    RowRms<false> src{xp, nullptr, nullptr, eps, {}, {}, nullptr};
+    return (int)launch_rms4096(src, wp, signs, packed, sp, (int)M, st);
 }
 
 extern "C" int nv4_silu_mul_rht_quant_pack(const void* gate_up, const int8_t* signs, int8_t* packed, void* scale,
@@ -202,9 +264,6 @@ extern "C" int nv4_silu_mul_rht_quant_pack(const void* gate_up, const int8_t* si
     hipStream_t st = static_cast<hipStream_t>(stream);
     const auto* gp = static_cast<const uint16_t*>(gate_up);
     auto* sp = static_cast<uint16_t*>(scale);
-    if (K == 4096)
-        hipLaunchKernelGGL(k1_k4096_silu, dim3((unsigned)M), dim3(256), 0, st, gp, signs, packed, sp);
-    else
-        hipLaunchKernelGGL(k1_k12288_silu, dim3((unsigned)M), dim3(K12_THREADS), 0, st, gp, signs, packed, sp);
-    return (int)hipGetLastError();
+    if (K == 4096) return (int)launch_k4096(RowSilu{gp, 4096}, signs, packed, sp, (int)M, st);
+    return (int)launch_k12288(RowSilu{gp, 12288}, signs, packed, sp, (int)M, st);
 }

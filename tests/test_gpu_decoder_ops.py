@@ -198,7 +198,7 @@ def test_silu_mul_extremes():
     assert torch.equal(out[~fin].float().nan_to_num(0.0), ref[~fin].float().nan_to_num(0.0))
 
 
-@pytest.mark.parametrize("rows", [1, 32, 300])
+@pytest.mark.parametrize("rows", [1, 32, 300, 2500])
 @pytest.mark.parametrize("with_residual", [False, True])
 def test_rmsnorm_rht_quant_pack_equals_two_step(rows, with_residual):
     g = torch.Generator(device=DEV).manual_seed(rows + 77)
@@ -226,7 +226,7 @@ def k1(x, signs):
 
 
 @pytest.mark.parametrize("K", [4096, 12288])
-@pytest.mark.parametrize("rows", [1, 32, 65])
+@pytest.mark.parametrize("rows", [1, 32, 65, 2500])
 def test_silu_mul_rht_quant_pack_equals_two_step(K, rows):
     g = torch.Generator(device=DEV).manual_seed(rows + K)
     gu = (torch.randn(rows, 2 * K, generator=g, device=DEV) * 2).to(torch.bfloat16)
