@@ -372,6 +372,300 @@ k3_reduce(const float* __restrict__ ws, void* __restrict__ out, int64_t MN, int 
         make_uint2((uint32_t)h[0] | ((uint32_t)h[1] << 16), (uint32_t)h[2] | ((uint32_t)h[3] << 16));
 }
 
+// ----------------------------------------------------------------------------
+// Decode-sized kernel in one launch (M <= 16, K <= K3O_MAXK).  A workgroup
+// of 8 waves owns NB = 32 output columns over the whole K, so every output is
+// finished inside the workgroup: no workspace, no second launch.
+//  * Weights: lane l (column slot c = l % 16, k-octet o = l / 16) loads the
+//    NB/16 words of columns n0 + (NB/16) c .. of one qweight row per 32-k
+//    step (16 lanes read NB * 4 contiguous bytes), all of a wave's steps up
+//    front.  Word j feeds the MFMA of column tile j, whose column i is
+//    n0 + (NB/16) i + j.
+//  * Dequantisation by group: the MFMA B operand is the biased code
+//    128 + q (bf16 0x4300 | q) or 1024 + q (fp16 0x6400 | q), exact, built
+//    with one shift and one and-or per two codes; a further MFMA with an
+//    all-ones B gives the activation sums X over the same k.  For the wave's
+//    steps of one quantisation group the product is then
+//        sum x (q - z - 1) s = s * (S - (bias + z + 1) X),
+//    two fmas per output and group instead of a rounded dequantised weight
+//    per code.  (The reference rounds each dequantised weight to the
+//    activation dtype; this form omits that rounding, a difference far
+//    inside the 1e-2 tolerance of a product the reference itself sums in a
+//    nondeterministic split-K order.)
+//  * Activations: codes of a k-octet are consumed in the order
+//    q0 q4 q1 q5 q2 q6 q3 q7, so activation octets are staged into LDS in
+//    that order.  Either all M rows over the whole K at once (M * K * 2 <=
+//    K3O_ONE_BYTES), or a two-slot ring of K3O_RING-byte chunks (ROWS x KC)
+//    loaded two chunks ahead, one barrier per chunk.  Rows at or beyond M are
+//    not read (A-operand rows alias row M - 1; their results are dropped).
+//  * Within a chunk wave w takes the SPW consecutive steps w*SPW ..; they lie
+//    in one quantisation group, so one scale and one zero word per lane and
+//    chunk.
+//  * At the end the 8 waves' fp32 tiles are added in wave order in LDS and
+//    rounded once (deterministic, no atomics).
+// ----------------------------------------------------------------------------
+constexpr int K3O_T = 512;
+constexpr int K3O_MAXK = 4096;
+constexpr int K3O_RING = 32768;        // bytes of activations per ring chunk
+constexpr int K3O_ONE_BYTES = 65536;   // all activations staged at once when M * K * 2 fits
+
+template <bool F16>
+struct BiasCode;
+template <>
+struct BiasCode<false> {
+    typedef v8bf vec;
+    static constexpr uint32_t HI = 0x43004300u;  // bf16 128 in both halves
+    static constexpr float BIAS = 128.0f;
+    static constexpr uint32_t ONE = 0x3F803F80u;
+    __device__ static inline float scale_of(uint16_t s_f16) {
+        return bf16_to_f32(f32_to_bf16_rne((float)__builtin_bit_cast(_Float16, s_f16)));
+    }
+};
+template <>
+struct BiasCode<true> {
+    typedef v8h vec;
+    static constexpr uint32_t HI = 0x64006400u;  // fp16 1024 in both halves
+    static constexpr float BIAS = 1024.0f;
+    static constexpr uint32_t ONE = 0x3C003C00u;
+    __device__ static inline float scale_of(uint16_t s_f16) { return (float)__builtin_bit_cast(_Float16, s_f16); }
+};
+
+// The eight biased codes of a qweight word in the order q0 q4 q1 q5 q2 q6 q3 q7.
+template <bool F16>
+__device__ __forceinline__ typename BiasCode<F16>::vec biased8(uint32_t w) {
+    const uint32_t m = 0x000F000Fu, hi = BiasCode<F16>::HI;
+    const v4u r = {(w & m) | hi, ((w >> 4) & m) | hi, ((w >> 8) & m) | hi, ((w >> 12) & m) | hi};
+    return __builtin_bit_cast(typename BiasCode<F16>::vec, r);
+}
+
+// An activation octet x0..x7 (16-bit pairs) reordered to x0 x4 x1 x5 x2 x6 x3 x7.
+__device__ __forceinline__ v4u octet_order(v4u v) {
+    return v4u{__builtin_amdgcn_perm(v[2], v[0], 0x05040100u), __builtin_amdgcn_perm(v[2], v[0], 0x07060302u),
+               __builtin_amdgcn_perm(v[3], v[1], 0x05040100u), __builtin_amdgcn_perm(v[3], v[1], 0x07060302u)};
+}
+
+template <int MB, int NB, int ST, bool ONE, bool XF16, bool OF16>
+__global__ void __launch_bounds__(K3O_T)
+k3_one(const uint16_t* __restrict__ x, const int32_t* __restrict__ qweight, const int32_t* __restrict__ qzeros,
+       const uint16_t* __restrict__ scales, void* __restrict__ out, int M, int N, int K) {
+    using BC = BiasCode<XF16>;
+    using vec = typename BC::vec;
+    constexpr int NT = NB / 16;                   // column tiles, words per lane and step
+    constexpr int ROWS = MB * 16;
+    constexpr int KC = K3O_RING / (2 * ROWS);    // k per chunk (the group geometry of both modes)
+    constexpr int SPC = KC / 32;                  // 32-k steps per chunk
+    constexpr int SPW = SPC / 8;                  // steps per wave and chunk (4, 2 or 1)
+    constexpr int CPR = KC / 8;                   // octets per row and chunk
+    constexpr int PPT = K3O_RING / 16 / K3O_T;    // ring octets per thread and chunk (4)
+    constexpr int PPT1 = ONE ? K3O_ONE_BYTES / 16 / K3O_T : 1;
+    static_assert(SPW >= 1 && ST % SPW == 0, "chunk shape");
+    extern __shared__ __align__(16) uint8_t smem[];
+    const int t = threadIdx.x, lane = t & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+    const int c = lane & 15, o = lane >> 4;
+    const int n0 = blockIdx.x * NB;
+    const int ncol = min(n0 + NT * c, N - NT);  // slots beyond N load the last valid columns (results dropped)
+    const int KS = K >> 5;
+    const int NCH = (KS + SPC - 1) / SPC;
+
+    const __amdgpu_buffer_rsrc_t rx =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(x), (short)0, (int)((uint32_t)M * K * 2u), K3_RSRC_WORD3);
+    auto load_chunk = [&](int ch, v4u (&xv)[PPT]) {
+        const int kbase = ch * KC, kvalid8 = min(KC, K - kbase) >> 3;
+#pragma unroll
+        for (int i = 0; i < PPT; ++i) {
+            const int p = t + i * K3O_T;
+            const int r = p / CPR, pc = min(p % CPR, kvalid8 - 1);
+            xv[i] = __builtin_bit_cast(v4u, __builtin_amdgcn_raw_buffer_load_b128(
+                                                rx, (int)(((uint32_t)r * K + kbase + pc * 8) * 2u), 0, 0));
+        }
+    };
+    auto store_chunk = [&](int ch, const v4u (&xv)[PPT]) {
+        uint8_t* base = smem + (ch & 1) * K3O_RING;
+#pragma unroll
+        for (int i = 0; i < PPT; ++i) {
+            const int p = t + i * K3O_T;
+            const int r = p / CPR, pc = p % CPR;
+            *reinterpret_cast<v4u*>(base + r * (KC * 2) + ((pc ^ (r & 7)) << 4)) = octet_order(xv[i]);
+        }
+    };
+    auto load_sz = [&](int ch, uint32_t& sw, uint32_t& zw) {
+        const int g = min((ch * SPC + wave * SPW) >> 2, (K >> 7) - 1);
+        if constexpr (NT == 2)
+            sw = *reinterpret_cast<const uint32_t*>(scales + (int64_t)g * N + ncol);
+        else
+            sw = (uint32_t)scales[(int64_t)g * N + ncol];
+        zw = (uint32_t)qzeros[(int64_t)g * (N >> 3) + (ncol >> 3)];
+    };
+
+    // ---- loads in the order their data is needed (vector loads complete in
+    // issue order): activations, the first scales, every weight step, and in
+    // ring mode the second chunk.
+    v4u x1[PPT1];
+    v4u xa[PPT], xb[PPT];
+    if constexpr (ONE) {
+        const int total = M * (K >> 3);
+#pragma unroll
+        for (int i = 0; i < PPT1; ++i) {
+            const int p = min(t + i * K3O_T, total - 1);
+            x1[i] = __builtin_bit_cast(v4u, __builtin_amdgcn_raw_buffer_load_b128(rx, (int)((uint32_t)p * 16u), 0, 0));
+        }
+    } else {
+        load_chunk(0, xa);
+    }
+    uint32_t sw, zw;
+    load_sz(0, sw, zw);
+    uint32_t wq[ST][NT];
+#pragma unroll
+    for (int i = 0; i < ST; ++i) {
+        const int ks = min((i / SPW) * SPC + wave * SPW + i % SPW, KS - 1);
+        const int32_t* src = qweight + (int64_t)(4 * ks + o) * N + ncol;
+        if constexpr (NT == 2) {
+            const uint2 v = *reinterpret_cast<const uint2*>(src);
+            wq[i][0] = v.x;
+            wq[i][NT - 1] = v.y;
+        } else {
+            wq[i][0] = (uint32_t)*src;
+        }
+    }
+    if constexpr (!ONE) load_chunk(min(1, NCH - 1), xb);
+
+    if constexpr (ONE) {
+        const int rowp = K >> 3, total = M * rowp;
+#pragma unroll
+        for (int i = 0; i < PPT1; ++i) {
+            const int p = min(t + i * K3O_T, total - 1);  // repeats of the last octet rewrite it unchanged
+            const int r = p / rowp, pc = p - r * rowp;
+            *reinterpret_cast<v4u*>(smem + r * (K * 2) + ((pc ^ (r & 7)) << 4)) = octet_order(x1[i]);
+        }
+        __syncthreads();
+    }
+
+    const vec ones = __builtin_bit_cast(vec, v4u{BC::ONE, BC::ONE, BC::ONE, BC::ONE});
+    const int zsh = 4 * (ncol & 7);
+    v4f total[MB][NT];
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+        for (int j = 0; j < NT; ++j) total[mb][j] = v4f{0.f, 0.f, 0.f, 0.f};
+    static_for<0, ST / SPW>([&](auto CH) {
+        constexpr int ch = CH;
+        if (ch >= NCH) return;  // uniform
+        if constexpr (!ONE) {
+            store_chunk(ch, (ch & 1) ? xb : xa);
+            if (ch + 2 < NCH) load_chunk(ch + 2, (ch & 1) ? xb : xa);  // uniform
+            __syncthreads();
+        }
+        float sj[NT], cj[NT];
+#pragma unroll
+        for (int j = 0; j < NT; ++j) {
+            sj[j] = BC::scale_of((uint16_t)(sw >> (16 * j)));
+            cj[j] = BC::BIAS + (float)((zw >> (zsh + 4 * j)) & 15u) + 1.0f;
+        }
+        load_sz(min(ch + 1, NCH - 1), sw, zw);
+        const uint8_t* base = ONE ? smem : smem + (ch & 1) * K3O_RING;
+        const int rstride = ONE ? K * 2 : KC * 2;
+        v4f S[MB][NT], X[MB];
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb) {
+            X[mb] = v4f{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int j = 0; j < NT; ++j) S[mb][j] = v4f{0.f, 0.f, 0.f, 0.f};
+        }
+#pragma unroll
+        for (int s = 0; s < SPW; ++s) {
+            const int cs = wave * SPW + s;  // step within the chunk
+            if (ch * SPC + cs < KS) {       // uniform
+                vec b[NT];
+#pragma unroll
+                for (int j = 0; j < NT; ++j) b[j] = biased8<XF16>(wq[ch * SPW + s][j]);
+                const int pc = (ONE ? ch * SPC : 0) * 4 + cs * 4 + o;  // octet in the staged row
+#pragma unroll
+                for (int mb = 0; mb < MB; ++mb) {
+                    const int r = min(mb * 16 + c, M - 1);
+                    const vec a = __builtin_bit_cast(
+                        vec, *reinterpret_cast<const v4u*>(base + r * rstride + ((pc ^ (r & 7)) << 4)));
+#pragma unroll
+                    for (int j = 0; j < NT; ++j) {
+                        if constexpr (XF16)
+                            S[mb][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b[j], S[mb][j], 0, 0, 0);
+                        else
+                            S[mb][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b[j], S[mb][j], 0, 0, 0);
+                    }
+                    if constexpr (XF16)
+                        X[mb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, ones, X[mb], 0, 0, 0);
+                    else
+                        X[mb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, ones, X[mb], 0, 0, 0);
+                }
+            }
+        }
+        // total += s * (S - (bias + z + 1) X) over this wave's steps of one group.
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+            for (int j = 0; j < NT; ++j)
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    total[mb][j][e] = __builtin_fmaf(sj[j], __builtin_fmaf(-cj[j], X[mb][e], S[mb][j][e]),
+                                                     total[mb][j][e]);
+    });
+    __syncthreads();  // the staged activations are dead; their LDS takes the wave partials [wave][mb][j][256]
+    float* part = reinterpret_cast<float*>(smem);
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+        for (int j = 0; j < NT; ++j)
+            *reinterpret_cast<v4f*>(&part[((wave * MB + mb) * NT + j) * 256 + lane * 4]) = total[mb][j];
+    __syncthreads();
+    // Entry e of tile (mb, j): MFMA lane e/4, result e%4 -> row 4 (lane/16) + e%4,
+    // column n0 + NT (lane%16) + j; summed over the waves in order.
+    constexpr int ENT = MB * NT * 256;
+#pragma unroll
+    for (int e0 = 0; e0 < ENT; e0 += K3O_T) {
+        const int e = e0 + t;
+        if (e < ENT) {
+            const int tile = e >> 8, el = (e & 255) >> 2, ei = e & 3;
+            const int mb = tile / NT, j = tile % NT;
+            float v = part[e];
+#pragma unroll
+            for (int w = 1; w < 8; ++w) v = v + part[w * ENT + e];
+            const int m = mb * 16 + 4 * (el >> 4) + ei, n = n0 + NT * (el & 15) + j;
+            if (m < M && n < N) {
+                const uint16_t h = OF16 ? __builtin_bit_cast(uint16_t, (_Float16)v) : (uint16_t)f32_to_bf16_rne(v);
+                static_cast<uint16_t*>(out)[(int64_t)m * N + n] = h;
+            }
+        }
+    }
+}
+
+template <int MB, int NB, int ST, bool XF, bool OF>
+hipError_t launch_one_k(const void* x, const int32_t* qw, const int32_t* qz, const void* sc, void* out, int M, int N,
+                        int K, hipStream_t st) {
+    const dim3 grid((unsigned)((N + NB - 1) / NB));
+    const auto* xp = static_cast<const uint16_t*>(x);
+    const auto* sp = static_cast<const uint16_t*>(sc);
+    const int parts = 8 * MB * (NB / 16) * 256 * 4;
+    if (MB == 1 && (int64_t)M * K * 2 <= K3O_ONE_BYTES) {
+        const int lds = max(((M * K * 2) + 15) & ~15, parts);
+        hipLaunchKernelGGL((k3_one<MB, NB, ST, true, XF, OF>), grid, dim3(K3O_T), lds, st, xp, qw, qz, sp, out, M, N,
+                           K);
+    } else {
+        const int lds = max(2 * K3O_RING, parts);
+        hipLaunchKernelGGL((k3_one<MB, NB, ST, false, XF, OF>), grid, dim3(K3O_T), lds, st, xp, qw, qz, sp, out, M, N,
+                           K);
+    }
+    return hipGetLastError();
+}
+
+// Dispatched for M <= 16 and K <= 4096 (the projections with K = 4096 at
+// decode batch sizes up to 16); wider M and longer K run the split-K form,
+// which measured faster there.
+template <bool XF, bool OF>
+hipError_t dispatch_one(const void* x, const int32_t* qw, const int32_t* qz, const void* sc, void* out, int M, int N,
+                        int K, hipStream_t st) {
+    return launch_one_k<1, 32, 16, XF, OF>(x, qw, qz, sc, out, M, N, K, st);
+}
+
 template <int MB, bool XF, bool OF>
 hipError_t launch_dec(const void* x, const int32_t* qw, const int32_t* qz, const void* sc, void* out, float* ws,
                       int M, int N, int K, hipStream_t st) {
@@ -492,6 +786,17 @@ extern "C" int nv4_w4a16_gemm(const void* x, int x_dtype, const int32_t* qweight
     hipStream_t st = static_cast<hipStream_t>(stream);
     const int m = (int)M, n = (int)N, k = (int)K;
     hipError_t e;
+    // Small decode batches: the one-launch kernel (8-byte weight and 4-byte scale loads).
+    if (M <= 16 && K <= K3O_MAXK && reinterpret_cast<uintptr_t>(qweight) % 8 == 0 &&
+        reinterpret_cast<uintptr_t>(scales) % 4 == 0) {
+        if (x_dtype == NV4_FP16)
+            e = out_dtype == NV4_FP16 ? dispatch_one<true, true>(x, qweight, qzeros, scales, out, m, n, k, st)
+                                      : dispatch_one<true, false>(x, qweight, qzeros, scales, out, m, n, k, st);
+        else
+            e = out_dtype == NV4_FP16 ? dispatch_one<false, true>(x, qweight, qzeros, scales, out, m, n, k, st)
+                                      : dispatch_one<false, false>(x, qweight, qzeros, scales, out, m, n, k, st);
+        return (int)e;
+    }
     if (x_dtype == NV4_FP16)
         e = out_dtype == NV4_FP16 ? dispatch<true, true>(x, qweight, qzeros, scales, out, m, n, k, st)
                                   : dispatch<true, false>(x, qweight, qzeros, scales, out, m, n, k, st);

@@ -9,13 +9,16 @@ reference (split-K 8 with bf16 atomics onto a zeroed output) the HIP kernel
 sums all of K in fp32 and writes each output once, so results do not depend
 on scheduling.  FP16 activations are accepted as well (output fp16).
 
-At decode sizes (M <= 64) the wrapper takes the split-K form
-(``nv4_w4a16_gemm_ws``): 64-column workgroups per 1024-deep K slice writing
-fp32 partials into a workspace from torch's caching allocator, added in slice
-order by a second launch -- still deterministic, and graph-capturable.  At
-prefill sizes (M > 64) the weight is dequantized once into a dense [K, N]
-tensor (``nv4_w4a16_dequant``, the same per-element rounding) and the
-product runs as a library GEMM (torch.mm on hipBLASLt, fp32 accumulation).
+Decode sizes: for M <= 16 and K <= 4096 ``nv4_w4a16_gemm`` runs one launch
+whose workgroups own 32 columns over the whole K (the K split over their
+waves and added in a fixed order in LDS); other M <= 64 take the split-K
+form (``nv4_w4a16_gemm_ws``): 64-column workgroups per 1024-deep K slice
+writing fp32 partials into a workspace from torch's caching allocator, added
+in slice order by a second launch.  Both are deterministic and
+graph-capturable.  At prefill sizes (M > 64) the weight is dequantized once
+into a dense [K, N] tensor (``nv4_w4a16_dequant``, the same per-element
+rounding) and the product runs as a library GEMM (torch.mm on hipBLASLt,
+fp32 accumulation).
 """
 from __future__ import annotations
 
@@ -27,6 +30,7 @@ from .. import _lib
 
 _DT = {torch.bfloat16: _lib.BF16, torch.float16: _lib.FP16}
 SLICE_K = 1024  # K per partial of the decode-size split
+ONE_LAUNCH_MAX_K = 4096  # nv4_w4a16_gemm runs one launch for M <= 16 up to this K
 
 
 def dequant_w4a16(qweight, qzeros, scales, dtype=torch.bfloat16, group_size=128):
@@ -78,7 +82,12 @@ def dequant_matmul_w4a16(x, qweight, qzeros, scales, group_size=128, out=None):
     lib = _lib.load()
     stream = torch.cuda.current_stream(x.device).cuda_stream
     with torch.cuda.device(x.device):
-        if M <= 64:
+        if M <= 16 and K <= ONE_LAUNCH_MAX_K:
+            rc = lib.nv4_w4a16_gemm(ctypes.c_void_p(x.data_ptr()), _DT[x.dtype],
+                                    ctypes.c_void_p(qweight.data_ptr()), ctypes.c_void_p(qzeros.data_ptr()),
+                                    ctypes.c_void_p(scales.data_ptr()), ctypes.c_void_p(out.data_ptr()),
+                                    _DT[out.dtype], M, N, K, group_size, ctypes.c_void_p(stream))
+        elif M <= 64:
             S = (K + SLICE_K - 1) // SLICE_K
             ws = torch.empty((S * M * N,), dtype=torch.float32, device=x.device)
             rc = lib.nv4_w4a16_gemm_ws(ctypes.c_void_p(x.data_ptr()), _DT[x.dtype],
