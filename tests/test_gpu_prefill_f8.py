@@ -52,7 +52,8 @@ def check_against_oracle(ap, wp, sa, sw, M, N, K, what):
 
 
 @pytest.mark.parametrize("M,N,K", [(17, 96, 512), (33, 136, 4096), (32, 128, 12288), (1, 8, 128), (129, 24, 384),
-                                   (200, 264, 1024), (257, 392, 2048), (300, 16, 1152), (128, 128, 8192)])
+                                   (200, 264, 1024), (257, 392, 2048), (300, 16, 1152), (128, 128, 8192),
+                                   (600, 264, 1024), (513, 136, 2048), (1030, 24, 3072)])
 @pytest.mark.parametrize("grouped", [True, False])
 def test_f8_matches_oracle(M, N, K, grouped):
     print(f"[f8] M={M} N={N} K={K} grouped={grouped}", flush=True)
@@ -82,7 +83,8 @@ def test_f8_scales_without_windows():
 
 
 @pytest.mark.parametrize("M,N,K,rows_special", [(200, 264, 1024, True), (257, 392, 2048, False),
-                                                 (150, 136, 12288, True), (130, 400, 1024, False)])
+                                                 (150, 136, 12288, True), (130, 400, 1024, False),
+                                                 (700, 264, 1024, True), (520, 400, 2048, False)])
 def test_f8_extreme_scales(M, N, K, rows_special):
     print(f"[f8-extreme] M={M} N={N} K={K}", flush=True)
     rng = np.random.default_rng(M * 7 + K)
