@@ -24,7 +24,7 @@
 //
 // Three kernels, no split-K, no atomics:
 //  * k2_dec (M <= 64): one workgroup per 16 output columns and all M rows.
-//    Its eight waves each take one K group per round, compute the exact
+//    Its 8 or 16 waves each take one K group per round, compute the exact
 //    int32 group dots with v_mfma_i32_16x16x64_i8 and hand them through LDS
 //    to the whole workgroup, which runs the fp32 epilogue in group order.
 //    Loads run several rounds ahead.
@@ -48,14 +48,14 @@ __device__ __forceinline__ void store_out(void* out, int64_t idx, float v) {
 
 // ----------------------------------------------------------------------------
 // Decode kernel (M <= 64).  Workgroup = one 16-column block, all M rows
-// (MB row blocks of 16), whole K; its eight waves split the K groups: in
-// round r wave w takes group 8r + w.  Per group the wave computes the exact
-// int32 dots of the 16-column x ROWS tile (v_mfma_i32_16x16x64_i8, two per
-// row block) and writes them to LDS as int16; after the round's barrier each
-// thread advances the in-order fp32 epilogue of the output(s) it owns over
-// the round's eight groups while later rounds' loads are in flight.  Dots,
-// activation slices and scales are double buffered, so one barrier per round
-// suffices.
+// (MB row blocks of 16), whole K; its NW waves (8, or 16 when one workgroup
+// per CU covers N) split the K groups: in round r wave w takes group
+// NW r + w.  Per group the wave computes the exact int32 dots of the
+// 16-column x ROWS tile (v_mfma_i32_16x16x64_i8, two per row block) and
+// writes them to LDS as int16; after the round's barrier each thread owning
+// an output advances its in-order fp32 epilogue over the round's NW groups
+// while later rounds' loads are in flight.  Dots, activation slices and
+// scales are double buffered, so one barrier per round suffices.
 //
 // Loads are shaped for the CU's load path, which moves whole contiguous
 // 128-byte lines several times faster than the 16 half-lines of a per-lane
@@ -64,102 +64,119 @@ __device__ __forceinline__ void store_out(void* out, int64_t idx, float v) {
 //    1 KiB, lane l's 16 bytes at l*16, so a wave loads whole lines; with the
 //    reference layout [N][K/2] lane l loads column l%16, bytes 16*(l/16) of
 //    the group's 64;
-//  * activations: the round's slice (ROWS rows x 512 bytes) is loaded in
+//  * activations: the round's slice (ROWS rows x NW*64 bytes) is loaded in
 //    whole lines by all threads, staged in LDS one round ahead and read back
 //    as MFMA operands.
-// All loads of a round ride in a register ring D rounds deep (every byte of
-// a K = 4096 projection is requested before the first MFMA), together with
-// the round's scales (sa of every row and sw of the 16 columns, 8 groups).
+// All loads of a round ride in a register ring D rounds deep, together with
+// the round's scales (sa of every row and sw of the 16 columns, NW groups).
+// They are buffer loads whose per-thread offsets are fixed for the kernel:
+// the round enters as a scalar offset, so the ring costs no vector address
+// arithmetic.
 //
 // Layouts.  MFMA 16x16x64 i8: A operand lane l supplies row l%16, B operand
 // column l%16, both the k-slots of set l/16; lane l of the result holds
-// C[4*(l/16) + i][l%16], i = 0..3.  LDS activation slice: row r at r*512
-// bytes, its 16-byte chunk c at chunk (c & ~7) | ((c ^ r) & 7), so the 16
-// rows of one operand load fall in distinct bank groups.  Tile output
+// C[4*(l/16) + i][l%16], i = 0..3.  LDS activation slice: row r at
+// r*NW*64 bytes, its 16-byte chunk c at chunk (c & ~7) | ((c ^ r) & 7), so
+// the 16 rows of one operand load fall in distinct bank groups.  Tile output
 // o = rb*256 + 4*l + i (row block rb, MFMA lane l, result i) is row
 // 16 rb + 4 (l/16) + i, column l%16: the epilogue's dot reads are
-// consecutive int16 over the threads.  Round scales: sal[row][group % 8]
-// and swl[column][group % 8], so a thread reads its eight in two 16-byte
-// loads.  Each phase issues all of its LDS reads before their first use
-// (the compiler would otherwise wait on each read in turn).
+// consecutive int16 over the threads.  Round scales: sal[row][group % NW]
+// and swl[column][group % NW], read four at a time.  Each phase issues all
+// of its LDS reads before their first use (the compiler would otherwise wait
+// on each read in turn).
 //
-// Every global load is unconditional (indices clamped into range): a load
+// Every global load is unconditional (offsets clamped into range): a load
 // under a thread-dependent branch makes the compiler drain all outstanding
 // loads at the branch join, which would serialise the ring.
 // ----------------------------------------------------------------------------
-constexpr int DC_WAVES = 8;
-constexpr int DC_T = DC_WAVES * 64;
+constexpr int DC_RSRC_WORD3 = 0x00020000;  // buffer resource word 3 (CDNA): 32-bit data format
 
-__device__ __forceinline__ int dc_swz(int r, int c) { return r * 512 + (((c & ~7) | ((c ^ r) & 7)) << 4); }
-
-template <int MB, int D, bool TW, bool SW_GROUPED, bool OUT_F32>
-__global__ void __launch_bounds__(DC_T, 2)
+template <int MB, int NW, int D, bool TW, bool SW_GROUPED, bool OUT_F32>
+__global__ void __launch_bounds__(NW * 64, 16 / NW)
 k2_dec(const int8_t* __restrict__ a, const int8_t* __restrict__ w,
        const uint16_t* __restrict__ sa, const uint16_t* __restrict__ sw,
        void* __restrict__ out, int M, int N, int K) {
+    constexpr int DC_T = NW * 64;
     constexpr int ROWS = MB * 16, NOUT = ROWS * 16;
+    constexpr int GR = NW;                                              // groups per round
+    constexpr int SLB = GR * 64;                                        // slice bytes per row and round
+    constexpr int CPR = SLB / 16;                                       // 16-byte chunks per row and round
     constexpr int OPT = (NOUT + DC_T - 1) / DC_T;                      // outputs per thread
-    constexpr int APT = ROWS * 32 / DC_T;                               // activation chunks per thread
-    constexpr int N_SA = ROWS * 8;                                      // scale entries per round
-    constexpr int N_SW = SW_GROUPED ? 16 * 8 : 0;
+    constexpr int APT = ROWS * CPR / DC_T;                              // activation chunks per thread
+    constexpr int N_SA = ROWS * GR;                                     // scale entries per round
+    constexpr int N_SW = SW_GROUPED ? 16 * GR : 0;
     constexpr int SPT = (N_SA + N_SW + DC_T - 1) / DC_T;
-    static_assert(APT * DC_T == ROWS * 32, "activation slice must split evenly");
-    __shared__ __align__(16) uint8_t a_l[2][ROWS * 512];
-    __shared__ __align__(16) int16_t dots[2][DC_WAVES][NOUT];
-    __shared__ __align__(16) float sal[2][ROWS][8];  // a row's 8 scales of the round together
-    __shared__ __align__(16) float swl[2][16][8];
+    static_assert(APT * DC_T == ROWS * CPR, "activation slice must split evenly");
+    static_assert(N_SA % 64 == 0 && N_SW % 64 == 0, "scale classes must be wave-uniform");
+    __shared__ __align__(16) uint8_t a_l[2][ROWS * SLB];
+    __shared__ __align__(16) int16_t dots[2][GR][NOUT];
+    __shared__ __align__(16) float sal[2][ROWS][GR];  // a row's scales of the round together
+    __shared__ __align__(16) float swl[2][16][GR];
     __shared__ float ssink[1];
 
     const int t = threadIdx.x;
-    const int lane = t & 63, wave = t >> 6;
+    const int lane = t & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
     const int n0 = blockIdx.x * 16;
     const int G = K >> 7;
-    const int R = (G + 7) >> 3;  // rounds
+    const int R = (G + GR - 1) / GR;  // rounds
     const int KB = K >> 1;
     const int rc = lane & 15, part = lane >> 4;
 
-    // Weights: the tiled layout is [N/16][G][64 lanes][16 bytes].
-    const int8_t* wbase = TW ? w + (int64_t)blockIdx.x * G * 1024 + lane * 16
-                             : w + (int64_t)min(n0 + rc, N - 1) * KB + part * 16;
+    // Every global load is a buffer load whose per-thread offset is fixed for
+    // the whole kernel; the round enters as a scalar offset, so the ring's
+    // address work is scalar.  All offsets are clamped into range.
+    // Weights: the column block's K/128 tiled 1 KiB groups (lane l's 16 bytes
+    // at l*16), or its rows of the reference layout [N][K/2].
+    const int8_t* wblk = TW ? w + (int64_t)blockIdx.x * G * 1024 : w + (int64_t)n0 * KB;
+    const __amdgpu_buffer_rsrc_t rsw_w = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<int8_t*>(wblk), (short)0, TW ? G * 1024 : min(16, N - n0) * KB, DC_RSRC_WORD3);
+    const int w_voff = TW ? lane * 16 : (min(n0 + rc, N - 1) - n0) * KB + part * 16;
     const int wstep = TW ? 1024 : 64;
-
-    // Activation staging: thread t moves chunks q = t + 512 i (row q/32,
-    // chunk q%32 of the row's 512-byte slice).  The slice of round r starts
-    // at byte 512 r, moved back so that it ends at the row end when the last
+    // Activations: thread t moves chunks q = t + DC_T i (row q / CPR, chunk
+    // q % CPR of the row's SLB-byte slice).  The slice of round r starts at
+    // byte SLB r, moved back so that it ends at the row end when the last
     // round is partial.
-    const int8_t* arow[APT];
-    int a_c16[APT], a_dst[APT];
+    const __amdgpu_buffer_rsrc_t rsw_a =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<int8_t*>(a), (short)0, M * KB, DC_RSRC_WORD3);
+    int a_voff[APT], a_dst[APT];
 #pragma unroll
     for (int i = 0; i < APT; ++i) {
         const int q = t + i * DC_T;
-        const int r = q >> 5, c = q & 31;
-        arow[i] = a + (int64_t)min(r, M - 1) * KB;
-        a_c16[i] = c * 16;
-        a_dst[i] = dc_swz(r, c);
+        const int r = q / CPR, c = q % CPR;
+        a_voff[i] = min(r, M - 1) * KB + c * 16;
+        a_dst[i] = r * SLB + (((c & ~7) | ((c ^ r) & 7)) << 4);
     }
-    auto slice_start = [&](int r) { return max(0, min(r * 512, KB - 512)); };
+    auto slice_start = [&](int r) { return max(0, min(r * SLB, KB - SLB)); };
 
-    // Scale staging: entry e < N_SA is sa[row = e/8][8r + e%8] (stored at
-    // sal[.][e/8][e%8]), then sw.
-    const uint16_t* sp[SPT];
+    // Scale staging: entry e < N_SA is sa[row = e/GR][GR r + e%GR] (stored at
+    // sal[.][e/GR][e%GR]), then sw.  Whether an entry is sa, sw or nothing is
+    // uniform over a wave, so each wave picks one buffer resource; the group
+    // index is clamped per thread (a min with a scalar), the rest of the
+    // offset is fixed.
+    const __amdgpu_buffer_rsrc_t rsw_sa =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(sa), (short)0, M * G * 2, DC_RSRC_WORD3);
+    const __amdgpu_buffer_rsrc_t rsw_sw = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint16_t*>(sw), (short)0, (SW_GROUPED ? N * G : N) * 2, DC_RSRC_WORD3);
+    int s_voff[SPT], sgl[SPT], sstride[SPT];
     float* sdst[SPT];
-    int sgl[SPT], sstride[SPT];
 #pragma unroll
     for (int q = 0; q < SPT; ++q) {
         const int e = t + q * DC_T;
-        sgl[q] = e & 7;
+        sgl[q] = e % GR;
         if (e < N_SA) {
-            const int row = e >> 3;
-            sp[q] = sa + (int64_t)min(row, M - 1) * G;
+            const int row = e / GR;
+            s_voff[q] = min(row, M - 1) * G * 2;
             sdst[q] = &sal[0][row][sgl[q]];
-            sstride[q] = 8 * ROWS;
+            sstride[q] = GR * ROWS;
         } else if (e < N_SA + N_SW) {
-            const int col = (e - N_SA) >> 3;
-            sp[q] = sw + (int64_t)min(n0 + col, N - 1) * G;
+            const int col = (e - N_SA) / GR;
+            s_voff[q] = min(n0 + col, N - 1) * G * 2;
             sdst[q] = &swl[0][col][sgl[q]];
-            sstride[q] = 8 * 16;
+            sstride[q] = GR * 16;
         } else {  // nothing to stage: load a valid scale, store to the sink
-            sp[q] = sa;
+            s_voff[q] = 0;
+            sgl[q] = 0;
             sdst[q] = ssink;
             sstride[q] = 0;
         }
@@ -168,26 +185,43 @@ k2_dec(const int8_t* __restrict__ a, const int8_t* __restrict__ w,
     v4u rw[D], ra[D][APT];
     uint16_t rs[D][SPT];
     auto issue = [&](int r, v4u& w_out, v4u (&a_out)[APT], uint16_t (&s_out)[SPT]) {
-        w_out = *reinterpret_cast<const v4u*>(wbase + (int64_t)min(r * 8 + wave, G - 1) * wstep);
-        const int aoff = slice_start(min(r, R - 1));
+        w_out = __builtin_bit_cast(
+            v4u, __builtin_amdgcn_raw_buffer_load_b128(rsw_w, w_voff, min(r * GR + wave, G - 1) * wstep, 0));
+        const int rr = min(r, R - 1);        // rounds past the end reload the last one (unused)
+        const int aoff = slice_start(rr);
 #pragma unroll
         for (int i = 0; i < APT; ++i)
-            a_out[i] = *reinterpret_cast<const v4u*>(arow[i] + min(aoff + a_c16[i], KB - 16));
+            a_out[i] = __builtin_bit_cast(v4u, __builtin_amdgcn_raw_buffer_load_b128(rsw_a, a_voff[i], aoff, 0));
+        const int glast = G - 1 - rr * GR;   // the round's last valid group, relative (>= 0)
 #pragma unroll
-        for (int q = 0; q < SPT; ++q) s_out[q] = sp[q][min(r * 8 + sgl[q], G - 1)];
+        for (int q = 0; q < SPT; ++q) {
+            const int ew = wave * 64 + q * DC_T;  // scalar: the wave's entry class
+            const bool live = ew < N_SA + N_SW;
+            const __amdgpu_buffer_rsrc_t rs_q = ew < N_SA || !live ? rsw_sa : rsw_sw;
+            s_out[q] = __builtin_amdgcn_raw_buffer_load_b16(rs_q, s_voff[q] + min(sgl[q], glast) * 2,
+                                                            live ? rr * GR * 2 : 0, 0);
+        }
+        // Keep each round's loads together and in round order: loads return
+        // in issue order, so a round's data must not queue behind later ones.
+        __builtin_amdgcn_sched_barrier(0);
     };
     auto stage_a = [&](int r, const v4u (&a_in)[APT]) {
 #pragma unroll
         for (int i = 0; i < APT; ++i) *reinterpret_cast<v4u*>(&a_l[r & 1][a_dst[i]]) = a_in[i];
     };
+    // A-operand LDS offsets: group g's chunk in the slice is 4 j + part with
+    // j = (64 g - slice start) / 64 (scalar), so its swizzled position is
+    // 128 (j >> 1) + x[j & 1] with x precomputed per lane.
+    const int ax0 = rc * SLB + (((part ^ rc) & 7) << 4);
+    const int ax1 = rc * SLB + ((((4 + part) ^ rc) & 7) << 4);
     auto mma = [&](int r, const v4u& w_in, const uint16_t (&s_in)[SPT]) {
         const int buf = r & 1;
-        if (r * 8 + wave < G) {  // uniform over the wave
-            const int cbase = (wave * 64 + r * 512 - slice_start(r)) >> 4;  // group's chunk in the slice
+        if (r * GR + wave < G) {  // uniform over the wave
+            const int j = ((r * GR + wave) * 64 - slice_start(r)) >> 6;
+            const int aoff = buf * (ROWS * SLB) + 128 * (j >> 1) + ((j & 1) ? ax1 : ax0);
             v4u av[MB];  // every operand read issued before the first use
 #pragma unroll
-            for (int mb = 0; mb < MB; ++mb)
-                av[mb] = *reinterpret_cast<const v4u*>(&a_l[buf][dc_swz(mb * 16 + rc, cbase + part)]);
+            for (int mb = 0; mb < MB; ++mb) av[mb] = *reinterpret_cast<const v4u*>(&a_l[0][aoff + mb * 16 * SLB]);
             __builtin_amdgcn_sched_barrier(0);
             const v4i w0 = unpack8_x16(w_in[0], w_in[1]);
             const v4i w1 = unpack8_x16(w_in[2], w_in[3]);
@@ -198,9 +232,10 @@ k2_dec(const int8_t* __restrict__ a, const int8_t* __restrict__ w,
                 v4i acc = {0, 0, 0, 0};
                 acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, w0, acc, 0, 0, 0);
                 acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, w1, acc, 0, 0, 0);
-                // 256 * dot -> dot (exact); |dot| <= 8192 fits int16.
-                const uint32_t lo = ((uint32_t)(acc[0] >> 8) & 0xffffu) | ((uint32_t)(acc[1] >> 8) << 16);
-                const uint32_t hi = ((uint32_t)(acc[2] >> 8) & 0xffffu) | ((uint32_t)(acc[3] >> 8) << 16);
+                // 256 * dot -> dot: |dot| <= 8192, so bytes 1..2 of 256 * dot
+                // are the int16 dot; one byte permute packs two of them.
+                const uint32_t lo = __builtin_amdgcn_perm((uint32_t)acc[1], (uint32_t)acc[0], 0x06050201u);
+                const uint32_t hi = __builtin_amdgcn_perm((uint32_t)acc[3], (uint32_t)acc[2], 0x06050201u);
                 *reinterpret_cast<uint2*>(&dots[buf][wave][mb * 256 + lane * 4]) = make_uint2(lo, hi);
             }
         }
@@ -213,30 +248,30 @@ k2_dec(const int8_t* __restrict__ a, const int8_t* __restrict__ w,
     for (int oi = 0; oi < OPT; ++oi) total[oi] = 0.0f;
     auto epilogue = [&](int r) {
         const int buf = r & 1;
-        const int ng = min(8, G - r * 8);
+        const int ng = min(GR, G - r * GR);
 #pragma unroll
         for (int oi = 0; oi < OPT; ++oi) {
             const int o = t + oi * DC_T;
             if (o < NOUT) {
                 const int l = (o >> 2) & 63;
                 const int row = (o >> 8) * 16 + 4 * (l >> 4) + (o & 3), col = l & 15;
-                if (ng == 8) {
+                if (ng == GR) {
                     // All LDS reads first (one wait), then the in-order chain.
-                    int dr[8];
+                    int dr[GR];
 #pragma unroll
-                    for (int gl = 0; gl < 8; ++gl) dr[gl] = dots[buf][gl][o];
-                    const v4f a0 = *reinterpret_cast<const v4f*>(&sal[buf][row][0]);
-                    const v4f a1 = *reinterpret_cast<const v4f*>(&sal[buf][row][4]);
-                    v4f w0 = {1.0f, 1.0f, 1.0f, 1.0f}, w1 = w0;
-                    if constexpr (SW_GROUPED) {
-                        w0 = *reinterpret_cast<const v4f*>(&swl[buf][col][0]);
-                        w1 = *reinterpret_cast<const v4f*>(&swl[buf][col][4]);
+                    for (int gl = 0; gl < GR; ++gl) dr[gl] = dots[buf][gl][o];
+                    v4f av[GR / 4], wv[GR / 4];
+#pragma unroll
+                    for (int i = 0; i < GR / 4; ++i) {
+                        av[i] = *reinterpret_cast<const v4f*>(&sal[buf][row][4 * i]);
+                        wv[i] = v4f{1.0f, 1.0f, 1.0f, 1.0f};
+                        if constexpr (SW_GROUPED) wv[i] = *reinterpret_cast<const v4f*>(&swl[buf][col][4 * i]);
                     }
                     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-                    for (int gl = 0; gl < 8; ++gl) {
-                        const float sa_g = gl < 4 ? a0[gl & 3] : a1[gl & 3];
-                        const float s = SW_GROUPED ? sa_g * (gl < 4 ? w0[gl & 3] : w1[gl & 3]) : sa_g;
+                    for (int gl = 0; gl < GR; ++gl) {
+                        const float sa_g = av[gl >> 2][gl & 3];
+                        const float s = SW_GROUPED ? sa_g * wv[gl >> 2][gl & 3] : sa_g;
                         total[oi] = __builtin_fmaf((float)dr[gl], s, total[oi]);
                     }
                 } else {
@@ -445,12 +480,27 @@ k2_wide(const int8_t* __restrict__ a, const int8_t* __restrict__ w,
     }
 }
 
+int cu_count();
+
 template <int MB, bool TW, bool SG, bool OF>
 hipError_t launch_dec(const int8_t* a, const int8_t* w, const void* sa, const void* sw, void* out,
                       int M, int N, int K, hipStream_t st) {
+    const int blocks = (N + 15) / 16;
+    const dim3 grid((unsigned)blocks);
+    const auto* sap = static_cast<const uint16_t*>(sa);
+    const auto* swp = static_cast<const uint16_t*>(sw);
+    // When one workgroup per CU covers every column block, 16 waves with a
+    // two-round ring (16 groups per round) hide more latency than 8 waves;
+    // with more column blocks than CUs, two 8-wave workgroups share a CU.
+    if constexpr (MB <= 2) {
+        if (K >= 2048 && blocks <= cu_count()) {
+            hipLaunchKernelGGL((k2_dec<MB, 16, 2, TW, SG, OF>), grid, dim3(16 * 64), 0, st, a, w, sap, swp, out, M,
+                               N, K);
+            return hipGetLastError();
+        }
+    }
     constexpr int D = 4;  // rounds in flight: all of them for K <= 4096
-    hipLaunchKernelGGL((k2_dec<MB, D, TW, SG, OF>), dim3((unsigned)((N + 15) / 16)), dim3(DC_T), 0, st, a, w,
-                       static_cast<const uint16_t*>(sa), static_cast<const uint16_t*>(sw), out, M, N, K);
+    hipLaunchKernelGGL((k2_dec<MB, 8, D, TW, SG, OF>), grid, dim3(8 * 64), 0, st, a, w, sap, swp, out, M, N, K);
     return hipGetLastError();
 }
 
@@ -622,3 +672,4 @@ extern "C" int nv4_w4a4_tile_weights(const int8_t* w, int8_t* w_tiled, int64_t N
 extern "C" int nv4_w4a4_untile_weights(const int8_t* w_tiled, int8_t* w, int64_t N, int64_t K, void* stream) {
     return nv4::tile_impl(w_tiled, w, false, N, K, stream);
 }
+

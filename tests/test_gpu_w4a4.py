@@ -151,6 +151,18 @@ def test_k2_decode_activations_in_lds(M, N, K):
         run_case(M, N, K, 4000 + M + K, grouped=False)
 
 
+@pytest.mark.parametrize("M,N,K", [(1, 4096, 4096), (32, 4096, 2176), (16, 4096, 6272), (9, 2048, 3200),
+                                   (32, 136, 12160), (20, 4000, 2048), (17, 1024, 12288)])
+def test_k2_decode_sixteen_waves(M, N, K):
+    """Shapes served by the 16-wave decode kernel (M <= 32, K >= 2048, no
+    more 16-column blocks than compute units: 16 K groups per round, a
+    two-round load ring): partial last rounds (K/128 = 17, 49, 25, 95), a
+    single round (K = 2048), column tails, grouped and per-channel scales."""
+    run_case(M, N, K, 7000 + M + K)
+    if M in (9, 32):
+        run_case(M, N, K, 8000 + M + K, grouped=False)
+
+
 @pytest.mark.parametrize("M,N,K", [(1, 16392, 4096), (17, 16392, 4096), (32, 16392, 2048), (32, 16384, 4096)])
 def test_k2_decode_wide_n(M, N, K):
     """Shapes served by the wide decode kernel (each wave owns 16 columns over

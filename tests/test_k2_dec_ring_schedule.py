@@ -4,7 +4,9 @@ nano-vllm-int4_amd/csrc/w4a4_gemm.hip).
 The kernel's main loop is replayed as a sequence of phases separated by
 workgroup barriers, with the LDS buffers each phase writes or reads: the
 activation slice ``a_l[2]``, the group dots ``dots[2]`` and the round's scales
-``sal[2]`` / ``swl[2]``, each double-buffered on the round's parity.  Threads
+``sal[2]`` / ``swl[2]``, each double-buffered on the round's parity.  A round
+is 8 K groups (8 waves, ring depth 4) or 16 (16 waves, ring depth 2); the
+schedule is the same, only the round count changes.  Threads
 of a workgroup run the phases of one barrier interval in any interleaving, so
 the schedule is race-free iff no buffer copy is written in an interval in
 which it is also read (every read in this kernel is of data other threads
@@ -138,14 +140,61 @@ def hazards(rp):
     return found
 
 
-# K of the four Qwen3-8B projections and the test shapes: G = K/128 groups,
-# R = ceil(G/8) rounds; the launcher's ring depth 4 and others.
-CASES = [(K, D) for K in (256, 512, 1024, 2048, 4096, 8192, 12288) for D in (2, 3, 4, 6)]
+def overlapped_with_ring(R, D, rp=None, ring=None):
+    """The overlapped order with its register ring: a prologue that forms
+    round 0's products and stages round 1, then per interval the products of
+    round r + 1, the epilogue of round r, the staging of round r + 2 and the
+    refill of round r + 1's slot with round r + 1 + D."""
+    rp = rp or Replay()
+    ring = ring or Ring(D)
+    for u in range(D):
+        ring.issue(u, u)
+    ring.use("ra", 0, 0)
+    rp.stage_a(0)
+    rp.barrier()
+    ring.use("rw", 0, 0), ring.use("rs", 0, 0)
+    rp.mma(0)
+    if R > 1:
+        ring.use("ra", 1 % D, 1)
+        rp.stage_a(1)
+    ring.issue(D, 0)
+    rp.barrier()
+
+    def interval(r, steady):
+        if steady or r + 1 < R:
+            ring.use("rw", (r + 1) % D, r + 1), ring.use("rs", (r + 1) % D, r + 1)
+            rp.mma(r + 1)
+        rp.epilogue(r)
+        if steady or r + 2 < R:
+            ring.use("ra", (r + 2) % D, r + 2)
+            rp.stage_a(r + 2)
+        if steady:
+            ring.issue(r + 1 + D, (r + 1) % D)
+    r0 = 0
+    while r0 + D + 1 < R:
+        for u in range(D):
+            interval(r0 + u, True)
+            rp.barrier()
+        r0 += D
+    for u in range(D + 1):
+        if r0 + u < R:
+            interval(r0 + u, False)
+            if r0 + u + 1 < R:
+                rp.barrier()
+    return rp
 
 
-@pytest.mark.parametrize("K,D", CASES)
-def test_shipped_schedule_is_race_free(K, D):
-    R = (K // 128 + 7) // 8
+# K of the four Qwen3-8B projections, the test shapes and K with a partial
+# last round; G = K/128 groups, GR groups per round (8 or 16 waves), R =
+# ceil(G/GR) rounds; the launcher's ring depths (4 with 8 waves, 2 with 16)
+# and others.
+KS = (256, 512, 1024, 2048, 2176, 3200, 4096, 6272, 8192, 12160, 12288)
+CASES = [(K, GR, D) for K in KS for GR in (8, 16) for D in (2, 3, 4, 6) if GR == 8 or K >= 2048]
+
+
+@pytest.mark.parametrize("K,GR,D", CASES)
+def test_shipped_schedule_is_race_free(K, GR, D):
+    R = (K // 128 + GR - 1) // GR
     rp = shipped(R, D)
     assert hazards(rp) == []
     epilogues = [e[4] for e in rp.events if e[1] == "dots" and e[3] == "R"]
@@ -153,10 +202,13 @@ def test_shipped_schedule_is_race_free(K, D):
     assert rp.interval == R + 1                  # the prologue's barrier, then one per round
 
 
-@pytest.mark.parametrize("K,D", CASES)
-def test_overlapped_schedule_is_race_free(K, D):
-    R = (K // 128 + 7) // 8
+@pytest.mark.parametrize("K,GR,D", CASES)
+def test_overlapped_schedule_is_race_free(K, GR, D):
+    R = (K // 128 + GR - 1) // GR
     assert hazards(overlapped(R, D)) == []
+    rp = overlapped_with_ring(R, D)
+    assert hazards(rp) == []
+    assert [e[4] for e in rp.events if e[1] == "dots" and e[3] == "R"] == list(range(R))
 
 
 def test_single_buffered_dots_is_rejected():
@@ -178,6 +230,8 @@ def test_ring_refill_into_a_live_slot_is_rejected():
             super().issue(r, u if r < self.D else (u + 1) % self.D)
     with pytest.raises(AssertionError):
         shipped(12, 4, ring=Early(4))
+    with pytest.raises(AssertionError):
+        overlapped_with_ring(12, 4, ring=Early(4))
 
 
 def test_missing_barrier_is_rejected():
