@@ -436,33 +436,55 @@ k2_wide(const int8_t* __restrict__ a, const int8_t* __restrict__ w,
     const float* sap = &sa_l[mb * 16 + 4 * part];
     const float* swq = &sw_l[cbl * 16 + rc];
 
-    auto consume = [&](int g, const v4u& w_in) {
+    // A group's LDS operands (two activation operands, the four rows'
+    // activation scales, the column's weight scale) are read one group ahead
+    // of their use, so the wave's MFMAs never wait on an LDS round trip.
+    struct Ops {
+        v4i a0, a1;
+        v4f s_a;
+        float s_w;
+    };
+    auto lds_ops = [&](int g, Ops& o) {
+        const int u0 = (g * 4 + part) * 2, u1 = u0 + 1;
+        o.a0 = *reinterpret_cast<const v4i*>(&a_l[r * K + (((u0 & ~7) | ((u0 ^ r) & 7)) << 4)]);
+        o.a1 = *reinterpret_cast<const v4i*>(&a_l[r * K + (((u1 & ~7) | ((u1 ^ r) & 7)) << 4)]);
+        o.s_a = *reinterpret_cast<const v4f*>(sap + g * ROWS);
+        o.s_w = SW_GROUPED ? swq[g * COLS] : 1.0f;
+    };
+    auto consume = [&](const v4u& w_in, const Ops& o) {
         const v4i w0 = unpack8_x16(w_in[0], w_in[1]);
         const v4i w1 = unpack8_x16(w_in[2], w_in[3]);
-        const int u0 = (g * 4 + part) * 2, u1 = u0 + 1;
-        const v4i a0 = *reinterpret_cast<const v4i*>(&a_l[r * K + (((u0 & ~7) | ((u0 ^ r) & 7)) << 4)]);
-        const v4i a1 = *reinterpret_cast<const v4i*>(&a_l[r * K + (((u1 & ~7) | ((u1 ^ r) & 7)) << 4)]);
-        const v4f s_a = *reinterpret_cast<const v4f*>(sap + g * ROWS);
-        const float s_w = SW_GROUPED ? swq[g * COLS] : 1.0f;
         v4i acc = {0, 0, 0, 0};
-        acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, w0, acc, 0, 0, 0);
-        acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, w1, acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(o.a0, w0, acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(o.a1, w1, acc, 0, 0, 0);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const float d = (float)(acc[i] >> 8);
-            total[i] = SW_GROUPED ? __builtin_fmaf(d, s_a[i] * s_w, total[i]) : __builtin_fmaf(d, s_a[i], total[i]);
+            total[i] = SW_GROUPED ? __builtin_fmaf(d, o.s_a[i] * o.s_w, total[i]) : __builtin_fmaf(d, o.s_a[i], total[i]);
         }
     };
 
+    Ops cur;
+    lds_ops(0, cur);
     int g0 = 0;
     for (; g0 + D < G; g0 += D) {
         static_for<0, D>([&](auto U) {
-            consume(g0 + U, rw[U]);
+            Ops nxt;
+            lds_ops(g0 + U + 1, nxt);  // g0 + U + 1 < G inside the loop
+            __builtin_amdgcn_sched_barrier(0);
+            consume(rw[U], cur);
             issue(g0 + U + D, rw[U]);
+            cur = nxt;
         });
     }
     static_for<0, D>([&](auto U) {
-        if (g0 + U < G) consume(g0 + U, rw[U]);
+        if (g0 + U < G) {
+            Ops nxt;
+            lds_ops(min(g0 + U + 1, G - 1), nxt);
+            __builtin_amdgcn_sched_barrier(0);
+            consume(rw[U], cur);
+            cur = nxt;
+        }
     });
 
     if (col < N) {
