@@ -404,9 +404,7 @@ k3_reduce(const float* __restrict__ ws, void* __restrict__ out, int64_t MN, int 
 //  * At the end the 8 waves' fp32 tiles are added in wave order in LDS and
 //    rounded once (deterministic, no atomics).
 // ----------------------------------------------------------------------------
-constexpr int K3O_T = 512;
 constexpr int K3O_MAXK = 4096;
-constexpr int K3O_RING = 32768;        // bytes of activations per ring chunk
 constexpr int K3O_ONE_BYTES = 65536;   // all activations staged at once when M * K * 2 fits
 
 template <bool F16>
@@ -444,19 +442,20 @@ __device__ __forceinline__ v4u octet_order(v4u v) {
                __builtin_amdgcn_perm(v[3], v[1], 0x05040100u), __builtin_amdgcn_perm(v[3], v[1], 0x07060302u)};
 }
 
-template <int MB, int NB, int ST, bool ONE, bool XF16, bool OF16>
-__global__ void __launch_bounds__(K3O_T)
+template <int MB, int NB, int ST, int NWV, int RING, bool ONE, bool XF16, bool OF16>
+__global__ void __launch_bounds__(NWV * 64)
 k3_one(const uint16_t* __restrict__ x, const int32_t* __restrict__ qweight, const int32_t* __restrict__ qzeros,
        const uint16_t* __restrict__ scales, void* __restrict__ out, int M, int N, int K) {
     using BC = BiasCode<XF16>;
     using vec = typename BC::vec;
     constexpr int NT = NB / 16;                   // column tiles, words per lane and step
     constexpr int ROWS = MB * 16;
-    constexpr int KC = K3O_RING / (2 * ROWS);    // k per chunk (the group geometry of both modes)
+    constexpr int K3O_T = NWV * 64;
+    constexpr int KC = RING / (2 * ROWS);         // k per chunk (the group geometry of both modes)
     constexpr int SPC = KC / 32;                  // 32-k steps per chunk
-    constexpr int SPW = SPC / 8;                  // steps per wave and chunk (4, 2 or 1)
+    constexpr int SPW = SPC / NWV;                // steps per wave and chunk (4, 2 or 1)
     constexpr int CPR = KC / 8;                   // octets per row and chunk
-    constexpr int PPT = K3O_RING / 16 / K3O_T;    // ring octets per thread and chunk (4)
+    constexpr int PPT = RING / 16 / K3O_T;        // ring octets per thread and chunk (4)
     constexpr int PPT1 = ONE ? K3O_ONE_BYTES / 16 / K3O_T : 1;
     static_assert(SPW >= 1 && ST % SPW == 0, "chunk shape");
     extern __shared__ __align__(16) uint8_t smem[];
@@ -481,7 +480,7 @@ k3_one(const uint16_t* __restrict__ x, const int32_t* __restrict__ qweight, cons
         }
     };
     auto store_chunk = [&](int ch, const v4u (&xv)[PPT]) {
-        uint8_t* base = smem + (ch & 1) * K3O_RING;
+        uint8_t* base = smem + (ch & 1) * RING;
 #pragma unroll
         for (int i = 0; i < PPT; ++i) {
             const int p = t + i * K3O_T;
@@ -563,7 +562,7 @@ k3_one(const uint16_t* __restrict__ x, const int32_t* __restrict__ qweight, cons
             cj[j] = BC::BIAS + (float)((zw >> (zsh + 4 * j)) & 15u) + 1.0f;
         }
         load_sz(min(ch + 1, NCH - 1), sw, zw);
-        const uint8_t* base = ONE ? smem : smem + (ch & 1) * K3O_RING;
+        const uint8_t* base = ONE ? smem : smem + (ch & 1) * RING;
         const int rstride = ONE ? K * 2 : KC * 2;
         v4f S[MB][NT], X[MB];
 #pragma unroll
@@ -628,7 +627,7 @@ k3_one(const uint16_t* __restrict__ x, const int32_t* __restrict__ qweight, cons
             const int mb = tile / NT, j = tile % NT;
             float v = part[e];
 #pragma unroll
-            for (int w = 1; w < 8; ++w) v = v + part[w * ENT + e];
+            for (int w = 1; w < NWV; ++w) v = v + part[w * ENT + e];
             const int m = mb * 16 + 4 * (el >> 4) + ei, n = n0 + NT * (el & 15) + j;
             if (m < M && n < N) {
                 const uint16_t h = OF16 ? __builtin_bit_cast(uint16_t, (_Float16)v) : (uint16_t)f32_to_bf16_rne(v);
@@ -638,32 +637,52 @@ k3_one(const uint16_t* __restrict__ x, const int32_t* __restrict__ qweight, cons
     }
 }
 
-template <int MB, int NB, int ST, bool XF, bool OF>
+template <int MB, int NB, int ST, int NWV, int RING, bool XF, bool OF>
 hipError_t launch_one_k(const void* x, const int32_t* qw, const int32_t* qz, const void* sc, void* out, int M, int N,
                         int K, hipStream_t st) {
     const dim3 grid((unsigned)((N + NB - 1) / NB));
     const auto* xp = static_cast<const uint16_t*>(x);
     const auto* sp = static_cast<const uint16_t*>(sc);
-    const int parts = 8 * MB * (NB / 16) * 256 * 4;
+    const int parts = NWV * MB * (NB / 16) * 256 * 4;
     if (MB == 1 && (int64_t)M * K * 2 <= K3O_ONE_BYTES) {
         const int lds = max(((M * K * 2) + 15) & ~15, parts);
-        hipLaunchKernelGGL((k3_one<MB, NB, ST, true, XF, OF>), grid, dim3(K3O_T), lds, st, xp, qw, qz, sp, out, M, N,
-                           K);
+        hipLaunchKernelGGL((k3_one<MB, NB, ST, NWV, RING, true, XF, OF>), grid, dim3(NWV * 64), lds, st, xp, qw, qz,
+                           sp, out, M, N, K);
     } else {
-        const int lds = max(2 * K3O_RING, parts);
-        hipLaunchKernelGGL((k3_one<MB, NB, ST, false, XF, OF>), grid, dim3(K3O_T), lds, st, xp, qw, qz, sp, out, M, N,
-                           K);
+        const int lds = max(2 * RING, parts);
+        hipLaunchKernelGGL((k3_one<MB, NB, ST, NWV, RING, false, XF, OF>), grid, dim3(NWV * 64), lds, st, xp, qw, qz,
+                           sp, out, M, N, K);
     }
     return hipGetLastError();
 }
 
-// Dispatched for M <= 16 and K <= 4096 (the projections with K = 4096 at
-// decode batch sizes up to 16); wider M and longer K run the split-K form,
-// which measured faster there.
+int k3_cu_count() {
+    static int cache[64];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0) dev = 0;
+    if (dev < 64 && cache[dev] > 0) return cache[dev];
+    int v = 0;
+    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v <= 0) v = 256;
+    if (dev < 64) cache[dev] = v;
+    return v;
+}
+
+// Whether the one-launch kernel serves this shape: K <= 4096 and M <= 16
+// (8 waves, 32 KiB activation chunks), or M <= 32 when the 32-column
+// workgroups fill more than half the CUs and at most all of them (16 waves,
+// two row blocks, 64 KiB chunks: one workgroup per CU; fused QKV at M = 32,
+// 10.9 us against 11.8 for split-K).  Other shapes run the split-K form,
+// which measured faster there (o at M = 32: 9.2 us against 10.6).
+bool one_launch_fits(int M, int N, int K) {
+    const int wg = (N + 31) / 32, cus = k3_cu_count();
+    return K <= K3O_MAXK && (M <= 16 || (M <= 32 && 2 * wg > cus && wg <= cus));
+}
+
 template <bool XF, bool OF>
 hipError_t dispatch_one(const void* x, const int32_t* qw, const int32_t* qz, const void* sc, void* out, int M, int N,
                         int K, hipStream_t st) {
-    return launch_one_k<1, 32, 16, XF, OF>(x, qw, qz, sc, out, M, N, K, st);
+    if (M <= 16) return launch_one_k<1, 32, 16, 8, 32768, XF, OF>(x, qw, qz, sc, out, M, N, K, st);
+    return launch_one_k<2, 32, 8, 16, 65536, XF, OF>(x, qw, qz, sc, out, M, N, K, st);
 }
 
 template <int MB, bool XF, bool OF>
@@ -787,7 +806,7 @@ extern "C" int nv4_w4a16_gemm(const void* x, int x_dtype, const int32_t* qweight
     const int m = (int)M, n = (int)N, k = (int)K;
     hipError_t e;
     // Small decode batches: the one-launch kernel (8-byte weight and 4-byte scale loads).
-    if (M <= 16 && K <= K3O_MAXK && reinterpret_cast<uintptr_t>(qweight) % 8 == 0 &&
+    if (one_launch_fits(m, n, k) && reinterpret_cast<uintptr_t>(qweight) % 8 == 0 &&
         reinterpret_cast<uintptr_t>(scales) % 4 == 0) {
         if (x_dtype == NV4_FP16)
             e = out_dtype == NV4_FP16 ? dispatch_one<true, true>(x, qweight, qzeros, scales, out, m, n, k, st)

@@ -9,9 +9,11 @@ reference (split-K 8 with bf16 atomics onto a zeroed output) the HIP kernel
 sums all of K in fp32 and writes each output once, so results do not depend
 on scheduling.  FP16 activations are accepted as well (output fp16).
 
-Decode sizes: for M <= 16 and K <= 4096 ``nv4_w4a16_gemm`` runs one launch
-whose workgroups own 32 columns over the whole K (the K split over their
-waves and added in a fixed order in LDS); other M <= 64 take the split-K
+Decode sizes: for K <= 4096 and M <= 16 (or M <= 32 when its 32-column
+workgroups fill between half and all of the CUs, as the fused QKV does)
+``nv4_w4a16_gemm`` runs one launch whose workgroups own 32 columns over the
+whole K (the K split over their waves and added in a fixed order in LDS);
+other M <= 64 take the split-K
 form (``nv4_w4a16_gemm_ws``): 64-column workgroups per 1024-deep K slice
 writing fp32 partials into a workspace from torch's caching allocator, added
 in slice order by a second launch.  Both are deterministic and
@@ -30,7 +32,7 @@ from .. import _lib
 
 _DT = {torch.bfloat16: _lib.BF16, torch.float16: _lib.FP16}
 SLICE_K = 1024  # K per partial of the decode-size split
-ONE_LAUNCH_MAX_K = 4096  # nv4_w4a16_gemm runs one launch for M <= 16 up to this K
+ONE_LAUNCH_MAX_K = 4096  # nv4_w4a16_gemm runs one launch up to this K (see one_launch)
 
 
 def dequant_w4a16(qweight, qzeros, scales, dtype=torch.bfloat16, group_size=128):
@@ -58,6 +60,24 @@ def dequant_w4a16(qweight, qzeros, scales, dtype=torch.bfloat16, group_size=128)
     return w
 
 
+_CUS = {}
+
+
+def one_launch(M, N, K, device):
+    """Whether ``nv4_w4a16_gemm`` runs these sizes in its one-launch kernel
+    (the rule it applies itself): K <= 4096 and M <= 16, or M <= 32 with
+    between half and all of the CUs filled by 32-column workgroups."""
+    if K > ONE_LAUNCH_MAX_K or M > 32:
+        return False
+    if M <= 16:
+        return True
+    idx = torch.device(device).index or 0
+    if idx not in _CUS:
+        _CUS[idx] = torch.cuda.get_device_properties(idx).multi_processor_count
+    wg = (N + 31) // 32
+    return 2 * wg > _CUS[idx] and wg <= _CUS[idx]
+
+
 def dequant_matmul_w4a16(x, qweight, qzeros, scales, group_size=128, out=None):
     """x [M,K] bf16/fp16 -> out [M,N] in x's dtype."""
     if x.ndim != 2 or x.dtype not in _DT:
@@ -82,7 +102,7 @@ def dequant_matmul_w4a16(x, qweight, qzeros, scales, group_size=128, out=None):
     lib = _lib.load()
     stream = torch.cuda.current_stream(x.device).cuda_stream
     with torch.cuda.device(x.device):
-        if M <= 16 and K <= ONE_LAUNCH_MAX_K:
+        if one_launch(M, N, K, x.device):
             rc = lib.nv4_w4a16_gemm(ctypes.c_void_p(x.data_ptr()), _DT[x.dtype],
                                     ctypes.c_void_p(qweight.data_ptr()), ctypes.c_void_p(qzeros.data_ptr()),
                                     ctypes.c_void_p(scales.data_ptr()), ctypes.c_void_p(out.data_ptr()),

@@ -38,7 +38,7 @@ def check_close(out, ref):
 
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
-@pytest.mark.parametrize("M", [1, 8, 9, 16, 32, 33, 64, 65, 100, 300])
+@pytest.mark.parametrize("M", [1, 8, 9, 16, 17, 31, 32, 33, 64, 65, 100, 300])
 def test_k3_w4a16_qkv(M, dtype):
     print(f"[k3] M={M} dtype={dtype}", flush=True)
     case = W.w4a16_case(M, dtype=dtype)
@@ -77,6 +77,25 @@ def test_k3_shapes(N, K, M):
     out = dequant_matmul_w4a16(*(t.to(DEV) for t in (case.x, case.qweight, case.qzeros, case.scales)))
     torch.cuda.synchronize()
     check_close(out, ref)
+
+
+@pytest.mark.parametrize("M,N,K", [(20, 4104, 2048), (32, 8192, 4096), (17, 6144, 640), (32, 4104, 3968)])
+def test_k3_one_launch_two_row_blocks(M, N, K):
+    """Shapes the one-launch kernel takes with two row blocks (17 <= M <= 32,
+    K <= 4096, between half and all of the CUs filled by 32-column
+    workgroups): a column tail, a partial activation chunk (K = 640, 3968),
+    fp16 and bf16 activations; deterministic across calls."""
+    for dtype in (torch.bfloat16, torch.float16):
+        case = W.w4a16_case(M, N=N, K=K, dtype=dtype)
+        xd = oracle.X_FP16 if dtype == torch.float16 else oracle.X_BF16
+        ref = oracle.w4a16_gemm(f16_bits(case.x), case.qweight.numpy(), case.qzeros.numpy(),
+                                case.scales.numpy().view(np.uint16), x_dtype=xd)
+        args = [t.to(DEV) for t in (case.x, case.qweight, case.qzeros, case.scales)]
+        out = dequant_matmul_w4a16(*args)
+        out2 = dequant_matmul_w4a16(*args)
+        torch.cuda.synchronize()
+        check_close(out, ref)
+        assert torch.equal(out, out2)
 
 
 def test_w4a16_linear_module():
