@@ -23,6 +23,19 @@ typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
 
 constexpr int kWave = 64;
 
+// Compute units of the current device (host side, cached per device): the
+// launchers size their grids and choose kernel forms by it.
+inline int device_cu_count() {
+    static int cache[64];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0) dev = 0;
+    if (dev < 64 && cache[dev] > 0) return cache[dev];
+    int v = 0;
+    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v <= 0) v = 256;
+    if (dev < 64) cache[dev] = v;
+    return v;
+}
+
 constexpr int ilog2c(int v) { return v <= 1 ? 0 : 1 + ilog2c(v / 2); }
 
 // Calls f(std::integral_constant<int, I>{}) for I = B .. E-1: indices into

@@ -656,17 +656,6 @@ hipError_t launch_one_k(const void* x, const int32_t* qw, const int32_t* qz, con
     return hipGetLastError();
 }
 
-int k3_cu_count() {
-    static int cache[64];
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0) dev = 0;
-    if (dev < 64 && cache[dev] > 0) return cache[dev];
-    int v = 0;
-    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v <= 0) v = 256;
-    if (dev < 64) cache[dev] = v;
-    return v;
-}
-
 // Whether the one-launch kernel serves this shape: K <= 4096 and M <= 16
 // (8 waves, 32 KiB activation chunks), or M <= 32 when the 32-column
 // workgroups fill more than half the CUs and at most all of them (16 waves,
@@ -674,7 +663,7 @@ int k3_cu_count() {
 // 10.9 us against 11.8 for split-K).  Other shapes run the split-K form,
 // which measured faster there (o at M = 32: 9.2 us against 10.6).
 bool one_launch_fits(int M, int N, int K) {
-    const int wg = (N + 31) / 32, cus = k3_cu_count();
+    const int wg = (N + 31) / 32, cus = device_cu_count();
     return K <= K3O_MAXK && (M <= 16 || (M <= 32 && 2 * wg > cus && wg <= cus));
 }
 

@@ -502,8 +502,6 @@ k2_wide(const int8_t* __restrict__ a, const int8_t* __restrict__ w,
     }
 }
 
-int cu_count();
-
 template <int MB, bool TW, bool SG, bool OF>
 hipError_t launch_dec(const int8_t* a, const int8_t* w, const void* sa, const void* sw, void* out,
                       int M, int N, int K, hipStream_t st) {
@@ -515,7 +513,7 @@ hipError_t launch_dec(const int8_t* a, const int8_t* w, const void* sa, const vo
     // two-round ring (16 groups per round) hide more latency than 8 waves;
     // with more column blocks than CUs, two 8-wave workgroups share a CU.
     if constexpr (MB <= 2) {
-        if (K >= 2048 && blocks <= cu_count()) {
+        if (K >= 2048 && blocks <= device_cu_count()) {
             hipLaunchKernelGGL((k2_dec<MB, 16, 2, TW, SG, OF>), grid, dim3(16 * 64), 0, st, a, w, sap, swp, out, M,
                                N, K);
             return hipGetLastError();
@@ -526,24 +524,12 @@ hipError_t launch_dec(const int8_t* a, const int8_t* w, const void* sa, const vo
     return hipGetLastError();
 }
 
-// Compute units of the current device (cached per device).
-int cu_count() {
-    static int cache[64];
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0) dev = 0;
-    if (dev < 64 && cache[dev] > 0) return cache[dev];
-    int v = 0;
-    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v <= 0) v = 256;
-    if (dev < 64) cache[dev] = v;
-    return v;
-}
-
 // The wide kernel needs the widened activation block and the scales to fit
 // in LDS, whole 8-chunk lines per row (swizzle), and at least 4 column blocks
 // per CU.
 bool wide_fits(int M, int N, int K) {
     const int mb = (M + 15) / 16;
-    const int per_cu = ((N + 15) / 16 + cu_count() - 1) / cu_count();
+    const int per_cu = ((N + 15) / 16 + device_cu_count() - 1) / device_cu_count();
     return M <= 32 && K % 256 == 0 && (int64_t)mb * 16 * K <= WIDE_A_BYTES &&
            (int64_t)(K / 128) * mb * 16 <= WIDE_SCALES && per_cu >= 4 && per_cu <= 8 &&
            (int64_t)(K / 128) * 16 * (per_cu <= 4 ? 4 : per_cu <= 6 ? 6 : 8) <= WIDE_WSCALES;
@@ -563,7 +549,7 @@ template <int MB, bool TW, bool SG, bool OF>
 hipError_t launch_wide(const int8_t* a, const int8_t* w, const void* sa, const void* sw, void* out,
                        int M, int N, int K, hipStream_t st) {
     // Column blocks per workgroup: enough that one workgroup per CU covers N.
-    const int per_cu = ((N + 15) / 16 + cu_count() - 1) / cu_count();
+    const int per_cu = ((N + 15) / 16 + device_cu_count() - 1) / device_cu_count();
     if (per_cu <= 4) return launch_wide_cbw<MB, 4, TW, SG, OF>(a, w, sa, sw, out, M, N, K, st);
     if (per_cu <= 6) return launch_wide_cbw<MB, 6, TW, SG, OF>(a, w, sa, sw, out, M, N, K, st);
     return launch_wide_cbw<MB, 8, TW, SG, OF>(a, w, sa, sw, out, M, N, K, st);
