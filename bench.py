@@ -80,6 +80,7 @@ def parse_args():
     ap.add_argument("--rotate", type=int, default=6, help="distinct weight sets cycled through")
     ap.add_argument("--no-detail", action="store_true", help="skip the per-projection M=32/M=4096 table")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
+    ap.add_argument("--no-peaks", action="store_true", help="skip the measured matrix-core / HBM peaks")
     ap.add_argument("--cpu-seconds", type=float, default=15.0, help="target CPU baseline sample length")
     ap.add_argument("--no-e2e", action="store_true", help="skip the end-to-end bs32 decode of the decoder")
     ap.add_argument("--e2e-layers", type=int, default=36, help="decoder layers of the end-to-end model")
@@ -502,6 +503,11 @@ def main():
         },
     }
 
+    if not args.no_peaks:
+        peaks = measured_peaks(torch, dev)
+        line["roofline"]["measured_peak"] = peaks["hbm_read_gbs"]
+        line["roofline"]["frac_of_measured"] = round(achieved / peaks["hbm_read_gbs"], 4)
+        line["measured_peaks"] = peaks
     if not args.no_detail:
         line["detail"] = detail_table(torch, nv4, W, dev, R)
     del graphs, sets, acts
@@ -512,6 +518,59 @@ def main():
         line["cpu_baseline"] = cpu_baseline(M, args.cpu_seconds)
         line["cpu_baseline"]["gpu_speedup"] = round(line["cpu_baseline"]["value"] / step_us, 1)
     print(json.dumps(line), flush=True)
+
+
+def measured_peaks(torch, dev):
+    """The device's sustained rates, measured by the library's probe kernels
+    (`nv4_probe_mfma`, `nv4_probe_read`): int8 and fp8 matrix-core
+    operations per second with every SIMD's matrix pipe fed by eight waves of
+    four independent products, and the HBM streaming-read rate over a 1 GiB
+    buffer (four times the Infinity Cache).  Medians of 5 timed launches after
+    one warm-up; reported beside the published peaks, not instead of them."""
+    import ctypes
+    from nv4 import _lib
+    lib = _lib.load()
+    cus = torch.cuda.get_device_properties(dev).multi_processor_count
+    wgs = 8 * cus
+    sink = torch.zeros(max(wgs, 1024), dtype=torch.int32, device=dev)
+    stream = lambda: ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+    def timed(launch, reps=5):
+        launch()
+        ts = []
+        for _ in range(reps):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            launch()
+            e1.record()
+            torch.cuda.synchronize()
+            ts.append(e0.elapsed_time(e1) * 1e-3)
+        return statistics.median(ts)
+
+    out = {}
+    for kind, name, iters, ops_per in ((0, "int8_mfma_tops", 2000, 2 * 16 * 16 * 64),
+                                       (1, "fp8_mfma_tops", 500, 2 * 32 * 32 * 64)):
+        def run(kind=kind, iters=iters):
+            rc = lib.nv4_probe_mfma(kind, iters, wgs, ctypes.c_void_p(sink.data_ptr()), stream())
+            if rc != 0:
+                raise RuntimeError(f"nv4_probe_mfma failed: {rc}")
+        sec = timed(run)
+        out[name] = round(wgs * 4 * iters * 4 * ops_per / sec / 1e12, 1)
+    buf = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
+    buf.fill_(1)
+
+    def rd():
+        rc = lib.nv4_probe_read(ctypes.c_void_p(buf.data_ptr()), buf.numel(), ctypes.c_void_p(sink.data_ptr()),
+                                stream())
+        if rc != 0:
+            raise RuntimeError(f"nv4_probe_read failed: {rc}")
+    out["hbm_read_gbs"] = round(buf.numel() / timed(rd, reps=9) / 1e9, 1)
+    del buf
+    out["published"] = {"int8_mfma_tops": 5000.0, "fp8_mfma_tops": 5000.0, "hbm_read_gbs": HBM_PEAK_GBS}
+    out["method"] = (f"{wgs} workgroups x 4 waves, 4 independent MFMAs per round (16x16x64 i8: 2000 rounds; "
+                     "32x32x64 f8: 500 rounds); streaming read of 1 GiB, 16 nontemporal 16-byte loads per "
+                     "thread; HIP events, median of 5 (9 for the read)")
+    return out
 
 
 def detail_table(torch, nv4, W, dev, R):

@@ -348,6 +348,22 @@ int nv4_gumbel_sample_ws(const void* logits, int64_t row_stride, int logits_dtyp
 void nv4_philox4x32_10(const uint32_t* counter, const uint32_t* key, uint32_t* out);
 
 /* Library version string. */
+/*
+ * Measurement probes (no counterpart in the reference; bench.py reports
+ * their rates beside the published peaks).
+ *   nv4_probe_mfma: `workgroups` workgroups of 4 waves, each wave running
+ *     `iters` (rounded up to even) rounds of four independent matrix-core
+ *     products: kind 0 = v_mfma_i32_16x16x64_i8 (32768 ops each), kind 1 =
+ *     v_mfma_scale_f32_32x32x64_f8f6f4 (131072 ops each).  `sink` is an int
+ *     array of at least max(workgroups, 1024) entries (written only on a
+ *     value the products practically never take).  1 <= iters <= 2^30,
+ *     1 <= workgroups <= 2^20.
+ *   nv4_probe_read: reads `bytes` (a multiple of 65536, 16-byte aligned
+ *     buffer) once with 16-byte nontemporal loads; same sink rule.
+ */
+int nv4_probe_mfma(int kind, int64_t iters, int64_t workgroups, int* sink, void* stream);
+int nv4_probe_read(const void* buf, int64_t bytes, int* sink, void* stream);
+
 const char* nv4_version(void);
 
 /* Human-readable text for an NV4_E* code (or "hip error" for positive codes). */

@@ -56,6 +56,8 @@ SIGNATURES = {
     "nv4_gumbel_sample_chunks": ([_I64, _I64], _I64),
     "nv4_gumbel_sample_ws": ([_P, _I64, _I, _P, _I64, _I64, ctypes.c_uint64, ctypes.c_uint64, _P, _I64, _P, _P], _I),
     "nv4_philox4x32_10": ([_P, _P, _P], None),
+    "nv4_probe_mfma": ([_I, _I64, _I64, _P, _P], _I),
+    "nv4_probe_read": ([_P, _I64, _P, _P], _I),
     "nv4_version": ([], ctypes.c_char_p),
     "nv4_strerror": ([_I], ctypes.c_char_p),
 }

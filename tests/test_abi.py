@@ -177,6 +177,20 @@ def test_decoder_ops_rejections():
     assert sq(P(A16 + 2), P(A16), P(A16), P(A16), 4, 12288, None) == _lib.NV4_E_ALIGN
 
 
+def test_probe_rejections():
+    lib = _lib.load()
+    sink = P(A16)
+    assert lib.nv4_probe_mfma(0, 10, 8, None, None) == _lib.NV4_E_NULL
+    assert lib.nv4_probe_mfma(2, 10, 8, sink, None) == _lib.NV4_E_SHAPE        # unknown kind
+    assert lib.nv4_probe_mfma(1, 0, 8, sink, None) == _lib.NV4_E_SHAPE         # no rounds
+    assert lib.nv4_probe_mfma(0, 10, 0, sink, None) == _lib.NV4_E_SHAPE        # no workgroups
+    assert lib.nv4_probe_mfma(0, 10, (1 << 20) + 1, sink, None) == _lib.NV4_E_SHAPE
+    assert lib.nv4_probe_read(None, 65536, sink, None) == _lib.NV4_E_NULL
+    assert lib.nv4_probe_read(P(A16), 65536 + 16, sink, None) == _lib.NV4_E_SHAPE  # not whole 64 KiB chunks
+    assert lib.nv4_probe_read(P(A16), 0, sink, None) == _lib.NV4_E_SHAPE
+    assert lib.nv4_probe_read(P(A16 + 8), 65536, sink, None) == _lib.NV4_E_ALIGN
+
+
 def test_python_wrappers_validate_like_the_reference():
     from nv4 import W4A4Linear, rht_quant_pack, w4a4_grouped_gemm
     x = torch.zeros(2, 4096, dtype=torch.bfloat16)
