@@ -49,6 +49,7 @@ for _p in (str(ROOT), str(ROOT / "nano-vllm-int4_amd")):
 PROJECTIONS = ("qkv", "o", "gate_up", "down")
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, published
 INT8_PEAK_TOPS = 5000.0        # MI355X dense int8 MFMA, published (no sparsity)
+FP6_PEAK_TOPS = 10100.0        # MI355X dense fp6 / fp4 MFMA, published (no sparsity)
 # Published reference numbers (one RTX A6000), full RHT+quant+pack+GEMM chain
 # at M = 32, benchmarks/README.md:126-129, in microseconds.
 PUBLISHED_CHAIN_M32_US = {"qkv": 28.12, "o": 21.87, "gate_up": 86.85, "down": 64.65}
@@ -86,7 +87,7 @@ def parse_args():
     ap.add_argument("--e2e-layers", type=int, default=36, help="decoder layers of the end-to-end model")
     ap.add_argument("--e2e-tokens", type=int, default=256, help="output tokens per request (end to end)")
     ap.add_argument("--pmc-prefill", action="store_true",
-                    help="for rocprofv3 --pmc: three launches of the fp8 prefill GEMM at gate_up M=4096 "
+                    help="for rocprofv3 --pmc: three launches of the fp6 prefill GEMM at gate_up M=4096 "
                          "(after its operand conversion) and three 256 MiB device copies, then exit")
     ap.add_argument("--pmc-pass", action="store_true",
                     help="for rocprofv3 --pmc: eager decode GEMM launches (3 rounds over the rotating sets) "
@@ -189,8 +190,8 @@ def decode_gemm_source_sha():
 def pmc_prefill(torch, W, dev):
     """Kernels for a hardware-counter run of the prefill GEMM: the W4A4
     grouped GEMM at gate_up M=4096 (K1 codes of seeded activations, MFMA-tiled
-    weights), three launches on the fp8 path (each: the operand conversion
-    kernel, then k2_prefill_f8), then three copies of COPY_BYTES for the
+    weights), three launches on the fp6 path (each: the operand conversion
+    kernel, then k2_prefill_f6), then three copies of COPY_BYTES for the
     FETCH_SIZE / WRITE_SIZE calibration."""
     import nv4
     M, (N, K) = 4096, W.PROJECTIONS["gate_up"]
@@ -206,14 +207,14 @@ def pmc_prefill(torch, W, dev):
     nv4.rht_quant_pack(x, sg, out_packed=pk, out_scale=sc)
     out = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
     for _ in range(3):
-        nv4.w4a4_grouped_gemm(pk, wp, sc, sw, out=out, weights_tiled=True, fp8=True)
+        nv4.w4a4_grouped_gemm(pk, wp, sc, sw, out=out, weights_tiled=True, path="fp6")
     src = torch.empty(COPY_BYTES, dtype=torch.uint8, device=dev)
     dst = torch.empty_like(src)
     src.fill_(1)
     for _ in range(3):
         dst.copy_(src)
     torch.cuda.synchronize()
-    print("pmc prefill pass done: 3 fp8 prefill GEMMs at gate_up M=4096, 3 copies of "
+    print("pmc prefill pass done: 3 fp6 prefill GEMMs at gate_up M=4096, 3 copies of "
           f"{COPY_BYTES} bytes", flush=True)
 
 
@@ -522,7 +523,7 @@ def main():
 
 def measured_peaks(torch, dev):
     """The device's sustained rates, measured by the library's probe kernels
-    (`nv4_probe_mfma`, `nv4_probe_read`): int8 and fp8 matrix-core
+    (`nv4_probe_mfma`, `nv4_probe_read`): int8, fp8 and fp6 matrix-core
     operations per second with every SIMD's matrix pipe fed by eight waves of
     four independent products, and the HBM streaming-read rate over a 1 GiB
     buffer (four times the Infinity Cache).  Medians of 5 timed launches after
@@ -549,7 +550,8 @@ def measured_peaks(torch, dev):
 
     out = {}
     for kind, name, iters, ops_per in ((0, "int8_mfma_tops", 2000, 2 * 16 * 16 * 64),
-                                       (1, "fp8_mfma_tops", 500, 2 * 32 * 32 * 64)):
+                                       (1, "fp8_mfma_tops", 500, 2 * 32 * 32 * 64),
+                                       (2, "fp6_mfma_tops", 1000, 2 * 32 * 32 * 64)):
         def run(kind=kind, iters=iters):
             rc = lib.nv4_probe_mfma(kind, iters, wgs, ctypes.c_void_p(sink.data_ptr()), stream())
             if rc != 0:
@@ -566,9 +568,11 @@ def measured_peaks(torch, dev):
             raise RuntimeError(f"nv4_probe_read failed: {rc}")
     out["hbm_read_gbs"] = round(buf.numel() / timed(rd, reps=9) / 1e9, 1)
     del buf
-    out["published"] = {"int8_mfma_tops": 5000.0, "fp8_mfma_tops": 5000.0, "hbm_read_gbs": HBM_PEAK_GBS}
+    out["published"] = {"int8_mfma_tops": 5000.0, "fp8_mfma_tops": 5000.0, "fp6_mfma_tops": FP6_PEAK_TOPS,
+                        "hbm_read_gbs": HBM_PEAK_GBS}
     out["method"] = (f"{wgs} workgroups x 4 waves, 4 independent MFMAs per round (16x16x64 i8: 2000 rounds; "
-                     "32x32x64 f8: 500 rounds); streaming read of 1 GiB, 16 nontemporal 16-byte loads per "
+                     "32x32x64 f8: 500 rounds; 32x32x64 f6: 1000 rounds); streaming read of 1 GiB, "
+                     "16 nontemporal 16-byte loads per "
                      "thread; HIP events, median of 5 (9 for the read)")
     return out
 
@@ -616,7 +620,12 @@ def detail_table(torch, nv4, W, dev, R):
                 entry["k2_hbm_frac"] = round(k2_bytes(M, N, K) / (us2 * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)
                 entry["ref_a6000_gemm_us"] = PUBLISHED_GEMM_M32_US[p]
             else:
+                # The size-chosen kernel runs on the fp6 matrix cores (exact for
+                # INT4 codes); reported against the int8 peak the target names
+                # and against the fp6 peak of the units it uses.
+                entry["k2_path"] = "fp6"
                 entry["k2_int8_frac"] = round(2 * M * N * K / (us2 * 1e-6) / 1e12 / INT8_PEAK_TOPS, 4)
+                entry["k2_fp6_frac"] = round(2 * M * N * K / (us2 * 1e-6) / 1e12 / FP6_PEAK_TOPS, 4)
                 entry["ref_a6000_gemm_us"] = PUBLISHED_GEMM_M4096_US[p]
             res[f"M{M}_{p}"] = entry
             print(f"[detail] M={M} {p}: {entry}", file=sys.stderr, flush=True)

@@ -28,6 +28,8 @@
  *   nv4_w4a4_gemm_f8    <- w4a4_grouped_gemm (w4a4_grouped_kernel.py:104) for
  *                          prefill-sized M: the same operator on the fp8 matrix
  *                          cores, with a caller workspace for the e4m3 operands
+ *   nv4_w4a4_gemm_f6, nv4_w4a4_gemm_f6_workspace <- the same, on the fp6 matrix
+ *                          cores (e3m2 operands in 128-row tiles)
  *   nv4_w4a16_gemm, nv4_w4a16_gemm_ws, nv4_w4a16_dequant <- nanovllm/layers/linear_w4a16.py:11
  *                          tl_dequant_matmul_w4a16 (called from W4A16Linear.forward
  *                          :128-148; the reference splits K 8 ways with bf16 atomics,
@@ -170,6 +172,23 @@ int nv4_w4a4_linear_tiled(const void* x, const int8_t* signs, const int8_t* w_ti
 int nv4_w4a4_gemm_f8(const int8_t* a, const int8_t* w, int w_tiled, const void* sa, const void* sw,
                      int sw_grouped, void* out, int out_fp32, int64_t M, int64_t N, int64_t K,
                      void* workspace, int64_t workspace_bytes, void* stream);
+
+/*
+ * The same operator on the fp6 matrix cores: the INT4 codes of both operands
+ * are first written as fp6 (e3m2) codes -- every integer of [-8, 8] is exact
+ * in e3m2 -- into the caller's workspace, in 128-row tiles of 12 KiB per
+ * 128-deep group (nv4_w4a4_gemm_f6_workspace(M, N, K) bytes, 16-byte
+ * aligned), then multiplied with v_mfma_scale_f32_32x32x64_f8f6f4 in its
+ * 6-bit form.  Every group dot is a small integer, exact in fp32, so the
+ * results are bit-identical to nv4_w4a4_gemm.  Same argument rules as
+ * nv4_w4a4_gemm_f8; the workspace is overwritten, and calls sharing one
+ * workspace must be stream-ordered.  nv4_w4a4_gemm_f6_workspace returns -1
+ * for shapes the operator rejects (M, N < 1; K not a positive multiple of 128).
+ */
+int nv4_w4a4_gemm_f6(const int8_t* a, const int8_t* w, int w_tiled, const void* sa, const void* sw,
+                     int sw_grouped, void* out, int out_fp32, int64_t M, int64_t N, int64_t K,
+                     void* workspace, int64_t workspace_bytes, void* stream);
+int64_t nv4_w4a4_gemm_f6_workspace(int64_t M, int64_t N, int64_t K);
 
 /*
  * W4A16 GEMM with GPTQ weights (zero-point convention w = (q - z - 1) * s).
@@ -354,7 +373,8 @@ void nv4_philox4x32_10(const uint32_t* counter, const uint32_t* key, uint32_t* o
  *   nv4_probe_mfma: `workgroups` workgroups of 4 waves, each wave running
  *     `iters` (rounded up to even) rounds of four independent matrix-core
  *     products: kind 0 = v_mfma_i32_16x16x64_i8 (32768 ops each), kind 1 =
- *     v_mfma_scale_f32_32x32x64_f8f6f4 (131072 ops each).  `sink` is an int
+ *     v_mfma_scale_f32_32x32x64_f8f6f4 on fp8 operands, kind 2 = the same on
+ *     fp6 (e3m2) operands (131072 ops each).  `sink` is an int
  *     array of at least max(workgroups, 1024) entries (written only on a
  *     value the products practically never take).  1 <= iters <= 2^30,
  *     1 <= workgroups <= 2^20.

@@ -1,4 +1,4 @@
-// Measurement probes: the sustained int8 / fp8 matrix-core rate and the HBM
+// Measurement probes: the sustained int8 / fp8 / fp6 matrix-core rate and the HBM
 // streaming-read rate of the device they run on.  bench.py reports the
 // published MI355X peaks as the roofline's `peak` and these measured figures
 // beside them.  No counterpart in the reference.
@@ -36,19 +36,21 @@ probe_mfma(int64_t iters, int* __restrict__ sink) {
         }
         acc_i = c0[0] ^ c1[1] ^ c2[2] ^ c3[3];
     } else {
+        // KIND 1: fp8 (e4m3) operands; KIND 2: fp6 (e3m2), six registers per operand.
+        constexpr int F = KIND == 1 ? 0 : 3;
         const v8i a = {lane, 1, 2, 3, 4, 5, 6, 7};
         const v8i b0 = {7, lane, 5, 4, 3, 2, 1, 0}, b1 = {lane, 6, 5, 4, 3, 2, 1, 0}, b2 = {1, 2, lane, 4, 5, 6, 7, 8},
                   b3 = {9, 8, 7, lane, 5, 4, 3, 2};
         v16f c0 = {}, c1 = {}, c2 = {}, c3 = {};
         for (int64_t i = 0; i < iters; i += 2) {  // two rounds per trip (iters is rounded up to even)
-            c0 = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b1, c0, 0, 0, 0, 127, 0, 127);
-            c1 = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b2, c1, 0, 0, 0, 127, 0, 127);
-            c2 = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b3, c2, 0, 0, 0, 127, 0, 127);
-            c3 = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b0, c3, 0, 0, 0, 127, 0, 127);
-            c0 = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b0, c0, 0, 0, 0, 127, 0, 127);
-            c1 = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b1, c1, 0, 0, 0, 127, 0, 127);
-            c2 = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b2, c2, 0, 0, 0, 127, 0, 127);
-            c3 = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b3, c3, 0, 0, 0, 127, 0, 127);
+            c0 = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b1, c0, F, F, 0, 127, 0, 127);
+            c1 = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b2, c1, F, F, 0, 127, 0, 127);
+            c2 = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b3, c2, F, F, 0, 127, 0, 127);
+            c3 = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b0, c3, F, F, 0, 127, 0, 127);
+            c0 = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b0, c0, F, F, 0, 127, 0, 127);
+            c1 = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b1, c1, F, F, 0, 127, 0, 127);
+            c2 = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b2, c2, F, F, 0, 127, 0, 127);
+            c3 = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b3, c3, F, F, 0, 127, 0, 127);
         }
         acc_f = c0[0] + c1[1] + c2[2] + c3[3];
     }
@@ -78,13 +80,15 @@ probe_read(const v4u* __restrict__ p, int* __restrict__ sink) {
 extern "C" int nv4_probe_mfma(int kind, int64_t iters, int64_t workgroups, int* sink, void* stream) {
     using namespace nv4;
     if (!sink) return NV4_E_NULL;
-    if ((kind != 0 && kind != 1) || iters < 1 || iters > (1LL << 30) || workgroups < 1 || workgroups > (1 << 20))
+    if (kind < 0 || kind > 2 || iters < 1 || iters > (1LL << 30) || workgroups < 1 || workgroups > (1 << 20))
         return NV4_E_SHAPE;
     hipStream_t st = static_cast<hipStream_t>(stream);
     if (kind == 0)
         hipLaunchKernelGGL(probe_mfma<0>, dim3((unsigned)workgroups), dim3(256), 0, st, iters, sink);
-    else
+    else if (kind == 1)
         hipLaunchKernelGGL(probe_mfma<1>, dim3((unsigned)workgroups), dim3(256), 0, st, iters, sink);
+    else
+        hipLaunchKernelGGL(probe_mfma<2>, dim3((unsigned)workgroups), dim3(256), 0, st, iters, sink);
     return (int)hipGetLastError();
 }
 

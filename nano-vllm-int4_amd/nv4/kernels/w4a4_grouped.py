@@ -10,8 +10,9 @@ Each output element is, for g in order, ``total = fmaf(float(dot_g),
 sa[m,g]*sw[n,g], total)`` with exact int32 group dots, rounded to bf16 at the
 end (or ``total = fmaf(float(dot_g), sa[m,g], total)``; ``bf16(total*sw[n])``
 for 1-D weight scales).  The HIP kernels (``nv4_w4a4_gemm``; for prefill-sized
-M ``nv4_w4a4_gemm_f8``, the same bits on the fp8 matrix cores) take M at run
-time: nothing is compiled per shape, and there is no split-K and no atomics.
+M ``nv4_w4a4_gemm_f6``, the same bits on the fp6 matrix cores, or on request
+``nv4_w4a4_gemm_f8`` on the fp8 ones) take M at run time: nothing is compiled
+per shape, and there is no split-K and no atomics.
 """
 from __future__ import annotations
 
@@ -44,33 +45,48 @@ def _validate_config(cfg: GroupedConfig) -> None:
         raise ValueError("Require positive dimensions, K divisible by 128, N divisible by 8, and whole warps")
 
 
-def use_fp8_path(M, N, K):
-    """Prefill-sized GEMMs run on the fp8 matrix cores (``nv4_w4a4_gemm_f8``).
-    The operand conversion costs about 1.5 (M + N) K bytes of traffic and one
-    launch; measured on the decoder's projections it pays from M = 384 on
-    weights of 4096 x 12288 or more, from M = 768 above 4096 x 4096, and from
-    M = 1024 on all of them."""
+PATHS = ("int8", "fp8", "fp6")
+
+
+def use_prefill_path(M, N, K):
+    """Prefill-sized GEMMs run on the fp6 matrix cores (``nv4_w4a4_gemm_f6``).
+    The operand conversion costs about 1.25 (M + N) K bytes of traffic and one
+    launch; measured on the decoder's projections (with the fp8 form, whose
+    conversion moves more bytes) it pays from M = 384 on weights of
+    4096 x 12288 or more, from M = 768 above 4096 x 4096, and from M = 1024 on
+    all of them."""
     nk = N * K
     return M >= 1024 or (M >= 768 and nk > 4096 * 4096) or (M >= 384 and nk >= 4096 * 12288)
 
 
-def _launch(a_packed, w_packed, a_scale, w_scale, out, output_fp32, weight_grouped, weights_tiled=False, fp8=None):
+def _resolve_path(path, M, N, K):
+    if path is None:
+        return "fp6" if use_prefill_path(M, N, K) else "int8"
+    if path not in PATHS:
+        raise ValueError(f"path must be None or one of {PATHS}")
+    return path
+
+
+def _launch(a_packed, w_packed, a_scale, w_scale, out, output_fp32, weight_grouped, weights_tiled=False, path=None):
     M, N, K = a_packed.shape[0], w_packed.shape[0], a_packed.shape[1] * 2
-    if fp8 is None:
-        fp8 = use_fp8_path(M, N, K)
+    path = _resolve_path(path, M, N, K)
     lib = _lib.load()
     stream = torch.cuda.current_stream(a_packed.device).cuda_stream
     with torch.cuda.device(a_packed.device):
-        if fp8:
-            # fp8 operand rows for this call (caching allocator: no hipMalloc
-            # once warm); the kernels only read it on this stream.
-            ws = torch.empty((M + N) * K, dtype=torch.uint8, device=a_packed.device)
-            rc = lib.nv4_w4a4_gemm_f8(ctypes.c_void_p(a_packed.data_ptr()), ctypes.c_void_p(w_packed.data_ptr()),
-                                      1 if weights_tiled else 0,
-                                      ctypes.c_void_p(a_scale.data_ptr()), ctypes.c_void_p(w_scale.data_ptr()),
-                                      1 if weight_grouped else 0, ctypes.c_void_p(out.data_ptr()),
-                                      1 if output_fp32 else 0, M, N, K, ctypes.c_void_p(ws.data_ptr()),
-                                      ws.numel(), ctypes.c_void_p(stream))
+        if path != "int8":
+            # Matrix-core operands for this call (caching allocator: no
+            # hipMalloc once warm); the kernels only read it on this stream.
+            if path == "fp6":
+                fn, nbytes = lib.nv4_w4a4_gemm_f6, lib.nv4_w4a4_gemm_f6_workspace(M, N, K)
+            else:
+                fn, nbytes = lib.nv4_w4a4_gemm_f8, (M + N) * K
+            ws = torch.empty(nbytes, dtype=torch.uint8, device=a_packed.device)
+            rc = fn(ctypes.c_void_p(a_packed.data_ptr()), ctypes.c_void_p(w_packed.data_ptr()),
+                    1 if weights_tiled else 0,
+                    ctypes.c_void_p(a_scale.data_ptr()), ctypes.c_void_p(w_scale.data_ptr()),
+                    1 if weight_grouped else 0, ctypes.c_void_p(out.data_ptr()),
+                    1 if output_fp32 else 0, M, N, K, ctypes.c_void_p(ws.data_ptr()),
+                    ws.numel(), ctypes.c_void_p(stream))
         else:
             fn = lib.nv4_w4a4_gemm_tiled if weights_tiled else lib.nv4_w4a4_gemm
             rc = fn(ctypes.c_void_p(a_packed.data_ptr()), ctypes.c_void_p(w_packed.data_ptr()),
@@ -108,11 +124,13 @@ def untile_weights(w_tiled):
 
 
 @lru_cache(None)
-def compile_grouped_gemm(M, N, K, cfg=GroupedConfig(), output_fp32=False, weight_grouped=False, fp8=None):
+def compile_grouped_gemm(M, N, K, cfg=GroupedConfig(), output_fp32=False, weight_grouped=False, path=None):
     """Return ``kernel(A, W, Sa, Sw, C)`` for exact (M, N, K), as the reference does
     (its kernel is JIT-specialised on M; this one only checks the shapes).
-    ``fp8``: force (True) or avoid (False) the fp8 matrix-core path; None
-    chooses by size (``use_fp8_path``)."""
+    ``path``: "int8", "fp8" or "fp6" forces a kernel family (same bits); None
+    chooses by size (``use_prefill_path``)."""
+    if path is not None and path not in PATHS:
+        raise ValueError(f"path must be None or one of {PATHS}")
     if min(M, N, K) < 1 or K % GROUP_SIZE or N % 8:
         raise ValueError("Require positive dimensions, K divisible by 128, N divisible by 8, and whole warps")
     _validate_config(cfg)
@@ -127,7 +145,7 @@ def compile_grouped_gemm(M, N, K, cfg=GroupedConfig(), output_fp32=False, weight
         tensors = (a_packed, w_packed, a_scale, w_scale, out)
         if any(not t.is_cuda or not t.is_contiguous() or t.device != a_packed.device for t in tensors):
             raise ValueError("All inputs must be contiguous CUDA tensors on one device")
-        _launch(a_packed, w_packed, a_scale, w_scale, out, output_fp32, weight_grouped, fp8=fp8)
+        _launch(a_packed, w_packed, a_scale, w_scale, out, output_fp32, weight_grouped, path=path)
     return kernel
 
 
@@ -138,11 +156,11 @@ def best_grouped_config(M, N, K, weight_grouped=False):
     return GroupedConfig() if M <= 32 else GroupedConfig(64, 128, 2, 128)
 
 
-def w4a4_grouped_gemm(a_packed, w_packed, a_scale, w_scale, out=None, config=None, *, weights_tiled=False, fp8=None):
+def w4a4_grouped_gemm(a_packed, w_packed, a_scale, w_scale, out=None, config=None, *, weights_tiled=False, path=None):
     """Packed INT4; BF16 Sa[M,K/128], Sw[N] or Sw[N,K/128], output[M,N].
     ``weights_tiled``: ``w_packed`` holds ``tile_weights`` output (N % 16 == 0);
-    the result is bit-identical.  ``fp8``: force (True) or avoid (False) the
-    fp8 matrix-core path (same bits); None chooses by size."""
+    the result is bit-identical.  ``path``: "int8", "fp8" or "fp6" forces a
+    kernel family (same bits); None chooses by size."""
     if a_packed.ndim != 2 or w_packed.ndim != 2 or a_packed.shape[1] != w_packed.shape[1]:
         raise ValueError("Packed inputs must have compatible [M,K/2] and [N,K/2] shapes")
     M, K = a_packed.shape[0], a_packed.shape[1] * 2
@@ -170,5 +188,5 @@ def w4a4_grouped_gemm(a_packed, w_packed, a_scale, w_scale, out=None, config=Non
         _validate_config(config)
     if weights_tiled and N % 16:
         raise ValueError("The tiled weight layout needs N divisible by 16")
-    _launch(a_packed, w_packed, a_scale, w_scale, out, False, weight_grouped, weights_tiled, fp8=fp8)
+    _launch(a_packed, w_packed, a_scale, w_scale, out, False, weight_grouped, weights_tiled, path=path)
     return out

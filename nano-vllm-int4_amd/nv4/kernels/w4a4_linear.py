@@ -5,8 +5,9 @@ is ``rht_quant_pack`` followed by ``w4a4_grouped_gemm``.  ``w4a4_linear`` runs
 the same two HIP kernels back to back through one C ABI call
 (``nv4_w4a4_linear``) on torch's current stream, so it can be captured in a
 HIP graph; the quantized activations are returned through ``out_packed`` /
-``out_scale`` (allocated when not given).  Prefill-sized M (``use_fp8_path``)
-runs K1 and then the fp8 matrix-core GEMM (``nv4_w4a4_gemm_f8``, same bits).
+``out_scale`` (allocated when not given).  Prefill-sized M
+(``use_prefill_path``) runs K1 and then the fp6 matrix-core GEMM
+(``nv4_w4a4_gemm_f6``, same bits).
 """
 from __future__ import annotations
 
@@ -16,7 +17,7 @@ import torch
 
 from .. import _lib
 from .rht_a4 import rht_quant_pack
-from .w4a4_grouped import _launch, use_fp8_path
+from .w4a4_grouped import _launch, use_prefill_path
 
 
 def w4a4_linear(x, signs, w_packed, w_scale, *, out=None, out_packed=None, out_scale=None, weights_tiled=False):
@@ -50,10 +51,10 @@ def w4a4_linear(x, signs, w_packed, w_scale, *, out=None, out_packed=None, out_s
     tensors = (x, signs, w_packed, w_scale, out, out_packed, out_scale)
     if any(not t.is_cuda or not t.is_contiguous() or t.device != dev for t in tensors):
         raise ValueError("All tensors must be contiguous on one CUDA device")
-    if use_fp8_path(M, N, K):
-        # Prefill-sized M: K1, then the grouped GEMM on the fp8 matrix cores.
+    if use_prefill_path(M, N, K):
+        # Prefill-sized M: K1, then the grouped GEMM on the fp6 matrix cores.
         rht_quant_pack(x, signs, out_packed=out_packed, out_scale=out_scale)
-        _launch(out_packed, w_packed, out_scale, w_scale, out, False, True, weights_tiled)
+        _launch(out_packed, w_packed, out_scale, w_scale, out, False, True, weights_tiled, path="fp6")
         return out
     lib = _lib.load()
     stream = torch.cuda.current_stream(dev).cuda_stream

@@ -89,6 +89,34 @@ def test_w4a4_gemm_f8_rejections():
     assert call(M=big, nbytes=(big + N) * K) == _lib.NV4_E_SHAPE
 
 
+def test_w4a4_gemm_f6_rejections():
+    lib = _lib.load()
+    f, size = lib.nv4_w4a4_gemm_f6, lib.nv4_w4a4_gemm_f6_workspace
+    a = w = sa = sw = out = P(A16)
+    M, N, K = 256, 64, 4096
+    need = size(M, N, K)
+    assert need == (2 + 1) * 32 * 12288                                  # 128-row tiles x groups x 12 KiB
+    assert size(300, 136, 1152) == (3 + 2) * 9 * 12288
+    assert size(0, N, K) == -1 and size(M, N, 4000) == -1 and size(M, 0, K) == -1
+
+    def call(a=a, w=w, tiled=0, sa=sa, sw=sw, out=out, fp32=0, M=M, N=N, K=K, ws=P(A16), nbytes=need):
+        return f(a, w, tiled, sa, sw, 1, out, fp32, M, N, K, ws, nbytes, None)
+
+    assert call(ws=None) == _lib.NV4_E_NULL
+    assert call(sw=None) == _lib.NV4_E_NULL
+    assert call(nbytes=need - 1) == _lib.NV4_E_SHAPE                     # workspace too small
+    assert call(N=60) == _lib.NV4_E_SHAPE                                # N % 8
+    assert call(N=40, tiled=1) == _lib.NV4_E_SHAPE                       # tiled needs N % 16
+    assert call(K=4000) == _lib.NV4_E_SHAPE                              # K % 128
+    assert call(M=0) == _lib.NV4_E_SHAPE
+    assert call(K=1 << 21) == _lib.NV4_E_SHAPE                           # K beyond 2^20
+    assert call(ws=P(A16 + 8)) == _lib.NV4_E_ALIGN
+    assert call(w=P(A16 + 4)) == _lib.NV4_E_ALIGN
+    assert call(out=P(A16 + 2), fp32=1) == _lib.NV4_E_ALIGN
+    big = 1 << 26                                                        # conversion grid beyond 32 bits
+    assert call(M=big, nbytes=size(big, N, K)) == _lib.NV4_E_SHAPE
+
+
 def test_w4a16_and_linear_rejections():
     f = _lib.load().nv4_w4a16_gemm
     ok = [P(A16)] * 4
@@ -181,7 +209,8 @@ def test_probe_rejections():
     lib = _lib.load()
     sink = P(A16)
     assert lib.nv4_probe_mfma(0, 10, 8, None, None) == _lib.NV4_E_NULL
-    assert lib.nv4_probe_mfma(2, 10, 8, sink, None) == _lib.NV4_E_SHAPE        # unknown kind
+    assert lib.nv4_probe_mfma(3, 10, 8, sink, None) == _lib.NV4_E_SHAPE        # unknown kind
+    assert lib.nv4_probe_mfma(-1, 10, 8, sink, None) == _lib.NV4_E_SHAPE
     assert lib.nv4_probe_mfma(1, 0, 8, sink, None) == _lib.NV4_E_SHAPE         # no rounds
     assert lib.nv4_probe_mfma(0, 10, 0, sink, None) == _lib.NV4_E_SHAPE        # no workgroups
     assert lib.nv4_probe_mfma(0, 10, (1 << 20) + 1, sink, None) == _lib.NV4_E_SHAPE

@@ -131,16 +131,16 @@ def test_linear_graph_replay(proj):
 
 
 @pytest.mark.parametrize("proj,M", [("qkv", 2048), ("down", 1024), ("gate_up", 1100)])
-def test_linear_prefill_fp8_route(proj, M):
-    """At prefill-sized M ``w4a4_linear`` runs K1 and then the fp8 matrix-core
+def test_linear_prefill_matrix_core_route(proj, M):
+    """At prefill-sized M ``w4a4_linear`` runs K1 and then the fp6 matrix-core
     GEMM: its codes, scales and output equal K1 followed by the int8 path, bit
     for bit, in both weight layouts."""
     from nv4 import rht_quant_pack, w4a4_grouped_gemm
-    from nv4.kernels.w4a4_grouped import use_fp8_path
+    from nv4.kernels.w4a4_grouped import use_prefill_path
     case = W.w4a4_case(proj, M)
     M, N, K = case.shape
-    assert use_fp8_path(M, N, K)
-    print(f"[linear-fp8] {proj} M={M} N={N} K={K}", flush=True)
+    assert use_prefill_path(M, N, K)
+    print(f"[linear-prefill] {proj} M={M} N={N} K={K}", flush=True)
     x, signs = case.x.to(DEV), case.signs.to(DEV)
     wpk, wsc = case.w_packed.to(DEV), case.w_scale.to(DEV)
     for tiled in (False, True):
@@ -151,7 +151,7 @@ def test_linear_prefill_fp8_route(proj, M):
         p2 = torch.empty_like(packed)
         s2 = torch.empty_like(scale)
         rht_quant_pack(x, signs, out_packed=p2, out_scale=s2)
-        ref = w4a4_grouped_gemm(p2, w, s2, wsc, weights_tiled=tiled, fp8=False)
+        ref = w4a4_grouped_gemm(p2, w, s2, wsc, weights_tiled=tiled, path="int8")
         torch.cuda.synchronize()
         assert torch.equal(packed, p2) and torch.equal(scale.view(torch.int16), s2.view(torch.int16))
         assert torch.equal(out.view(torch.int16), ref.view(torch.int16)), f"tiled={tiled}"

@@ -1,9 +1,11 @@
-"""GPU parity of the fp8 matrix-core form of K2 (``nv4_w4a4_gemm_f8``).
+"""GPU parity of the matrix-core forms of K2 for prefill-sized M:
+``nv4_w4a4_gemm_f6`` (INT4 codes as fp6 e3m2 values, the size-chosen kernel)
+and ``nv4_w4a4_gemm_f8`` (codes as fp8 e4m3 values).
 
 The grouped W4A4 GEMM of nanovllm/kernels/w4a4_grouped_kernel.py:64-90 for
-prefill-sized M, with the INT4 codes carried as e4m3 values: results must
-equal the oracle (benchmarks/verify_w4a4_aw_grouped.py:13-29) bit for bit,
-like every other K2 path.  Covers the reference shapes, tails in M and N,
+prefill-sized M: results must equal the oracle
+(benchmarks/verify_w4a4_aw_grouped.py:13-29) bit for bit, like every other K2
+path.  Covers the reference shapes, tails in M and N (partial 128-row tiles),
 K from one group (no scale windows) to 12288, scale pointers that rule the
 windows out, both weight layouts, both weight-scale forms, bf16 and fp32
 outputs, the extreme scales of the int8 prefill test (bf16 subnormals, tiny
@@ -24,9 +26,10 @@ from test_gpu_w4a4 import assert_bits_equal, extreme_scales, gemm_inputs, to_dev
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda:0"
+PATHS = ["fp6", "fp8"]
 
 
-def check_against_oracle(ap, wp, sa, sw, M, N, K, what):
+def check_against_oracle(ap, wp, sa, sw, M, N, K, what, path):
     grouped = sw.ndim == 2
     a, w, s_a, s_w = to_dev(ap, wp, sa, sw)
     exp16 = oracle.w4a4_gemm(ap, wp, sa, sw)
@@ -36,17 +39,17 @@ def check_against_oracle(ap, wp, sa, sw, M, N, K, what):
     out = storage[64:-64].view(M, N)
     for rep in range(2):
         out.fill_(float("nan"))
-        w4a4_grouped_gemm(a, w, s_a, s_w, out=out, fp8=True)
+        w4a4_grouped_gemm(a, w, s_a, s_w, out=out, path=path)
         torch.cuda.synchronize()
         assert_bits_equal(bf16_bits(out), exp16, f"{what}: bf16 output (call {rep})")
         assert torch.equal(storage[:64], sentinel) and torch.equal(storage[-64:], sentinel)
     out32 = torch.full((M, N), float("nan"), device=DEV, dtype=torch.float32)
-    compile_grouped_gemm(M, N, K, output_fp32=True, weight_grouped=grouped, fp8=True)(a, w, s_a, s_w, out32)
+    compile_grouped_gemm(M, N, K, output_fp32=True, weight_grouped=grouped, path=path)(a, w, s_a, s_w, out32)
     torch.cuda.synchronize()
     assert_bits_equal(out32.cpu().numpy().view(np.uint32), exp32.view(np.uint32), f"{what}: fp32 output")
     if N % 16 == 0:
         out.fill_(float("nan"))
-        w4a4_grouped_gemm(a, tile_weights(w), s_a, s_w, out=out, weights_tiled=True, fp8=True)
+        w4a4_grouped_gemm(a, tile_weights(w), s_a, s_w, out=out, weights_tiled=True, path=path)
         torch.cuda.synchronize()
         assert_bits_equal(bf16_bits(out), exp16, f"{what}: bf16 output, tiled weights")
 
@@ -55,19 +58,21 @@ def check_against_oracle(ap, wp, sa, sw, M, N, K, what):
                                    (200, 264, 1024), (257, 392, 2048), (300, 16, 1152), (128, 128, 8192),
                                    (600, 264, 1024), (513, 136, 2048), (1030, 24, 3072)])
 @pytest.mark.parametrize("grouped", [True, False])
-def test_f8_matches_oracle(M, N, K, grouped):
-    print(f"[f8] M={M} N={N} K={K} grouped={grouped}", flush=True)
+@pytest.mark.parametrize("path", PATHS)
+def test_matches_oracle(M, N, K, grouped, path):
+    print(f"[{path}] M={M} N={N} K={K} grouped={grouped}", flush=True)
     ap, wp, sa, sw = gemm_inputs(M, N, K, M * 3 + N + K)
     if not grouped:
         sw = sw[:, 0].copy()
-    check_against_oracle(ap, wp, sa, sw, M, N, K, f"M={M} N={N} K={K}")
+    check_against_oracle(ap, wp, sa, sw, M, N, K, f"{path} M={M} N={N} K={K}", path)
 
 
-def test_f8_scales_without_windows():
+@pytest.mark.parametrize("path", PATHS)
+def test_scales_without_windows(path):
     """Scale tensors 2 bytes off a 16-byte boundary: the kernel reads each
     group's scales on its own instead of 8-group windows."""
     M, N, K = 160, 144, 2048
-    print(f"[f8-unaligned-scales] M={M} N={N} K={K}", flush=True)
+    print(f"[{path}-unaligned-scales] M={M} N={N} K={K}", flush=True)
     ap, wp, sa, sw = gemm_inputs(M, N, K, 99)
     exp = oracle.w4a4_gemm(ap, wp, sa, sw)
     a, w, s_a, s_w = to_dev(ap, wp, sa, sw)
@@ -77,7 +82,7 @@ def test_f8_scales_without_windows():
     s_w2 = sw_buf[1:].view(N, K // 128)
     s_a2.copy_(s_a)
     s_w2.copy_(s_w)
-    out = w4a4_grouped_gemm(a, w, s_a2, s_w2, fp8=True)
+    out = w4a4_grouped_gemm(a, w, s_a2, s_w2, path=path)
     torch.cuda.synchronize()
     assert_bits_equal(bf16_bits(out), exp, "bf16 output, unaligned scales")
 
@@ -85,8 +90,9 @@ def test_f8_scales_without_windows():
 @pytest.mark.parametrize("M,N,K,rows_special", [(200, 264, 1024, True), (257, 392, 2048, False),
                                                  (150, 136, 12288, True), (130, 400, 1024, False),
                                                  (700, 264, 1024, True), (520, 400, 2048, False)])
-def test_f8_extreme_scales(M, N, K, rows_special):
-    print(f"[f8-extreme] M={M} N={N} K={K}", flush=True)
+@pytest.mark.parametrize("path", PATHS)
+def test_extreme_scales(M, N, K, rows_special, path):
+    print(f"[{path}-extreme] M={M} N={N} K={K}", flush=True)
     rng = np.random.default_rng(M * 7 + K)
     ap, wp, _, _ = gemm_inputs(M, N, K, M + N + K)
     G = K // 128
@@ -96,15 +102,16 @@ def test_f8_extreme_scales(M, N, K, rows_special):
         sa[130:] = extreme_scales(rng, M - 130, G)
     else:
         sw[:128] = extreme_scales(rng, 128, G)
-    check_against_oracle(ap, wp, sa, sw, M, N, K, f"extreme M={M} N={N} K={K}")
+    check_against_oracle(ap, wp, sa, sw, M, N, K, f"{path} extreme M={M} N={N} K={K}", path)
 
 
 @pytest.mark.parametrize("M,N,K", [(1024, 6144, 4096), (2048, 4096, 4096), (4097, 24576, 4096),
                                    (1100, 4096, 12288)])
-def test_f8_equals_int8_path(M, N, K):
-    """Full-matrix equality with the int8 prefill kernel (itself pinned to the
-    oracle) at projection shapes, random packed bytes, tiled weights."""
-    print(f"[f8-vs-int8] M={M} N={N} K={K}", flush=True)
+def test_equals_int8_path(M, N, K):
+    """Full-matrix equality of both matrix-core forms with the int8 prefill
+    kernel (itself pinned to the oracle) at projection shapes, random packed
+    bytes, tiled and reference weight layouts."""
+    print(f"[mc-vs-int8] M={M} N={N} K={K}", flush=True)
     g = torch.Generator(device=DEV)
     g.manual_seed(M + N + K)
     a = torch.randint(-128, 128, (M, K // 2), generator=g, device=DEV, dtype=torch.int16).to(torch.int8)
@@ -112,26 +119,33 @@ def test_f8_equals_int8_path(M, N, K):
     sa = (0.01 + torch.rand(M, K // 128, generator=g, device=DEV)).to(torch.bfloat16)
     sw = (0.005 + 0.015 * torch.rand(N, K // 128, generator=g, device=DEV)).to(torch.bfloat16)
     wt = tile_weights(w)
-    o8 = w4a4_grouped_gemm(a, wt, sa, sw, weights_tiled=True, fp8=False)
-    of = w4a4_grouped_gemm(a, wt, sa, sw, weights_tiled=True, fp8=True)
+    o8 = w4a4_grouped_gemm(a, wt, sa, sw, weights_tiled=True, path="int8")
+    for path in PATHS:
+        of = w4a4_grouped_gemm(a, wt, sa, sw, weights_tiled=True, path=path)
+        torch.cuda.synchronize()
+        assert torch.equal(o8.view(torch.int16), of.view(torch.int16)), f"{path}, tiled weights"
+    of = w4a4_grouped_gemm(a, w, sa, sw, path="fp6")
     torch.cuda.synchronize()
-    assert torch.equal(o8.view(torch.int16), of.view(torch.int16))
+    assert torch.equal(o8.view(torch.int16), of.view(torch.int16)), "fp6, reference weight layout"
 
 
-def test_f8_workspace_reused_smaller_call():
+@pytest.mark.parametrize("path", PATHS)
+def test_workspace_reused_smaller_call(path):
     """Two calls in a row on one workspace, the second smaller: each result
     equals the oracle (the workspace holds nothing that carries over)."""
     lib = _lib.load()
-    ws = torch.empty((300 + 264) * 2048, dtype=torch.uint8, device=DEV)
+    fn = lib.nv4_w4a4_gemm_f6 if path == "fp6" else lib.nv4_w4a4_gemm_f8
+    size = (lambda M, N, K: lib.nv4_w4a4_gemm_f6_workspace(M, N, K)) if path == "fp6" else (lambda M, N, K: (M + N) * K)
+    ws = torch.empty(size(300, 264, 2048), dtype=torch.uint8, device=DEV)
     for (M, N, K) in [(300, 264, 2048), (70, 136, 1024)]:
-        print(f"[f8-ws] M={M} N={N} K={K}", flush=True)
+        print(f"[{path}-ws] M={M} N={N} K={K}", flush=True)
         ap, wp, sa, sw = gemm_inputs(M, N, K, M + K)
         exp = oracle.w4a4_gemm(ap, wp, sa, sw)
         a, w, s_a, s_w = to_dev(ap, wp, sa, sw)
         out = torch.empty((M, N), dtype=torch.bfloat16, device=DEV)
         P = lambda t: ctypes.c_void_p(t.data_ptr())
-        rc = lib.nv4_w4a4_gemm_f8(P(a), P(w), 0, P(s_a), P(s_w), 1, P(out), 0, M, N, K, P(ws), ws.numel(),
-                                  ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
-        _lib.check(rc, "nv4_w4a4_gemm_f8")
+        rc = fn(P(a), P(w), 0, P(s_a), P(s_w), 1, P(out), 0, M, N, K, P(ws), ws.numel(),
+                ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+        _lib.check(rc, f"w4a4 gemm {path}")
         torch.cuda.synchronize()
-        assert_bits_equal(bf16_bits(out), exp, f"workspace call M={M}")
+        assert_bits_equal(bf16_bits(out), exp, f"{path} workspace call M={M}")

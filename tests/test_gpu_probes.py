@@ -17,7 +17,7 @@ def test_probe_kernels_run():
     lib = _lib.load()
     stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
     sink = torch.full((1024,), 7, dtype=torch.int32, device=DEV)
-    for kind in (0, 1):
+    for kind in (0, 1, 2):
         assert lib.nv4_probe_mfma(kind, 10, 64, ctypes.c_void_p(sink.data_ptr()), stream) == 0
     buf = torch.ones(1 << 22, dtype=torch.uint8, device=DEV)
     assert lib.nv4_probe_read(ctypes.c_void_p(buf.data_ptr()), buf.numel(), ctypes.c_void_p(sink.data_ptr()),
@@ -30,5 +30,5 @@ def test_bench_measured_peaks_are_plausible():
     import bench
     peaks = bench.measured_peaks(torch, torch.device(DEV))
     print(peaks, flush=True)
-    for key in ("int8_mfma_tops", "fp8_mfma_tops", "hbm_read_gbs"):
+    for key in ("int8_mfma_tops", "fp8_mfma_tops", "fp6_mfma_tops", "hbm_read_gbs"):
         assert 0 < peaks[key] < 2 * peaks["published"][key], key

@@ -202,15 +202,15 @@ def test_k2_chain_qwen3_shapes_m32(proj, tiled):
     assert_bits_equal(bf16_bits(out), o_ref, f"{proj} M=32 chain")
 
 
-@pytest.mark.parametrize("fp8", [None, False])
+@pytest.mark.parametrize("path", [None, "int8", "fp8"])
 @pytest.mark.parametrize("tiled", [False, True])
 @pytest.mark.parametrize("proj", ["o", "qkv", "gate_up", "down"])
-def test_k2_chain_qwen3_shapes_m4096_sampled(proj, tiled, fp8):
-    """fp8=None takes the size-chosen path (the fp8 matrix cores at M = 4096);
-    fp8=False the int8 prefill kernel."""
+def test_k2_chain_qwen3_shapes_m4096_sampled(proj, tiled, path):
+    """path=None takes the size-chosen kernels (the fp6 matrix cores at
+    M = 4096); "int8" the int8 prefill kernel, "fp8" the fp8 one."""
     case = W.w4a4_case(proj, 4096)
     M, N, K = case.shape
-    print(f"[chain] {proj} M={M} N={N} K={K} tiled={tiled} fp8={fp8} (row sample)", flush=True)
+    print(f"[chain] {proj} M={M} N={N} K={K} tiled={tiled} path={path} (row sample)", flush=True)
     x, signs = case.x.to(DEV), case.signs.to(DEV)
     wpk, wsc = case.w_packed.to(DEV), case.w_scale.to(DEV)
     if tiled:
@@ -218,7 +218,7 @@ def test_k2_chain_qwen3_shapes_m4096_sampled(proj, tiled, fp8):
     packed = torch.empty((M, K // 2), dtype=torch.int8, device=DEV)
     scale = torch.empty((M, K // 128), dtype=torch.bfloat16, device=DEV)
     rht_quant_pack(x, signs, out_packed=packed, out_scale=scale)
-    out = w4a4_grouped_gemm(packed, wpk, scale, wsc, weights_tiled=tiled, fp8=fp8)
+    out = w4a4_grouped_gemm(packed, wpk, scale, wsc, weights_tiled=tiled, path=path)
     torch.cuda.synchronize()
     rows = np.unique(np.concatenate([np.arange(0, 3), np.linspace(0, M - 1, 21).round().astype(int),
                                      np.arange(M - 3, M), [127, 128, 129]]))
