@@ -78,7 +78,10 @@ __device__ __forceinline__ uint64_t packed4_to_e3m2(uint32_t d) {
 
 // Packed INT4 rows -> fp6 tile blocks, both operands in one launch.  Thread u
 // converts one quarter (16 packed bytes, 32 codes) of one group row: u =
-// ((tile * G + g) * 4 + q) * 128 + row, A tiles first, then W tiles.  A is in
+// ((tile * G + g) * 128 + row) * 4 + q, A tiles first, then W tiles, so four
+// consecutive lanes read one row's 64 contiguous group bytes (and a wave the
+// whole 1 KiB block of a tiled weight group) and a wave's stores are four
+// contiguous runs of P and of R.  A is in
 // the reference layout [M][K/2]; W in the reference layout or, with W_TILED,
 // the MFMA-tiled one ([N/16][G][64 lanes][16 bytes], lane l holding packed
 // bytes 64g + 16(l/16) .. +15 of row 16cb + l%16).  Rows past the matrix
@@ -91,7 +94,7 @@ i4_to_f6_tiles(const int8_t* __restrict__ a, uint8_t* __restrict__ a6, int64_t u
     const bool is_a = u < ua;
     if (!is_a) u -= ua;
     if (!is_a && u >= uw) return;
-    const int r = (int)(u & 127), q = (int)((u >> 7) & 3);
+    const int q = (int)(u & 3), r = (int)((u >> 2) & 127);
     const int64_t tg = u >> 9;
     const int g = (int)(tg % G);
     const int64_t tile = tg / G;
