@@ -583,6 +583,7 @@ def detail_table(torch, nv4, W, dev, R):
     Cache), their roofline fractions, and the BF16 hipBLASLt GEMM (torch.mm)
     on the same shape; then the W4A16 GPTQ GEMM on the fused QKV at M = 1, 8,
     32 (fp16 activations, microseconds per call and HBM fraction)."""
+    from nv4.kernels.w4a4_grouped import keep_weights_f6
     res = {}
     g = torch.Generator(device=dev)
     g.manual_seed(W.BASE_SEED + 2000)
@@ -598,12 +599,17 @@ def detail_table(torch, nv4, W, dev, R):
                 wp = torch.randint(-128, 128, (N, K // 2), generator=g, device=dev,
                                    dtype=torch.int16).to(torch.int8)
                 sw = (0.005 + 0.015 * torch.rand(N, K // 128, generator=g, device=dev)).to(torch.bfloat16)
-                wsets.append((nv4.tile_weights(wp), sw))
+                wt = nv4.tile_weights(wp)
+                # As W4A4Linear keeps them: tiled INT4 weights and, for the
+                # prefill sizes of qkv, o and down, their fp6 tile form
+                # (converted once; gate_up's weights are converted per call).
+                keep = M > 32 and keep_weights_f6(N, K)
+                wsets.append((wt, sw, nv4.weights_to_f6(wt, True) if keep else None))
             pkb = torch.empty((M, K // 2), dtype=torch.int8, device=dev)
             scb = torch.empty((M, K // 128), dtype=torch.bfloat16, device=dev)
             ob = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
             l1 = [lambda: nv4.rht_quant_pack(x, sg, out_packed=pkb, out_scale=scb)] * rot
-            l2 = [lambda w=w: nv4.w4a4_grouped_gemm(pkb, w[0], scb, w[1], out=ob, weights_tiled=True)
+            l2 = [lambda w=w: nv4.w4a4_grouped_gemm(pkb, w[0], scb, w[1], out=ob, weights_tiled=True, weights_f6=w[2])
                   for w in wsets]
             us1 = graph_launch_us(torch, l1, reps)
             us2 = graph_launch_us(torch, l2, reps)

@@ -30,6 +30,9 @@
  *                          cores, with a caller workspace for the e4m3 operands
  *   nv4_w4a4_gemm_f6, nv4_w4a4_gemm_f6_workspace <- the same, on the fp6 matrix
  *                          cores (e3m2 operands in 128-row tiles)
+ *   nv4_w4a4_weights_to_f6, nv4_w4a4_weights_f6_bytes <- no counterpart in the
+ *                          reference: the weight half of that conversion, done
+ *                          once per layer and kept beside the INT4 weights
  *   nv4_w4a16_gemm, nv4_w4a16_gemm_ws, nv4_w4a16_dequant <- nanovllm/layers/linear_w4a16.py:11
  *                          tl_dequant_matmul_w4a16 (called from W4A16Linear.forward
  *                          :128-148; the reference splits K 8 ways with bf16 atomics,
@@ -184,11 +187,28 @@ int nv4_w4a4_gemm_f8(const int8_t* a, const int8_t* w, int w_tiled, const void* 
  * nv4_w4a4_gemm_f8; the workspace is overwritten, and calls sharing one
  * workspace must be stream-ordered.  nv4_w4a4_gemm_f6_workspace returns -1
  * for shapes the operator rejects (M, N < 1; K not a positive multiple of 128).
+ *   w_form  0: w is packed int8 [N,K/2]; 1: MFMA-tiled (N % 16 == 0);
+ *           2: w is the fp6 tile form written by nv4_w4a4_weights_to_f6 for
+ *              this N and K -- only A is converted, and the workspace needs
+ *              only its A part, ceil(M/128) * (K/128) * 12288 bytes.
  */
-int nv4_w4a4_gemm_f6(const int8_t* a, const int8_t* w, int w_tiled, const void* sa, const void* sw,
+int nv4_w4a4_gemm_f6(const int8_t* a, const int8_t* w, int w_form, const void* sa, const void* sw,
                      int sw_grouped, void* out, int out_fp32, int64_t M, int64_t N, int64_t K,
                      void* workspace, int64_t workspace_bytes, void* stream);
 int64_t nv4_w4a4_gemm_f6_workspace(int64_t M, int64_t N, int64_t K);
+
+/*
+ * Weights converted once for nv4_w4a4_gemm_f6 (w_form 2): packed int8
+ * [N,K/2] (w_tiled 0) or MFMA-tiled (w_tiled 1, N % 16 == 0) -> w6, the
+ * e3m2 tile blocks the per-call conversion would write for W
+ * (nv4_w4a4_weights_f6_bytes(N, K) = ceil(N/128) * (K/128) * 12288 bytes;
+ * -1 for N < 1 or K not a positive multiple of 128).  Same shape and
+ * alignment rules as nv4_w4a4_gemm_f6; w6 must not overlap w.  A layer keeps
+ * w6 for as long as its weights do, so prefill calls convert activations only.
+ */
+int nv4_w4a4_weights_to_f6(const int8_t* w, int w_tiled, uint8_t* w6, int64_t N, int64_t K,
+                           int64_t w6_bytes, void* stream);
+int64_t nv4_w4a4_weights_f6_bytes(int64_t N, int64_t K);
 
 /*
  * W4A16 GEMM with GPTQ weights (zero-point convention w = (q - z - 1) * s).

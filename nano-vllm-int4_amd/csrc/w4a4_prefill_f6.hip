@@ -17,8 +17,8 @@
 // fewer bytes to stage than fp8).  The scale product sa * sw comes from a
 // bf16 MFMA as in the fp8 kernel; one VALU fma per output and group remains.
 //
-// Operand format (written by i4_to_f6_tiles into the caller's workspace):
-// rows in tiles of 128; per tile and group one 12 KiB block laid out as LDS
+// Operand format (written by i4_to_f6_tiles into the caller's workspace, or
+// for weights converted once by nv4_w4a4_weights_to_f6): rows in tiles of 128; per tile and group one 12 KiB block laid out as LDS
 // reads it.  A group row's 128 codes are four quarters of 32 (k = 32q ..
 // 32q + 31, 24 bytes each, code k at bit 6k of the quarter, little endian),
 // and each quarter is split into its first 16 bytes (P) and last 8 (R):
@@ -85,7 +85,9 @@ __device__ __forceinline__ uint64_t packed4_to_e3m2(uint32_t d) {
 // the reference layout [M][K/2]; W in the reference layout or, with W_TILED,
 // the MFMA-tiled one ([N/16][G][64 lanes][16 bytes], lane l holding packed
 // bytes 64g + 16(l/16) .. +15 of row 16cb + l%16).  Rows past the matrix
-// edge repeat its last row (their results are never stored).
+// edge repeat its last row (their results are never stored).  Either half
+// may be empty: ua = 0 converts weights only, uw = 0 activations only (the
+// threads past A then return without touching w6).
 template <bool W_TILED>
 __global__ void __launch_bounds__(256)
 i4_to_f6_tiles(const int8_t* __restrict__ a, uint8_t* __restrict__ a6, int64_t ua, int M, const int8_t* __restrict__ w,
@@ -360,12 +362,44 @@ extern "C" int64_t nv4_w4a4_gemm_f6_workspace(int64_t M, int64_t N, int64_t K) {
     return ((M + F6_BM - 1) / F6_BM + (N + F6_BN - 1) / F6_BN) * (K / 128) * (int64_t)F6_BLOCK;
 }
 
-extern "C" int nv4_w4a4_gemm_f6(const int8_t* a, const int8_t* w, int w_tiled, const void* sa, const void* sw,
+extern "C" int64_t nv4_w4a4_weights_f6_bytes(int64_t N, int64_t K) {
+    using namespace nv4;
+    if (N < 1 || K < 128 || K % 128) return -1;
+    return (N + F6_BN - 1) / F6_BN * (K / 128) * (int64_t)F6_BLOCK;
+}
+
+// Packed weights -> the fp6 tile blocks the GEMM reads (the W half of the
+// per-call conversion), for weights converted once and kept.
+extern "C" int nv4_w4a4_weights_to_f6(const int8_t* w, int w_tiled, uint8_t* w6, int64_t N, int64_t K,
+                                      int64_t w6_bytes, void* stream) {
+    using namespace nv4;
+    if (!w || !w6) return NV4_E_NULL;
+    if (N < 1 || K < 128 || K % 128 || N % 8 || (w_tiled != 0 && w_tiled != 1) || (w_tiled && N % 16))
+        return NV4_E_SHAPE;
+    if (N > 0x7fffffffLL || K > (1LL << 20)) return NV4_E_SHAPE;
+    const int64_t G = K / 128, tn = (N + F6_BN - 1) / F6_BN;
+    if (G * F6_BLOCK > 0x7fffffffLL || N * G > 0x7fffffffLL || tn * G * 512 > 0xffffff00LL) return NV4_E_SHAPE;
+    if (w6_bytes < tn * G * F6_BLOCK) return NV4_E_SHAPE;
+    if (reinterpret_cast<uintptr_t>(w) % 16 || reinterpret_cast<uintptr_t>(w6) % 16) return NV4_E_ALIGN;
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    const int64_t uw = tn * G * 512;
+    const unsigned cgrid = (unsigned)((uw + 255) / 256);
+    if (w_tiled)
+        hipLaunchKernelGGL(i4_to_f6_tiles<true>, dim3(cgrid), dim3(256), 0, st, nullptr, nullptr, (int64_t)0, 1, w,
+                           w6, uw, (int)N, (int)G, (int)K);
+    else
+        hipLaunchKernelGGL(i4_to_f6_tiles<false>, dim3(cgrid), dim3(256), 0, st, nullptr, nullptr, (int64_t)0, 1, w,
+                           w6, uw, (int)N, (int)G, (int)K);
+    return (int)hipGetLastError();
+}
+
+extern "C" int nv4_w4a4_gemm_f6(const int8_t* a, const int8_t* w, int w_form, const void* sa, const void* sw,
                                 int sw_grouped, void* out, int out_fp32, int64_t M, int64_t N, int64_t K,
                                 void* workspace, int64_t workspace_bytes, void* stream) {
     using namespace nv4;
     if (!a || !w || !sa || !sw || !out || !workspace) return NV4_E_NULL;
-    if (M < 1 || N < 1 || K < 128 || K % 128 || N % 8 || (w_tiled && N % 16)) return NV4_E_SHAPE;
+    if (w_form < 0 || w_form > 2) return NV4_E_SHAPE;
+    if (M < 1 || N < 1 || K < 128 || K % 128 || N % 8 || (w_form == 1 && N % 16)) return NV4_E_SHAPE;
     if (M > 0x7fffffffLL || N > 0x7fffffffLL || K > (1LL << 20)) return NV4_E_SHAPE;
     const int64_t G = K / 128;
     const int64_t tm = (M + F6_BM - 1) / F6_BM, tn = (N + F6_BN - 1) / F6_BN;
@@ -374,17 +408,19 @@ extern "C" int nv4_w4a4_gemm_f6(const int8_t* a, const int8_t* w, int w_tiled, c
     // group row of both padded operands, the GEMM 256 per output tile.
     if (G * F6_BLOCK > 0x7fffffffLL || M * G > 0x7fffffffLL || N * G > 0x7fffffffLL) return NV4_E_SHAPE;
     if (tm * tn * F6_T > 0xffffffffLL || (tm + tn) * G * 512 > 0xffffff00LL) return NV4_E_SHAPE;
-    if (workspace_bytes < (tm + tn) * G * F6_BLOCK) return NV4_E_SHAPE;
+    // Weights already in fp6 tiles (w_form 2) need workspace for A only.
+    if (workspace_bytes < (w_form == 2 ? tm : tm + tn) * G * F6_BLOCK) return NV4_E_SHAPE;
     if (reinterpret_cast<uintptr_t>(a) % 16 || reinterpret_cast<uintptr_t>(w) % 16 ||
         reinterpret_cast<uintptr_t>(sa) % 2 || reinterpret_cast<uintptr_t>(sw) % 2 ||
         reinterpret_cast<uintptr_t>(out) % (out_fp32 ? 4 : 2) || reinterpret_cast<uintptr_t>(workspace) % 16)
         return NV4_E_ALIGN;
     hipStream_t st = static_cast<hipStream_t>(stream);
     uint8_t* a6 = static_cast<uint8_t*>(workspace);
-    uint8_t* w6 = a6 + tm * G * F6_BLOCK;
-    const int64_t ua = tm * G * 512, uw = tn * G * 512;
+    const bool w_ready = w_form == 2;
+    uint8_t* w6 = w_ready ? const_cast<uint8_t*>(reinterpret_cast<const uint8_t*>(w)) : a6 + tm * G * F6_BLOCK;
+    const int64_t ua = tm * G * 512, uw = w_ready ? 0 : tn * G * 512;
     const unsigned cgrid = (unsigned)((ua + uw + 255) / 256);
-    if (w_tiled)
+    if (w_form == 1)
         hipLaunchKernelGGL(i4_to_f6_tiles<true>, dim3(cgrid), dim3(256), 0, st, a, a6, ua, (int)M, w, w6, uw, (int)N,
                            (int)G, (int)K);
     else

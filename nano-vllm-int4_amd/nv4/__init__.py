@@ -7,12 +7,12 @@ the reference's Python operator and module interfaces.
 from . import _lib
 from .kernels import (Config, GroupedConfig, best_config, best_grouped_config, compile_grouped_gemm,
                       compile_kernel, dequant_matmul_w4a16, rht_quant_pack, tile_weights,
-                      untile_weights, w4a4_grouped_gemm, w4a4_linear)
+                      untile_weights, w4a4_grouped_gemm, w4a4_linear, weights_to_f6)
 from .layers import W4A4Linear, W4A16Linear
 
 __version__ = "0.1.0"
 
 __all__ = ["Config", "GroupedConfig", "best_config", "best_grouped_config", "compile_grouped_gemm",
            "compile_kernel", "dequant_matmul_w4a16", "rht_quant_pack", "w4a4_grouped_gemm",
-           "w4a4_linear", "tile_weights", "untile_weights",
+           "w4a4_linear", "tile_weights", "untile_weights", "weights_to_f6",
            "W4A4Linear", "W4A16Linear"]

@@ -67,7 +67,60 @@ def _resolve_path(path, M, N, K):
     return path
 
 
-def _launch(a_packed, w_packed, a_scale, w_scale, out, output_fp32, weight_grouped, weights_tiled=False, path=None):
+def weights_f6_bytes(N, K):
+    """Size of the fp6 tile form of [N, K] weights (``weights_to_f6``)."""
+    n = _lib.load().nv4_w4a4_weights_f6_bytes(N, K)
+    if n < 0:
+        raise ValueError("Require N >= 1 and K a positive multiple of 128")
+    return n
+
+
+# Largest fp6 weight form a layer keeps (``keep_weights_f6``).
+KEEP_F6_MAX_BYTES = 48 << 20
+
+
+def keep_weights_f6(N, K):
+    """Whether a layer keeps the fp6 form of its [N, K] weights.  Measured on
+    the decoder's projections at M = 4096 (same box, interleaved), calls on
+    kept weights beat converting them per call for qkv, o and down (12.6 to
+    37.7 MB of fp6 tiles: 111.6 / 78.6 / 207.1 against 114.5 / 81.4 / 212.7
+    us) but not for gate_up (75.5 MB: 474 against 439 us): the GEMM fetches
+    each operand byte about nine times from beyond the L2, and the per-call
+    conversion leaves fresh weight tiles in the 256 MB Infinity Cache, which
+    weights read from HBM lack."""
+    return weights_f6_bytes(N, K) <= KEEP_F6_MAX_BYTES
+
+
+def weights_to_f6(w_packed, weights_tiled=False):
+    """Packed [N,K/2] weights (or their ``tile_weights`` form) -> the fp6 tile
+    blocks that the prefill GEMM reads, as a uint8 tensor.  Made once per
+    layer, it lets prefill-sized calls convert only the activations; results
+    are bit-identical."""
+    if w_packed.ndim != 2 or w_packed.dtype != torch.int8 or not w_packed.is_cuda or not w_packed.is_contiguous():
+        raise ValueError("Packed weights must be a contiguous int8 CUDA tensor [N,K/2]")
+    N, K = w_packed.shape[0], w_packed.shape[1] * 2
+    if N % 8 or K % GROUP_SIZE or (weights_tiled and N % 16):
+        raise ValueError("Require N divisible by 8 (16 when tiled) and K divisible by 128")
+    w6 = torch.empty(weights_f6_bytes(N, K), dtype=torch.uint8, device=w_packed.device)
+    lib = _lib.load()
+    stream = torch.cuda.current_stream(w_packed.device).cuda_stream
+    with torch.cuda.device(w_packed.device):
+        rc = lib.nv4_w4a4_weights_to_f6(ctypes.c_void_p(w_packed.data_ptr()), 1 if weights_tiled else 0,
+                                        ctypes.c_void_p(w6.data_ptr()), N, K, w6.numel(), ctypes.c_void_p(stream))
+    _lib.check(rc, "weights_to_f6")
+    return w6
+
+
+def _check_weights_f6(weights_f6, N, K, device):
+    if weights_f6 is None:
+        return
+    if (weights_f6.dtype != torch.uint8 or weights_f6.ndim != 1 or not weights_f6.is_contiguous()
+            or weights_f6.device != device or weights_f6.numel() != weights_f6_bytes(N, K)):
+        raise ValueError("weights_f6 must be the weights_to_f6 tensor of these weights, on the input device")
+
+
+def _launch(a_packed, w_packed, a_scale, w_scale, out, output_fp32, weight_grouped, weights_tiled=False, path=None,
+            weights_f6=None):
     M, N, K = a_packed.shape[0], w_packed.shape[0], a_packed.shape[1] * 2
     path = _resolve_path(path, M, N, K)
     lib = _lib.load()
@@ -76,13 +129,18 @@ def _launch(a_packed, w_packed, a_scale, w_scale, out, output_fp32, weight_group
         if path != "int8":
             # Matrix-core operands for this call (caching allocator: no
             # hipMalloc once warm); the kernels only read it on this stream.
+            # Weights already in fp6 tiles (``weights_f6``) leave only the
+            # activations to convert.
+            w_form, w_ptr = (1 if weights_tiled else 0), w_packed.data_ptr()
             if path == "fp6":
                 fn, nbytes = lib.nv4_w4a4_gemm_f6, lib.nv4_w4a4_gemm_f6_workspace(M, N, K)
+                if weights_f6 is not None:
+                    w_form, w_ptr = 2, weights_f6.data_ptr()
+                    nbytes -= weights_f6.numel()
             else:
                 fn, nbytes = lib.nv4_w4a4_gemm_f8, (M + N) * K
             ws = torch.empty(nbytes, dtype=torch.uint8, device=a_packed.device)
-            rc = fn(ctypes.c_void_p(a_packed.data_ptr()), ctypes.c_void_p(w_packed.data_ptr()),
-                    1 if weights_tiled else 0,
+            rc = fn(ctypes.c_void_p(a_packed.data_ptr()), ctypes.c_void_p(w_ptr), w_form,
                     ctypes.c_void_p(a_scale.data_ptr()), ctypes.c_void_p(w_scale.data_ptr()),
                     1 if weight_grouped else 0, ctypes.c_void_p(out.data_ptr()),
                     1 if output_fp32 else 0, M, N, K, ctypes.c_void_p(ws.data_ptr()),
@@ -156,11 +214,14 @@ def best_grouped_config(M, N, K, weight_grouped=False):
     return GroupedConfig() if M <= 32 else GroupedConfig(64, 128, 2, 128)
 
 
-def w4a4_grouped_gemm(a_packed, w_packed, a_scale, w_scale, out=None, config=None, *, weights_tiled=False, path=None):
+def w4a4_grouped_gemm(a_packed, w_packed, a_scale, w_scale, out=None, config=None, *, weights_tiled=False, path=None,
+                      weights_f6=None):
     """Packed INT4; BF16 Sa[M,K/128], Sw[N] or Sw[N,K/128], output[M,N].
     ``weights_tiled``: ``w_packed`` holds ``tile_weights`` output (N % 16 == 0);
     the result is bit-identical.  ``path``: "int8", "fp8" or "fp6" forces a
-    kernel family (same bits); None chooses by size."""
+    kernel family (same bits); None chooses by size.  ``weights_f6``: the
+    ``weights_to_f6`` form of these weights, used by the fp6 path instead of
+    converting them again."""
     if a_packed.ndim != 2 or w_packed.ndim != 2 or a_packed.shape[1] != w_packed.shape[1]:
         raise ValueError("Packed inputs must have compatible [M,K/2] and [N,K/2] shapes")
     M, K = a_packed.shape[0], a_packed.shape[1] * 2
@@ -188,5 +249,7 @@ def w4a4_grouped_gemm(a_packed, w_packed, a_scale, w_scale, out=None, config=Non
         _validate_config(config)
     if weights_tiled and N % 16:
         raise ValueError("The tiled weight layout needs N divisible by 16")
-    _launch(a_packed, w_packed, a_scale, w_scale, out, False, weight_grouped, weights_tiled, path=path)
+    _check_weights_f6(weights_f6, N, K, a_packed.device)
+    _launch(a_packed, w_packed, a_scale, w_scale, out, False, weight_grouped, weights_tiled, path=path,
+            weights_f6=weights_f6)
     return out

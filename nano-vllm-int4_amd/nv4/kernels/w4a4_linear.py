@@ -17,12 +17,15 @@ import torch
 
 from .. import _lib
 from .rht_a4 import rht_quant_pack
-from .w4a4_grouped import _launch, use_prefill_path
+from .w4a4_grouped import _check_weights_f6, _launch, use_prefill_path
 
 
-def w4a4_linear(x, signs, w_packed, w_scale, *, out=None, out_packed=None, out_scale=None, weights_tiled=False):
+def w4a4_linear(x, signs, w_packed, w_scale, *, out=None, out_packed=None, out_scale=None, weights_tiled=False,
+                weights_f6=None):
     """x bf16 [M,K] (K = 4096 or 12288) -> bf16 [M,N].  ``weights_tiled``:
-    ``w_packed`` is in the MFMA-tiled order (``tile_weights``)."""
+    ``w_packed`` is in the MFMA-tiled order (``tile_weights``).
+    ``weights_f6``: the ``weights_to_f6`` form of the weights, used by
+    prefill-sized calls instead of converting them again."""
     if x.ndim != 2 or x.dtype != torch.bfloat16 or x.shape[1] not in (4096, 12288) or x.shape[0] < 1:
         raise ValueError("Expected BF16 X[M,K], M>0, K=4096/12288")
     M, K = x.shape
@@ -51,10 +54,12 @@ def w4a4_linear(x, signs, w_packed, w_scale, *, out=None, out_packed=None, out_s
     tensors = (x, signs, w_packed, w_scale, out, out_packed, out_scale)
     if any(not t.is_cuda or not t.is_contiguous() or t.device != dev for t in tensors):
         raise ValueError("All tensors must be contiguous on one CUDA device")
+    _check_weights_f6(weights_f6, N, K, dev)
     if use_prefill_path(M, N, K):
         # Prefill-sized M: K1, then the grouped GEMM on the fp6 matrix cores.
         rht_quant_pack(x, signs, out_packed=out_packed, out_scale=out_scale)
-        _launch(out_packed, w_packed, out_scale, w_scale, out, False, True, weights_tiled, path="fp6")
+        _launch(out_packed, w_packed, out_scale, w_scale, out, False, True, weights_tiled, path="fp6",
+                weights_f6=weights_f6)
         return out
     lib = _lib.load()
     stream = torch.cuda.current_stream(dev).cuda_stream

@@ -12,15 +12,27 @@ allocator, so the forward can be captured in a HIP graph.
 ``tile_weights_()`` (called by the loaders once the weights are in) reorders
 ``packed_weight`` in place into the MFMA-tiled order that the decode
 kernels read in whole cache lines; the forward then uses the tiled entry
-point, with bit-identical results.  ``state_dict()`` and
-``load_state_dict()`` still see the reference [out, in/2] layout.
+point, with bit-identical results.  It also keeps ``weight_f6``, the fp6 tile
+form the prefill GEMM reads (0.75 bytes per weight, rebuilt whenever the
+weights are loaded), so prefill-sized calls convert only their activations --
+for weights up to ``KEEP_F6_MAX_BYTES`` of fp6 tiles (``keep_weights_f6``:
+qkv, o and down of Qwen3-8B; gate_up converts per call).
+``state_dict()`` and ``load_state_dict()`` still see the reference
+[out, in/2] layout and do not hold ``weight_f6``.
 """
 import torch
 from torch import nn
 import torch.distributed as dist
 
-from ..kernels.w4a4_grouped import tile_weights, untile_weights, w4a4_grouped_gemm
+from ..kernels.w4a4_grouped import keep_weights_f6, tile_weights, untile_weights, w4a4_grouped_gemm, weights_to_f6
 from ..kernels.w4a4_linear import w4a4_linear
+
+
+def _version_of(t):
+    try:
+        return t._version
+    except RuntimeError:  # inference tensors track no version
+        return None
 
 
 class W4A4Linear(nn.Module):
@@ -34,15 +46,34 @@ class W4A4Linear(nn.Module):
         self.register_buffer("packed_weight", torch.empty(output_size, input_size // 2, dtype=torch.int8))
         self.register_buffer("weight_scale", torch.empty(output_size, input_size // 128, dtype=torch.bfloat16))
         self.register_buffer("signs", torch.empty(input_size, dtype=torch.int8))
+        self.register_buffer("weight_f6", None, persistent=False)
         self.weights_tiled = False
 
     @torch.no_grad()
     def tile_weights_(self) -> "W4A4Linear":
-        """Reorder ``packed_weight`` into the MFMA-tiled layout (GPU, once)."""
+        """Reorder ``packed_weight`` into the MFMA-tiled layout (GPU, once) and
+        build its fp6 tile form for prefill."""
         if not self.weights_tiled and self.out_features % 16 == 0 and self.packed_weight.is_cuda:
             self.packed_weight.copy_(tile_weights(self.packed_weight))
             self.weights_tiled = True
+        self._refresh_f6()
         return self
+
+    @torch.no_grad()
+    def _refresh_f6(self) -> None:
+        keep = self.packed_weight.is_cuda and keep_weights_f6(self.out_features, self.in_features)
+        self.weight_f6 = weights_to_f6(self.packed_weight, self.weights_tiled) if keep else None
+        self._f6_version = _version_of(self.packed_weight)
+
+    def _f6(self):
+        """``weight_f6`` while ``packed_weight`` is unchanged since it was made
+        (an in-place write bumps the tensor's version); otherwise None, and
+        prefill calls convert the weights themselves.  Weights created under
+        ``torch.inference_mode`` carry no version: their copy is trusted as
+        made by ``tile_weights_`` / ``load_state_dict``."""
+        if self.weight_f6 is None or getattr(self, "_f6_version", -1) != _version_of(self.packed_weight):
+            return None
+        return self.weight_f6
 
     @torch.no_grad()
     def assign_quantized_(self, packed: torch.Tensor, scale: torch.Tensor, signs: torch.Tensor) -> "W4A4Linear":
@@ -65,6 +96,8 @@ class W4A4Linear(nn.Module):
         if self.weights_tiled and prefix + "packed_weight" in state_dict:
             with torch.no_grad():
                 self.packed_weight.copy_(tile_weights(self.packed_weight))
+        if self.weight_f6 is not None and prefix + "packed_weight" in state_dict:
+            self._refresh_f6()
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         if x.shape[-1] != self.in_features or x.dtype != torch.bfloat16:
@@ -73,7 +106,8 @@ class W4A4Linear(nn.Module):
         # RHT + quantize + pack, then the grouped INT4 GEMM; packed codes and
         # scales come from the caching allocator, so the forward can be
         # captured in a HIP graph.
-        out = w4a4_linear(flat, self.signs, self.packed_weight, self.weight_scale, weights_tiled=self.weights_tiled)
+        out = w4a4_linear(flat, self.signs, self.packed_weight, self.weight_scale, weights_tiled=self.weights_tiled,
+                          weights_f6=self._f6())
         return out.reshape(*x.shape[:-1], self.out_features)
 
     def forward_quantized(self, packed: torch.Tensor, scale: torch.Tensor) -> torch.Tensor:
@@ -82,4 +116,4 @@ class W4A4Linear(nn.Module):
         with this module's signs: packed int8 [M, in/2], scale bf16 [M, in/128]
         -> bf16 [M, out]."""
         return w4a4_grouped_gemm(packed, self.packed_weight, scale, self.weight_scale,
-                                 weights_tiled=self.weights_tiled)
+                                 weights_tiled=self.weights_tiled, weights_f6=self._f6())

@@ -115,6 +115,34 @@ def test_w4a4_gemm_f6_rejections():
     assert call(out=P(A16 + 2), fp32=1) == _lib.NV4_E_ALIGN
     big = 1 << 26                                                        # conversion grid beyond 32 bits
     assert call(M=big, nbytes=size(big, N, K)) == _lib.NV4_E_SHAPE
+    assert call(tiled=3) == _lib.NV4_E_SHAPE                             # weight forms are 0, 1 and 2
+    assert call(tiled=-1) == _lib.NV4_E_SHAPE
+    a_part = 2 * 32 * 12288                                              # fp6 weights: workspace for A only
+    assert call(tiled=2, nbytes=a_part - 1) == _lib.NV4_E_SHAPE
+    assert call(tiled=2, nbytes=a_part, w=P(A16 + 8)) == _lib.NV4_E_ALIGN
+
+
+def test_w4a4_weights_to_f6_rejections():
+    lib = _lib.load()
+    f, size = lib.nv4_w4a4_weights_to_f6, lib.nv4_w4a4_weights_f6_bytes
+    N, K = 200, 1024
+    need = size(N, K)
+    assert need == 2 * 8 * 12288                                         # 128-row tiles x groups x 12 KiB
+    assert size(0, K) == -1 and size(N, 1000) == -1 and size(N, 0) == -1
+
+    def call(w=P(A16), tiled=0, w6=P(A16), N=N, K=K, nbytes=need):
+        return f(w, tiled, w6, N, K, nbytes, None)
+
+    assert call(w=None) == _lib.NV4_E_NULL
+    assert call(w6=None) == _lib.NV4_E_NULL
+    assert call(nbytes=need - 1) == _lib.NV4_E_SHAPE
+    assert call(N=204) == _lib.NV4_E_SHAPE                               # N % 8
+    assert call(N=200, tiled=1) == _lib.NV4_E_SHAPE                      # tiled needs N % 16
+    assert call(tiled=2) == _lib.NV4_E_SHAPE                             # source forms are 0 and 1
+    assert call(K=1000) == _lib.NV4_E_SHAPE
+    assert call(K=1 << 21) == _lib.NV4_E_SHAPE
+    assert call(w=P(A16 + 8)) == _lib.NV4_E_ALIGN
+    assert call(w6=P(A16 + 4)) == _lib.NV4_E_ALIGN
 
 
 def test_w4a16_and_linear_rejections():

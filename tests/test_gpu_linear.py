@@ -155,3 +155,37 @@ def test_linear_prefill_matrix_core_route(proj, M):
         torch.cuda.synchronize()
         assert torch.equal(packed, p2) and torch.equal(scale.view(torch.int16), s2.view(torch.int16))
         assert torch.equal(out.view(torch.int16), ref.view(torch.int16)), f"tiled={tiled}"
+
+
+def test_linear_module_keeps_fp6_weights():
+    """``tile_weights_`` keeps the fp6 form of the weights (not for gate_up's):
+    prefill-sized forwards use it, with the bits of converting per call; it
+    stays out of the state dict, follows ``load_state_dict``, and is not used
+    once ``packed_weight`` is written in place."""
+    from nv4 import weights_to_f6
+    assert W4A4Linear(4096, 24576).to(DEV).tile_weights_().weight_f6 is None
+    case = W.w4a4_case("qkv", 1024)
+    M, N, K = case.shape
+    print(f"[linear-fp6-weights] M={M} N={N} K={K}", flush=True)
+    x = case.x.to(DEV)
+    m = W4A4Linear(K, N).to(DEV)
+    m.assign_quantized_(case.w_packed.to(DEV), case.w_scale.to(DEV), case.signs.to(DEV))
+    assert m.weights_tiled and m._f6() is m.weight_f6 is not None
+    assert "weight_f6" not in m.state_dict()
+    assert torch.equal(m.weight_f6, weights_to_f6(case.w_packed.to(DEV)))
+    out = m(x)
+    ref = w4a4_linear(x, m.signs, m.packed_weight, m.weight_scale, weights_tiled=True)   # converts per call
+    torch.cuda.synchronize()
+    assert torch.equal(out.view(torch.int16), ref.view(torch.int16))
+    with torch.no_grad():
+        m.packed_weight[:64].zero_()                  # in place: the fp6 copy is now stale
+    assert m._f6() is None
+    out2 = m(x)
+    ref2 = w4a4_linear(x, m.signs, m.packed_weight, m.weight_scale, weights_tiled=True)
+    torch.cuda.synchronize()
+    assert torch.equal(out2.view(torch.int16), ref2.view(torch.int16))
+    assert not torch.equal(out2.view(torch.int16), out.view(torch.int16))
+    m2 = W4A4Linear(K, N).to(DEV).tile_weights_()
+    m2.load_state_dict(m.state_dict())
+    assert m2._f6() is not None and torch.equal(m2.weight_f6, weights_to_f6(m.packed_weight, True))
+    assert torch.equal(m2(x).view(torch.int16), out2.view(torch.int16))

@@ -10,8 +10,9 @@ K from one group (no scale windows) to 12288, scale pointers that rule the
 windows out, both weight layouts, both weight-scale forms, bf16 and fp32
 outputs, the extreme scales of the int8 prefill test (bf16 subnormals, tiny
 normals, 2^70, zeros: the scale product is formed on the matrix cores and
-must still be the exact fp32 product), repeated calls on one workspace, and
-full-matrix equality with the int8 path at Qwen3-8B projection shapes.
+must still be the exact fp32 product), repeated calls on one workspace,
+full-matrix equality with the int8 path at Qwen3-8B projection shapes, and
+weights converted to fp6 once (``weights_to_f6``) instead of per call.
 """
 import ctypes
 
@@ -21,7 +22,7 @@ import torch
 
 import oracle
 from conftest import bf16_bits
-from nv4 import _lib, compile_grouped_gemm, tile_weights, w4a4_grouped_gemm
+from nv4 import _lib, compile_grouped_gemm, tile_weights, w4a4_grouped_gemm, weights_to_f6
 from test_gpu_w4a4 import assert_bits_equal, extreme_scales, gemm_inputs, to_dev
 
 pytestmark = pytest.mark.gpu
@@ -149,3 +150,51 @@ def test_workspace_reused_smaller_call(path):
         _lib.check(rc, f"w4a4 gemm {path}")
         torch.cuda.synchronize()
         assert_bits_equal(bf16_bits(out), exp, f"{path} workspace call M={M}")
+
+
+@pytest.mark.parametrize("M,N,K", [(17, 96, 512), (300, 264, 2048), (129, 24, 384), (1030, 136, 3072),
+                                   (257, 392, 12288)])
+@pytest.mark.parametrize("grouped", [True, False])
+def test_prepared_fp6_weights(M, N, K, grouped):
+    """Weights converted once by ``weights_to_f6``: the blocks equal the W half
+    of the per-call conversion (from either weight layout), the fp6 GEMM on
+    them gives the oracle's bits (bf16 and fp32 outputs, a workspace for A
+    only), and the calls leave them unchanged."""
+    print(f"[fp6-prepared] M={M} N={N} K={K} grouped={grouped}", flush=True)
+    lib = _lib.load()
+    ap, wp, sa, sw = gemm_inputs(M, N, K, 5 * M + N + K)
+    if not grouped:
+        sw = sw[:, 0].copy()
+    exp16 = oracle.w4a4_gemm(ap, wp, sa, sw)
+    exp32 = oracle.w4a4_gemm(ap, wp, sa, sw, out_fp32=True)
+    a, w, s_a, s_w = to_dev(ap, wp, sa, sw)
+    w6 = weights_to_f6(w)
+    if N % 16 == 0:
+        assert torch.equal(weights_to_f6(tile_weights(w), True), w6), "tiled source"
+    a_part = (M + 127) // 128 * (K // 128) * 12288
+    ws = torch.full((lib.nv4_w4a4_gemm_f6_workspace(M, N, K),), 7, dtype=torch.uint8, device=DEV)
+    P = lambda t: ctypes.c_void_p(t.data_ptr())
+    st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    sg = 1 if grouped else 0
+    out = torch.empty((M, N), dtype=torch.bfloat16, device=DEV)
+    _lib.check(lib.nv4_w4a4_gemm_f6(P(a), P(w), 0, P(s_a), P(s_w), sg, P(out), 0, M, N, K, P(ws), ws.numel(), st),
+               "fp6 gemm, per-call conversion")
+    torch.cuda.synchronize()
+    assert torch.equal(ws[a_part:], w6), "W half of the per-call conversion"
+    keep = w6.clone()
+    ws_a = torch.empty(a_part, dtype=torch.uint8, device=DEV)
+    for fp32 in (0, 1):
+        o = torch.full((M, N), float("nan"), dtype=torch.float32 if fp32 else torch.bfloat16, device=DEV)
+        _lib.check(lib.nv4_w4a4_gemm_f6(P(a), P(w6), 2, P(s_a), P(s_w), sg, P(o), fp32, M, N, K, P(ws_a), a_part,
+                                        st), "fp6 gemm, prepared weights")
+        torch.cuda.synchronize()
+        if fp32:
+            assert_bits_equal(o.cpu().numpy().view(np.uint32), exp32.view(np.uint32), "fp32 output")
+        else:
+            assert_bits_equal(bf16_bits(o), exp16, "bf16 output")
+    o = w4a4_grouped_gemm(a, w, s_a, s_w, path="fp6", weights_f6=w6)
+    torch.cuda.synchronize()
+    assert_bits_equal(bf16_bits(o), exp16, "w4a4_grouped_gemm(weights_f6=...)")
+    assert torch.equal(w6, keep), "prepared weights unchanged"
+    with pytest.raises(ValueError):
+        w4a4_grouped_gemm(a, w, s_a, s_w, path="fp6", weights_f6=w6[:-16])
