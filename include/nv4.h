@@ -38,6 +38,8 @@
  *                          :128-148; the reference splits K 8 ways with bf16 atomics,
  *                          the _ws form splits K into 1024-deep fp32 partials, and
  *                          prefill-sized M dequantizes once for a library GEMM)
+ *   nv4_prefill_attention <- flash_attn_varlen_func in the prefill branch of
+ *                          nanovllm/layers/attention.py:64-70 (causal, no prefix cache)
  *   nv4_paged_decode_attention <- flash_attn_with_kvcache in the decode branch of
  *                          nanovllm/layers/attention.py:72-74 (caller of the hot path)
  *   nv4_rmsnorm         <- RMSNorm.rms_forward / add_rms_forward,
@@ -254,6 +256,25 @@ int nv4_w4a16_gemm_ws(const void* x, int x_dtype, const int32_t* qweight, const 
  */
 int nv4_w4a16_dequant(const int32_t* qweight, const int32_t* qzeros, const void* scales, void* w, int w_dtype,
                       int64_t N, int64_t K, int group, void* stream);
+
+/*
+ * Prefill attention: causal GQA attention over packed sequences.
+ * Replaces flash_attn_varlen_func(q, k, v, cu_seqlens_q=cu_seqlens_k=cu_seqlens,
+ * softmax_scale, causal=True) in nanovllm/layers/attention.py:64-70 (without a
+ * prefix cache: queries and keys are the same rows).
+ *   q            bf16 [T, Hq, 128]: rows q_row elements apart (>= Hq*128)
+ *   k, v         bf16 [T, Hkv, 128]: rows k_row / v_row elements apart (>= Hkv*128)
+ *   out          bf16 [T, Hq, 128]: rows o_row elements apart (>= Hq*128)
+ *   cu_seqlens   int32 [B+1]: sequence b is rows cu_seqlens[b] .. cu_seqlens[b+1]-1,
+ *                each at most max_seqlen long (longer ones are not fully written)
+ * o[i] = softmax_{j <= i}(scale * q[i].k[j]) v[j] per sequence and query head;
+ * KV head of query head h: h / (Hq/Hkv), Hq/Hkv in {1, 2, 4, 8}; fp32
+ * arithmetic, P rounded to bf16 for the P.V product.  Row strides multiples
+ * of 8 elements, tensors 16-byte aligned; scale > 0; B <= 65535.
+ */
+int nv4_prefill_attention(const void* q, int64_t q_row, const void* k, int64_t k_row, const void* v, int64_t v_row,
+                          void* out, int64_t o_row, const int32_t* cu_seqlens, int64_t B, int64_t max_seqlen,
+                          int64_t Hq, int64_t Hkv, int64_t D, float scale, void* stream);
 
 /*
  * Paged decode attention (one new token per sequence; GQA).

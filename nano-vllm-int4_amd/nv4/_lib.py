@@ -40,6 +40,7 @@ SIGNATURES = {
     "nv4_w4a4_gemm_f6_workspace": ([_I64, _I64, _I64], _I64),
     "nv4_w4a4_weights_to_f6": ([_P, _I, _P, _I64, _I64, _I64, _P], _I),
     "nv4_w4a4_weights_f6_bytes": ([_I64, _I64], _I64),
+    "nv4_prefill_attention": ([_P, _I64, _P, _I64, _P, _I64, _P, _I64, _P, _I64, _I64, _I64, _I64, _I64, ctypes.c_float, _P], _I),
     "nv4_w4a4_linear_tiled": ([_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _P], _I),
     "nv4_w4a4_tile_weights": ([_P, _P, _I64, _I64, _P], _I),
     "nv4_w4a4_untile_weights": ([_P, _P, _I64, _I64, _P], _I),

@@ -10,9 +10,10 @@ of which this build uses:
   producer of the rotated keys (``nv4.kernels.decoder_ops.qk_norm_rope_store``,
   called by Qwen3Attention before this module), so ``Attention.forward``
   receives caches that already hold the step's tokens.
-* Prefill (causal, GQA): ``scaled_dot_product_attention`` restricted to its
-  fused flash kernel, one call per sequence of the batch (it raises rather
-  than fall back to the unfused path).
+* Prefill (causal, GQA): ``prefill_attention``, the HIP kernel
+  ``nv4_prefill_attention`` (flash-style online softmax on the matrix cores,
+  all packed sequences in one launch; replaces flash_attn_varlen_func,
+  :64-70).
 * Decode: ``paged_decode_attention``, the HIP kernel ``nv4_paged_decode_attention``
   (split over the context, one workgroup per (sequence, KV head, split);
   online softmax in fp32; a second pass merges the splits).
@@ -22,7 +23,6 @@ from __future__ import annotations
 import ctypes
 
 import torch
-import torch.nn.functional as F
 from torch import nn
 
 from . import _lib
@@ -72,18 +72,34 @@ def paged_decode_attention(q, k_cache, v_cache, block_tables, context_lens, scal
 
 def prefill_attention(q, k, v, seqlens, scale):
     """Causal GQA attention over packed sequences of lengths ``seqlens``
-    (q [T, Hq, D], k/v [T, Hkv, D]) with the fused flash kernel only."""
-    from torch.nn.attention import SDPBackend, sdpa_kernel
-    out = torch.empty_like(q)
-    start = 0
-    with sdpa_kernel([SDPBackend.FLASH_ATTENTION]):
-        for n in seqlens:
-            qs = q[start:start + n].transpose(0, 1).unsqueeze(0)
-            ks = k[start:start + n].transpose(0, 1).unsqueeze(0)
-            vs = v[start:start + n].transpose(0, 1).unsqueeze(0)
-            o = F.scaled_dot_product_attention(qs, ks, vs, is_causal=True, scale=scale, enable_gqa=True)
-            out[start:start + n] = o.squeeze(0).transpose(0, 1)
-            start += n
+    (q [T, Hq, 128], k/v [T, Hkv, 128] bf16, rows of each tensor contiguous
+    in its last two dims) -> bf16 [T, Hq, 128], in one launch of
+    ``nv4_prefill_attention``."""
+    if q.ndim != 3 or k.ndim != 3 or v.ndim != 3 or q.shape[2] != 128 or k.shape != v.shape:
+        raise ValueError("Expected q [T, Hq, 128] and k, v [T, Hkv, 128]")
+    if q.dtype != torch.bfloat16 or k.dtype != torch.bfloat16 or v.dtype != torch.bfloat16:
+        raise TypeError("q, k and v must be bf16")
+    T, Hq, D = q.shape
+    Hkv = k.shape[1]
+    lens = [int(n) for n in seqlens]
+    if k.shape[0] != T or sum(lens) != T or any(n < 1 for n in lens):
+        raise ValueError("seqlens must be positive and sum to the number of rows")
+    for t in (q, k, v):
+        if not t.is_cuda or t.device != q.device or t.stride(2) != 1 or t.stride(1) != D:
+            raise ValueError("q, k and v must be CUDA tensors on one device with contiguous heads")
+    cu = torch.zeros(len(lens) + 1, dtype=torch.int32)
+    cu[1:] = torch.tensor(lens, dtype=torch.int32).cumsum(0)
+    cu = cu.to(q.device)
+    out = torch.empty_like(q, memory_format=torch.contiguous_format)
+    lib = _lib.load()
+    stream = torch.cuda.current_stream(q.device).cuda_stream
+    with torch.cuda.device(q.device):
+        rc = lib.nv4_prefill_attention(
+            ctypes.c_void_p(q.data_ptr()), q.stride(0), ctypes.c_void_p(k.data_ptr()), k.stride(0),
+            ctypes.c_void_p(v.data_ptr()), v.stride(0), ctypes.c_void_p(out.data_ptr()), out.stride(0),
+            ctypes.c_void_p(cu.data_ptr()), len(lens), max(lens), Hq, Hkv, D, ctypes.c_float(scale),
+            ctypes.c_void_p(stream))
+    _lib.check(rc, "prefill_attention")
     return out
 
 

@@ -145,6 +145,30 @@ def test_w4a4_weights_to_f6_rejections():
     assert call(w6=P(A16 + 4)) == _lib.NV4_E_ALIGN
 
 
+def test_prefill_attention_rejections():
+    f = _lib.load().nv4_prefill_attention
+    Hq, Hkv, D = 32, 8, 128
+
+    def call(q=P(A16), qr=Hq * D, k=P(A16), kr=Hkv * D, v=P(A16), vr=Hkv * D, o=P(A16), orow=Hq * D, cu=P(A16),
+             B=2, maxlen=100, hq=Hq, hkv=Hkv, d=D, scale=0.088):
+        return f(q, qr, k, kr, v, vr, o, orow, cu, B, maxlen, hq, hkv, d, ctypes.c_float(scale), None)
+
+    assert call(q=None) == _lib.NV4_E_NULL
+    assert call(cu=None) == _lib.NV4_E_NULL
+    assert call(d=64) == _lib.NV4_E_SHAPE                                # head dim 128 only
+    assert call(hq=12, hkv=8) == _lib.NV4_E_SHAPE                        # Hq % Hkv
+    assert call(hq=48, hkv=3) == _lib.NV4_E_SHAPE                        # group of 16
+    assert call(B=0) == _lib.NV4_E_SHAPE
+    assert call(maxlen=0) == _lib.NV4_E_SHAPE
+    assert call(qr=Hq * D - 8) == _lib.NV4_E_SHAPE                       # row shorter than the heads
+    assert call(scale=0.0) == _lib.NV4_E_SHAPE
+    assert call(scale=-1.0) == _lib.NV4_E_SHAPE
+    assert call(scale=float("nan")) == _lib.NV4_E_SHAPE
+    assert call(kr=Hkv * D + 4) == _lib.NV4_E_ALIGN                     # row stride % 8
+    assert call(v=P(A16 + 8)) == _lib.NV4_E_ALIGN
+    assert call(cu=P(A16 + 2)) == _lib.NV4_E_ALIGN
+
+
 def test_w4a16_and_linear_rejections():
     f = _lib.load().nv4_w4a16_gemm
     ok = [P(A16)] * 4

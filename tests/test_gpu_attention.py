@@ -9,10 +9,14 @@ groups 1/2/4, block sizes 256, 16 (one block-table read per 16 tokens) and
 chunked loop), every compile-time split count of the merge (bit-equal to the
 chunked form), and queries read as a strided view of a fused qkv tensor;
 against softmax(scale q.K^T) V computed in fp32.  Bar:
-|out - ref| <= 1e-2 + 1e-2 |ref| (bf16 output).  Prefill attention (causal
-GQA through the fused flash SDPA kernel) against the same fp32 reference on
-packed sequences up to the 4096-token prompt of the end-to-end workload,
-same bar.  Rows with an empty context give zeros.
+|out - ref| <= 1e-2 + 1e-2 |ref| (bf16 output).  Rows with an empty context
+give zeros.  Prefill attention (``nv4_prefill_attention``, the replacement of
+flash_attn_varlen_func in nanovllm/layers/attention.py:64-70: causal GQA over
+packed sequences in one launch) against the same fp32 reference and bar:
+lengths around its 32-row query tiles, 64-row workgroups and 64-key blocks
+up to the 4096-token prompt of the end-to-end workload, query-to-KV head
+ratios 1/2/4/8, q/k/v as strided slices of a fused tensor, and large score
+peaks that move the running max.
 """
 import math
 
@@ -149,23 +153,69 @@ def test_empty_context_rows_are_zero(max_ctx):
     check(out[live], reference(q[live], kc, vc, bt[live], cl[live], 0.1), f"live rows max_ctx={max_ctx}")
 
 
-@pytest.mark.parametrize("lens", [[1, 17, 300], [4096, 33]])
-def test_prefill_attention_flash(lens):
-    g = torch.Generator(device=DEV).manual_seed(3)
+def prefill_reference(q, k, v, lens, scale):
+    """fp32 causal GQA attention of each packed sequence."""
+    G = q.shape[1] // k.shape[1]
+    outs, start = [], 0
+    for n in lens:
+        qf = q[start:start + n].float().transpose(0, 1).contiguous()
+        kf = k[start:start + n].float().repeat_interleave(G, dim=1).transpose(0, 1).contiguous()
+        vf = v[start:start + n].float().repeat_interleave(G, dim=1).transpose(0, 1).contiguous()
+        s = torch.matmul(qf, kf.transpose(1, 2).contiguous()) * scale
+        s = s + torch.triu(torch.full((n, n), float("-inf"), device=DEV), 1)
+        outs.append(torch.matmul(torch.softmax(s, dim=-1), vf).transpose(0, 1))
+        start += n
+    return torch.cat(outs, 0)
+
+
+@pytest.mark.parametrize("lens", [[1, 17, 300], [4096, 33], [64, 65, 127, 128, 129], [31, 32, 33, 63, 257, 1000]])
+def test_prefill_attention(lens):
+    """nv4_prefill_attention (one launch for all packed sequences) against fp32;
+    lengths around the 32-row query tiles, 64-row workgroups and 64-key blocks."""
+    print(f"[prefill-attn] lens={lens}", flush=True)
+    g = torch.Generator(device=DEV).manual_seed(3 + len(lens))
     T = sum(lens)
     q = torch.randn(T, 32, 128, generator=g, device=DEV).to(torch.bfloat16)
     k = torch.randn(T, 8, 128, generator=g, device=DEV).to(torch.bfloat16)
     v = torch.randn(T, 8, 128, generator=g, device=DEV).to(torch.bfloat16)
     scale = 1 / math.sqrt(128)
-    out = prefill_attention(q, k, v, lens, scale)
+    out = torch.full_like(q, float("nan"))
+    out.copy_(prefill_attention(q, k, v, lens, scale))
     torch.cuda.synchronize()
+    ref = prefill_reference(q, k, v, lens, scale)
     start = 0
     for n in lens:
-        qf = q[start:start + n].float().transpose(0, 1).contiguous()
-        kf = k[start:start + n].float().repeat_interleave(4, dim=1).transpose(0, 1).contiguous()
-        vf = v[start:start + n].float().repeat_interleave(4, dim=1).transpose(0, 1).contiguous()
-        s = torch.matmul(qf, kf.transpose(1, 2).contiguous()) * scale
-        s = s + torch.triu(torch.full((n, n), float("-inf"), device=DEV), 1)
-        ref = torch.matmul(torch.softmax(s, dim=-1), vf).transpose(0, 1)
-        check(out[start:start + n], ref, f"prefill n={n}")
+        check(out[start:start + n], ref[start:start + n], f"prefill n={n}")
         start += n
+
+
+@pytest.mark.parametrize("G,Hkv", [(1, 8), (2, 4), (8, 2)])
+def test_prefill_attention_gqa_groups(G, Hkv):
+    """Other query-to-KV head ratios (the workgroup then covers 256/G rows)."""
+    lens = [5, 300, 129]
+    print(f"[prefill-attn-gqa] G={G} Hkv={Hkv} lens={lens}", flush=True)
+    g = torch.Generator(device=DEV).manual_seed(11 * G)
+    T = sum(lens)
+    q = torch.randn(T, G * Hkv, 128, generator=g, device=DEV).to(torch.bfloat16)
+    k = torch.randn(T, Hkv, 128, generator=g, device=DEV).to(torch.bfloat16)
+    v = torch.randn(T, Hkv, 128, generator=g, device=DEV).to(torch.bfloat16)
+    out = prefill_attention(q, k, v, lens, 0.125)
+    torch.cuda.synchronize()
+    check(out, prefill_reference(q, k, v, lens, 0.125), f"G={G}")
+
+
+def test_prefill_attention_strided_and_peaked():
+    """q, k, v as column slices of one fused [T, (32+8+8)*128] tensor (row
+    strides larger than the head block), and scores with large peaks (a
+    scale of 0.5: the running max moves often, the rescale runs)."""
+    lens = [700, 64]
+    print(f"[prefill-attn-strided] lens={lens}", flush=True)
+    g = torch.Generator(device=DEV).manual_seed(5)
+    T = sum(lens)
+    qkv = torch.randn(T, 48 * 128, generator=g, device=DEV).to(torch.bfloat16)
+    q = qkv[:, :4096].view(T, 32, 128)
+    k = qkv[:, 4096:5120].view(T, 8, 128)
+    v = qkv[:, 5120:].view(T, 8, 128)
+    out = prefill_attention(q, k, v, lens, 0.5)
+    torch.cuda.synchronize()
+    check(out, prefill_reference(q, k, v, lens, 0.5), "strided")
