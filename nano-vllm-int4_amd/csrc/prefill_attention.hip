@@ -5,10 +5,11 @@
 //   o[i] = softmax_j<=i(scale * q[i] . k[j]) v[j]
 // with GQA (query head h reads KV head h / G), head_dim 128, bf16 in and out.
 //
-// Layout: one workgroup of 8 waves per (sequence, KV head, block of QW =
-// 256/G query rows); wave w takes query head w % G of the group and the 32
-// query rows 32 (w / G) .. of the block, so the G heads of a KV head share
-// every staged key and value.  Keys run in blocks of 64 up to the block's
+// Layout: one workgroup of NW = 8 waves (4 when that grid would leave CUs
+// idle: short prompts, G <= 4) per (sequence, KV head, block of QW = 32 NW/G
+// query rows); wave w takes query head w % G of the group and the 32 query
+// rows 32 (w / G) .. of the block, so the G heads of a KV head share every
+// staged key and value.  Keys run in blocks of 64 up to the block's
 // last query row; each block is staged in LDS once for the 8 waves (K as
 // rows, V transposed), with the next block's loads in flight during the
 // current one's arithmetic and one barrier per block.  Workgroups of the
@@ -32,7 +33,7 @@
 // LDS per stage: K[64][136] bf16 (a 272-byte row stride: the 16-byte reads
 // of 16 consecutive rows fall in distinct bank groups) and V^T[128][68] bf16
 // (136-byte rows: the 8-byte reads of 32 consecutive rows are conflict-free);
-// two stages, 68 KiB, one workgroup per CU.  All global loads are clamped
+// two stages, 68 KiB: one 8-wave or two 4-wave workgroups per CU.  All global loads are clamped
 // into the sequence and unconditional; rows past a sequence are never
 // stored.
 #include "nv4_common.h"
@@ -42,8 +43,6 @@ namespace {
 
 constexpr int FA_D = 128;                                   // head dim
 constexpr int FA_KB = 64;                                   // keys per block
-constexpr int FA_WAVES = 8;
-constexpr int FA_T = FA_WAVES * 64;
 constexpr int FA_KS = FA_D + 8;                             // K row stride (bf16)
 constexpr int FA_VS = FA_KB + 4;                            // V^T row stride (bf16)
 constexpr int FA_STAGE = FA_KB * FA_KS + FA_D * FA_VS;      // bf16 per stage
@@ -52,13 +51,16 @@ static_assert(2 * FA_STAGE * 2 == 69632, "68 KiB of LDS");
 typedef __bf16 v2bf __attribute__((ext_vector_type(2)));
 typedef float v2f __attribute__((ext_vector_type(2)));
 
-template <int G>
-__global__ void __launch_bounds__(FA_T, 1)
+template <int G, int NW>
+__global__ void __launch_bounds__(NW * 64, 8 / NW)
 fa_prefill(const uint16_t* __restrict__ q, int64_t q_row, const uint16_t* __restrict__ k, int64_t k_row,
            const uint16_t* __restrict__ v, int64_t v_row, uint16_t* __restrict__ out, int64_t o_row,
            const int32_t* __restrict__ cu, int Hkv, int nqb, float qscale) {
-    constexpr int QT = FA_WAVES / G;  // 32-row query tiles per workgroup
+    constexpr int T = NW * 64;
+    constexpr int QT = NW / G;        // 32-row query tiles per workgroup
     constexpr int QW = 32 * QT;       // query rows per workgroup
+    constexpr int KU = FA_KB * FA_D / 8 / T, VU = FA_KB / 2 * FA_D / 8 / T;  // staging units per thread
+    static_assert(QT >= 1 && KU * T * 8 == FA_KB * FA_D && VU * T * 16 == FA_KB * FA_D, "staging split");
     __shared__ __align__(16) uint16_t lds[2 * FA_STAGE];
 
     const int b = blockIdx.y;
@@ -84,32 +86,44 @@ fa_prefill(const uint16_t* __restrict__ q, int64_t q_row, const uint16_t* __rest
         for (int s = 0; s < 8; ++s) qv[s] = *reinterpret_cast<const v4u*>(qp + 16 * s);
     }
 
-    // Staging.  K: chunks c = t, t + 512 of the block (key c / 16, dims
-    // 8 (c % 16) ..).  V: keys 2 kp, 2 kp + 1 (kp = t % 32), dims 8 dc ..
-    // (dc = t / 32), written transposed as bf16 pairs.
-    const int kk0 = t >> 4, kd0 = (t & 15) * 8, kk1 = (t + FA_T) >> 4;
-    const int kp = t & 31, vdc = t >> 5;
+    // Staging.  K: chunks c = t + T i of the block (key c / 16, dims
+    // 8 (c % 16) ..).  V: units u = t + T i, keys 2 kp, 2 kp + 1 (kp =
+    // u % 32), dims 8 dc .. (dc = u / 32), written transposed as bf16 pairs.
     const uint16_t* kbase = k + (int64_t)start * k_row + (int64_t)kvh * FA_D;
-    const uint16_t* vbase = v + (int64_t)start * v_row + (int64_t)kvh * FA_D + 8 * vdc;
-    v4u kr[2], vr[2];
+    const uint16_t* vbase = v + (int64_t)start * v_row + (int64_t)kvh * FA_D;
+    v4u kr[KU], vr[VU][2];
     auto load = [&](int kb) {
         const int key0 = kb * FA_KB;
-        kr[0] = *reinterpret_cast<const v4u*>(kbase + (int64_t)min(key0 + kk0, L - 1) * k_row + kd0);
-        kr[1] = *reinterpret_cast<const v4u*>(kbase + (int64_t)min(key0 + kk1, L - 1) * k_row + kd0);
-        vr[0] = *reinterpret_cast<const v4u*>(vbase + (int64_t)min(key0 + 2 * kp, L - 1) * v_row);
-        vr[1] = *reinterpret_cast<const v4u*>(vbase + (int64_t)min(key0 + 2 * kp + 1, L - 1) * v_row);
+#pragma unroll
+        for (int i = 0; i < KU; ++i) {
+            const int c = t + T * i;
+            kr[i] = *reinterpret_cast<const v4u*>(kbase + (int64_t)min(key0 + (c >> 4), L - 1) * k_row + (c & 15) * 8);
+        }
+#pragma unroll
+        for (int i = 0; i < VU; ++i) {
+            const int u = t + T * i, kp = u & 31, dc = u >> 5;
+            vr[i][0] = *reinterpret_cast<const v4u*>(vbase + (int64_t)min(key0 + 2 * kp, L - 1) * v_row + 8 * dc);
+            vr[i][1] = *reinterpret_cast<const v4u*>(vbase + (int64_t)min(key0 + 2 * kp + 1, L - 1) * v_row + 8 * dc);
+        }
     };
     auto store = [&](int stage) {
         uint16_t* Ks = lds + stage * FA_STAGE;
         uint16_t* Vt = Ks + FA_KB * FA_KS;
-        *reinterpret_cast<v4u*>(Ks + kk0 * FA_KS + kd0) = kr[0];
-        *reinterpret_cast<v4u*>(Ks + kk1 * FA_KS + kd0) = kr[1];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const uint32_t lo = __builtin_amdgcn_perm(vr[1][j], vr[0][j], 0x05040100u);  // dim 2j
-            const uint32_t hi = __builtin_amdgcn_perm(vr[1][j], vr[0][j], 0x07060302u);  // dim 2j + 1
-            *reinterpret_cast<uint32_t*>(Vt + (8 * vdc + 2 * j) * FA_VS + 2 * kp) = lo;
-            *reinterpret_cast<uint32_t*>(Vt + (8 * vdc + 2 * j + 1) * FA_VS + 2 * kp) = hi;
+        for (int i = 0; i < KU; ++i) {
+            const int c = t + T * i;
+            *reinterpret_cast<v4u*>(Ks + (c >> 4) * FA_KS + (c & 15) * 8) = kr[i];
+        }
+#pragma unroll
+        for (int i = 0; i < VU; ++i) {
+            const int u = t + T * i, kp = u & 31, dc = u >> 5;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const uint32_t lo = __builtin_amdgcn_perm(vr[i][1][j], vr[i][0][j], 0x05040100u);  // dim 2j
+                const uint32_t hi = __builtin_amdgcn_perm(vr[i][1][j], vr[i][0][j], 0x07060302u);  // dim 2j + 1
+                *reinterpret_cast<uint32_t*>(Vt + (8 * dc + 2 * j) * FA_VS + 2 * kp) = lo;
+                *reinterpret_cast<uint32_t*>(Vt + (8 * dc + 2 * j + 1) * FA_VS + 2 * kp) = hi;
+            }
         }
     };
 
@@ -222,12 +236,23 @@ fa_prefill(const uint16_t* __restrict__ q, int64_t q_row, const uint16_t* __rest
     }
 }
 
+// Eight waves per workgroup (G heads x 8/G query tiles) when the grid fills
+// the CUs; otherwise four (short prompts: twice the workgroups).
 template <int G>
 hipError_t launch_fa(const uint16_t* q, int64_t q_row, const uint16_t* k, int64_t k_row, const uint16_t* v,
-                     int64_t v_row, uint16_t* out, int64_t o_row, const int32_t* cu, int B, int nqb, int Hkv,
-                     float qscale, hipStream_t st) {
-    hipLaunchKernelGGL(fa_prefill<G>, dim3((unsigned)(nqb * Hkv), (unsigned)B), dim3(FA_T), 0, st, q, q_row, k,
-                       k_row, v, v_row, out, o_row, cu, Hkv, nqb, qscale);
+                     int64_t v_row, uint16_t* out, int64_t o_row, const int32_t* cu, int B, int64_t max_seqlen,
+                     int Hkv, float qscale, hipStream_t st) {
+    constexpr int NW = G > 4 ? 8 : 4;
+    const int64_t nqb8 = (max_seqlen + 32 * (8 / G) - 1) / (32 * (8 / G));
+    if (G > 4 || nqb8 * Hkv * B >= device_cu_count()) {
+        const int nqb = (int)nqb8;
+        hipLaunchKernelGGL((fa_prefill<G, 8>), dim3((unsigned)(nqb * Hkv), (unsigned)B), dim3(512), 0, st, q, q_row,
+                           k, k_row, v, v_row, out, o_row, cu, Hkv, nqb, qscale);
+    } else {
+        const int nqb = (int)((max_seqlen + 32 * (NW / G) - 1) / (32 * (NW / G)));
+        hipLaunchKernelGGL((fa_prefill<G, NW>), dim3((unsigned)(nqb * Hkv), (unsigned)B), dim3(NW * 64), 0, st, q,
+                           q_row, k, k_row, v, v_row, out, o_row, cu, Hkv, nqb, qscale);
+    }
     return hipGetLastError();
 }
 
@@ -250,8 +275,7 @@ extern "C" int nv4_prefill_attention(const void* q, int64_t q_row, const void* k
         reinterpret_cast<uintptr_t>(v) % 16 || reinterpret_cast<uintptr_t>(out) % 16 ||
         reinterpret_cast<uintptr_t>(cu_seqlens) % 4)
         return NV4_E_ALIGN;
-    const int64_t qw = 32 * (FA_WAVES / G);
-    const int64_t nqb = (max_seqlen + qw - 1) / qw;
+    const int64_t nqb = (max_seqlen + 31) / 32;  // the most query blocks any form launches
     if (nqb * Hkv > 0x7fffffffLL) return NV4_E_SHAPE;
     const float qscale = scale * 1.44269504088896340736f;  // scores in base-2 units
     const auto* qp = static_cast<const uint16_t*>(q);
@@ -259,7 +283,8 @@ extern "C" int nv4_prefill_attention(const void* q, int64_t q_row, const void* k
     const auto* vp = static_cast<const uint16_t*>(v);
     auto* op = static_cast<uint16_t*>(out);
     hipStream_t st = static_cast<hipStream_t>(stream);
-    const int b = (int)B, n = (int)nqb, hk = (int)Hkv;
+    const int b = (int)B, hk = (int)Hkv;
+    const int64_t n = max_seqlen;
     hipError_t e;
     switch (G) {
         case 1: e = launch_fa<1>(qp, q_row, kp, k_row, vp, v_row, op, o_row, cu_seqlens, b, n, hk, qscale, st); break;
