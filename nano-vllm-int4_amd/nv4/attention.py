@@ -21,6 +21,7 @@ of which this build uses:
 from __future__ import annotations
 
 import ctypes
+import functools
 
 import torch
 from torch import nn
@@ -70,6 +71,15 @@ def paged_decode_attention(q, k_cache, v_cache, block_tables, context_lens, scal
     return out
 
 
+@functools.lru_cache(maxsize=64)
+def _cu_seqlens(lens, device):
+    """int32 [B+1] sequence starts on ``device``, made once per batch shape
+    (every layer of a prefill reuses it instead of copying it again)."""
+    cu = torch.zeros(len(lens) + 1, dtype=torch.int32)
+    cu[1:] = torch.tensor(lens, dtype=torch.int32).cumsum(0)
+    return cu.to(device)
+
+
 def prefill_attention(q, k, v, seqlens, scale):
     """Causal GQA attention over packed sequences of lengths ``seqlens``
     (q [T, Hq, 128], k/v [T, Hkv, 128] bf16, rows of each tensor contiguous
@@ -87,9 +97,7 @@ def prefill_attention(q, k, v, seqlens, scale):
     for t in (q, k, v):
         if not t.is_cuda or t.device != q.device or t.stride(2) != 1 or t.stride(1) != D:
             raise ValueError("q, k and v must be CUDA tensors on one device with contiguous heads")
-    cu = torch.zeros(len(lens) + 1, dtype=torch.int32)
-    cu[1:] = torch.tensor(lens, dtype=torch.int32).cumsum(0)
-    cu = cu.to(q.device)
+    cu = _cu_seqlens(tuple(lens), q.device)
     out = torch.empty_like(q, memory_format=torch.contiguous_format)
     lib = _lib.load()
     stream = torch.cuda.current_stream(q.device).cuda_stream
