@@ -346,7 +346,8 @@ int nv4_rmsnorm(const void* x, const void* residual_in, void* residual_out, cons
  *                token t's rotated key and its value go to slot slot_mapping[t];
  *                slots outside [0, num_slots) (the reference's -1) are not stored
  *   k_out/v_out  optional bf16 [T, Hkv, 128] copies of the rotated keys / values
- * Positions outside [0, max_position) read row 0 of the table.
+ * Positions outside [0, max_position) read row 0 of the table.  qkv_row_stride
+ * a multiple of 4; bf16 tensors 8-byte and cos_sin 16-byte aligned.
  */
 int nv4_qk_norm_rope_store(const void* qkv, int64_t qkv_row_stride, int64_t T, int64_t Hq, int64_t Hkv,
                            const void* q_norm_w, const void* k_norm_w, const float* cos_sin, int64_t max_position,

@@ -15,9 +15,9 @@
 //    and the sum rounded separately) on the bf16 normalised values; queries go
 //    to q_out, keys and values to their cache slot (and, when given, to
 //    k_out / v_out).  Slots outside [0, num_slots) -- the reference's -1 --
-//    are not stored; positions outside the cos/sin table read its row 0.  One
-//    wave per (token, head): lane l owns dims l and l+64, the two halves the
-//    rotation pairs.
+//    are not stored; positions outside the cos/sin table read its row 0.
+//    Sixteen lanes per (token, head): lane j owns dims 4j .. 4j+3 and their
+//    rotation partners 64 + 4j .. 64 + 4j+3, in 8-byte accesses.
 //  * nv4_silu_mul (nanovllm/layers/activation.py:8-11): bf16(bf16(silu(g)) * u)
 //    with silu(g) = g / (1 + exp(-g)) in fp32.
 #include "norm_ops.h"
@@ -67,7 +67,10 @@ rmsnorm_rows(const uint16_t* x, const uint16_t* resid_in, uint16_t* resid_out,
     }
 }
 
-// One wave per (token, head) of the fused qkv row [T, (Hq + 2 Hkv) * 128].
+// Sixteen lanes per (token, head) of the fused qkv row [T, (Hq + 2 Hkv) * 128]
+// (four per wave): lane j of an item holds dims 4j .. 4j + 3 and their rotary
+// partners 64 + 4j .. 64 + 4j + 3, so every access is 8 bytes (16 for the
+// cos/sin table) and the head's sum of squares is a 16-lane reduction.
 __global__ void __launch_bounds__(256)
 qk_norm_rope_store(const uint16_t* __restrict__ qkv, int64_t qkv_row, int T, int Hq, int Hkv,
                    const uint16_t* __restrict__ qw, const uint16_t* __restrict__ kw,
@@ -76,61 +79,87 @@ qk_norm_rope_store(const uint16_t* __restrict__ qkv, int64_t qkv_row, int T, int
                    uint16_t* __restrict__ q_out, uint16_t* __restrict__ k_cache, uint16_t* __restrict__ v_cache,
                    uint16_t* __restrict__ k_out, uint16_t* __restrict__ v_out, float eps) {
     const int heads = Hq + 2 * Hkv;
-    const int64_t item = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (item >= (int64_t)T * heads) return;  // whole waves
+    const int64_t item = (int64_t)blockIdx.x * 16 + (threadIdx.x >> 4);
+    if (item >= (int64_t)T * heads) return;  // whole 16-lane groups
     const int64_t tok = item / heads;
     const int h = (int)(item % heads);
-    const int l = threadIdx.x & 63;
+    const int j4 = (threadIdx.x & 15) * 4;
     const uint16_t* src = qkv + tok * qkv_row + (int64_t)h * 128;
-    // Every load that depends on no other load is written first.  The
-    // compiler still moves the position and norm-weight loads into the
-    // query/key path, so the wave waits on memory three times (the head
-    // values and slot, the position with the norm weights, then the cos/sin
-    // row of the position) instead of once per operand.
+    // Every load that depends on no other load is written first; the cos/sin
+    // row needs the position.
     const bool is_q = h < Hq;
     const uint16_t* wt = is_q ? qw : kw;
     int64_t pos = positions[tok];
     const int64_t slot = slots[tok];
-    const uint16_t xb1 = src[l], xb2 = src[l + 64];
-    const uint16_t wb1 = wt[l], wb2 = wt[l + 64];
+    const uint2 xa = *reinterpret_cast<const uint2*>(src + j4), xb = *reinterpret_cast<const uint2*>(src + 64 + j4);
+    const uint2 wa = *reinterpret_cast<const uint2*>(wt + j4), wb = *reinterpret_cast<const uint2*>(wt + 64 + j4);
     if (pos < 0 || pos >= max_position) pos = 0;  // out-of-table positions: never read outside the table
     const float* cs = cos_sin + pos * 128;
-    const float c = cs[l], s = cs[64 + l];
-    float x1 = bf16_to_f32(xb1), x2 = bf16_to_f32(xb2);
+    const v4f c = *reinterpret_cast<const v4f*>(cs + j4), s = *reinterpret_cast<const v4f*>(cs + 64 + j4);
     if (h >= Hq + Hkv) {  // value head: copy to its slot (and v_out)
         const int kvh = h - Hq - Hkv;
         if (slot >= 0 && slot < num_slots) {
             uint16_t* dst = v_cache + (slot * Hkv + kvh) * 128;
-            dst[l] = xb1;
-            dst[l + 64] = xb2;
+            *reinterpret_cast<uint2*>(dst + j4) = xa;
+            *reinterpret_cast<uint2*>(dst + 64 + j4) = xb;
         }
         if (v_out) {
-            v_out[(tok * Hkv + kvh) * 128 + l] = xb1;
-            v_out[(tok * Hkv + kvh) * 128 + l + 64] = xb2;
+            uint16_t* dst = v_out + (tok * Hkv + kvh) * 128;
+            *reinterpret_cast<uint2*>(dst + j4) = xa;
+            *reinterpret_cast<uint2*>(dst + 64 + j4) = xb;
         }
         return;
     }
-    const float var = wave_sum(x1 * x1 + x2 * x2) / 128.0f;
-    const float r = rsqrtf(var + eps);
-    x1 = round_bf16(round_bf16(x1 * r) * bf16_to_f32(wb1));
-    x2 = round_bf16(round_bf16(x2 * r) * bf16_to_f32(wb2));
-    const float a = x1 * c, b = x2 * s, d = x2 * c, e = x1 * s;
-    const uint16_t y1 = (uint16_t)f32_to_bf16_rne(a - b);
-    const uint16_t y2 = (uint16_t)f32_to_bf16_rne(d + e);
+    float x1[4], x2[4], w1[4], w2[4];
+    const uint32_t xs[4] = {xa.x, xa.y, xb.x, xb.y}, ws[4] = {wa.x, wa.y, wb.x, wb.y};
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        x1[2 * i] = bf16_to_f32(xs[i] & 0xffffu);
+        x1[2 * i + 1] = bf16_to_f32(xs[i] >> 16);
+        x2[2 * i] = bf16_to_f32(xs[2 + i] & 0xffffu);
+        x2[2 * i + 1] = bf16_to_f32(xs[2 + i] >> 16);
+        w1[2 * i] = bf16_to_f32(ws[i] & 0xffffu);
+        w1[2 * i + 1] = bf16_to_f32(ws[i] >> 16);
+        w2[2 * i] = bf16_to_f32(ws[2 + i] & 0xffffu);
+        w2[2 * i + 1] = bf16_to_f32(ws[2 + i] >> 16);
+    }
+    float ss = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) ss += x1[i] * x1[i] + x2[i] * x2[i];
+#pragma unroll
+    for (int off = 8; off >= 1; off >>= 1) ss += __shfl_xor(ss, off);
+    const float r = rsqrtf(ss / 128.0f + eps);
+    uint32_t y1p[2], y2p[2];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const float a1 = round_bf16(round_bf16(x1[i] * r) * w1[i]);
+        const float a2 = round_bf16(round_bf16(x2[i] * r) * w2[i]);
+        const uint32_t y1 = f32_to_bf16_rne(a1 * c[i] - a2 * s[i]);
+        const uint32_t y2 = f32_to_bf16_rne(a2 * c[i] + a1 * s[i]);
+        if (i & 1) {
+            y1p[i >> 1] |= y1 << 16;
+            y2p[i >> 1] |= y2 << 16;
+        } else {
+            y1p[i >> 1] = y1;
+            y2p[i >> 1] = y2;
+        }
+    }
+    const uint2 o1 = make_uint2(y1p[0], y1p[1]), o2 = make_uint2(y2p[0], y2p[1]);
     if (is_q) {
         uint16_t* dst = q_out + (tok * Hq + h) * 128;
-        dst[l] = y1;
-        dst[l + 64] = y2;
+        *reinterpret_cast<uint2*>(dst + j4) = o1;
+        *reinterpret_cast<uint2*>(dst + 64 + j4) = o2;
     } else {
         const int kvh = h - Hq;
         if (slot >= 0 && slot < num_slots) {
             uint16_t* dst = k_cache + (slot * Hkv + kvh) * 128;
-            dst[l] = y1;
-            dst[l + 64] = y2;
+            *reinterpret_cast<uint2*>(dst + j4) = o1;
+            *reinterpret_cast<uint2*>(dst + 64 + j4) = o2;
         }
         if (k_out) {
-            k_out[(tok * Hkv + kvh) * 128 + l] = y1;
-            k_out[(tok * Hkv + kvh) * 128 + l + 64] = y2;
+            uint16_t* dst = k_out + (tok * Hkv + kvh) * 128;
+            *reinterpret_cast<uint2*>(dst + j4) = o1;
+            *reinterpret_cast<uint2*>(dst + 64 + j4) = o2;
         }
     }
 }
@@ -193,10 +222,16 @@ extern "C" int nv4_qk_norm_rope_store(const void* qkv, int64_t qkv_row_stride, i
     if (!qkv || !q_norm_w || !k_norm_w || !cos_sin || !positions || !slot_mapping || !q_out || !k_cache || !v_cache)
         return NV4_E_NULL;
     if (T < 1 || Hq < 1 || Hkv < 1 || max_position < 1 || num_slots < 0 ||
-        qkv_row_stride < (Hq + 2 * Hkv) * 128 || T * (Hq + 2 * Hkv) > 0x7fffffffLL * 4)
+        qkv_row_stride < (Hq + 2 * Hkv) * 128 || T * (Hq + 2 * Hkv) > 0x7fffffffLL * 16)
         return NV4_E_SHAPE;
+    // 8-byte accesses to bf16 data, 16-byte reads of the cos/sin table.
+    auto a8 = [](const void* p) { return reinterpret_cast<uintptr_t>(p) % 8 == 0; };
+    if (qkv_row_stride % 4 || !a8(qkv) || !a8(q_norm_w) || !a8(k_norm_w) || !a8(q_out) || !a8(k_cache) ||
+        !a8(v_cache) || (k_out && !a8(k_out)) || (v_out && !a8(v_out)) ||
+        reinterpret_cast<uintptr_t>(cos_sin) % 16)
+        return NV4_E_ALIGN;
     const int64_t items = T * (Hq + 2 * Hkv);
-    hipLaunchKernelGGL(qk_norm_rope_store, dim3((unsigned)((items + 3) / 4)), dim3(256), 0,
+    hipLaunchKernelGGL(qk_norm_rope_store, dim3((unsigned)((items + 15) / 16)), dim3(256), 0,
                        static_cast<hipStream_t>(stream), static_cast<const uint16_t*>(qkv), qkv_row_stride, (int)T,
                        (int)Hq, (int)Hkv, static_cast<const uint16_t*>(q_norm_w),
                        static_cast<const uint16_t*>(k_norm_w), cos_sin, positions, max_position, slot_mapping,

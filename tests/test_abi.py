@@ -239,6 +239,8 @@ def test_decoder_ops_rejections():
     assert call(row=6000) == _lib.NV4_E_SHAPE
     assert call(T=0) == _lib.NV4_E_SHAPE
     assert call(max_pos=0) == _lib.NV4_E_SHAPE
+    assert call(row=6146) == _lib.NV4_E_ALIGN                            # 8-byte row accesses
+    assert call(qkv=P(A16 + 4)) == _lib.NV4_E_ALIGN
     silu = lib.nv4_silu_mul
     assert silu(None, P(A16), 4, 12288, None) == _lib.NV4_E_NULL
     assert silu(P(A16), P(A16), 4, 12, None) == _lib.NV4_E_SHAPE
