@@ -79,7 +79,7 @@ qk_norm_rope_store(const uint16_t* __restrict__ qkv, int64_t qkv_row, int T, int
                    uint16_t* __restrict__ q_out, uint16_t* __restrict__ k_cache, uint16_t* __restrict__ v_cache,
                    uint16_t* __restrict__ k_out, uint16_t* __restrict__ v_out, float eps) {
     const int heads = Hq + 2 * Hkv;
-    const int64_t item = (int64_t)blockIdx.x * 16 + (threadIdx.x >> 4);
+    const int64_t item = (int64_t)blockIdx.x * (blockDim.x >> 4) + (threadIdx.x >> 4);
     if (item >= (int64_t)T * heads) return;  // whole 16-lane groups
     const int64_t tok = item / heads;
     const int h = (int)(item % heads);
@@ -231,7 +231,10 @@ extern "C" int nv4_qk_norm_rope_store(const void* qkv, int64_t qkv_row_stride, i
         reinterpret_cast<uintptr_t>(cos_sin) % 16)
         return NV4_E_ALIGN;
     const int64_t items = T * (Hq + 2 * Hkv);
-    hipLaunchKernelGGL(qk_norm_rope_store, dim3((unsigned)((items + 15) / 16)), dim3(256), 0,
+    // Decode-sized calls: one wave (4 items) per workgroup, to spread over the
+    // CUs; otherwise 256 threads (16 items).
+    const int per = T <= 256 ? 4 : 16;
+    hipLaunchKernelGGL(qk_norm_rope_store, dim3((unsigned)((items + per - 1) / per)), dim3(per * 16), 0,
                        static_cast<hipStream_t>(stream), static_cast<const uint16_t*>(qkv), qkv_row_stride, (int)T,
                        (int)Hq, (int)Hkv, static_cast<const uint16_t*>(q_norm_w),
                        static_cast<const uint16_t*>(k_norm_w), cos_sin, positions, max_position, slot_mapping,
