@@ -9,11 +9,12 @@
 // idle: short prompts, G <= 4) per (sequence, KV head, block of QW = 32 NW/G
 // query rows); wave w takes query head w % G of the group and the 32 query
 // rows 32 (w / G) .. of the block, so the G heads of a KV head share every
-// staged key and value.  Keys run in blocks of 64 up to the block's
-// last query row; each block is staged in LDS once for the 8 waves (K as
-// rows, V transposed), with the next block's loads in flight during the
-// current one's arithmetic and one barrier per block.  Workgroups of the
-// longest causal extent are dispatched first.
+// staged key and value.  Keys run in blocks of KB (128 in the 8-wave form,
+// 64 in the 4-wave form) up to the block's last query row; each block is
+// staged in LDS once for the workgroup (K as rows, V transposed), with the
+// next block's loads in flight during the current one's arithmetic and one
+// barrier per block.  Workgroups of the longest causal extent are dispatched
+// first.
 //
 // Matrix cores (v_mfma_f32_32x32x16_bf16; operand lane l supplies row /
 // column l%32 and the 8 k-slots 8(l/32) .. +7, result lane l holds
@@ -30,33 +31,36 @@
 //    output accumulator of a lane belongs to its own query, so the softmax
 //    rescale is a per-lane factor (skipped when no running max moved).
 //
-// LDS per stage: K[64][136] bf16 (a 272-byte row stride: the 16-byte reads
-// of 16 consecutive rows fall in distinct bank groups) and V^T[128][68] bf16
-// (136-byte rows: the 8-byte reads of 32 consecutive rows are conflict-free);
-// two stages, 68 KiB: one 8-wave or two 4-wave workgroups per CU.  All global loads are clamped
-// into the sequence and unconditional; rows past a sequence are never
-// stored.
+// LDS per stage: K[KB][136] bf16 (a 272-byte row stride: the 16-byte reads
+// of 16 consecutive rows fall in distinct bank groups) and V^T[128][KB + 4]
+// bf16 (rows of 136 or 264 bytes, 8 times an odd number: the 8-byte reads of
+// 32 consecutive rows are conflict-free); two stages: 134 KiB for one
+// 8-wave workgroup per CU, 68 KiB for two 4-wave ones.  All global loads are
+// clamped into the sequence and unconditional; rows past a sequence are
+// never stored.
 #include "nv4_common.h"
 
 namespace nv4 {
 namespace {
 
 constexpr int FA_D = 128;                                   // head dim
-constexpr int FA_KB = 64;                                   // keys per block
 constexpr int FA_KS = FA_D + 8;                             // K row stride (bf16)
-constexpr int FA_VS = FA_KB + 4;                            // V^T row stride (bf16)
-constexpr int FA_STAGE = FA_KB * FA_KS + FA_D * FA_VS;      // bf16 per stage
-static_assert(2 * FA_STAGE * 2 == 69632, "68 KiB of LDS");
+// V^T row stride and bf16 per stage for KB-key blocks.
+constexpr int fa_vs(int KB) { return KB + 4; }
+constexpr int fa_stage(int KB) { return KB * FA_KS + FA_D * fa_vs(KB); }
+static_assert(2 * fa_stage(64) * 2 == 69632 && 2 * fa_stage(128) * 2 == 137216, "68 / 134 KiB of LDS");
 
 typedef __bf16 v2bf __attribute__((ext_vector_type(2)));
 typedef float v2f __attribute__((ext_vector_type(2)));
 
-template <int G, int NW>
-__global__ void __launch_bounds__(NW * 64, 8 / NW)
+template <int G, int NW, int FA_KB>
+__global__ void __launch_bounds__(NW * 64, FA_KB == 64 ? 8 / NW : 1)
 fa_prefill(const uint16_t* __restrict__ q, int64_t q_row, const uint16_t* __restrict__ k, int64_t k_row,
            const uint16_t* __restrict__ v, int64_t v_row, uint16_t* __restrict__ out, int64_t o_row,
            const int32_t* __restrict__ cu, int Hkv, int nqb, float qscale) {
     constexpr int T = NW * 64;
+    constexpr int FA_VS = fa_vs(FA_KB), FA_STAGE = fa_stage(FA_KB);
+    constexpr int NC = FA_KB / 32;    // 32-key tiles per block
     constexpr int QT = NW / G;        // 32-row query tiles per workgroup
     constexpr int QW = 32 * QT;       // query rows per workgroup
     constexpr int KU = FA_KB * FA_D / 8 / T, VU = FA_KB / 2 * FA_D / 8 / T;  // staging units per thread
@@ -88,7 +92,8 @@ fa_prefill(const uint16_t* __restrict__ q, int64_t q_row, const uint16_t* __rest
 
     // Staging.  K: chunks c = t + T i of the block (key c / 16, dims
     // 8 (c % 16) ..).  V: units u = t + T i, keys 2 kp, 2 kp + 1 (kp =
-    // u % 32), dims 8 dc .. (dc = u / 32), written transposed as bf16 pairs.
+    // u % (KB/2)), dims 8 dc .. (dc = u / (KB/2)), written transposed as
+    // bf16 pairs.
     const uint16_t* kbase = k + (int64_t)start * k_row + (int64_t)kvh * FA_D;
     const uint16_t* vbase = v + (int64_t)start * v_row + (int64_t)kvh * FA_D;
     v4u kr[KU], vr[VU][2];
@@ -101,7 +106,7 @@ fa_prefill(const uint16_t* __restrict__ q, int64_t q_row, const uint16_t* __rest
         }
 #pragma unroll
         for (int i = 0; i < VU; ++i) {
-            const int u = t + T * i, kp = u & 31, dc = u >> 5;
+            const int u = t + T * i, kp = u % (FA_KB / 2), dc = u / (FA_KB / 2);
             vr[i][0] = *reinterpret_cast<const v4u*>(vbase + (int64_t)min(key0 + 2 * kp, L - 1) * v_row + 8 * dc);
             vr[i][1] = *reinterpret_cast<const v4u*>(vbase + (int64_t)min(key0 + 2 * kp + 1, L - 1) * v_row + 8 * dc);
         }
@@ -116,7 +121,7 @@ fa_prefill(const uint16_t* __restrict__ q, int64_t q_row, const uint16_t* __rest
         }
 #pragma unroll
         for (int i = 0; i < VU; ++i) {
-            const int u = t + T * i, kp = u & 31, dc = u >> 5;
+            const int u = t + T * i, kp = u % (FA_KB / 2), dc = u / (FA_KB / 2);
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 const uint32_t lo = __builtin_amdgcn_perm(vr[i][1][j], vr[i][0][j], 0x05040100u);  // dim 2j
@@ -135,9 +140,9 @@ fa_prefill(const uint16_t* __restrict__ q, int64_t q_row, const uint16_t* __rest
     auto compute = [&](int kb) {
         const uint16_t* Ks = lds + (kb & 1) * FA_STAGE;
         const uint16_t* Vt = Ks + FA_KB * FA_KS;
-        v16f sc[2];
+        v16f sc[NC];
 #pragma unroll
-        for (int c = 0; c < 2; ++c) {
+        for (int c = 0; c < NC; ++c) {
             sc[c] = v16f{};
             const uint16_t* kp_row = Ks + (32 * c + rc) * FA_KS + 8 * hh;
 #pragma unroll
@@ -152,7 +157,7 @@ fa_prefill(const uint16_t* __restrict__ q, int64_t q_row, const uint16_t* __rest
         const int key0 = kb * FA_KB;
         if (key0 + FA_KB - 1 > wave_q0 || key0 + FA_KB > L) {
 #pragma unroll
-            for (int c = 0; c < 2; ++c)
+            for (int c = 0; c < NC; ++c)
 #pragma unroll
                 for (int i = 0; i < 16; ++i) {
                     const int key = key0 + 32 * c + 8 * (i >> 2) + 4 * hh + (i & 3);
@@ -161,7 +166,7 @@ fa_prefill(const uint16_t* __restrict__ q, int64_t q_row, const uint16_t* __rest
         }
         float mx = -__builtin_inff();
 #pragma unroll
-        for (int c = 0; c < 2; ++c)
+        for (int c = 0; c < NC; ++c)
 #pragma unroll
             for (int i = 0; i < 16; ++i) mx = fmaxf(mx, sc[c][i]);
         mx = fmaxf(mx, __shfl_xor(mx, 32));
@@ -170,10 +175,10 @@ fa_prefill(const uint16_t* __restrict__ q, int64_t q_row, const uint16_t* __rest
         const float corr = __builtin_amdgcn_exp2f(__builtin_fmaf(m, qscale, off));
         m = mn;
         // P^T operands: step t of tile c takes values 8t .. 8t + 7.
-        v4u pw[2][2];
+        v4u pw[NC][2];
         float ls = 0.0f;
 #pragma unroll
-        for (int c = 0; c < 2; ++c)
+        for (int c = 0; c < NC; ++c)
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
                 const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[c][2 * j], qscale, off));
@@ -189,7 +194,7 @@ fa_prefill(const uint16_t* __restrict__ q, int64_t q_row, const uint16_t* __rest
                 for (int i = 0; i < 16; ++i) o[dt][i] *= corr;
         }
 #pragma unroll
-        for (int c = 0; c < 2; ++c)
+        for (int c = 0; c < NC; ++c)
 #pragma unroll
             for (int st = 0; st < 2; ++st) {
                 const int kofs = 32 * c + 16 * st + 4 * hh;
@@ -246,11 +251,11 @@ hipError_t launch_fa(const uint16_t* q, int64_t q_row, const uint16_t* k, int64_
     const int64_t nqb8 = (max_seqlen + 32 * (8 / G) - 1) / (32 * (8 / G));
     if (G > 4 || nqb8 * Hkv * B >= device_cu_count()) {
         const int nqb = (int)nqb8;
-        hipLaunchKernelGGL((fa_prefill<G, 8>), dim3((unsigned)(nqb * Hkv), (unsigned)B), dim3(512), 0, st, q, q_row,
+        hipLaunchKernelGGL((fa_prefill<G, 8, 128>), dim3((unsigned)(nqb * Hkv), (unsigned)B), dim3(512), 0, st, q, q_row,
                            k, k_row, v, v_row, out, o_row, cu, Hkv, nqb, qscale);
     } else {
         const int nqb = (int)((max_seqlen + 32 * (NW / G) - 1) / (32 * (NW / G)));
-        hipLaunchKernelGGL((fa_prefill<G, NW>), dim3((unsigned)(nqb * Hkv), (unsigned)B), dim3(NW * 64), 0, st, q,
+        hipLaunchKernelGGL((fa_prefill<G, NW, 64>), dim3((unsigned)(nqb * Hkv), (unsigned)B), dim3(NW * 64), 0, st, q,
                            q_row, k, k_row, v, v_row, out, o_row, cu, Hkv, nqb, qscale);
     }
     return hipGetLastError();
