@@ -169,12 +169,13 @@ def prefill_reference(q, k, v, lens, scale):
 
 
 @pytest.mark.parametrize("lens", [[1, 17, 300], [4096, 33], [64, 65, 127, 128, 129], [31, 32, 33, 63, 257, 1000],
-                                  [1900], [2000]])
+                                  [1900], [2000], [8192, 129]])
 def test_prefill_attention(lens):
     """nv4_prefill_attention (one launch for all packed sequences) against fp32;
     lengths around the 32-row query tiles, 64-row workgroups and 64-key blocks;
     both workgroup forms (4 waves while 8-wave workgroups would number fewer
-    than the CUs, as for 1900 tokens; 8 waves from 2000 tokens on)."""
+    than the CUs, as for 1900 tokens; 8 waves from 2000 tokens on); a prompt
+    twice the end-to-end one."""
     print(f"[prefill-attn] lens={lens}", flush=True)
     g = torch.Generator(device=DEV).manual_seed(3 + len(lens))
     T = sum(lens)
