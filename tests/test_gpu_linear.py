@@ -189,3 +189,20 @@ def test_linear_module_keeps_fp6_weights():
     m2.load_state_dict(m.state_dict())
     assert m2._f6() is not None and torch.equal(m2.weight_f6, weights_to_f6(m.packed_weight, True))
     assert torch.equal(m2(x).view(torch.int16), out2.view(torch.int16))
+
+
+def test_linear_fp6_weights_made_under_inference_mode():
+    """Weights created under torch.inference_mode carry no version counter:
+    the kept fp6 form is used as made, with the bits of converting per call."""
+    case = W.w4a4_case("down", 1024)
+    M, N, K = case.shape
+    print(f"[linear-fp6-inference-mode] M={M} N={N} K={K}", flush=True)
+    with torch.inference_mode():
+        m = W4A4Linear(K, N).to(DEV)
+        m.assign_quantized_(case.w_packed.to(DEV), case.w_scale.to(DEV), case.signs.to(DEV))
+        assert m._f6() is m.weight_f6 is not None
+        x = case.x.to(DEV)
+        out = m(x)
+        ref = w4a4_linear(x, m.signs, m.packed_weight, m.weight_scale, weights_tiled=True)
+    torch.cuda.synchronize()
+    assert torch.equal(out.view(torch.int16), ref.view(torch.int16))
