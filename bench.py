@@ -294,8 +294,9 @@ def e2e_decode(torch, layers, out_tokens):
 # ---------------------------------------------------------------- CPU leg
 def cpu_threads():
     """Host threads for the CPU baseline: every core this process may run on
-    (its affinity set), bounded by OMP_NUM_THREADS when the host sets it (the
-    GPU box gives a job a 16-core share and says so there)."""
+    (its affinity set), bounded by OMP_NUM_THREADS when the host sets it (a
+    host that shares its cores among GPU jobs sets it to the job's share, 16
+    cores per GPU)."""
     n = len(os.sched_getaffinity(0))
     cap = os.environ.get("OMP_NUM_THREADS", "")
     return min(n, int(cap)) if cap.isdigit() and int(cap) > 0 else n, n

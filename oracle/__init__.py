@@ -1,7 +1,7 @@
 """CPU oracle for the quantized-linear path -- TEST INFRASTRUCTURE ONLY.
 
 Only tests/, ``__graft_entry__.smoke()`` and bench.py's CPU-baseline leg may
-import this package, and only as the checker; the product (the ``nv4``
+import this package, and only to check results against; the product (the ``nv4``
 package and its HIP library) never imports it and has no CPU fallback.
 
 The numerics live in ``oracle.c`` (a C restatement of the reference's RHT,

@@ -1,9 +1,9 @@
 /*
  * oracle.c -- CPU restatement of Nano-vLLM-INT4's quantized-linear numerics.
  *
- * TEST INFRASTRUCTURE ONLY.  This file is the checker for the HIP kernels in
- * nano-vllm-int4_amd/csrc and the CPU baseline that bench.py times beside
- * them.  Nothing in the product path links, loads or calls it; the product
+ * TEST INFRASTRUCTURE ONLY.  The tests compare the HIP kernels of
+ * nano-vllm-int4_amd/csrc against this file, and bench.py times it as the
+ * CPU baseline beside them.  Nothing in the product path links, loads or calls it; the product
  * raises when its HIP library is missing instead of falling back here.
  *
  * Every function restates the reference's algorithm in plain C, with the

@@ -36,7 +36,7 @@ _ensure_built()
 
 def pytest_collection_modifyitems(config, items):
     """Skip GPU tests cleanly on a host without a GPU (they are selected
-    explicitly with -m gpu on the GPU box)."""
+    explicitly with -m gpu on a host with one)."""
     try:
         import torch
         has_gpu = torch.cuda.is_available()

@@ -172,7 +172,7 @@ def test_k1_stream_and_graph_replay(k):
 
 
 def test_k1_negative_control():
-    # bench_rht_a4.py:142-152: a checker that accepts a corrupted answer is useless.
+    # bench_rht_a4.py:142-152: a comparison that accepts a corrupted answer is useless.
     x_cpu = make_input(1, 4096)
     signs_cpu = W.signs(4096, 1)
 
