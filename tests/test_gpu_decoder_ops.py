@@ -235,3 +235,39 @@ def test_silu_mul_rht_quant_pack_equals_two_step(K, rows):
     p2, s2 = k1(silu_mul(gu), signs)
     torch.cuda.synchronize()
     assert torch.equal(packed, p2) and torch.equal(scale.view(torch.int16), s2.view(torch.int16))
+
+
+def silu_bf16_reference(g32):
+    """round_bf16(g / (1 + e)) in fp32 arithmetic with e the correctly rounded
+    fp32 exp(-g): exp in float64 rounded to fp32 (overflowing to inf past
+    88.72), the fp32 sum, and the correctly rounded fp32 quotient."""
+    import numpy as np
+    g = g32.astype(np.float64)
+    with np.errstate(over="ignore", invalid="ignore", divide="ignore"):
+        e = np.exp(-g).astype(np.float32)
+        d = (np.float32(1.0) + e).astype(np.float32)
+        s = (g / d.astype(np.float64)).astype(np.float32)
+    return s
+
+
+def test_silu_every_bf16_gate():
+    """silu_mul with up = 1 over every bf16 gate value (all 65536 patterns):
+    bf16(silu(g)) equals the fp32 formula with a correctly rounded exp, bit
+    for bit (any NaN for NaN gates)."""
+    import numpy as np
+    bits = np.arange(65536, dtype=np.uint32)
+    g32 = (bits << 16).view(np.float32)
+    ref = silu_bf16_reference(g32)
+    rb = ref.view(np.uint32)
+    # bf16 round-to-nearest-even of the fp32 result
+    rnd = ((rb + 0x7FFF + ((rb >> 16) & 1)) >> 16).astype(np.uint16)
+    gate = torch.from_numpy(bits.astype(np.uint16).view(np.int16)).view(torch.bfloat16).to(DEV)
+    gu = torch.cat([gate, torch.ones_like(gate)]).view(1, -1)
+    out = silu_mul(gu).view(torch.int16).cpu().numpy().view(np.uint16).reshape(-1)
+    nan_g = np.isnan(g32)
+    out_f = (out.astype(np.uint32) << 16).view(np.float32)
+    assert np.isnan(out_f[nan_g]).all()
+    ok = nan_g | (out == rnd)
+    bad = np.nonzero(~ok)[0]
+    assert bad.size == 0, f"{bad.size} gates differ, e.g. g bits {[hex(b) for b in bad[:8]]}: " \
+                          f"{[hex(out[b]) for b in bad[:8]]} vs {[hex(rnd[b]) for b in bad[:8]]}"
