@@ -242,8 +242,8 @@ def silu_bf16_reference(g32):
     fp32 exp(-g): exp in float64 rounded to fp32 (overflowing to inf past
     88.72), the fp32 sum, and the correctly rounded fp32 quotient."""
     import numpy as np
-    g = g32.astype(np.float64)
     with np.errstate(over="ignore", invalid="ignore", divide="ignore"):
+        g = g32.astype(np.float64)  # signaling NaN patterns raise "invalid" here
         e = np.exp(-g).astype(np.float32)
         d = (np.float32(1.0) + e).astype(np.float32)
         s = (g / d.astype(np.float64)).astype(np.float32)
