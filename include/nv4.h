@@ -59,6 +59,12 @@
  *                          gate_up projections, SiluAndMul (activation.py:8-11)
  *                          before down (nanovllm/models/qwen3.py:96-135 with
  *                          nanovllm/layers/linear_w4a4.py:30-34)
+ *   nv4_rht_quant_pack_rowtiled, nv4_rmsnorm_rht_quant_pack_rowtiled,
+ *   nv4_silu_mul_rht_quant_pack_rowtiled, nv4_w4a4_gemm_rowtiled,
+ *   nv4_w4a4_linear_rowtiled <- the same operators for decode-sized M with the
+ *                          packed activations in a row-tiled order (no
+ *                          counterpart in the reference, whose kernels pass
+ *                          [M,K/2] from rht_quant_pack to w4a4_grouped_gemm)
  */
 #ifndef NV4_H
 #define NV4_H
@@ -162,6 +168,32 @@ int nv4_w4a4_gemm_tiled(const int8_t* a, const int8_t* w_tiled, const void* sa, 
 int nv4_w4a4_linear_tiled(const void* x, const int8_t* signs, const int8_t* w_tiled, const void* sw,
                           void* out, int8_t* a_packed, void* a_scale,
                           int64_t M, int64_t N, int64_t K, void* stream);
+
+/*
+ * Row-tiled packed activations: the packed codes of M rows in 16-row blocks,
+ * ceil(M/16) * 16 * K/2 bytes (rows past M in the last block are never
+ * written and never change a result).  The 16 rows x 128 k of row block rb
+ * and K group g are the 1 KiB at byte (rb*(K/128) + g) * 1024, in the order
+ * the matrix-core lanes consume them:
+ *   16-byte unit  (rb*(K/128) + g)*64 + l  holds packed bytes
+ *   64*g + 16*(l/16) .. +15 of row 16*rb + l%16             (l = 0..63),
+ * the activation counterpart of the tiled weight layout.  The decode GEMM then
+ * loads every operand as whole cache lines straight into registers.
+ * nv4_rht_quant_pack_rowtiled: nv4_rht_quant_pack (reference layout, K in
+ *   {4096, 12288}) writing packed_rt in this order; scale stays [M,K/128].
+ * nv4_w4a4_gemm_rowtiled: nv4_w4a4_gemm_tiled for 1 <= M <= 32 on row-tiled
+ *   activations (a_rt 16-byte aligned); bit-identical results.
+ * nv4_w4a4_linear_rowtiled: nv4_w4a4_linear_tiled for 1 <= M <= 32 with the
+ *   row-tiled activation workspace a_packed_rt.
+ */
+int nv4_rht_quant_pack_rowtiled(const void* x, const int8_t* signs, int8_t* packed_rt, void* scale,
+                                int64_t M, int64_t K, void* stream);
+int nv4_w4a4_gemm_rowtiled(const int8_t* a_rt, const int8_t* w_tiled, const void* sa, const void* sw,
+                           int sw_grouped, void* out, int out_fp32,
+                           int64_t M, int64_t N, int64_t K, void* stream);
+int nv4_w4a4_linear_rowtiled(const void* x, const int8_t* signs, const int8_t* w_tiled, const void* sw,
+                             void* out, int8_t* a_packed_rt, void* a_scale,
+                             int64_t M, int64_t N, int64_t K, void* stream);
 
 /*
  * nv4_w4a4_gemm (w_tiled = 0) / nv4_w4a4_gemm_tiled (w_tiled = 1) for
@@ -380,6 +412,12 @@ int nv4_rmsnorm_rht_quant_pack(const void* x, const void* residual_in, void* res
                                void* stream);
 int nv4_silu_mul_rht_quant_pack(const void* gate_up, const int8_t* signs, int8_t* packed, void* scale, int64_t M,
                                 int64_t K, void* stream);
+/* The same two, writing the codes in the row-tiled order (ceil(M/16)*16*K/2 bytes). */
+int nv4_rmsnorm_rht_quant_pack_rowtiled(const void* x, const void* residual_in, void* residual_out,
+                                        const void* norm_weight, float eps, const int8_t* signs, int8_t* packed_rt,
+                                        void* scale, int64_t M, int64_t K, void* stream);
+int nv4_silu_mul_rht_quant_pack_rowtiled(const void* gate_up, const int8_t* signs, int8_t* packed_rt, void* scale,
+                                         int64_t M, int64_t K, void* stream);
 
 /*
  * Next-token sampling at per-row temperatures (nanovllm/layers/sampler.py:5-12):

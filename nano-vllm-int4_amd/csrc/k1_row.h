@@ -190,6 +190,22 @@ __device__ __forceinline__ void codes_pack(const float (&v)[N], float s, uint32_
     }
 }
 
+// Where the 8 packed bytes of one row's 16-column unit u (columns 16u ..
+// 16u+15) go.  Reference layout: [M][K/2], bytes 8u.. of the row.  Row-tiled
+// layout (the decode GEMM's activation operand): 1 KiB blocks, one per
+// 16-row block rb and group g at (rb*G + g) KiB, lane l = 16*part + r of a
+// block holding bytes 16*part .. +15 of the group's 64 for row 16*rb + r:
+// unit u is group u/8, part (u/2)%4, half u%2 of that lane's 16 bytes.
+template <bool RT>
+__device__ __forceinline__ int8_t* packed_dst(int8_t* __restrict__ packed, int64_t row, int u, int K) {
+    if constexpr (RT) {
+        const int G = K >> 7;
+        return packed + ((((row >> 4) * G + (u >> 3)) * 64 + ((u >> 1) & 3) * 16 + (row & 15)) << 4) + 8 * (u & 1);
+    } else {
+        return packed + row * (K >> 1) + 8 * u;
+    }
+}
+
 // 16 values per lane, 8 lanes per group: 8 packed bytes and, from the
 // group's first lane, the bf16 scale.
 __device__ __forceinline__ void quantize16_store(const float (&v)[16], int8_t* __restrict__ dst8,
@@ -236,7 +252,7 @@ __device__ __forceinline__ v4u k1_signs12288(const int8_t* __restrict__ signs) {
 }
 
 template <class Prologue>
-__device__ __forceinline__ void k1_row12288(Prologue&& prologue, const v4u sv, int8_t* __restrict__ prow,
+__device__ __forceinline__ void k1_row12288(Prologue&& prologue, const v4u sv, int8_t* __restrict__ pdst,
                                             uint16_t* __restrict__ srow, float* __restrict__ buf) {
     const int t = threadIdx.x, w = t >> 6, l = t & 63;
     if (w < 12) {
@@ -271,7 +287,7 @@ __device__ __forceinline__ void k1_row12288(Prologue&& prologue, const v4u sv, i
         float v[16];
 #pragma unroll
         for (int i = 0; i < 16; ++i) v[i] = pu[i];
-        quantize16_store(v, prow + 8 * t, srow + (t >> 3), (t & 7) == 0);
+        quantize16_store(v, pdst, srow + (t >> 3), (t & 7) == 0);
     }
 }
 
@@ -279,7 +295,8 @@ __device__ __forceinline__ void k1_row12288(Prologue&& prologue, const v4u sv, i
 // its 1024-column quarter, one workgroup transpose brings bits 8-11 into
 // registers (thread t: columns t + 256 r), a second one the contiguous
 // units back for quantization.  Every thread calls the prologue once, with
-// col0 = 16 t; sv are its 16 signs (k1_signs4096).
+// col0 = 16 t; sv are its 16 signs (k1_signs4096).  pdst is where the
+// thread's 8 packed bytes go (packed_dst of its unit t).
 constexpr int K4_THREADS = 256;
 constexpr int K4_LDS = 4 * K1_BLOCK;
 
@@ -288,7 +305,7 @@ __device__ __forceinline__ v4u k1_signs4096(const int8_t* __restrict__ signs) {
 }
 
 template <class Prologue>
-__device__ __forceinline__ void k1_row4096(Prologue&& prologue, const v4u sv, int8_t* __restrict__ prow,
+__device__ __forceinline__ void k1_row4096(Prologue&& prologue, const v4u sv, int8_t* __restrict__ pdst,
                                            uint16_t* __restrict__ srow, float* __restrict__ buf) {
     const int t = threadIdx.x, w = t >> 6, l = t & 63;
     float a[16];
@@ -317,7 +334,7 @@ __device__ __forceinline__ void k1_row4096(Prologue&& prologue, const v4u sv, in
     __syncthreads();
 #pragma unroll
     for (int i = 0; i < 16; ++i) a[i] = pu[i];
-    quantize16_store(a, prow + 8 * t, srow + (t >> 3), (t & 7) == 0);
+    quantize16_store(a, pdst, srow + (t >> 3), (t & 7) == 0);
 }
 
 }  // namespace

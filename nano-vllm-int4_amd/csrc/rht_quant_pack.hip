@@ -76,8 +76,9 @@ struct RowRms {
     }
 };
 
-// K = 4096: one workgroup of K4_THREADS threads per row.
-template <class Src>
+// K = 4096: one workgroup of K4_THREADS threads per row.  RT: the codes go
+// to the row-tiled layout (packed_dst) instead of [M][K/2].
+template <bool RT, class Src>
 __device__ __forceinline__ void k1_k4096_body(const Src& src, const int8_t* __restrict__ signs,
                                               int8_t* __restrict__ packed, uint16_t* __restrict__ scale,
                                               float* buf) {
@@ -86,19 +87,19 @@ __device__ __forceinline__ void k1_k4096_body(const Src& src, const int8_t* __re
     const int c0 = 16 * threadIdx.x;
     typename Src::Raw raw;
     src.load(row, c0, raw);
-    k1_row4096([&](int, float (&v)[16]) { src.values(raw, row, c0, v); }, sv, packed + row * 2048,
-               scale + row * 32, buf);
+    k1_row4096([&](int, float (&v)[16]) { src.values(raw, row, c0, v); }, sv,
+               packed_dst<RT>(packed, row, threadIdx.x, 4096), scale + row * 32, buf);
 }
 
-template <class Src>
+template <class Src, bool RT>
 __global__ void __launch_bounds__(K4_THREADS)
 k1_k4096(Src src, const int8_t* __restrict__ signs, int8_t* __restrict__ packed, uint16_t* __restrict__ scale) {
     __shared__ float buf[K4_LDS];
-    k1_k4096_body(src, signs, packed, scale, buf);
+    k1_k4096_body<RT>(src, signs, packed, scale, buf);
 }
 
 // add + RMSNorm in front: the norm weights are loaded ahead of the row.
-template <bool RESID>
+template <bool RESID, bool RT>
 __global__ void __launch_bounds__(K4_THREADS)
 k1_k4096_rms(RowRms<RESID> src, const uint16_t* __restrict__ nw, const int8_t* __restrict__ signs,
              int8_t* __restrict__ packed, uint16_t* __restrict__ scale) {
@@ -107,13 +108,13 @@ k1_k4096_rms(RowRms<RESID> src, const uint16_t* __restrict__ nw, const int8_t* _
     src.w0 = *reinterpret_cast<const v4u*>(nw + 16 * threadIdx.x);
     src.w1 = *reinterpret_cast<const v4u*>(nw + 16 * threadIdx.x + 8);
     src.red = red;
-    k1_k4096_body(src, signs, packed, scale, buf);
+    k1_k4096_body<RT>(src, signs, packed, scale, buf);
 }
 
 // K = 12288: one workgroup of 1024 threads per row.  Waves 12-15 hold no
 // columns in the butterfly phases (they join the H12 stage); their loads
 // repeat the row's last 16 columns, so that every load is unconditional.
-template <class Src>
+template <class Src, bool RT>
 __global__ void __launch_bounds__(K12_THREADS)
 k1_k12288(Src src, const int8_t* __restrict__ signs, int8_t* __restrict__ packed, uint16_t* __restrict__ scale) {
     __shared__ float buf[K12_LDS];
@@ -122,28 +123,43 @@ k1_k12288(Src src, const int8_t* __restrict__ signs, int8_t* __restrict__ packed
     const int c0 = 16 * min((int)threadIdx.x, 767);
     typename Src::Raw raw;
     src.load(row, c0, raw);
-    k1_row12288([&](int, float (&v)[16]) { src.values(raw, row, c0, v); }, sv, packed + row * 6144,
-                scale + row * 96, buf);
+    k1_row12288([&](int, float (&v)[16]) { src.values(raw, row, c0, v); }, sv,
+                packed_dst<RT>(packed, row, min((int)threadIdx.x, 767), 12288), scale + row * 96, buf);
 }
 
 template <class Src>
-hipError_t launch_k4096(const Src& src, const int8_t* signs, int8_t* packed, uint16_t* scale, int M, hipStream_t st) {
-    hipLaunchKernelGGL((k1_k4096<Src>), dim3((unsigned)M), dim3(K4_THREADS), 0, st, src, signs, packed, scale);
+hipError_t launch_k4096(const Src& src, const int8_t* signs, int8_t* packed, uint16_t* scale, int M, bool rt,
+                        hipStream_t st) {
+    if (rt)
+        hipLaunchKernelGGL((k1_k4096<Src, true>), dim3((unsigned)M), dim3(K4_THREADS), 0, st, src, signs, packed,
+                           scale);
+    else
+        hipLaunchKernelGGL((k1_k4096<Src, false>), dim3((unsigned)M), dim3(K4_THREADS), 0, st, src, signs, packed,
+                           scale);
     return hipGetLastError();
 }
 
 template <class Src>
-hipError_t launch_k12288(const Src& src, const int8_t* signs, int8_t* packed, uint16_t* scale, int M,
+hipError_t launch_k12288(const Src& src, const int8_t* signs, int8_t* packed, uint16_t* scale, int M, bool rt,
                          hipStream_t st) {
-    hipLaunchKernelGGL((k1_k12288<Src>), dim3((unsigned)M), dim3(K12_THREADS), 0, st, src, signs, packed, scale);
+    if (rt)
+        hipLaunchKernelGGL((k1_k12288<Src, true>), dim3((unsigned)M), dim3(K12_THREADS), 0, st, src, signs, packed,
+                           scale);
+    else
+        hipLaunchKernelGGL((k1_k12288<Src, false>), dim3((unsigned)M), dim3(K12_THREADS), 0, st, src, signs, packed,
+                           scale);
     return hipGetLastError();
 }
 
 template <bool RESID>
 hipError_t launch_rms4096(const RowRms<RESID>& src, const uint16_t* nw, const int8_t* signs, int8_t* packed,
-                          uint16_t* scale, int M, hipStream_t st) {
-    hipLaunchKernelGGL((k1_k4096_rms<RESID>), dim3((unsigned)M), dim3(K4_THREADS), 0, st, src, nw, signs, packed,
-                       scale);
+                          uint16_t* scale, int M, bool rt, hipStream_t st) {
+    if (rt)
+        hipLaunchKernelGGL((k1_k4096_rms<RESID, true>), dim3((unsigned)M), dim3(K4_THREADS), 0, st, src, nw, signs,
+                           packed, scale);
+    else
+        hipLaunchKernelGGL((k1_k4096_rms<RESID, false>), dim3((unsigned)M), dim3(K4_THREADS), 0, st, src, nw, signs,
+                           packed, scale);
     return hipGetLastError();
 }
 
@@ -200,9 +216,11 @@ k1_block128(const uint16_t* __restrict__ x, const int8_t* __restrict__ signs,
 }  // namespace
 }  // namespace nv4
 
-extern "C" int nv4_rht_quant_pack(const void* x, const int8_t* signs, int8_t* packed, void* scale,
-                                  int64_t M, int64_t K, int layout, void* stream) {
-    using namespace nv4;
+namespace nv4 {
+namespace {
+
+int quant_pack_impl(const void* x, const int8_t* signs, int8_t* packed, void* scale, int64_t M, int64_t K,
+                    int layout, bool rt, void* stream) {
     if (!x || !signs || !packed || !scale) return NV4_E_NULL;
     if (M < 1 || M > 0x7fffffffLL) return NV4_E_SHAPE;
     if (reinterpret_cast<uintptr_t>(x) % 16 || reinterpret_cast<uintptr_t>(packed) % 8 ||
@@ -212,11 +230,11 @@ extern "C" int nv4_rht_quant_pack(const void* x, const int8_t* signs, int8_t* pa
     if (layout == NV4_LAYOUT_REFERENCE) {
         const auto* xp = static_cast<const uint16_t*>(x);
         auto* sp = static_cast<uint16_t*>(scale);
-        if (K == 4096) return (int)launch_k4096(RowX{xp, 4096}, signs, packed, sp, (int)M, st);
-        if (K == 12288) return (int)launch_k12288(RowX{xp, 12288}, signs, packed, sp, (int)M, st);
+        if (K == 4096) return (int)launch_k4096(RowX{xp, 4096}, signs, packed, sp, (int)M, rt, st);
+        if (K == 12288) return (int)launch_k12288(RowX{xp, 12288}, signs, packed, sp, (int)M, rt, st);
         return NV4_E_SHAPE;
     }
-    if (layout == NV4_LAYOUT_BLOCK128) {
+    if (layout == NV4_LAYOUT_BLOCK128 && !rt) {
         if (K < 128 || K % 128 || K > 65536) return NV4_E_SHAPE;
         const int64_t units = M * (K / 16);
         const int64_t blocks = (units + 255) / 256;
@@ -229,10 +247,9 @@ extern "C" int nv4_rht_quant_pack(const void* x, const int8_t* signs, int8_t* pa
     return NV4_E_LAYOUT;
 }
 
-extern "C" int nv4_rmsnorm_rht_quant_pack(const void* x, const void* residual_in, void* residual_out,
-                                          const void* norm_weight, float eps, const int8_t* signs, int8_t* packed,
-                                          void* scale, int64_t M, int64_t K, void* stream) {
-    using namespace nv4;
+int rmsnorm_quant_impl(const void* x, const void* residual_in, void* residual_out, const void* norm_weight,
+                       float eps, const int8_t* signs, int8_t* packed, void* scale, int64_t M, int64_t K, bool rt,
+                       void* stream) {
     if (!x || !norm_weight || !signs || !packed || !scale || (!residual_in) != (!residual_out)) return NV4_E_NULL;
     if (M < 1 || M > 0x7fffffffLL || K != 4096) return NV4_E_SHAPE;
     if (reinterpret_cast<uintptr_t>(x) % 16 || reinterpret_cast<uintptr_t>(residual_in) % 16 ||
@@ -247,15 +264,14 @@ extern "C" int nv4_rmsnorm_rht_quant_pack(const void* x, const void* residual_in
     if (residual_in) {
         RowRms<true> src{xp, static_cast<const uint16_t*>(residual_in), static_cast<uint16_t*>(residual_out), eps,
                          {}, {}, nullptr};
-        return (int)launch_rms4096(src, wp, signs, packed, sp, (int)M, st);
+        return (int)launch_rms4096(src, wp, signs, packed, sp, (int)M, rt, st);
     }
     RowRms<false> src{xp, nullptr, nullptr, eps, {}, {}, nullptr};
-    return (int)launch_rms4096(src, wp, signs, packed, sp, (int)M, st);
+    return (int)launch_rms4096(src, wp, signs, packed, sp, (int)M, rt, st);
 }
 
-extern "C" int nv4_silu_mul_rht_quant_pack(const void* gate_up, const int8_t* signs, int8_t* packed, void* scale,
-                                           int64_t M, int64_t K, void* stream) {
-    using namespace nv4;
+int silu_quant_impl(const void* gate_up, const int8_t* signs, int8_t* packed, void* scale, int64_t M, int64_t K,
+                    bool rt, void* stream) {
     if (!gate_up || !signs || !packed || !scale) return NV4_E_NULL;
     if (M < 1 || M > 0x7fffffffLL || (K != 4096 && K != 12288)) return NV4_E_SHAPE;
     if (reinterpret_cast<uintptr_t>(gate_up) % 16 || reinterpret_cast<uintptr_t>(packed) % 8 ||
@@ -264,6 +280,44 @@ extern "C" int nv4_silu_mul_rht_quant_pack(const void* gate_up, const int8_t* si
     hipStream_t st = static_cast<hipStream_t>(stream);
     const auto* gp = static_cast<const uint16_t*>(gate_up);
     auto* sp = static_cast<uint16_t*>(scale);
-    if (K == 4096) return (int)launch_k4096(RowSilu{gp, 4096}, signs, packed, sp, (int)M, st);
-    return (int)launch_k12288(RowSilu{gp, 12288}, signs, packed, sp, (int)M, st);
+    if (K == 4096) return (int)launch_k4096(RowSilu{gp, 4096}, signs, packed, sp, (int)M, rt, st);
+    return (int)launch_k12288(RowSilu{gp, 12288}, signs, packed, sp, (int)M, rt, st);
+}
+
+}  // namespace
+}  // namespace nv4
+
+extern "C" int nv4_rht_quant_pack(const void* x, const int8_t* signs, int8_t* packed, void* scale,
+                                  int64_t M, int64_t K, int layout, void* stream) {
+    return nv4::quant_pack_impl(x, signs, packed, scale, M, K, layout, false, stream);
+}
+
+extern "C" int nv4_rht_quant_pack_rowtiled(const void* x, const int8_t* signs, int8_t* packed_rt, void* scale,
+                                           int64_t M, int64_t K, void* stream) {
+    return nv4::quant_pack_impl(x, signs, packed_rt, scale, M, K, NV4_LAYOUT_REFERENCE, true, stream);
+}
+
+extern "C" int nv4_rmsnorm_rht_quant_pack(const void* x, const void* residual_in, void* residual_out,
+                                          const void* norm_weight, float eps, const int8_t* signs, int8_t* packed,
+                                          void* scale, int64_t M, int64_t K, void* stream) {
+    return nv4::rmsnorm_quant_impl(x, residual_in, residual_out, norm_weight, eps, signs, packed, scale, M, K, false,
+                                   stream);
+}
+
+extern "C" int nv4_rmsnorm_rht_quant_pack_rowtiled(const void* x, const void* residual_in, void* residual_out,
+                                                   const void* norm_weight, float eps, const int8_t* signs,
+                                                   int8_t* packed_rt, void* scale, int64_t M, int64_t K,
+                                                   void* stream) {
+    return nv4::rmsnorm_quant_impl(x, residual_in, residual_out, norm_weight, eps, signs, packed_rt, scale, M, K,
+                                   true, stream);
+}
+
+extern "C" int nv4_silu_mul_rht_quant_pack(const void* gate_up, const int8_t* signs, int8_t* packed, void* scale,
+                                           int64_t M, int64_t K, void* stream) {
+    return nv4::silu_quant_impl(gate_up, signs, packed, scale, M, K, false, stream);
+}
+
+extern "C" int nv4_silu_mul_rht_quant_pack_rowtiled(const void* gate_up, const int8_t* signs, int8_t* packed_rt,
+                                                    void* scale, int64_t M, int64_t K, void* stream) {
+    return nv4::silu_quant_impl(gate_up, signs, packed_rt, scale, M, K, true, stream);
 }

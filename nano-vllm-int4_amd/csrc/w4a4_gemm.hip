@@ -91,7 +91,7 @@ __device__ __forceinline__ void store_out(void* out, int64_t idx, float v) {
 // ----------------------------------------------------------------------------
 constexpr int DC_RSRC_WORD3 = 0x00020000;  // buffer resource word 3 (CDNA): 32-bit data format
 
-template <int MB, int NW, int D, bool TW, bool SW_GROUPED, bool OUT_F32>
+template <int MB, int NW, int D, bool TW, bool RT, bool SW_GROUPED, bool OUT_F32>
 __global__ void __launch_bounds__(NW * 64, 16 / NW)
 k2_dec(const int8_t* __restrict__ a, const int8_t* __restrict__ w,
        const uint16_t* __restrict__ sa, const uint16_t* __restrict__ sw,
@@ -103,12 +103,14 @@ k2_dec(const int8_t* __restrict__ a, const int8_t* __restrict__ w,
     constexpr int CPR = SLB / 16;                                       // 16-byte chunks per row and round
     constexpr int OPT = (NOUT + DC_T - 1) / DC_T;                      // outputs per thread
     constexpr int APT = ROWS * CPR / DC_T;                              // activation chunks per thread
+    constexpr int NA = RT ? MB : APT;                                   // activation loads per thread and round
     constexpr int N_SA = ROWS * GR;                                     // scale entries per round
     constexpr int N_SW = SW_GROUPED ? 16 * GR : 0;
     constexpr int SPT = (N_SA + N_SW + DC_T - 1) / DC_T;
-    static_assert(APT * DC_T == ROWS * CPR, "activation slice must split evenly");
+    static_assert(RT || APT * DC_T == ROWS * CPR, "activation slice must split evenly");
+    static_assert(!RT || TW, "row-tiled activations go with tiled weights");
     static_assert(N_SA % 64 == 0 && N_SW % 64 == 0, "scale classes must be wave-uniform");
-    __shared__ __align__(16) uint8_t a_l[2][ROWS * SLB];
+    __shared__ __align__(16) uint8_t a_l[2][RT ? 16 : ROWS * SLB];
     __shared__ __align__(16) int16_t dots[2][GR][NOUT];
     __shared__ __align__(16) float sal[2][ROWS][GR];  // a row's scales of the round together
     __shared__ __align__(16) float swl[2][16][GR];
@@ -137,11 +139,13 @@ k2_dec(const int8_t* __restrict__ a, const int8_t* __restrict__ w,
     // q % CPR of the row's SLB-byte slice).  The slice of round r starts at
     // byte SLB r, moved back so that it ends at the row end when the last
     // round is partial.
-    const __amdgpu_buffer_rsrc_t rsw_a =
-        __builtin_amdgcn_make_buffer_rsrc(const_cast<int8_t*>(a), (short)0, M * KB, DC_RSRC_WORD3);
-    int a_voff[APT], a_dst[APT];
+    // Row-tiled activations (RT): row block mb of group g is the 1 KiB at
+    // (mb * G + g) KiB, lane l's operand bytes at 16 l.
+    const __amdgpu_buffer_rsrc_t rsw_a = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<int8_t*>(a), (short)0, RT ? MB * G * 1024 : M * KB, DC_RSRC_WORD3);
+    int a_voff[RT ? 1 : APT], a_dst[RT ? 1 : APT];
 #pragma unroll
-    for (int i = 0; i < APT; ++i) {
+    for (int i = 0; i < (RT ? 0 : APT); ++i) {
         const int q = t + i * DC_T;
         const int r = q / CPR, c = q % CPR;
         a_voff[i] = min(r, M - 1) * KB + c * 16;
@@ -182,16 +186,24 @@ k2_dec(const int8_t* __restrict__ a, const int8_t* __restrict__ w,
         }
     }
 
-    v4u rw[D], ra[D][APT];
+    v4u rw[D], ra[D][NA];
     uint16_t rs[D][SPT];
-    auto issue = [&](int r, v4u& w_out, v4u (&a_out)[APT], uint16_t (&s_out)[SPT]) {
-        w_out = __builtin_bit_cast(
-            v4u, __builtin_amdgcn_raw_buffer_load_b128(rsw_w, w_voff, min(r * GR + wave, G - 1) * wstep, 0));
+    auto issue = [&](int r, v4u& w_out, v4u (&a_out)[NA], uint16_t (&s_out)[SPT]) {
+        const int gw = min(r * GR + wave, G - 1);  // the wave's group of round r
+        w_out = __builtin_bit_cast(v4u, __builtin_amdgcn_raw_buffer_load_b128(rsw_w, w_voff, gw * wstep, 0));
         const int rr = min(r, R - 1);        // rounds past the end reload the last one (unused)
-        const int aoff = slice_start(rr);
+        if constexpr (RT) {
 #pragma unroll
-        for (int i = 0; i < APT; ++i)
-            a_out[i] = __builtin_bit_cast(v4u, __builtin_amdgcn_raw_buffer_load_b128(rsw_a, a_voff[i], aoff, 0));
+            for (int mb = 0; mb < MB; ++mb)
+                a_out[mb] = __builtin_bit_cast(
+                    v4u, __builtin_amdgcn_raw_buffer_load_b128(rsw_a, lane * 16, (mb * G + gw) * 1024, 0));
+        } else {
+            const int aoff = slice_start(rr);
+#pragma unroll
+            for (int i = 0; i < APT; ++i)
+                a_out[i] =
+                    __builtin_bit_cast(v4u, __builtin_amdgcn_raw_buffer_load_b128(rsw_a, a_voff[i], aoff, 0));
+        }
         const int glast = G - 1 - rr * GR;   // the round's last valid group, relative (>= 0)
 #pragma unroll
         for (int q = 0; q < SPT; ++q) {
@@ -205,24 +217,32 @@ k2_dec(const int8_t* __restrict__ a, const int8_t* __restrict__ w,
         // in issue order, so a round's data must not queue behind later ones.
         __builtin_amdgcn_sched_barrier(0);
     };
-    auto stage_a = [&](int r, const v4u (&a_in)[APT]) {
+    auto stage_a = [&](int r, const v4u (&a_in)[NA]) {
+        if constexpr (!RT) {
 #pragma unroll
-        for (int i = 0; i < APT; ++i) *reinterpret_cast<v4u*>(&a_l[r & 1][a_dst[i]]) = a_in[i];
+            for (int i = 0; i < APT; ++i) *reinterpret_cast<v4u*>(&a_l[r & 1][a_dst[i]]) = a_in[i];
+        }
     };
     // A-operand LDS offsets: group g's chunk in the slice is 4 j + part with
     // j = (64 g - slice start) / 64 (scalar), so its swizzled position is
     // 128 (j >> 1) + x[j & 1] with x precomputed per lane.
     const int ax0 = rc * SLB + (((part ^ rc) & 7) << 4);
     const int ax1 = rc * SLB + ((((4 + part) ^ rc) & 7) << 4);
-    auto mma = [&](int r, const v4u& w_in, const uint16_t (&s_in)[SPT]) {
+    auto mma = [&](int r, const v4u& w_in, const v4u (&a_in)[NA], const uint16_t (&s_in)[SPT]) {
         const int buf = r & 1;
         if (r * GR + wave < G) {  // uniform over the wave
-            const int j = ((r * GR + wave) * 64 - slice_start(r)) >> 6;
-            const int aoff = buf * (ROWS * SLB) + 128 * (j >> 1) + ((j & 1) ? ax1 : ax0);
             v4u av[MB];  // every operand read issued before the first use
+            if constexpr (RT) {
 #pragma unroll
-            for (int mb = 0; mb < MB; ++mb) av[mb] = *reinterpret_cast<const v4u*>(&a_l[0][aoff + mb * 16 * SLB]);
-            __builtin_amdgcn_sched_barrier(0);
+                for (int mb = 0; mb < MB; ++mb) av[mb] = a_in[mb];
+            } else {
+                const int j = ((r * GR + wave) * 64 - slice_start(r)) >> 6;
+                const int aoff = buf * (ROWS * SLB) + 128 * (j >> 1) + ((j & 1) ? ax1 : ax0);
+#pragma unroll
+                for (int mb = 0; mb < MB; ++mb)
+                    av[mb] = *reinterpret_cast<const v4u*>(&a_l[0][aoff + mb * 16 * SLB]);
+                __builtin_amdgcn_sched_barrier(0);
+            }
             const v4i w0 = unpack8_x16(w_in[0], w_in[1]);
             const v4i w1 = unpack8_x16(w_in[2], w_in[3]);
 #pragma unroll
@@ -286,15 +306,17 @@ k2_dec(const int8_t* __restrict__ a, const int8_t* __restrict__ w,
     };
 
     static_for<0, D>([&](auto U) { issue(U, rw[U], ra[U], rs[U]); });
-    stage_a(0, ra[0]);
-    __syncthreads();
+    if constexpr (!RT) {
+        stage_a(0, ra[0]);
+        __syncthreads();
+    }
     // Steady state: round r uses slot r % D, stages the activation slice of
     // round r + 1 (slot (r+1) % D) and refills slot r % D with round r + D.
     int r0 = 0;
     for (; r0 + D < R; r0 += D) {
         static_for<0, D>([&](auto U) {
             constexpr int u = U, un = (u + 1) % D;
-            mma(r0 + u, rw[u], rs[u]);
+            mma(r0 + u, rw[u], ra[u], rs[u]);
             stage_a(r0 + u + 1, ra[un]);
             issue(r0 + u + D, rw[u], ra[u], rs[u]);
             __syncthreads();
@@ -305,7 +327,7 @@ k2_dec(const int8_t* __restrict__ a, const int8_t* __restrict__ w,
     static_for<0, D>([&](auto U) {
         constexpr int u = U, un = (u + 1) % D;
         if (r0 + u < R) {
-            mma(r0 + u, rw[u], rs[u]);
+            mma(r0 + u, rw[u], ra[u], rs[u]);
             if (r0 + u + 1 < R) stage_a(r0 + u + 1, ra[un]);
             __syncthreads();
             epilogue(r0 + u);
@@ -352,7 +374,7 @@ constexpr int WIDE_A_BYTES = 128 * 1024;  // widened activation block limit (M x
 constexpr int WIDE_SCALES = 1024;         // G * ROWS limit
 constexpr int WIDE_WSCALES = 3072;        // G * CBW * 16 limit
 
-template <int MB, int CBW, int D, bool TW, bool SW_GROUPED, bool OUT_F32>
+template <int MB, int CBW, int D, bool TW, bool RT, bool SW_GROUPED, bool OUT_F32>
 __global__ void __launch_bounds__(CBW * MB * 64)
 k2_wide(const int8_t* __restrict__ a, const int8_t* __restrict__ w,
         const uint16_t* __restrict__ sa, const uint16_t* __restrict__ sw,
@@ -381,13 +403,29 @@ k2_wide(const int8_t* __restrict__ a, const int8_t* __restrict__ w,
     constexpr int WSTEP = TW ? 1024 : 64;
 
     // ---- activation block + scales: loads first, then the weight ring.
+    // Packed chunk q (16 bytes): row r, chunk c of the row.  Reference layout:
+    // rows of KB bytes; row-tiled layout (RT): the buffer is the MB row blocks'
+    // G KiB blocks in order, lane l of block (rb, g) holding chunk 4 g + l/16
+    // of row 16 rb + l%16, so chunk q sits at byte 16 q.
+    auto chunk_rc = [&](int q, int& r, int& c) {
+        if constexpr (RT) {
+            const int l = q & 63, blk = q >> 6;
+            r = (blk / G) * 16 + (l & 15);
+            c = (blk % G) * 4 + (l >> 4);
+        } else {
+            r = q / chunks_row;
+            c = q - r * chunks_row;
+        }
+    };
     v4u ra[AC];
     uint16_t rsa[SC], rsw[WC > 0 ? WC : 1];
 #pragma unroll
     for (int i = 0; i < AC; ++i) {
         const int q = min(t + i * T, a_chunks - 1);
-        const int r = q / chunks_row, c = q - r * chunks_row;
-        ra[i] = *reinterpret_cast<const v4u*>(a + (int64_t)min(r, M - 1) * KB + c * 16);
+        int r, c;
+        chunk_rc(q, r, c);
+        ra[i] = RT ? *reinterpret_cast<const v4u*>(a + (int64_t)q * 16)
+                   : *reinterpret_cast<const v4u*>(a + (int64_t)min(r, M - 1) * KB + c * 16);
     }
 #pragma unroll
     for (int i = 0; i < SC; ++i) {
@@ -408,7 +446,8 @@ k2_wide(const int8_t* __restrict__ a, const int8_t* __restrict__ w,
 #pragma unroll
     for (int i = 0; i < AC; ++i) {
         const int q = t + i * T;
-        const int r = q / chunks_row, c = q - r * chunks_row;
+        int r, c;
+        chunk_rc(min(q, a_chunks - 1), r, c);
         const bool live = q < a_chunks;
         const int u0 = 2 * c, u1 = 2 * c + 1;
         const int s0 = (u0 & ~7) | ((u0 ^ r) & 7), s1 = (u1 & ~7) | ((u1 ^ r) & 7);
@@ -417,11 +456,30 @@ k2_wide(const int8_t* __restrict__ a, const int8_t* __restrict__ w,
         *reinterpret_cast<v4i*>(&a_l[live ? r * K + s0 * 16 : WIDE_A_BYTES]) = lo;
         *reinterpret_cast<v4i*>(&a_l[live ? r * K + s1 * 16 : WIDE_A_BYTES + 16]) = hi;
     }
+    // The >> 8 that turns the MFMA's 256 * dot into the dot can ride on the
+    // activation scale instead: cvt(256 d) * (sa * 2^-8) * sw inside the fma is
+    // the same exact product as d * (sa * sw) whenever sa * 2^-8 and the
+    // scale product stay normal fp32, which holds when every scale of the
+    // workgroup is 0 or of magnitude in [2^-59, 2^63) (per-channel weight
+    // scales multiply the finished total, so only sa counts there).
+    // Otherwise the workgroup runs the literal sequence.
+    auto fold_ok = [](uint32_t b) {
+        const uint32_t e = (b >> 7) & 0xffu;
+        return (b & 0x7fffu) == 0 || (e >= 127 - 59 && e < 127 + 63);
+    };
+    bool bad = false;
+#pragma unroll
+    for (int i = 0; i < SC; ++i) bad |= !fold_ok(rsa[i]);
+#pragma unroll
+    for (int i = 0; i < WC; ++i) bad |= !fold_ok(rsw[i]);
+    // (Not with 8 column blocks: the second loop body would not fit 128 VGPRs.)
+    const bool fold = !__syncthreads_or(bad) && CBW < 8;
+    const float sa_mul = fold ? 0x1p-8f : 1.0f;
 #pragma unroll
     for (int i = 0; i < SC; ++i) {
         const int e = t + i * T;
         const int ec = min(e, G * ROWS - 1);
-        sa_l[e < G * ROWS ? (ec % G) * ROWS + ec / G : WIDE_SCALES] = bf16_to_f32(rsa[i]);
+        sa_l[e < G * ROWS ? (ec % G) * ROWS + ec / G : WIDE_SCALES] = bf16_to_f32(rsa[i]) * sa_mul;
     }
 #pragma unroll
     for (int i = 0; i < WC; ++i) {
@@ -451,41 +509,53 @@ k2_wide(const int8_t* __restrict__ a, const int8_t* __restrict__ w,
         o.s_a = *reinterpret_cast<const v4f*>(sap + g * ROWS);
         o.s_w = SW_GROUPED ? swq[g * COLS] : 1.0f;
     };
-    auto consume = [&](const v4u& w_in, const Ops& o) {
-        const v4i w0 = unpack8_x16(w_in[0], w_in[1]);
-        const v4i w1 = unpack8_x16(w_in[2], w_in[3]);
-        v4i acc = {0, 0, 0, 0};
-        acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(o.a0, w0, acc, 0, 0, 0);
-        acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(o.a1, w1, acc, 0, 0, 0);
+    // FOLD: the staged sa carries the 2^-8 and the dot is taken as 256 d.
+    auto main_loop = [&](auto FOLD) {
+        auto consume = [&](const v4u& w_in, const Ops& o) {
+            const v4i w0 = unpack8_x16(w_in[0], w_in[1]);
+            const v4i w1 = unpack8_x16(w_in[2], w_in[3]);
+            v4i acc = {0, 0, 0, 0};
+            acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(o.a0, w0, acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(o.a1, w1, acc, 0, 0, 0);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const float d = (float)(acc[i] >> 8);
-            total[i] = SW_GROUPED ? __builtin_fmaf(d, o.s_a[i] * o.s_w, total[i]) : __builtin_fmaf(d, o.s_a[i], total[i]);
+            for (int i = 0; i < 4; ++i) {
+                const float d = FOLD ? (float)acc[i] : (float)(acc[i] >> 8);
+                total[i] = SW_GROUPED ? __builtin_fmaf(d, o.s_a[i] * o.s_w, total[i])
+                                      : __builtin_fmaf(d, o.s_a[i], total[i]);
+            }
+        };
+        Ops cur;
+        lds_ops(0, cur);
+        int g0 = 0;
+        for (; g0 + D < G; g0 += D) {
+            static_for<0, D>([&](auto U) {
+                Ops nxt;
+                lds_ops(g0 + U + 1, nxt);  // g0 + U + 1 < G inside the loop
+                __builtin_amdgcn_sched_barrier(0);
+                consume(rw[U], cur);
+                issue(g0 + U + D, rw[U]);
+                cur = nxt;
+            });
         }
-    };
-
-    Ops cur;
-    lds_ops(0, cur);
-    int g0 = 0;
-    for (; g0 + D < G; g0 += D) {
         static_for<0, D>([&](auto U) {
-            Ops nxt;
-            lds_ops(g0 + U + 1, nxt);  // g0 + U + 1 < G inside the loop
-            __builtin_amdgcn_sched_barrier(0);
-            consume(rw[U], cur);
-            issue(g0 + U + D, rw[U]);
-            cur = nxt;
+            if (g0 + U < G) {
+                Ops nxt;
+                lds_ops(min(g0 + U + 1, G - 1), nxt);
+                __builtin_amdgcn_sched_barrier(0);
+                consume(rw[U], cur);
+                cur = nxt;
+            }
         });
-    }
-    static_for<0, D>([&](auto U) {
-        if (g0 + U < G) {
-            Ops nxt;
-            lds_ops(min(g0 + U + 1, G - 1), nxt);
-            __builtin_amdgcn_sched_barrier(0);
-            consume(rw[U], cur);
-            cur = nxt;
+    };
+    if constexpr (CBW < 8) {
+        if (fold) {
+            main_loop(std::true_type{});
+        } else {
+            main_loop(std::false_type{});
         }
-    });
+    } else {
+        main_loop(std::false_type{});
+    }
 
     if (col < N) {
         float swn = 1.0f;
@@ -502,7 +572,7 @@ k2_wide(const int8_t* __restrict__ a, const int8_t* __restrict__ w,
     }
 }
 
-template <int MB, bool TW, bool SG, bool OF>
+template <int MB, bool TW, bool RT, bool SG, bool OF>
 hipError_t launch_dec(const int8_t* a, const int8_t* w, const void* sa, const void* sw, void* out,
                       int M, int N, int K, hipStream_t st) {
     const int blocks = (N + 15) / 16;
@@ -514,13 +584,13 @@ hipError_t launch_dec(const int8_t* a, const int8_t* w, const void* sa, const vo
     // with more column blocks than CUs, two 8-wave workgroups share a CU.
     if constexpr (MB <= 2) {
         if (K >= 2048 && blocks <= device_cu_count()) {
-            hipLaunchKernelGGL((k2_dec<MB, 16, 2, TW, SG, OF>), grid, dim3(16 * 64), 0, st, a, w, sap, swp, out, M,
+            hipLaunchKernelGGL((k2_dec<MB, 16, 2, TW, RT, SG, OF>), grid, dim3(16 * 64), 0, st, a, w, sap, swp, out, M,
                                N, K);
             return hipGetLastError();
         }
     }
     constexpr int D = 4;  // rounds in flight: all of them for K <= 4096
-    hipLaunchKernelGGL((k2_dec<MB, 8, D, TW, SG, OF>), grid, dim3(8 * 64), 0, st, a, w, sap, swp, out, M, N, K);
+    hipLaunchKernelGGL((k2_dec<MB, 8, D, TW, RT, SG, OF>), grid, dim3(8 * 64), 0, st, a, w, sap, swp, out, M, N, K);
     return hipGetLastError();
 }
 
@@ -535,24 +605,24 @@ bool wide_fits(int M, int N, int K) {
            (int64_t)(K / 128) * 16 * (per_cu <= 4 ? 4 : per_cu <= 6 ? 6 : 8) <= WIDE_WSCALES;
 }
 
-template <int MB, int CBW, bool TW, bool SG, bool OF>
+template <int MB, int CBW, bool TW, bool RT, bool SG, bool OF>
 hipError_t launch_wide_cbw(const int8_t* a, const int8_t* w, const void* sa, const void* sw, void* out,
                            int M, int N, int K, hipStream_t st) {
     constexpr int D = 8;  // groups in flight per wave
     const int ncb = (N + 15) / 16;
-    hipLaunchKernelGGL((k2_wide<MB, CBW, D, TW, SG, OF>), dim3((unsigned)((ncb + CBW - 1) / CBW)), dim3(CBW * MB * 64),
+    hipLaunchKernelGGL((k2_wide<MB, CBW, D, TW, RT, SG, OF>), dim3((unsigned)((ncb + CBW - 1) / CBW)), dim3(CBW * MB * 64),
                        0, st, a, w, static_cast<const uint16_t*>(sa), static_cast<const uint16_t*>(sw), out, M, N, K);
     return hipGetLastError();
 }
 
-template <int MB, bool TW, bool SG, bool OF>
+template <int MB, bool TW, bool RT, bool SG, bool OF>
 hipError_t launch_wide(const int8_t* a, const int8_t* w, const void* sa, const void* sw, void* out,
                        int M, int N, int K, hipStream_t st) {
     // Column blocks per workgroup: enough that one workgroup per CU covers N.
     const int per_cu = ((N + 15) / 16 + device_cu_count() - 1) / device_cu_count();
-    if (per_cu <= 4) return launch_wide_cbw<MB, 4, TW, SG, OF>(a, w, sa, sw, out, M, N, K, st);
-    if (per_cu <= 6) return launch_wide_cbw<MB, 6, TW, SG, OF>(a, w, sa, sw, out, M, N, K, st);
-    return launch_wide_cbw<MB, 8, TW, SG, OF>(a, w, sa, sw, out, M, N, K, st);
+    if (per_cu <= 4) return launch_wide_cbw<MB, 4, TW, RT, SG, OF>(a, w, sa, sw, out, M, N, K, st);
+    if (per_cu <= 6) return launch_wide_cbw<MB, 6, TW, RT, SG, OF>(a, w, sa, sw, out, M, N, K, st);
+    return launch_wide_cbw<MB, 8, TW, RT, SG, OF>(a, w, sa, sw, out, M, N, K, st);
 }
 
 template <bool TW, bool SG, bool OF>
@@ -560,14 +630,26 @@ hipError_t dispatch(const int8_t* a, const int8_t* w, const void* sa, const void
                     int M, int N, int K, hipStream_t st) {
     // Wide N: waves own column blocks, activations fetched once per CU.
     if (wide_fits(M, N, K)) {
-        return M <= 16 ? launch_wide<1, TW, SG, OF>(a, w, sa, sw, out, M, N, K, st)
-                       : launch_wide<2, TW, SG, OF>(a, w, sa, sw, out, M, N, K, st);
+        return M <= 16 ? launch_wide<1, TW, false, SG, OF>(a, w, sa, sw, out, M, N, K, st)
+                       : launch_wide<2, TW, false, SG, OF>(a, w, sa, sw, out, M, N, K, st);
     }
-    if (M <= 16) return launch_dec<1, TW, SG, OF>(a, w, sa, sw, out, M, N, K, st);
-    if (M <= 32) return launch_dec<2, TW, SG, OF>(a, w, sa, sw, out, M, N, K, st);
-    if (M <= 48) return launch_dec<3, TW, SG, OF>(a, w, sa, sw, out, M, N, K, st);
-    if (M <= 64) return launch_dec<4, TW, SG, OF>(a, w, sa, sw, out, M, N, K, st);
+    if (M <= 16) return launch_dec<1, TW, false, SG, OF>(a, w, sa, sw, out, M, N, K, st);
+    if (M <= 32) return launch_dec<2, TW, false, SG, OF>(a, w, sa, sw, out, M, N, K, st);
+    if (M <= 48) return launch_dec<3, TW, false, SG, OF>(a, w, sa, sw, out, M, N, K, st);
+    if (M <= 64) return launch_dec<4, TW, false, SG, OF>(a, w, sa, sw, out, M, N, K, st);
     return k2_prefill_launch(a, w, sa, sw, SG, out, OF, TW, M, N, K, st);
+}
+
+// Row-tiled activations (M <= 32) on tiled weights.
+template <bool SG, bool OF>
+hipError_t dispatch_rt(const int8_t* a, const int8_t* w, const void* sa, const void* sw, void* out,
+                       int M, int N, int K, hipStream_t st) {
+    if (wide_fits(M, N, K)) {
+        return M <= 16 ? launch_wide<1, true, true, SG, OF>(a, w, sa, sw, out, M, N, K, st)
+                       : launch_wide<2, true, true, SG, OF>(a, w, sa, sw, out, M, N, K, st);
+    }
+    return M <= 16 ? launch_dec<1, true, true, SG, OF>(a, w, sa, sw, out, M, N, K, st)
+                   : launch_dec<2, true, true, SG, OF>(a, w, sa, sw, out, M, N, K, st);
 }
 
 // MFMA-tiled weight layout <-> reference layout [N][K/2]: 16-byte unit
@@ -590,10 +672,11 @@ tile_weights(const int8_t* __restrict__ src, int8_t* __restrict__ dst, int64_t u
 }
 
 int gemm_impl(const int8_t* a, const int8_t* w, const void* sa, const void* sw, int sw_grouped, void* out,
-              int out_fp32, bool tiled, int64_t M, int64_t N, int64_t K, void* stream) {
+              int out_fp32, bool tiled, bool rowtiled, int64_t M, int64_t N, int64_t K, void* stream) {
     if (!a || !w || !sa || !sw || !out) return NV4_E_NULL;
     if (M < 1 || N < 1 || K < 128 || K % 128 || N % 8 || (tiled && N % 16)) return NV4_E_SHAPE;
     if (M > 0x7fffffffLL || N > 0x7fffffffLL || K > (1LL << 20)) return NV4_E_SHAPE;
+    if (rowtiled && (M > 32 || !tiled)) return NV4_E_SHAPE;
     if (M * (K / 128) > 0x7fffffffLL || N * (K / 128) > 0x7fffffffLL) return NV4_E_SHAPE;
     if (((M + 127) / 128) * ((N + 127) / 128) > 0x7fffffffLL) return NV4_E_SHAPE;
     if (reinterpret_cast<uintptr_t>(a) % 16 || reinterpret_cast<uintptr_t>(w) % 16 ||
@@ -603,7 +686,14 @@ int gemm_impl(const int8_t* a, const int8_t* w, const void* sa, const void* sw, 
     hipStream_t st = static_cast<hipStream_t>(stream);
     const int m = (int)M, n = (int)N, k = (int)K;
     hipError_t e;
-    if (tiled) {
+    if (rowtiled) {
+        if (sw_grouped)
+            e = out_fp32 ? dispatch_rt<true, true>(a, w, sa, sw, out, m, n, k, st)
+                         : dispatch_rt<true, false>(a, w, sa, sw, out, m, n, k, st);
+        else
+            e = out_fp32 ? dispatch_rt<false, true>(a, w, sa, sw, out, m, n, k, st)
+                         : dispatch_rt<false, false>(a, w, sa, sw, out, m, n, k, st);
+    } else if (tiled) {
         if (sw_grouped)
             e = out_fp32 ? dispatch<true, true, true>(a, w, sa, sw, out, m, n, k, st)
                          : dispatch<true, true, false>(a, w, sa, sw, out, m, n, k, st);
@@ -622,13 +712,16 @@ int gemm_impl(const int8_t* a, const int8_t* w, const void* sa, const void* sw, 
 }
 
 int linear_impl(const void* x, const int8_t* signs, const int8_t* w, const void* sw, void* out,
-                int8_t* a_packed, void* a_scale, bool tiled, int64_t M, int64_t N, int64_t K, void* stream) {
+                int8_t* a_packed, void* a_scale, bool tiled, bool rowtiled, int64_t M, int64_t N, int64_t K,
+                void* stream) {
     if (!x || !signs || !w || !sw || !out || !a_packed || !a_scale) return NV4_E_NULL;
     if (K != 4096 && K != 12288) return NV4_E_SHAPE;
     if (N < 1 || N % 8 || (tiled && N % 16)) return NV4_E_SHAPE;  // checked before K1 runs
-    const int rc = nv4_rht_quant_pack(x, signs, a_packed, a_scale, M, K, NV4_LAYOUT_REFERENCE, stream);
+    if (rowtiled && (M < 1 || M > 32)) return NV4_E_SHAPE;
+    const int rc = rowtiled ? nv4_rht_quant_pack_rowtiled(x, signs, a_packed, a_scale, M, K, stream)
+                            : nv4_rht_quant_pack(x, signs, a_packed, a_scale, M, K, NV4_LAYOUT_REFERENCE, stream);
     if (rc != NV4_OK) return rc;
-    return gemm_impl(a_packed, w, a_scale, sw, 1, out, 0, tiled, M, N, K, stream);
+    return gemm_impl(a_packed, w, a_scale, sw, 1, out, 0, tiled, rowtiled, M, N, K, stream);
 }
 
 int tile_impl(const int8_t* src, int8_t* dst, bool to_tiled, int64_t N, int64_t K, void* stream) {
@@ -652,25 +745,37 @@ int tile_impl(const int8_t* src, int8_t* dst, bool to_tiled, int64_t N, int64_t 
 extern "C" int nv4_w4a4_linear(const void* x, const int8_t* signs, const int8_t* w, const void* sw,
                                void* out, int8_t* a_packed, void* a_scale,
                                int64_t M, int64_t N, int64_t K, void* stream) {
-    return nv4::linear_impl(x, signs, w, sw, out, a_packed, a_scale, false, M, N, K, stream);
+    return nv4::linear_impl(x, signs, w, sw, out, a_packed, a_scale, false, false, M, N, K, stream);
 }
 
 extern "C" int nv4_w4a4_linear_tiled(const void* x, const int8_t* signs, const int8_t* w_tiled, const void* sw,
                                      void* out, int8_t* a_packed, void* a_scale,
                                      int64_t M, int64_t N, int64_t K, void* stream) {
-    return nv4::linear_impl(x, signs, w_tiled, sw, out, a_packed, a_scale, true, M, N, K, stream);
+    return nv4::linear_impl(x, signs, w_tiled, sw, out, a_packed, a_scale, true, false, M, N, K, stream);
+}
+
+extern "C" int nv4_w4a4_linear_rowtiled(const void* x, const int8_t* signs, const int8_t* w_tiled, const void* sw,
+                                        void* out, int8_t* a_packed_rt, void* a_scale,
+                                        int64_t M, int64_t N, int64_t K, void* stream) {
+    return nv4::linear_impl(x, signs, w_tiled, sw, out, a_packed_rt, a_scale, true, true, M, N, K, stream);
 }
 
 extern "C" int nv4_w4a4_gemm(const int8_t* a, const int8_t* w, const void* sa, const void* sw,
                              int sw_grouped, void* out, int out_fp32,
                              int64_t M, int64_t N, int64_t K, void* stream) {
-    return nv4::gemm_impl(a, w, sa, sw, sw_grouped, out, out_fp32, false, M, N, K, stream);
+    return nv4::gemm_impl(a, w, sa, sw, sw_grouped, out, out_fp32, false, false, M, N, K, stream);
 }
 
 extern "C" int nv4_w4a4_gemm_tiled(const int8_t* a, const int8_t* w_tiled, const void* sa, const void* sw,
                                    int sw_grouped, void* out, int out_fp32,
                                    int64_t M, int64_t N, int64_t K, void* stream) {
-    return nv4::gemm_impl(a, w_tiled, sa, sw, sw_grouped, out, out_fp32, true, M, N, K, stream);
+    return nv4::gemm_impl(a, w_tiled, sa, sw, sw_grouped, out, out_fp32, true, false, M, N, K, stream);
+}
+
+extern "C" int nv4_w4a4_gemm_rowtiled(const int8_t* a_rt, const int8_t* w_tiled, const void* sa, const void* sw,
+                                      int sw_grouped, void* out, int out_fp32,
+                                      int64_t M, int64_t N, int64_t K, void* stream) {
+    return nv4::gemm_impl(a_rt, w_tiled, sa, sw, sw_grouped, out, out_fp32, true, true, M, N, K, stream);
 }
 
 extern "C" int nv4_w4a4_tile_weights(const int8_t* w, int8_t* w_tiled, int64_t N, int64_t K, void* stream) {

@@ -124,22 +124,25 @@ def silu_mul(gate_up, out=None):
     return out
 
 
-def _k1_outputs(M, K, dev, out_packed, out_scale):
+def _k1_outputs(M, K, dev, out_packed, out_scale, rowtiled=False):
+    rows = (M + 15) // 16 * 16 if rowtiled else M
     if out_packed is None:
-        out_packed = torch.empty((M, K // 2), dtype=torch.int8, device=dev)
+        out_packed = torch.empty((rows, K // 2), dtype=torch.int8, device=dev)
     if out_scale is None:
         out_scale = torch.empty((M, K // 128), dtype=torch.bfloat16, device=dev)
-    if (tuple(out_packed.shape) != (M, K // 2) or out_packed.dtype != torch.int8 or not out_packed.is_contiguous()
+    if (tuple(out_packed.shape) != (rows, K // 2) or out_packed.dtype != torch.int8 or not out_packed.is_contiguous()
             or tuple(out_scale.shape) != (M, K // 128) or out_scale.dtype != torch.bfloat16
             or not out_scale.is_contiguous()):
         raise ValueError("Outputs must be contiguous INT8 [M,K/2] and BF16 [M,K/128]")
     return out_packed, out_scale
 
 
-def rmsnorm_rht_quant_pack(x, weight, eps, signs, residual=None, out_packed=None, out_scale=None):
+def rmsnorm_rht_quant_pack(x, weight, eps, signs, residual=None, out_packed=None, out_scale=None, rowtiled=False):
     """x bf16 [M, 4096] -> (packed, scale) of rht_quant_pack(rmsnorm(x)); with
     ``residual`` the norm input is x + residual, whose bf16 rounding is written
-    into ``residual`` and returned as a third element."""
+    into ``residual`` and returned as a third element.  ``rowtiled``: the codes
+    in the row-tiled order of ``rht_quant_pack_rowtiled`` ([ceil(M/16)*16, K/2],
+    read by ``w4a4_gemm_rowtiled``)."""
     if x.ndim != 2 or x.shape[1] != 4096 or x.dtype != torch.bfloat16 or not x.is_contiguous():
         raise ValueError("Expected contiguous BF16 x[M,4096]")
     if weight.dtype != torch.bfloat16 or tuple(weight.shape) != (4096,) or signs.dtype != torch.int8 \
@@ -150,21 +153,22 @@ def rmsnorm_rht_quant_pack(x, weight, eps, signs, residual=None, out_packed=None
         raise ValueError("residual must match x")
     M, K = x.shape
     dev = x.device
-    out_packed, out_scale = _k1_outputs(M, K, dev, out_packed, out_scale)
+    out_packed, out_scale = _k1_outputs(M, K, dev, out_packed, out_scale, rowtiled)
     _check_dev((x, weight, signs, residual, out_packed, out_scale), dev)
     lib = _lib.load()
     stream = torch.cuda.current_stream(dev).cuda_stream
+    fn = lib.nv4_rmsnorm_rht_quant_pack_rowtiled if rowtiled else lib.nv4_rmsnorm_rht_quant_pack
     with torch.cuda.device(dev):
-        rc = lib.nv4_rmsnorm_rht_quant_pack(_ptr(x), _ptr(residual), _ptr(residual), _ptr(weight),
-                                            ctypes.c_float(eps), _ptr(signs), _ptr(out_packed), _ptr(out_scale),
-                                            M, K, ctypes.c_void_p(stream))
+        rc = fn(_ptr(x), _ptr(residual), _ptr(residual), _ptr(weight),
+                ctypes.c_float(eps), _ptr(signs), _ptr(out_packed), _ptr(out_scale), M, K, ctypes.c_void_p(stream))
     _lib.check(rc, "rmsnorm_rht_quant_pack")
     return (out_packed, out_scale) if residual is None else (out_packed, out_scale, residual)
 
 
-def silu_mul_rht_quant_pack(gate_up, signs, out_packed=None, out_scale=None):
+def silu_mul_rht_quant_pack(gate_up, signs, out_packed=None, out_scale=None, rowtiled=False):
     """gate_up bf16 [M, 2K] (K = 4096 or 12288) -> (packed, scale) of
-    rht_quant_pack(silu_mul(gate_up))."""
+    rht_quant_pack(silu_mul(gate_up)); ``rowtiled`` as in
+    ``rmsnorm_rht_quant_pack``."""
     if gate_up.ndim != 2 or gate_up.dtype != torch.bfloat16 or not gate_up.is_contiguous() \
             or gate_up.shape[1] not in (8192, 24576):
         raise ValueError("Expected contiguous BF16 gate_up[M,2K], K = 4096 or 12288")
@@ -172,12 +176,12 @@ def silu_mul_rht_quant_pack(gate_up, signs, out_packed=None, out_scale=None):
     if signs.dtype != torch.int8 or tuple(signs.shape) != (K,):
         raise TypeError("Expected int8 signs [K]")
     dev = gate_up.device
-    out_packed, out_scale = _k1_outputs(M, K, dev, out_packed, out_scale)
+    out_packed, out_scale = _k1_outputs(M, K, dev, out_packed, out_scale, rowtiled)
     _check_dev((gate_up, signs, out_packed, out_scale), dev)
     lib = _lib.load()
     stream = torch.cuda.current_stream(dev).cuda_stream
+    fn = lib.nv4_silu_mul_rht_quant_pack_rowtiled if rowtiled else lib.nv4_silu_mul_rht_quant_pack
     with torch.cuda.device(dev):
-        rc = lib.nv4_silu_mul_rht_quant_pack(_ptr(gate_up), _ptr(signs), _ptr(out_packed), _ptr(out_scale), M, K,
-                                             ctypes.c_void_p(stream))
+        rc = fn(_ptr(gate_up), _ptr(signs), _ptr(out_packed), _ptr(out_scale), M, K, ctypes.c_void_p(stream))
     _lib.check(rc, "silu_mul_rht_quant_pack")
     return out_packed, out_scale

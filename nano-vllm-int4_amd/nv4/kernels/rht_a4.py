@@ -103,3 +103,40 @@ def rht_quant_pack(x, signs, *, out_packed, out_scale, config=None, layout="refe
         _validate_config(config)
     _launch(x, signs, out_packed, out_scale, lay)
     return out_packed, out_scale
+
+
+def rowtiled_rows(m):
+    """Rows of a row-tiled packed-activation buffer for M rows (16-row blocks)."""
+    return (m + 15) // 16 * 16
+
+
+def rht_quant_pack_rowtiled(x, signs, *, out_packed=None, out_scale=None):
+    """``rht_quant_pack`` with the packed codes in the row-tiled order that the
+    decode GEMM reads (``nv4_rht_quant_pack_rowtiled``): out_packed int8
+    [ceil(M/16)*16, K/2] holds the same codes as the [M,K/2] form, in 1 KiB
+    blocks of 16 rows x 128 k in matrix-core lane order; out_scale bf16
+    [M,K/128] as usual.  Returns (out_packed, out_scale)."""
+    if x.ndim != 2 or x.dtype != torch.bfloat16 or x.shape[1] not in (4096, 12288) or x.shape[0] < 1:
+        raise ValueError('Expected BF16 X[M,K], M>0, K=4096/12288')
+    m, k = x.shape
+    if signs.shape != (k,) or signs.dtype != torch.int8:
+        raise ValueError('Expected INT8 signs[K]')
+    if out_packed is None:
+        out_packed = torch.empty((rowtiled_rows(m), k // 2), dtype=torch.int8, device=x.device)
+    if out_scale is None:
+        out_scale = torch.empty((m, k // 128), dtype=torch.bfloat16, device=x.device)
+    if tuple(out_packed.shape) != (rowtiled_rows(m), k // 2) or out_packed.dtype != torch.int8:
+        raise ValueError('Expected INT8 row-tiled output[ceil(M/16)*16,K/2]')
+    if tuple(out_scale.shape) != (m, k // 128) or out_scale.dtype != torch.bfloat16:
+        raise ValueError('Expected BF16 scales[M,K/128]')
+    if any(not t.is_cuda or not t.is_contiguous() or t.device != x.device
+           for t in [x, signs, out_packed, out_scale]):
+        raise ValueError('All tensors must be contiguous on one CUDA device')
+    lib = _lib.load()
+    stream = torch.cuda.current_stream(x.device).cuda_stream
+    with torch.cuda.device(x.device):
+        rc = lib.nv4_rht_quant_pack_rowtiled(ctypes.c_void_p(x.data_ptr()), ctypes.c_void_p(signs.data_ptr()),
+                                             ctypes.c_void_p(out_packed.data_ptr()),
+                                             ctypes.c_void_p(out_scale.data_ptr()), m, k, ctypes.c_void_p(stream))
+    _lib.check(rc, "rht_quant_pack_rowtiled")
+    return out_packed, out_scale

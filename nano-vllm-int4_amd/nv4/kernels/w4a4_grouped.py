@@ -253,3 +253,45 @@ def w4a4_grouped_gemm(a_packed, w_packed, a_scale, w_scale, out=None, config=Non
     _launch(a_packed, w_packed, a_scale, w_scale, out, False, weight_grouped, weights_tiled, path=path,
             weights_f6=weights_f6)
     return out
+
+
+# Largest M of the row-tiled decode GEMM (nv4_w4a4_gemm_rowtiled).
+ROWTILED_MAX_M = 32
+
+
+def w4a4_gemm_rowtiled(a_rt, w_tiled, a_scale, w_scale, out=None, *, output_fp32=False):
+    """``w4a4_grouped_gemm`` for decode-sized M (1..32) on row-tiled packed
+    activations (``rht_quant_pack_rowtiled``: int8 [ceil(M/16)*16, K/2]) and
+    tiled weights (``tile_weights``); M is taken from ``a_scale`` [M, K/128].
+    Bit-identical to the reference-layout call."""
+    if a_scale.ndim != 2 or w_tiled.ndim != 2 or a_rt.ndim != 2:
+        raise ValueError("Expected Sa[M,K/128], tiled weights [N,K/2] and row-tiled activations")
+    M, N, K = a_scale.shape[0], w_tiled.shape[0], w_tiled.shape[1] * 2
+    if a_rt.dtype != torch.int8 or w_tiled.dtype != torch.int8:
+        raise TypeError("Packed inputs must use int8 storage")
+    if a_scale.dtype != torch.bfloat16 or w_scale.dtype != torch.bfloat16:
+        raise TypeError("Both scale tensors must be BF16")
+    if not 1 <= M <= ROWTILED_MAX_M or K % GROUP_SIZE or N % 16 or K < GROUP_SIZE:
+        raise ValueError("Require 1 <= M <= 32, K divisible by 128 and N divisible by 16")
+    if tuple(a_rt.shape) != ((M + 15) // 16 * 16, K // 2) or tuple(a_scale.shape) != (M, K // GROUP_SIZE):
+        raise ValueError("Require row-tiled activations [ceil(M/16)*16,K/2] and Sa[M,K/128]")
+    weight_grouped = w_scale.ndim == 2
+    if tuple(w_scale.shape) != ((N, K // GROUP_SIZE) if weight_grouped else (N,)):
+        raise ValueError("Require Sw[N] or Sw[N,K/128]")
+    dtype = torch.float32 if output_fp32 else torch.bfloat16
+    if out is None:
+        out = torch.empty((M, N), device=a_rt.device, dtype=dtype)
+    if tuple(out.shape) != (M, N) or out.dtype != dtype:
+        raise ValueError("Output must be [M,N] of the requested dtype")
+    if any(not t.is_cuda or not t.is_contiguous() or t.device != a_rt.device
+           for t in (a_rt, w_tiled, a_scale, w_scale, out)):
+        raise ValueError("All tensors must be contiguous CUDA tensors on one device")
+    lib = _lib.load()
+    stream = torch.cuda.current_stream(a_rt.device).cuda_stream
+    with torch.cuda.device(a_rt.device):
+        rc = lib.nv4_w4a4_gemm_rowtiled(ctypes.c_void_p(a_rt.data_ptr()), ctypes.c_void_p(w_tiled.data_ptr()),
+                                        ctypes.c_void_p(a_scale.data_ptr()), ctypes.c_void_p(w_scale.data_ptr()),
+                                        1 if weight_grouped else 0, ctypes.c_void_p(out.data_ptr()),
+                                        1 if output_fp32 else 0, M, N, K, ctypes.c_void_p(stream))
+    _lib.check(rc, "w4a4_gemm_rowtiled")
+    return out

@@ -5,7 +5,10 @@ is ``rht_quant_pack`` followed by ``w4a4_grouped_gemm``.  ``w4a4_linear`` runs
 the same two HIP kernels back to back through one C ABI call
 (``nv4_w4a4_linear``) on torch's current stream, so it can be captured in a
 HIP graph; the quantized activations are returned through ``out_packed`` /
-``out_scale`` (allocated when not given).  Prefill-sized M
+``out_scale`` (allocated when not given).  With tiled weights, M <= 32 and
+no ``out_packed`` given, K1 writes the codes in the row-tiled order and the
+decode GEMM reads them from there (``nv4_w4a4_linear_rowtiled``, same bits).
+Prefill-sized M
 (``use_prefill_path``) runs K1 and then the fp6 matrix-core GEMM
 (``nv4_w4a4_gemm_f6``, same bits).
 """
@@ -16,8 +19,8 @@ import ctypes
 import torch
 
 from .. import _lib
-from .rht_a4 import rht_quant_pack
-from .w4a4_grouped import _check_weights_f6, _launch, use_prefill_path
+from .rht_a4 import rht_quant_pack, rowtiled_rows
+from .w4a4_grouped import ROWTILED_MAX_M, _check_weights_f6, _launch, use_prefill_path
 
 
 def w4a4_linear(x, signs, w_packed, w_scale, *, out=None, out_packed=None, out_scale=None, weights_tiled=False,
@@ -43,11 +46,16 @@ def w4a4_linear(x, signs, w_packed, w_scale, *, out=None, out_packed=None, out_s
     dev = x.device
     if out is None:
         out = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+    # Decode-sized M whose codes only the GEMM needs: K1 writes them in the
+    # row-tiled order that the decode GEMM loads straight into registers
+    # (same bits).
+    rowtiled = weights_tiled and M <= ROWTILED_MAX_M and out_packed is None
     if out_packed is None:
-        out_packed = torch.empty((M, K // 2), dtype=torch.int8, device=dev)
+        out_packed = torch.empty((rowtiled_rows(M) if rowtiled else M, K // 2), dtype=torch.int8, device=dev)
     if out_scale is None:
         out_scale = torch.empty((M, K // 128), dtype=torch.bfloat16, device=dev)
-    if (tuple(out.shape) != (M, N) or out.dtype != torch.bfloat16 or tuple(out_packed.shape) != (M, K // 2)
+    if (tuple(out.shape) != (M, N) or out.dtype != torch.bfloat16
+            or tuple(out_packed.shape) != ((rowtiled_rows(M) if rowtiled else M), K // 2)
             or out_packed.dtype != torch.int8 or tuple(out_scale.shape) != (M, K // 128)
             or out_scale.dtype != torch.bfloat16):
         raise ValueError("Outputs must be BF16 [M,N], INT8 [M,K/2] and BF16 [M,K/128]")
@@ -64,6 +72,8 @@ def w4a4_linear(x, signs, w_packed, w_scale, *, out=None, out_packed=None, out_s
     lib = _lib.load()
     stream = torch.cuda.current_stream(dev).cuda_stream
     fn = lib.nv4_w4a4_linear_tiled if weights_tiled else lib.nv4_w4a4_linear
+    if rowtiled:
+        fn = lib.nv4_w4a4_linear_rowtiled
     with torch.cuda.device(dev):
         rc = fn(ctypes.c_void_p(x.data_ptr()), ctypes.c_void_p(signs.data_ptr()),
                 ctypes.c_void_p(w_packed.data_ptr()), ctypes.c_void_p(w_scale.data_ptr()),

@@ -24,7 +24,8 @@ import torch
 from torch import nn
 import torch.distributed as dist
 
-from ..kernels.w4a4_grouped import keep_weights_f6, tile_weights, untile_weights, w4a4_grouped_gemm, weights_to_f6
+from ..kernels.w4a4_grouped import (ROWTILED_MAX_M, keep_weights_f6, tile_weights, untile_weights, w4a4_gemm_rowtiled,
+                                   w4a4_grouped_gemm, weights_to_f6)
 from ..kernels.w4a4_linear import w4a4_linear
 
 
@@ -110,10 +111,20 @@ class W4A4Linear(nn.Module):
                           weights_f6=self._f6())
         return out.reshape(*x.shape[:-1], self.out_features)
 
-    def forward_quantized(self, packed: torch.Tensor, scale: torch.Tensor) -> torch.Tensor:
+    def uses_rowtiled(self, m: int) -> bool:
+        """Whether a call with M rows takes the row-tiled decode path
+        (tiled weights and M <= 32), so its producer should quantize with
+        ``rowtiled=True``."""
+        return self.weights_tiled and m <= ROWTILED_MAX_M
+
+    def forward_quantized(self, packed: torch.Tensor, scale: torch.Tensor, rowtiled: bool = False) -> torch.Tensor:
         """The GEMM half of ``forward`` on activations already quantized by
         ``rht_quant_pack`` (or a fused producer + K1: ``nv4.kernels.decoder_ops``)
         with this module's signs: packed int8 [M, in/2], scale bf16 [M, in/128]
-        -> bf16 [M, out]."""
+        -> bf16 [M, out].  ``rowtiled``: the codes are in the row-tiled order
+        ([ceil(M/16)*16, in/2], ``rht_quant_pack_rowtiled``; needs
+        ``uses_rowtiled(M)``)."""
+        if rowtiled:
+            return w4a4_gemm_rowtiled(packed, self.packed_weight, scale, self.weight_scale)
         return w4a4_grouped_gemm(packed, self.packed_weight, scale, self.weight_scale,
                                  weights_tiled=self.weights_tiled, weights_f6=self._f6())

@@ -197,10 +197,13 @@ class Qwen3MLP(nn.Module):
     def forward_fused(self, x, residual, norm):
         """W4A4: post-attention add+RMSNorm inside gate_up's quantization,
         SiLU-mul inside down's; returns (output, residual)."""
-        packed, scale, residual = rmsnorm_rht_quant_pack(x, norm.weight, norm.eps, self.gate_up_proj.signs, residual)
-        gate_up = self.gate_up_proj.forward_quantized(packed, scale)
-        packed, scale = silu_mul_rht_quant_pack(gate_up, self.down_proj.signs)
-        return self.down_proj.forward_quantized(packed, scale), residual
+        rt = self.gate_up_proj.uses_rowtiled(x.shape[0])
+        packed, scale, residual = rmsnorm_rht_quant_pack(x, norm.weight, norm.eps, self.gate_up_proj.signs, residual,
+                                                         rowtiled=rt)
+        gate_up = self.gate_up_proj.forward_quantized(packed, scale, rowtiled=rt)
+        rt = self.down_proj.uses_rowtiled(x.shape[0])
+        packed, scale = silu_mul_rht_quant_pack(gate_up, self.down_proj.signs, rowtiled=rt)
+        return self.down_proj.forward_quantized(packed, scale, rowtiled=rt), residual
 
 
 class Qwen3DecoderLayer(nn.Module):
@@ -221,13 +224,15 @@ class Qwen3DecoderLayer(nn.Module):
         if self.fused:
             attn = self.self_attn
             norm = self.input_layernorm
+            rt = attn.qkv_proj.uses_rowtiled(hidden_states.shape[0])
             if residual is None:
-                packed, scale = rmsnorm_rht_quant_pack(hidden_states, norm.weight, norm.eps, attn.qkv_proj.signs)
+                packed, scale = rmsnorm_rht_quant_pack(hidden_states, norm.weight, norm.eps, attn.qkv_proj.signs,
+                                                       rowtiled=rt)
                 residual = hidden_states
             else:
                 packed, scale, residual = rmsnorm_rht_quant_pack(hidden_states, norm.weight, norm.eps,
-                                                                 attn.qkv_proj.signs, residual)
-            hidden_states = attn(positions, qkv=attn.qkv_proj.forward_quantized(packed, scale))
+                                                                 attn.qkv_proj.signs, residual, rowtiled=rt)
+            hidden_states = attn(positions, qkv=attn.qkv_proj.forward_quantized(packed, scale, rowtiled=rt))
             return self.mlp.forward_fused(hidden_states, residual, self.post_attention_layernorm)
         if residual is None:
             hidden_states, residual = self.input_layernorm(hidden_states), hidden_states

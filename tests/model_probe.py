@@ -33,6 +33,16 @@ from nv4.kernels.decoder_ops import rmsnorm, silu_mul
 from nv4.layers.linear_w4a4 import W4A4Linear
 
 
+def rowtiled_to_reference(packed, m):
+    """Row-tiled packed codes [ceil(M/16)*16, K/2] -> the [M, K/2] layout (torch,
+    same device): unit (rb*G + g)*64 + 16*part + r of the row-tiled buffer holds
+    bytes 64*g + 16*part .. +15 of row 16*rb + r."""
+    rows, kb = packed.shape
+    g = kb // 64
+    t = packed.reshape(rows // 16, g, 4, 16, 16).permute(0, 3, 1, 2, 4).reshape(rows, kb)
+    return t[:m].contiguous()
+
+
 class ProjectionProbe:
     def __init__(self, model, layer_ids):
         self.model = model
@@ -60,23 +70,26 @@ class ProjectionProbe:
                       "residual": None if residual is None else residual.clone()}
             out = rms_k1(x, weight, eps, signs, residual, **kw)
             inputs["residual_out"] = None if residual is None else out[2].clone()
-            probe.k1s.append((hit[0], "rmsnorm", inputs, out[0].clone(), out[1].clone()))
+            packed = rowtiled_to_reference(out[0], x.shape[0]) if kw.get("rowtiled") else out[0].clone()
+            probe.k1s.append((hit[0], "rmsnorm", inputs, packed, out[1].clone()))
             return out
 
         def silu_wrap(gate_up, signs, **kw):
             hit = probe._by_signs.get(signs.data_ptr())
             out = silu_k1(gate_up, signs, **kw)
             if hit is not None:
+                packed = rowtiled_to_reference(out[0], gate_up.shape[0]) if kw.get("rowtiled") else out[0].clone()
                 probe.k1s.append((hit[0], "silu_mul", {"gate_up": gate_up.clone(), "signs": signs},
-                                  out[0].clone(), out[1].clone()))
+                                  packed, out[1].clone()))
             return out
 
         qwen3.rmsnorm_rht_quant_pack, qwen3.silu_mul_rht_quant_pack = rms_wrap, silu_wrap
         self._patched = []
         for name, m in self._by_signs.values():
-            def fq(packed, scale, _m=m, _name=name, _orig=m.forward_quantized):
-                out = _orig(packed, scale)
-                probe.gemms.append((_name, _m, packed.clone(), scale.clone(), out.clone()))
+            def fq(packed, scale, rowtiled=False, _m=m, _name=name, _orig=m.forward_quantized):
+                out = _orig(packed, scale, rowtiled=rowtiled)
+                ref_packed = rowtiled_to_reference(packed, scale.shape[0]) if rowtiled else packed.clone()
+                probe.gemms.append((_name, _m, ref_packed, scale.clone(), out.clone()))
                 return out
             def fw(x, _m=m, _name=name, _orig=m.forward):
                 out = _orig(x)
