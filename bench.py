@@ -122,13 +122,43 @@ def make_layer_sets(torch, W, M, rotate, dev):
     return acts, sets
 
 
+def make_gemm_sets(torch, W, p, dev):
+    """Tiled weight sets (and scales) of one projection for its GEMM-alone
+    timing, drawn on the GPU with the workload recipe, rotation_sets(N, K)
+    of them."""
+    import nv4
+    N, K = W.PROJECTIONS[p]
+    g = torch.Generator(device=dev)
+    g.manual_seed(W.BASE_SEED + 5000 + N + K)
+    out = []
+    for _ in range(rotation_sets(N, K)):
+        wp = torch.randint(-128, 128, (N, K // 2), generator=g, device=dev, dtype=torch.int16).to(torch.int8)
+        sw = (0.005 + 0.015 * torch.rand(N, K // 128, generator=g, device=dev)).to(torch.bfloat16)
+        out.append((nv4.tile_weights(wp), sw))
+    return out
+
+
+STEPS_PER_GRAPH = 60
+
+
 # ------------------------------------------------------------- graph timing
+GRAPH_MIN_LAUNCHES = 48   # launches per captured graph (the list is repeated up to this)
+
+
 def graph_launch_us(torch, launches, replays):
     """Average microseconds per launch of ``launches`` (callables that each
     enqueue exactly one kernel on the current stream), captured back to back
-    in one HIP graph and replayed ``replays`` times between two HIP events on
-    the capturing stream.  Inside a graph consecutive kernels start as the
-    previous one ends, so this is kernel time, not host launch time."""
+    in one HIP graph and replayed between two HIP events on the capturing
+    stream.  Inside a graph consecutive kernels start as the previous one
+    ends, so this is kernel time, not host launch time.  The list is repeated
+    until the graph holds at least GRAPH_MIN_LAUNCHES launches (the replays
+    shrink to keep about ``replays`` x the original launch count): a graph of
+    a few short kernels replays faster on the GPU than the host can submit
+    it, and would otherwise time the host (an empty kernel measured 3.3 us per
+    launch in 6-launch graphs against 1.7 us in 48-launch ones)."""
+    rep = max(1, -(-GRAPH_MIN_LAUNCHES // len(launches)))
+    launches = list(launches) * rep
+    replays = max(2, -(-replays // rep))
     side = torch.cuda.Stream()
     side.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(side):
@@ -236,11 +266,21 @@ def measured_traffic():
     return rec
 
 
-def k2_medians(torch, gemm, R, rounds=9, replays=20):
+ROTATE_BYTES = 320 << 20   # distinct weight bytes a per-projection timing rotates through (> 256 MB MALL)
+
+
+def rotation_sets(N, K):
+    """Weight sets one projection's GEMM timing rotates through: enough that
+    their bytes exceed the 256 MB Infinity Cache, so every launch streams its
+    weights from HBM."""
+    return max(2, -(-ROTATE_BYTES // (N * K // 2 + N * K // 64)))
+
+
+def k2_medians(torch, gemm, nsets, rounds=9, replays=20):
     """Per projection, the median over ``rounds`` rounds of the decode GEMM's
-    microseconds per launch (a graph of back-to-back launches over the R
-    rotating weight sets, replayed between HIP events), the projections in a
-    freshly shuffled order every round."""
+    microseconds per launch (a graph of back-to-back launches over the
+    projection's ``nsets[p]`` rotating weight sets, replayed between HIP
+    events), the projections in a freshly shuffled order every round."""
     import random
     rng = random.Random(20261108)
     samples = {p: [] for p in PROJECTIONS}
@@ -248,7 +288,8 @@ def k2_medians(torch, gemm, R, rounds=9, replays=20):
     for _ in range(rounds):
         rng.shuffle(order)
         for p in order:
-            samples[p].append(graph_launch_us(torch, [lambda l=l, p=p: gemm(l, p) for l in range(R)], replays))
+            samples[p].append(graph_launch_us(torch, [lambda l=l, p=p: gemm(l, p) for l in range(nsets[p])],
+                                              replays))
     return {p: statistics.median(v) for p, v in samples.items()}
 
 
@@ -403,18 +444,22 @@ def main():
     if args.pmc_prefill:
         pmc_prefill(torch, W, dev)
         return
+    from nv4.kernels.rht_a4 import rowtiled_rows
+    from nv4.kernels.w4a4_grouped import ROWTILED_MAX_M, w4a4_gemm_rowtiled
+
     M, R = args.m, max(1, args.rotate)
+    # Decode-sized M runs as W4A4Linear runs it: K1 writes the codes in the
+    # row-tiled order that the decode GEMM reads.
+    rt = M <= ROWTILED_MAX_M
     acts, sets = make_layer_sets(torch, W, M, R, dev)
-    pk = {p: torch.empty((M, W.PROJECTIONS[p][1] // 2), dtype=torch.int8, device=dev) for p in PROJECTIONS}
+    pk = {p: torch.empty((rowtiled_rows(M) if rt else M, W.PROJECTIONS[p][1] // 2), dtype=torch.int8, device=dev)
+          for p in PROJECTIONS}
     sc = {p: torch.empty((M, W.PROJECTIONS[p][1] // 128), dtype=torch.bfloat16, device=dev) for p in PROJECTIONS}
     out = {p: torch.empty((M, W.PROJECTIONS[p][0]), dtype=torch.bfloat16, device=dev) for p in PROJECTIONS}
 
     def linear(l, p):  # W4A4Linear.forward: RHT+quant+pack, then the grouped GEMM (tiled weights)
         nv4.w4a4_linear(acts[p], sets[l][p][0], sets[l][p][1], sets[l][p][2],
-                        out=out[p], out_packed=pk[p], out_scale=sc[p], weights_tiled=True)
-
-    def gemm(l, p):  # the GEMM alone, on the codes the last linear call left in pk/sc
-        nv4.w4a4_grouped_gemm(pk[p], sets[l][p][1], sc[p], sets[l][p][2], out=out[p], weights_tiled=True)
+                        out=out[p], out_packed=pk[p], out_scale=sc[p], weights_tiled=True, packed_rowtiled=rt)
 
     def step(l):
         for p in PROJECTIONS:
@@ -423,6 +468,18 @@ def main():
     if args.pmc_pass:
         pmc_pass(torch, linear, R)
         return
+
+    # The GEMM alone, on the codes the last linear call left in pk/sc, over
+    # each projection's own rotation of weight sets (> 256 MB per projection).
+    k2sets = {p: make_gemm_sets(torch, W, p, dev) for p in PROJECTIONS}
+    nsets = {p: len(v) for p, v in k2sets.items()}
+
+    def gemm(l, p):
+        w, sw = k2sets[p][l]
+        if rt:
+            w4a4_gemm_rowtiled(pk[p], w, sc[p], sw, out=out[p])
+        else:
+            nv4.w4a4_grouped_gemm(pk[p], w, sc[p], sw, out=out[p], weights_tiled=True)
 
 
     # Eager reference outputs of set 0, then one graph per weight set.
@@ -447,22 +504,39 @@ def main():
         if not torch.equal(out[p].view(torch.int16), eager[p].view(torch.int16)):
             raise RuntimeError(f"graph replay of {p} differs from the eager launch")
 
-    for i in range(args.warmup):
-        graphs[i % R].replay()
+    del graphs
+    # Timed steps: graphs of up to STEPS_PER_GRAPH consecutive steps (weight
+    # set i % R for step i), so the GPU, not the host's graph submission,
+    # sets the pace; exactly --steps steps between the events.
+    chunk = min(args.steps, STEPS_PER_GRAPH)
+
+    def steps_graph(n):
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            for i in range(n):
+                step(i % R)
+        return g
+    g_chunk = steps_graph(chunk)
+    g_rem = steps_graph(args.steps % chunk) if args.steps % chunk else None
+    for _ in range(-(-args.warmup // chunk)):
+        g_chunk.replay()
     torch.cuda.synchronize()
     ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     ev0.record()
-    for i in range(args.steps):
-        graphs[i % R].replay()
+    for _ in range(args.steps // chunk):
+        g_chunk.replay()
+    if g_rem is not None:
+        g_rem.replay()
     ev1.record()
     torch.cuda.synchronize()
     ms_per_step = ev0.elapsed_time(ev1) / args.steps
     step_us = ms_per_step * 1e3
+    del g_chunk, g_rem
 
     # Dominant kernel: the decode GEMM, timed per projection over the rotating
     # weight sets (equal launch counts per projection, so the mean of the
     # per-projection averages is the kernel's average launch).
-    k2_us = k2_medians(torch, gemm, R, rounds=9, replays=20)
+    k2_us = k2_medians(torch, gemm, nsets, rounds=9, replays=20)
     avg_launch_us = statistics.mean(k2_us.values())
     avg_bytes = statistics.mean(k2_bytes(M, *W.PROJECTIONS[p]) for p in PROJECTIONS)
     achieved = avg_bytes / (avg_launch_us * 1e-6) / 1e9       # GB/s
@@ -491,17 +565,17 @@ def main():
             "M": M, "rotate": R,
         },
         "roofline": {
-            "kernel": ("decode grouped INT4 GEMM on MFMA-tiled weights (k2_dec for qkv/o/down, k2_wide for "
-                       "gate_up), M=32"),
+            "kernel": ("decode grouped INT4 GEMM on row-tiled activations and MFMA-tiled weights (k2_dec for "
+                       "qkv/o/down, k2_wide for gate_up), M=32"),
             "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
             "traffic": (traffic or {}).get("bytes_per_launch"),
             "traffic_source": (traffic or {}).get("source"),
             "avg_launch_us": round(avg_launch_us, 3), "algorithmic_bytes_per_launch": int(avg_bytes),
             "per_projection_us": {p: round(v, 3) for p, v in k2_us.items()},
-            "timing": (f"median over 9 rounds (projections in shuffled order each round) of HIP events "
-                       f"around 20 replays of a graph of {R} back-to-back launches per projection (one per "
-                       "weight set)"),
+            "timing": ("median over 9 rounds (projections in shuffled order each round) of HIP events "
+                       "around replays of a graph of >= 48 back-to-back launches per projection, cycling "
+                       f"through the projection's own weight sets ({nsets}, > 256 MB each)"),
         },
     }
 
@@ -512,7 +586,7 @@ def main():
         line["measured_peaks"] = peaks
     if not args.no_detail:
         line["detail"] = detail_table(torch, nv4, W, dev, R)
-    del graphs, sets, acts
+    del sets, acts, k2sets
     torch.cuda.empty_cache()
     if not args.no_e2e:
         line["e2e_decode"] = e2e_decode(torch, args.e2e_layers, args.e2e_tokens)
@@ -584,15 +658,18 @@ def detail_table(torch, nv4, W, dev, R):
     Cache), their roofline fractions, and the BF16 hipBLASLt GEMM (torch.mm)
     on the same shape; then the W4A16 GPTQ GEMM on the fused QKV at M = 1, 8,
     32 (fp16 activations, microseconds per call and HBM fraction)."""
-    from nv4.kernels.w4a4_grouped import keep_weights_f6
+    from nv4.kernels.rht_a4 import rht_quant_pack_rowtiled, rowtiled_rows
+    from nv4.kernels.w4a4_grouped import keep_weights_f6, w4a4_gemm_rowtiled
     res = {}
     g = torch.Generator(device=dev)
     g.manual_seed(W.BASE_SEED + 2000)
     for M in (32, 4096):
         reps = 20 if M == 32 else 3
-        rot = R if M == 32 else 2
         for p in PROJECTIONS:
             N, K = W.PROJECTIONS[p]
+            # Decode: the projection's own weights rotate past the Infinity
+            # Cache; prefill is matrix-core bound and rotates two sets.
+            rot = rotation_sets(N, K) if M == 32 else 2
             x = torch.randn(M, K, generator=g, device=dev).to(torch.bfloat16)
             sg = (torch.randint(0, 2, (K,), generator=g, device=dev, dtype=torch.int8) * 2 - 1)
             wsets = []
@@ -606,16 +683,22 @@ def detail_table(torch, nv4, W, dev, R):
                 # (converted once; gate_up's weights are converted per call).
                 keep = M > 32 and keep_weights_f6(N, K)
                 wsets.append((wt, sw, nv4.weights_to_f6(wt, True) if keep else None))
-            pkb = torch.empty((M, K // 2), dtype=torch.int8, device=dev)
             scb = torch.empty((M, K // 128), dtype=torch.bfloat16, device=dev)
             ob = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
-            l1 = [lambda: nv4.rht_quant_pack(x, sg, out_packed=pkb, out_scale=scb)] * rot
-            l2 = [lambda w=w: nv4.w4a4_grouped_gemm(pkb, w[0], scb, w[1], out=ob, weights_tiled=True, weights_f6=w[2])
-                  for w in wsets]
+            if M == 32:  # as W4A4Linear runs decode sizes: row-tiled codes
+                pkb = torch.empty((rowtiled_rows(M), K // 2), dtype=torch.int8, device=dev)
+                l1 = [lambda: rht_quant_pack_rowtiled(x, sg, out_packed=pkb, out_scale=scb)] * rot
+                l2 = [lambda w=w: w4a4_gemm_rowtiled(pkb, w[0], scb, w[1], out=ob) for w in wsets]
+            else:
+                pkb = torch.empty((M, K // 2), dtype=torch.int8, device=dev)
+                l1 = [lambda: nv4.rht_quant_pack(x, sg, out_packed=pkb, out_scale=scb)] * rot
+                l2 = [lambda w=w: nv4.w4a4_grouped_gemm(pkb, w[0], scb, w[1], out=ob, weights_tiled=True,
+                                                        weights_f6=w[2]) for w in wsets]
             us1 = graph_launch_us(torch, l1, reps)
             us2 = graph_launch_us(torch, l2, reps)
             del wsets
-            wb = [torch.randn(N, K, generator=g, device=dev).to(torch.bfloat16) for _ in range(2)]
+            nb = max(2, -(-ROTATE_BYTES // (2 * N * K))) if M == 32 else 2
+            wb = [torch.randn(N, K, generator=g, device=dev).to(torch.bfloat16) for _ in range(nb)]
             ob16 = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
             l3 = [lambda w=w: torch.mm(x, w.t(), out=ob16) for w in wb]
             us3 = graph_launch_us(torch, l3, reps)

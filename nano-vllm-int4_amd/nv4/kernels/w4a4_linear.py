@@ -24,11 +24,14 @@ from .w4a4_grouped import ROWTILED_MAX_M, _check_weights_f6, _launch, use_prefil
 
 
 def w4a4_linear(x, signs, w_packed, w_scale, *, out=None, out_packed=None, out_scale=None, weights_tiled=False,
-                weights_f6=None):
+                weights_f6=None, packed_rowtiled=None):
     """x bf16 [M,K] (K = 4096 or 12288) -> bf16 [M,N].  ``weights_tiled``:
     ``w_packed`` is in the MFMA-tiled order (``tile_weights``).
     ``weights_f6``: the ``weights_to_f6`` form of the weights, used by
-    prefill-sized calls instead of converting them again."""
+    prefill-sized calls instead of converting them again.
+    ``packed_rowtiled``: whether ``out_packed`` receives the codes in the
+    row-tiled order ([ceil(M/16)*16, K/2]; tiled weights, M <= 32); None
+    chooses it exactly when ``out_packed`` is not given."""
     if x.ndim != 2 or x.dtype != torch.bfloat16 or x.shape[1] not in (4096, 12288) or x.shape[0] < 1:
         raise ValueError("Expected BF16 X[M,K], M>0, K=4096/12288")
     M, K = x.shape
@@ -49,7 +52,10 @@ def w4a4_linear(x, signs, w_packed, w_scale, *, out=None, out_packed=None, out_s
     # Decode-sized M whose codes only the GEMM needs: K1 writes them in the
     # row-tiled order that the decode GEMM loads straight into registers
     # (same bits).
-    rowtiled = weights_tiled and M <= ROWTILED_MAX_M and out_packed is None
+    rowtiled = (weights_tiled and M <= ROWTILED_MAX_M and out_packed is None) if packed_rowtiled is None \
+        else bool(packed_rowtiled)
+    if rowtiled and (not weights_tiled or M > ROWTILED_MAX_M):
+        raise ValueError("Row-tiled activation codes need tiled weights and M <= 32")
     if out_packed is None:
         out_packed = torch.empty((rowtiled_rows(M) if rowtiled else M, K // 2), dtype=torch.int8, device=dev)
     if out_scale is None:
