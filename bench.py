@@ -313,7 +313,9 @@ def e2e_decode(torch, layers, out_tokens):
         if not (r["graph_equals_eager"] and r["logits_finite"]):
             raise RuntimeError(f"end-to-end {which}: graph replay differs from eager or logits not finite")
         steps = sorted(r["decode_ms"])
+        model_bytes = eng.model_bytes()
         res[which] = {"tokens_per_s": round(r["tokens_per_s"], 1), "decode_ms_mean": round(r["decode_ms_mean"], 4),
+                      "model_tensor_bytes": model_bytes, "model_tensor_gib": round(model_bytes / 2**30, 3),
                       "decode_ms_p50": round(steps[len(steps) // 2], 4),
                       "prefill_ms_mean": round(sum(r["prefill_ms"][1:]) / (len(r["prefill_ms"]) - 1), 2),
                       "published_a6000_tokens_per_s": PUBLISHED_E2E_TOKS[which]}
@@ -324,6 +326,9 @@ def e2e_decode(torch, layers, out_tokens):
     del kv
     torch.cuda.empty_cache()
     res["w4a4_over_bf16"] = round(res["w4a4"]["tokens_per_s"] / res["bf16"]["tokens_per_s"], 4)
+    res["model_tensor_gib_published_a6000"] = {"bf16": 15.28, "w4a4": 5.67}  # benchmarks/README.md:68-69
+    res["model_tensor_bytes_note"] = ("parameters and buffers of the model on the GPU (no KV cache); W4A4 "
+                                      "without the opt-in fp6 prefill copies of the weights")
     res["w4a16_over_bf16"] = round(res["w4a16"]["tokens_per_s"] / res["bf16"]["tokens_per_s"], 4)
     res["workload"] = (f"Qwen3-8B-shaped decoder ({layers} layers, hidden 4096, intermediate 12288, 32 q / 8 kv "
                        "heads, vocab 151936), random weights; 32 requests x 4096 seeded token ids, serial "

@@ -410,9 +410,12 @@ int pa_check(const void* q, int64_t q_row_stride, const void* k_cache, const voi
              int64_t B, int64_t Hq, int64_t Hkv, int64_t D, int64_t block_size, int64_t max_context,
              int64_t* splits) {
     if (!q || !k_cache || !v_cache || !block_tables || !context_lens || !out) return NV4_E_NULL;
-    if (D != PA_D || B < 1 || Hkv < 1 || Hq < 1 || Hq % Hkv || block_size < 1 || max_blocks < 1 ||
-        max_context < 1 || max_context > max_blocks * block_size || max_context > (1 << 30) || B > 65535 ||
-        Hkv > 65535 || q_row_stride < Hq * D)
+    // Every factor is bounded before any product, so no size computation
+    // below can wrap (max_blocks * block_size <= 2^46, Hq * D <= 2^25).
+    if (D != PA_D || B < 1 || Hkv < 1 || Hq < 1 || Hq % Hkv || block_size < 1 || block_size > (1 << 16) ||
+        max_blocks < 1 || max_blocks > (1 << 30) || max_context < 1 || max_context > (1 << 30) ||
+        max_context > max_blocks * block_size || B > 65535 || Hkv > 65535 || Hq > 4 * 65535 ||
+        q_row_stride < Hq * D)
         return NV4_E_SHAPE;
     const int64_t G = Hq / Hkv;
     if (G != 1 && G != 2 && G != 4) return NV4_E_SHAPE;  // the merge keeps 16 x G x 128 fp32 in LDS
@@ -421,6 +424,16 @@ int pa_check(const void* q, int64_t q_row_stride, const void* k_cache, const voi
         return NV4_E_ALIGN;
     *splits = (max_context + PA_SPLIT - 1) / PA_SPLIT;
     return NV4_OK;
+}
+
+// Bytes of the split partials, B * Hq * S rows of D + 2 floats, or -1 when
+// the product does not fit in int64.
+int64_t pa_partials_bytes(int64_t B, int64_t Hq, int64_t S, int64_t D) {
+    int64_t n = 0;
+    if (__builtin_mul_overflow(B, Hq, &n) || __builtin_mul_overflow(n, S, &n) ||
+        __builtin_mul_overflow(n, D + 2, &n) || __builtin_mul_overflow(n, (int64_t)4, &n))
+        return -1;
+    return n;
 }
 
 int pa_run(const void* q, int64_t q_row_stride, const void* k_cache, const void* v_cache,
@@ -477,7 +490,8 @@ extern "C" int nv4_paged_decode_attention(const void* q, int64_t q_row_stride, c
                             Hkv, D, block_size, max_context, &S);
     if (rc != NV4_OK) return rc;
     if (!workspace) return NV4_E_NULL;
-    if (workspace_bytes < B * Hq * S * (D + 2) * 4) return NV4_E_SHAPE;
+    const int64_t need = pa_partials_bytes(B, Hq, S, D);
+    if (need < 0 || workspace_bytes < need) return NV4_E_SHAPE;
     if (reinterpret_cast<uintptr_t>(workspace) % 8) return NV4_E_ALIGN;
     return pa_run(q, q_row_stride, k_cache, v_cache, block_tables, max_blocks, context_lens, out, workspace, B, Hq,
                   Hkv, block_size, max_context, S, scale, stream);
@@ -495,7 +509,10 @@ extern "C" int nv4_paged_decode_attention_noalloc(const void* q, int64_t q_row_s
     if (rc != NV4_OK) return rc;
     // Only the split partials (S > 1) use the scratch; their size is checked
     // before anything is launched.
-    if (S > 1 && B * Hq * S * (D + 2) * 4 > NV4_PA_SCRATCH_BYTES) return NV4_E_SCRATCH;
+    if (S > 1) {
+        const int64_t need = pa_partials_bytes(B, Hq, S, D);
+        if (need < 0 || need > NV4_PA_SCRATCH_BYTES) return NV4_E_SCRATCH;
+    }
     float* ws = nullptr;
     rc = scratch_on_current_device(&ws);
     if (rc != NV4_OK) return rc;

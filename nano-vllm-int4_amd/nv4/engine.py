@@ -74,10 +74,25 @@ def random_init(model: Qwen3ForCausalLM, seed: int) -> None:
             m.tile_weights_()
 
 
+def model_tensor_bytes(model) -> int:
+    """Bytes of every parameter and registered buffer of ``model``, each
+    storage counted once."""
+    seen, total = set(), 0
+    for t in list(model.parameters()) + list(model.buffers()):
+        if t is None or t.numel() == 0:
+            continue
+        key = (t.untyped_storage().data_ptr(), t.device)
+        if key in seen:
+            continue
+        seen.add(key)
+        total += t.untyped_storage().nbytes()
+    return total
+
+
 class Engine:
     def __init__(self, hf_config, use_w4a4: bool, max_num_seqs: int, max_model_len: int, block_size: int = 256,
                  device="cuda:0", model: Qwen3ForCausalLM | None = None, kv_cache: torch.Tensor | None = None,
-                 seed: int = 0, use_w4a16: bool = False):
+                 seed: int = 0, use_w4a16: bool = False, keep_weights_f6: bool = False):
         self.cfg, self.device = hf_config, torch.device(device)
         self.max_num_seqs, self.max_model_len, self.block_size = max_num_seqs, max_model_len, block_size
         self.blocks_per_seq = math.ceil(max_model_len / block_size)
@@ -93,6 +108,10 @@ class Engine:
             if use_w4a16:
                 model.fuse_projections_()
         self.model = model.eval()
+        if keep_weights_f6:  # fp6 tiles of the W4A4 weights for prefill-sized calls (opt-in)
+            for m in self.model.modules():
+                if isinstance(m, W4A4Linear):
+                    m.keep_weights_f6_(True)
         cfg = hf_config
         head_dim = getattr(cfg, "head_dim", None) or cfg.hidden_size // cfg.num_attention_heads
         nblocks = max_num_seqs * self.blocks_per_seq
@@ -110,6 +129,13 @@ class Engine:
         self.graphs: dict[int, torch.cuda.CUDAGraph] = {}
         self.graph_vars: dict[str, torch.Tensor] = {}
         self.sampler = Sampler()
+
+    def model_bytes(self) -> int:
+        """Device bytes of the model's tensors (parameters and buffers: quantized
+        codes, scales, signs, kept fp6 weight tiles, embeddings, norms, LM
+        head), without the KV cache and the attention workspace -- the figure
+        the reference reports as model tensor bytes."""
+        return model_tensor_bytes(self.model)
 
     # ------------------------------------------------------------ helpers
     def _slots(self, seq_slot: int, start: int, end: int):

@@ -12,13 +12,20 @@ allocator, so the forward can be captured in a HIP graph.
 ``tile_weights_()`` (called by the loaders once the weights are in) reorders
 ``packed_weight`` in place into the MFMA-tiled order that the decode
 kernels read in whole cache lines; the forward then uses the tiled entry
-point, with bit-identical results.  It also keeps ``weight_f6``, the fp6 tile
-form the prefill GEMM reads (0.75 bytes per weight, rebuilt whenever the
-weights are loaded), so prefill-sized calls convert only their activations --
-for weights up to ``KEEP_F6_MAX_BYTES`` of fp6 tiles (``keep_weights_f6``:
-qkv, o and down of Qwen3-8B; gate_up converts per call).
-``state_dict()`` and ``load_state_dict()`` still see the reference
-[out, in/2] layout and do not hold ``weight_f6``.
+point, with bit-identical results.
+
+On request (``keep_weights_f6_(True)``, or ``Engine(keep_weights_f6=True)``)
+a layer also keeps ``weight_f6``, the fp6 tile form the prefill GEMM reads
+(0.75 bytes per weight on top of the 0.5 of the INT4 codes, rebuilt whenever
+the weights are loaded), so prefill-sized calls convert only their
+activations -- for weights up to ``KEEP_F6_MAX_BYTES`` of fp6 tiles
+(``keep_weights_f6``: qkv, o and down of Qwen3-8B; gate_up converts per
+call).  It is off by default: it buys about 3 % per prefill GEMM call for
++72 % of those layers' weight bytes.  The copy is used only while
+``packed_weight`` is the tensor version it was made from; weights without a
+version counter (inference tensors) never keep one, so no in-place write can
+leave it stale.  ``state_dict()`` and ``load_state_dict()`` still see the
+reference [out, in/2] layout and do not hold ``weight_f6``.
 """
 import torch
 from torch import nn
@@ -37,7 +44,7 @@ def _version_of(t):
 
 
 class W4A4Linear(nn.Module):
-    def __init__(self, input_size: int, output_size: int, bias: bool = False):
+    def __init__(self, input_size: int, output_size: int, bias: bool = False, keep_weights_f6: bool = False):
         super().__init__()
         if dist.is_available() and dist.is_initialized() and dist.get_world_size() != 1:
             raise ValueError("W4A4Linear supports one GPU only")
@@ -49,6 +56,7 @@ class W4A4Linear(nn.Module):
         self.register_buffer("signs", torch.empty(input_size, dtype=torch.int8))
         self.register_buffer("weight_f6", None, persistent=False)
         self.weights_tiled = False
+        self.keep_f6 = keep_weights_f6
 
     @torch.no_grad()
     def tile_weights_(self) -> "W4A4Linear":
@@ -61,20 +69,35 @@ class W4A4Linear(nn.Module):
         return self
 
     @torch.no_grad()
+    def keep_weights_f6_(self, enable: bool = True) -> "W4A4Linear":
+        """Keep (or drop) the fp6 tile form of the weights for prefill-sized
+        calls; made now if the weights are loaded and tiled."""
+        self.keep_f6 = enable
+        self._refresh_f6()
+        return self
+
+    @torch.no_grad()
     def _refresh_f6(self) -> None:
-        keep = self.packed_weight.is_cuda and keep_weights_f6(self.out_features, self.in_features)
+        version = _version_of(self.packed_weight)
+        keep = (self.keep_f6 and self.packed_weight.is_cuda and version is not None
+                and keep_weights_f6(self.out_features, self.in_features))
         self.weight_f6 = weights_to_f6(self.packed_weight, self.weights_tiled) if keep else None
-        self._f6_version = _version_of(self.packed_weight)
+        self._f6_version = version
 
     def _f6(self):
         """``weight_f6`` while ``packed_weight`` is unchanged since it was made
         (an in-place write bumps the tensor's version); otherwise None, and
-        prefill calls convert the weights themselves.  Weights created under
-        ``torch.inference_mode`` carry no version: their copy is trusted as
-        made by ``tile_weights_`` / ``load_state_dict``."""
-        if self.weight_f6 is None or getattr(self, "_f6_version", -1) != _version_of(self.packed_weight):
+        prefill calls convert the weights themselves."""
+        version = _version_of(self.packed_weight)
+        if self.weight_f6 is None or version is None or getattr(self, "_f6_version", -1) != version:
             return None
         return self.weight_f6
+
+    def weight_bytes(self) -> int:
+        """Device bytes of the layer's tensors: INT4 codes, scales, signs and
+        (when kept) the fp6 tile form."""
+        n = sum(t.numel() * t.element_size() for t in (self.packed_weight, self.weight_scale, self.signs))
+        return n + (self.weight_f6.numel() if self.weight_f6 is not None else 0)
 
     @torch.no_grad()
     def assign_quantized_(self, packed: torch.Tensor, scale: torch.Tensor, signs: torch.Tensor) -> "W4A4Linear":

@@ -208,6 +208,48 @@ def test_paged_decode_attention_rejections():
     assert call(q=P(A16 + 4)) == _lib.NV4_E_ALIGN
 
 
+def test_paged_decode_attention_size_checks_do_not_wrap():
+    """Sizes at the accepted maxima whose workspace size does not fit in int64
+    (B * Hq * splits * 130 * 4 ~ 2^65) are rejected -- NV4_E_SHAPE for the
+    workspace form whatever workspace size is claimed, NV4_E_SCRATCH for the
+    allocation-free form -- and block counts whose product with the block
+    size would wrap are rejected as shapes."""
+    lib = _lib.load()
+    f, g = lib.nv4_paged_decode_attention, lib.nv4_paged_decode_attention_noalloc
+    B, Hkv, Hq, D, bs, max_blocks, max_ctx = 65535, 65535, 4 * 65535, 128, 1 << 14, 1 << 16, 1 << 30
+    args = (P(A16), Hq * D, P(A16), P(A16), P(A16), max_blocks, P(A16), P(A16))
+    assert f(*args, P(A16), (1 << 62), B, Hq, Hkv, D, bs, max_ctx, 0.1, None) == _lib.NV4_E_SHAPE
+    assert g(*args, B, Hq, Hkv, D, bs, max_ctx, 0.1, None) == _lib.NV4_E_SCRATCH
+    # max_blocks * block_size = 2^33 * (2^31 + 1) wraps to 2^33 in int64 arithmetic
+    wrap = (P(A16), 4096, P(A16), P(A16), P(A16), 1 << 33, P(A16), P(A16))
+    assert f(*wrap, P(A16), 1 << 30, 32, 32, 8, 128, (1 << 31) + 1, 4352, 0.1, None) == _lib.NV4_E_SHAPE
+    assert g(*wrap, 32, 32, 8, 128, (1 << 31) + 1, 4352, 0.1, None) == _lib.NV4_E_SHAPE
+
+
+def test_rowtiled_entry_point_rejections():
+    lib = _lib.load()
+    ok = [P(A16)] * 4
+    g = lib.nv4_w4a4_gemm_rowtiled
+    assert g(None, *ok[1:], 1, P(A16), 0, 4, 64, 4096, None) == _lib.NV4_E_NULL
+    assert g(*ok, 1, P(A16), 0, 33, 64, 4096, None) == _lib.NV4_E_SHAPE    # M > 32
+    assert g(*ok, 1, P(A16), 0, 0, 64, 4096, None) == _lib.NV4_E_SHAPE     # M = 0
+    assert g(*ok, 1, P(A16), 0, 4, 72, 4096, None) == _lib.NV4_E_SHAPE     # N % 16
+    assert g(*ok, 1, P(A16), 0, 4, 64, 4000, None) == _lib.NV4_E_SHAPE     # K % 128
+    assert g(P(A16 + 8), *ok[1:], 1, P(A16), 0, 4, 64, 4096, None) == _lib.NV4_E_ALIGN
+    k = lib.nv4_rht_quant_pack_rowtiled
+    assert k(None, P(A16), P(A16), P(A16), 4, 4096, None) == _lib.NV4_E_NULL
+    assert k(P(A16), P(A16), P(A16), P(A16), 4, 2048, None) == _lib.NV4_E_SHAPE
+    assert k(P(A16), P(A16), P(A16), P(A16), 0, 4096, None) == _lib.NV4_E_SHAPE
+    lin = lib.nv4_w4a4_linear_rowtiled
+    assert lin(*([P(A16)] * 7), 33, 64, 4096, None) == _lib.NV4_E_SHAPE
+    assert lin(*([P(A16)] * 7), 4, 72, 4096, None) == _lib.NV4_E_SHAPE
+    assert lin(*([P(A16)] * 7), 4, 64, 2048, None) == _lib.NV4_E_SHAPE
+    r = lib.nv4_rmsnorm_rht_quant_pack_rowtiled
+    assert r(P(A16), None, None, P(A16), 1e-6, P(A16), P(A16), P(A16), 4, 12288, None) == _lib.NV4_E_SHAPE
+    sm = lib.nv4_silu_mul_rht_quant_pack_rowtiled
+    assert sm(P(A16), P(A16), P(A16), P(A16), 4, 2048, None) == _lib.NV4_E_SHAPE
+
+
 def test_gumbel_split_rejections():
     lib = _lib.load()
     assert lib.nv4_gumbel_sample_chunks(32, 151936) == 64     # 2048 workgroups over 32 rows

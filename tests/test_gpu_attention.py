@@ -193,10 +193,14 @@ def test_prefill_attention(lens):
         start += n
 
 
-@pytest.mark.parametrize("G,Hkv", [(1, 8), (2, 4), (8, 2)])
-def test_prefill_attention_gqa_groups(G, Hkv):
-    """Other query-to-KV head ratios (the workgroup then covers 256/G rows)."""
-    lens = [5, 300, 129]
+@pytest.mark.parametrize("G,Hkv,lens", [(1, 8, [5, 300, 129]), (2, 4, [5, 300, 129]), (8, 2, [5, 300, 129]),
+                                        (1, 8, [4096, 40]), (2, 4, [4096, 100])])
+def test_prefill_attention_gqa_groups(G, Hkv, lens):
+    """Other query-to-KV head ratios (the workgroup then covers 256/G rows).
+    The short prompts run the 4-wave form; a 4096-token prompt beside a short
+    one at G = 1 / Hkv = 8 and G = 2 / Hkv = 4 gives 256 8-wave workgroups, as
+    many as the CUs, so those run the 8-wave form with 128-key blocks (256 and
+    128 query rows per workgroup)."""
     print(f"[prefill-attn-gqa] G={G} Hkv={Hkv} lens={lens}", flush=True)
     g = torch.Generator(device=DEV).manual_seed(11 * G)
     T = sum(lens)

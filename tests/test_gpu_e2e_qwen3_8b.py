@@ -6,14 +6,15 @@ graph, as the reference's latency benchmark runs it
 (benchmarks/bench_nano_latency.py:32-121).
 
 * Prefill: every request's first token is in the vocabulary; inside the
-  first request's prefill (M = 4096: the fp8 prefill GEMM), every W4A4
+  first request's prefill (M = 4096: the fp6 matrix-core prefill GEMM, the
+  size-chosen path), every W4A4
   projection of the first and the last layer equals the oracle on a sample
   of rows, and every fused K1 the oracle K1 (``model_probe``).
 * Decode at ~4.1k context: the graph-replayed step's full logits equal the
   eager step's bit for bit and are finite (bench_nano_latency.py:96-107);
-  inside the eager step, every W4A4 projection of the first and last layer
-  equals the oracle on all 32 rows; a few more graph steps sample tokens in
-  the vocabulary.
+  inside the eager step (row-tiled codes from the fused K1s into the decode
+  GEMM), every W4A4 projection of the first and last layer equals the oracle
+  on all 32 rows; a few more graph steps sample tokens in the vocabulary.
 """
 import pytest
 import torch

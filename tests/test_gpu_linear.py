@@ -158,25 +158,32 @@ def test_linear_prefill_matrix_core_route(proj, M):
 
 
 def test_linear_module_keeps_fp6_weights():
-    """``tile_weights_`` keeps the fp6 form of the weights (not for gate_up's):
-    prefill-sized forwards use it, with the bits of converting per call; it
-    stays out of the state dict, follows ``load_state_dict``, and is not used
-    once ``packed_weight`` is written in place."""
+    """The fp6 form of the weights is opt-in (``keep_weights_f6``): off by
+    default; when kept (not for gate_up's size) prefill-sized forwards use it,
+    with the bits of converting per call; it stays out of the state dict,
+    follows ``load_state_dict``, and is not used once ``packed_weight`` is
+    written in place."""
     from nv4 import weights_to_f6
-    assert W4A4Linear(4096, 24576).to(DEV).tile_weights_().weight_f6 is None
+    assert W4A4Linear(4096, 24576, keep_weights_f6=True).to(DEV).tile_weights_().weight_f6 is None
     case = W.w4a4_case("qkv", 1024)
     M, N, K = case.shape
     print(f"[linear-fp6-weights] M={M} N={N} K={K}", flush=True)
     x = case.x.to(DEV)
-    m = W4A4Linear(K, N).to(DEV)
+    plain = W4A4Linear(K, N).to(DEV)
+    plain.assign_quantized_(case.w_packed.to(DEV), case.w_scale.to(DEV), case.signs.to(DEV))
+    assert plain.weights_tiled and plain.weight_f6 is None and plain._f6() is None
+    assert plain.weight_bytes() == N * K // 2 + N * K // 128 * 2 + K
+    m = W4A4Linear(K, N, keep_weights_f6=True).to(DEV)
     m.assign_quantized_(case.w_packed.to(DEV), case.w_scale.to(DEV), case.signs.to(DEV))
     assert m.weights_tiled and m._f6() is m.weight_f6 is not None
+    assert m.weight_bytes() == plain.weight_bytes() + m.weight_f6.numel()
     assert "weight_f6" not in m.state_dict()
     assert torch.equal(m.weight_f6, weights_to_f6(case.w_packed.to(DEV)))
     out = m(x)
     ref = w4a4_linear(x, m.signs, m.packed_weight, m.weight_scale, weights_tiled=True)   # converts per call
     torch.cuda.synchronize()
     assert torch.equal(out.view(torch.int16), ref.view(torch.int16))
+    assert torch.equal(plain(x).view(torch.int16), out.view(torch.int16))
     with torch.no_grad():
         m.packed_weight[:64].zero_()                  # in place: the fp6 copy is now stale
     assert m._f6() is None
@@ -185,24 +192,40 @@ def test_linear_module_keeps_fp6_weights():
     torch.cuda.synchronize()
     assert torch.equal(out2.view(torch.int16), ref2.view(torch.int16))
     assert not torch.equal(out2.view(torch.int16), out.view(torch.int16))
-    m2 = W4A4Linear(K, N).to(DEV).tile_weights_()
+    m2 = W4A4Linear(K, N).to(DEV).keep_weights_f6_(True).tile_weights_()
     m2.load_state_dict(m.state_dict())
     assert m2._f6() is not None and torch.equal(m2.weight_f6, weights_to_f6(m.packed_weight, True))
     assert torch.equal(m2(x).view(torch.int16), out2.view(torch.int16))
+    m2.keep_weights_f6_(False)
+    assert m2.weight_f6 is None and m2._f6() is None
 
 
-def test_linear_fp6_weights_made_under_inference_mode():
-    """Weights created under torch.inference_mode carry no version counter:
-    the kept fp6 form is used as made, with the bits of converting per call."""
+def test_linear_fp6_weights_refused_under_inference_mode():
+    """Weights created under torch.inference_mode carry no version counter,
+    so an in-place write could not be noticed: such a layer keeps no fp6
+    copy even when asked, and a prefill-sized forward after writing new
+    weights in place (under inference_mode) follows them, bit for bit with
+    the oracle's K1 + GEMM chain on the new weights."""
     case = W.w4a4_case("down", 1024)
     M, N, K = case.shape
     print(f"[linear-fp6-inference-mode] M={M} N={N} K={K}", flush=True)
+    rows = np.r_[0:8, 517:521, M - 8:M]
+    g = torch.Generator().manual_seed(4321)
+    new_w = torch.randint(-128, 128, (N, K // 2), generator=g, dtype=torch.int16).to(torch.int8)
     with torch.inference_mode():
-        m = W4A4Linear(K, N).to(DEV)
+        m = W4A4Linear(K, N, keep_weights_f6=True).to(DEV)
         m.assign_quantized_(case.w_packed.to(DEV), case.w_scale.to(DEV), case.signs.to(DEV))
-        assert m._f6() is m.weight_f6 is not None
+        assert m.weight_f6 is None and m._f6() is None
         x = case.x.to(DEV)
         out = m(x)
         ref = w4a4_linear(x, m.signs, m.packed_weight, m.weight_scale, weights_tiled=True)
+        # new weights written in place, through the tiled layout the module keeps
+        m.packed_weight.copy_(tile_weights(new_w.to(DEV)))
+        out2 = m(x)
     torch.cuda.synchronize()
     assert torch.equal(out.view(torch.int16), ref.view(torch.int16))
+    xb = bf16_bits(case.x)[rows]
+    p_ref, s_ref = oracle.rht_quant_pack(xb, case.signs.numpy())
+    exp = oracle.w4a4_gemm(p_ref, new_w.numpy(), s_ref, bf16_bits(case.w_scale))
+    assert np.array_equal(bf16_bits(out2)[rows], exp)
+    assert not torch.equal(out2.view(torch.int16), out.view(torch.int16))

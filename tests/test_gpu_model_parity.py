@@ -171,11 +171,13 @@ def test_loaded_checkpoint_on_gpu_matches_oracle(tmp_path):
     info = L.load_w4a4_model(model, str(base), str(tmp_path / "ckpt"))
     assert info["projections"] == 14 and info["native_linear_modules"] == 8
     assert all(m.weights_tiled for m in model.modules() if isinstance(m, W4A4Linear))
-    # The loaded layers keep the fp6 form of their weights for prefill where it pays (qkv, o,
-    # down of Qwen3-8B), matching the weights just loaded.
+    # The loaded layers keep no fp6 copy of their weights by default; on request they keep it
+    # where it pays (qkv, o, down of Qwen3-8B), matching the weights just loaded.
     from nv4.kernels.w4a4_grouped import keep_weights_f6, weights_to_f6
     for m in model.modules():
         if isinstance(m, W4A4Linear):
+            assert m.weight_f6 is None and m._f6() is None
+            m.keep_weights_f6_(True)
             keep = keep_weights_f6(m.out_features, m.in_features)
             assert (m._f6() is not None) == keep
             if keep:

@@ -228,6 +228,55 @@ def test_k2_chain_qwen3_shapes_m4096_sampled(proj, tiled, path):
     assert_bits_equal(bf16_bits(out)[rows], o_ref, f"{proj} M=4096 sampled rows")
 
 
+@pytest.mark.parametrize("proj", ["o", "down", "gate_up"])
+def test_k2_chain_m4096_every_row(proj):
+    """The prefill-sized chain (K1, then the size-chosen fp6 matrix-core GEMM
+    on tiled weights, as W4A4Linear runs it) at M = 4096, every row and
+    every element against the oracle's K1 + grouped GEMM."""
+    from nv4 import W4A4Linear
+    case = W.w4a4_case(proj, 4096)
+    M, N, K = case.shape
+    print(f"[chain] {proj} M={M} N={N} K={K} every row", flush=True)
+    lin = W4A4Linear(K, N).to(DEV)
+    lin.assign_quantized_(case.w_packed.to(DEV), case.w_scale.to(DEV), case.signs.to(DEV))
+    packed = torch.empty((M, K // 2), dtype=torch.int8, device=DEV)
+    scale = torch.empty((M, K // 128), dtype=torch.bfloat16, device=DEV)
+    x = case.x.to(DEV)
+    rht_quant_pack(x, lin.signs, out_packed=packed, out_scale=scale)
+    out = lin.forward_quantized(packed, scale)
+    whole = lin(x)
+    torch.cuda.synchronize()
+    p_ref, s_ref, o_ref = chain_expected(case)
+    assert np.array_equal(packed.cpu().numpy(), p_ref)
+    assert np.array_equal(bf16_bits(scale), s_ref)
+    assert_bits_equal(bf16_bits(out), o_ref, f"{proj} M=4096 every row")
+    assert_bits_equal(bf16_bits(whole), o_ref, f"{proj} M=4096 W4A4Linear.forward")
+
+
+@pytest.mark.parametrize("M", [32, 4096])
+def test_k2_chain_config0_block128(M):
+    """Config 0 (o_proj, 1 % x20 outlier channels) with the block128 RHT
+    layout: K1 on the workload's inputs chained into the grouped GEMM,
+    codes, scales and every output element against the oracle."""
+    case = W.w4a4_case("o", M)
+    _, N, K = case.shape
+    print(f"[chain-block128] o M={M}", flush=True)
+    x, signs = case.x.to(DEV), case.signs.to(DEV)
+    packed = torch.empty((M, K // 2), dtype=torch.int8, device=DEV)
+    scale = torch.empty((M, K // 128), dtype=torch.bfloat16, device=DEV)
+    rht_quant_pack(x, signs, out_packed=packed, out_scale=scale, layout="block128")
+    for tiled in (False, True):
+        wpk = case.w_packed.to(DEV)
+        out = w4a4_grouped_gemm(packed, tile_weights(wpk) if tiled else wpk, scale, case.w_scale.to(DEV),
+                                weights_tiled=tiled)
+        torch.cuda.synchronize()
+        p_ref, s_ref = oracle.rht_quant_pack(bf16_bits(case.x), case.signs.numpy(), layout=oracle.LAYOUT_BLOCK128)
+        assert np.array_equal(packed.cpu().numpy(), p_ref)
+        assert np.array_equal(bf16_bits(scale), s_ref)
+        o_ref = oracle.w4a4_gemm(p_ref, case.w_packed.numpy(), s_ref, bf16_bits(case.w_scale))
+        assert_bits_equal(bf16_bits(out), o_ref, f"block128 chain M={M} tiled={tiled}")
+
+
 def rtn_inputs(M, N, K, seed):
     """Operands as the reference's kernel benchmarks make them
     (benchmarks/tune_w4a4_aw_grouped.py:41-49): bf16 x ~ N(0,1) and
