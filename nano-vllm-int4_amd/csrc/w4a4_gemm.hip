@@ -390,6 +390,7 @@ k2_wide(const int8_t* __restrict__ a, const int8_t* __restrict__ w,
     __shared__ __align__(16) uint8_t a_l[WIDE_A_BYTES + 32];  // + sink
     __shared__ __align__(16) float sa_l[WIDE_SCALES + 4];     // [g][row] + sink
     __shared__ float sw_l[WIDE_WSCALES + 1];                  // [g][col] + sink
+    __shared__ uint32_t wave_bad[CBW * MB];                   // scale-range flags, one per wave
 
     const int t = threadIdx.x;
     const int lane = t & 63, wave = t >> 6;
@@ -413,7 +414,9 @@ k2_wide(const int8_t* __restrict__ a, const int8_t* __restrict__ w,
     // of row 16 rb + l%16, so chunk q sits at byte 16 q.
     auto chunk_rc = [&](int q, int& r, int& c) {
         if constexpr (RT) {
-            const int l = q & 63, blk = q >> 6;
+            // T is a multiple of 64, so the block of a thread's chunk is
+            // uniform over its wave: divide on the scalar unit.
+            const int l = q & 63, blk = __builtin_amdgcn_readfirstlane(q >> 6);
             r = (blk / G) * 16 + (l & 15);
             c = (blk % G) * 4 + (l >> 4);
         } else {
@@ -461,12 +464,14 @@ k2_wide(const int8_t* __restrict__ a, const int8_t* __restrict__ w,
         *reinterpret_cast<v4i*>(&a_l[live ? r * K + s1 * 16 : WIDE_A_BYTES + 16]) = hi;
     }
     // The >> 8 that turns the MFMA's 256 * dot into the dot can ride on the
-    // activation scale instead: cvt(256 d) * (sa * 2^-8) * sw inside the fma is
-    // the same exact product as d * (sa * sw) whenever sa * 2^-8 and the
+    // weight scale instead: cvt(256 d) * sa * (sw * 2^-8) inside the fma is
+    // the same exact product as d * (sa * sw) whenever sw * 2^-8 and the
     // scale product stay normal fp32, which holds when every scale of the
-    // workgroup is 0 or of magnitude in [2^-59, 2^63) (per-channel weight
-    // scales multiply the finished total, so only sa counts there).
-    // Otherwise the workgroup runs the literal sequence.
+    // workgroup is 0 or of magnitude in [2^-59, 2^63).  Each wave flags the
+    // scales it staged; after the prologue's barrier the workgroup folds only
+    // if no wave flagged one, else it runs the literal sequence.  (Grouped
+    // weight scales only; not with 8 column blocks, whose second loop body
+    // would not fit 128 VGPRs.)
     auto fold_ok = [](uint32_t b) {
         const uint32_t e = (b >> 7) & 0xffu;
         return (b & 0x7fffu) == 0 || (e >= 127 - 59 && e < 127 + 63);
@@ -476,14 +481,13 @@ k2_wide(const int8_t* __restrict__ a, const int8_t* __restrict__ w,
     for (int i = 0; i < SC; ++i) bad |= !fold_ok(rsa[i]);
 #pragma unroll
     for (int i = 0; i < WC; ++i) bad |= !fold_ok(rsw[i]);
-    // (Not with 8 column blocks: the second loop body would not fit 128 VGPRs.)
-    const bool fold = !__syncthreads_or(bad) && CBW < 8;
-    const float sa_mul = fold ? 0x1p-8f : 1.0f;
+    const bool wave_flag = __builtin_amdgcn_ballot_w64(bad) != 0;
+    if (lane == 0) wave_bad[wave] = wave_flag ? 1u : 0u;
 #pragma unroll
     for (int i = 0; i < SC; ++i) {
         const int e = t + i * T;
         const int ec = min(e, G * ROWS - 1);
-        sa_l[e < G * ROWS ? (ec % G) * ROWS + ec / G : WIDE_SCALES] = bf16_to_f32(rsa[i]) * sa_mul;
+        sa_l[e < G * ROWS ? (ec % G) * ROWS + ec / G : WIDE_SCALES] = bf16_to_f32(rsa[i]);
     }
 #pragma unroll
     for (int i = 0; i < WC; ++i) {
@@ -492,6 +496,9 @@ k2_wide(const int8_t* __restrict__ a, const int8_t* __restrict__ w,
         sw_l[e < G * COLS ? (ec % G) * COLS + ec / G : WIDE_WSCALES] = bf16_to_f32(rsw[i]);
     }
     __syncthreads();
+    bool fold = SW_GROUPED && CBW < 8;
+#pragma unroll
+    for (int i = 0; i < CBW * MB; ++i) fold = fold && wave_bad[i] == 0;
 
     float total[4] = {0.0f, 0.0f, 0.0f, 0.0f};
     const int r = mb * 16 + rc;
@@ -513,7 +520,8 @@ k2_wide(const int8_t* __restrict__ a, const int8_t* __restrict__ w,
         o.s_a = *reinterpret_cast<const v4f*>(sap + g * ROWS);
         o.s_w = SW_GROUPED ? swq[g * COLS] : 1.0f;
     };
-    // FOLD: the staged sa carries the 2^-8 and the dot is taken as 256 d.
+    // FOLD: the column's weight scale carries the 2^-8 and the dot is taken
+    // as 256 d.
     auto main_loop = [&](auto FOLD) {
         auto consume = [&](const v4u& w_in, const Ops& o) {
             const v4i w0 = unpack8_x16(w_in[0], w_in[1]);
@@ -521,10 +529,11 @@ k2_wide(const int8_t* __restrict__ a, const int8_t* __restrict__ w,
             v4i acc = {0, 0, 0, 0};
             acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(o.a0, w0, acc, 0, 0, 0);
             acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(o.a1, w1, acc, 0, 0, 0);
+            const float s_w = FOLD ? o.s_w * 0x1p-8f : o.s_w;
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const float d = FOLD ? (float)acc[i] : (float)(acc[i] >> 8);
-                total[i] = SW_GROUPED ? __builtin_fmaf(d, o.s_a[i] * o.s_w, total[i])
+                total[i] = SW_GROUPED ? __builtin_fmaf(d, o.s_a[i] * s_w, total[i])
                                       : __builtin_fmaf(d, o.s_a[i], total[i]);
             }
         };
@@ -551,7 +560,7 @@ k2_wide(const int8_t* __restrict__ a, const int8_t* __restrict__ w,
             }
         });
     };
-    if constexpr (CBW < 8) {
+    if constexpr (SW_GROUPED && CBW < 8) {
         if (fold) {
             main_loop(std::true_type{});
         } else {
