@@ -181,19 +181,29 @@ int nv4_w4a4_linear_tiled(const void* x, const int8_t* signs, const int8_t* w_ti
  * loads every operand as whole cache lines straight into registers.
  * nv4_rht_quant_pack_rowtiled: nv4_rht_quant_pack (reference layout, K in
  *   {4096, 12288}) writing packed_rt in this order; scale stays [M,K/128].
+ *   prefetch / prefetch_bytes (NULL / 0 for none; else a 16-byte aligned
+ *   buffer and a positive multiple of 16 bytes): workgroups beyond the M rows
+ *   of the launch read that many bytes of the buffer and discard them -- at
+ *   decode sizes K1 occupies few CUs, so the weights of the GEMM that follows
+ *   are read from HBM into the Infinity Cache meanwhile.  Nothing is written
+ *   and no result changes.
  * nv4_w4a4_gemm_rowtiled: nv4_w4a4_gemm_tiled for 1 <= M <= 32 on row-tiled
  *   activations (a_rt 16-byte aligned); bit-identical results.
  * nv4_w4a4_linear_rowtiled: nv4_w4a4_linear_tiled for 1 <= M <= 32 with the
- *   row-tiled activation workspace a_packed_rt.
+ *   row-tiled activation workspace a_packed_rt; its K1 prefetches the first
+ *   nv4_w4a4_prefetch_bytes(N, K) bytes of w_tiled.
+ * nv4_w4a4_prefetch_bytes: how many bytes of an [N,K] layer's packed weights
+ *   a decode-sized K1 reads ahead of the GEMM (0 for invalid shapes).
  */
 int nv4_rht_quant_pack_rowtiled(const void* x, const int8_t* signs, int8_t* packed_rt, void* scale,
-                                int64_t M, int64_t K, void* stream);
+                                int64_t M, int64_t K, const void* prefetch, int64_t prefetch_bytes, void* stream);
 int nv4_w4a4_gemm_rowtiled(const int8_t* a_rt, const int8_t* w_tiled, const void* sa, const void* sw,
                            int sw_grouped, void* out, int out_fp32,
                            int64_t M, int64_t N, int64_t K, void* stream);
 int nv4_w4a4_linear_rowtiled(const void* x, const int8_t* signs, const int8_t* w_tiled, const void* sw,
                              void* out, int8_t* a_packed_rt, void* a_scale,
                              int64_t M, int64_t N, int64_t K, void* stream);
+int64_t nv4_w4a4_prefetch_bytes(int64_t N, int64_t K);
 
 /*
  * nv4_w4a4_gemm (w_tiled = 0) / nv4_w4a4_gemm_tiled (w_tiled = 1) for
@@ -412,12 +422,15 @@ int nv4_rmsnorm_rht_quant_pack(const void* x, const void* residual_in, void* res
                                void* stream);
 int nv4_silu_mul_rht_quant_pack(const void* gate_up, const int8_t* signs, int8_t* packed, void* scale, int64_t M,
                                 int64_t K, void* stream);
-/* The same two, writing the codes in the row-tiled order (ceil(M/16)*16*K/2 bytes). */
+/* The same two, writing the codes in the row-tiled order (ceil(M/16)*16*K/2 bytes), with the
+ * prefetch arguments of nv4_rht_quant_pack_rowtiled. */
 int nv4_rmsnorm_rht_quant_pack_rowtiled(const void* x, const void* residual_in, void* residual_out,
                                         const void* norm_weight, float eps, const int8_t* signs, int8_t* packed_rt,
-                                        void* scale, int64_t M, int64_t K, void* stream);
+                                        void* scale, int64_t M, int64_t K, const void* prefetch,
+                                        int64_t prefetch_bytes, void* stream);
 int nv4_silu_mul_rht_quant_pack_rowtiled(const void* gate_up, const int8_t* signs, int8_t* packed_rt, void* scale,
-                                         int64_t M, int64_t K, void* stream);
+                                         int64_t M, int64_t K, const void* prefetch, int64_t prefetch_bytes,
+                                         void* stream);
 
 /*
  * Next-token sampling at per-row temperatures (nanovllm/layers/sampler.py:5-12):

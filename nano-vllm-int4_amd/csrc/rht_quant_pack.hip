@@ -76,6 +76,40 @@ struct RowRms {
     }
 };
 
+// Prefetch tail of decode-sized launches.  At M <= 32 K1 keeps one
+// workgroup per row busy (32 of the CUs) for a few microseconds while HBM
+// idles.  Workgroups past the M rows read `bytes` of a buffer -- the weights
+// of the GEMM that consumes these codes -- and discard them, so that the
+// GEMM launched next finds them in the memory-side Infinity Cache instead of
+// HBM.  Nothing is written, and no result depends on it.
+struct Prefetch {
+    const int8_t* p = nullptr;
+    int64_t bytes = 0;  // a multiple of 16
+    int rows = 0;       // workgroups 0..rows-1 run K1, the others prefetch
+};
+constexpr int PF_LOADS = 8;  // 16-byte loads per thread of a prefetch workgroup
+
+// True for a prefetch workgroup (which has then issued its loads).  The loads
+// are unconditional (offsets clamped into the buffer), so none waits alone.
+template <int T>
+__device__ __forceinline__ bool prefetch_tail(const Prefetch& pf) {
+    if ((int)blockIdx.x < pf.rows) return false;
+    const int64_t base = (int64_t)(blockIdx.x - pf.rows) * (T * 16 * PF_LOADS);
+    v4u acc = {0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int i = 0; i < PF_LOADS; ++i) {
+        const int64_t off = min(base + (int64_t)(i * T + threadIdx.x) * 16, pf.bytes - 16);
+        acc ^= *reinterpret_cast<const v4u*>(pf.p + off);
+    }
+    asm volatile("" ::"v"(acc[0] ^ acc[1] ^ acc[2] ^ acc[3]));  // keep the loads
+    return true;
+}
+
+inline unsigned prefetch_grid(int M, const Prefetch& pf, int threads) {
+    const int64_t per = (int64_t)threads * 16 * PF_LOADS;
+    return (unsigned)(M + (pf.bytes > 0 ? (pf.bytes + per - 1) / per : 0));
+}
+
 // K = 4096: one workgroup of K4_THREADS threads per row.  RT: the codes go
 // to the row-tiled layout (packed_dst) instead of [M][K/2].
 template <bool RT, class Src>
@@ -93,8 +127,10 @@ __device__ __forceinline__ void k1_k4096_body(const Src& src, const int8_t* __re
 
 template <class Src, bool RT>
 __global__ void __launch_bounds__(K4_THREADS)
-k1_k4096(Src src, const int8_t* __restrict__ signs, int8_t* __restrict__ packed, uint16_t* __restrict__ scale) {
+k1_k4096(Src src, const int8_t* __restrict__ signs, int8_t* __restrict__ packed, uint16_t* __restrict__ scale,
+         Prefetch pf) {
     __shared__ float buf[K4_LDS];
+    if (prefetch_tail<K4_THREADS>(pf)) return;
     k1_k4096_body<RT>(src, signs, packed, scale, buf);
 }
 
@@ -102,9 +138,10 @@ k1_k4096(Src src, const int8_t* __restrict__ signs, int8_t* __restrict__ packed,
 template <bool RESID, bool RT>
 __global__ void __launch_bounds__(K4_THREADS)
 k1_k4096_rms(RowRms<RESID> src, const uint16_t* __restrict__ nw, const int8_t* __restrict__ signs,
-             int8_t* __restrict__ packed, uint16_t* __restrict__ scale) {
+             int8_t* __restrict__ packed, uint16_t* __restrict__ scale, Prefetch pf) {
     __shared__ float buf[K4_LDS];
     __shared__ float red[4];
+    if (prefetch_tail<K4_THREADS>(pf)) return;
     src.w0 = *reinterpret_cast<const v4u*>(nw + 16 * threadIdx.x);
     src.w1 = *reinterpret_cast<const v4u*>(nw + 16 * threadIdx.x + 8);
     src.red = red;
@@ -116,8 +153,10 @@ k1_k4096_rms(RowRms<RESID> src, const uint16_t* __restrict__ nw, const int8_t* _
 // repeat the row's last 16 columns, so that every load is unconditional.
 template <class Src, bool RT>
 __global__ void __launch_bounds__(K12_THREADS)
-k1_k12288(Src src, const int8_t* __restrict__ signs, int8_t* __restrict__ packed, uint16_t* __restrict__ scale) {
+k1_k12288(Src src, const int8_t* __restrict__ signs, int8_t* __restrict__ packed, uint16_t* __restrict__ scale,
+          Prefetch pf) {
     __shared__ float buf[K12_LDS];
+    if (prefetch_tail<K12_THREADS>(pf)) return;
     const v4u sv = k1_signs12288(signs);
     const int64_t row = blockIdx.x;
     const int c0 = 16 * min((int)threadIdx.x, 767);
@@ -129,37 +168,39 @@ k1_k12288(Src src, const int8_t* __restrict__ signs, int8_t* __restrict__ packed
 
 template <class Src>
 hipError_t launch_k4096(const Src& src, const int8_t* signs, int8_t* packed, uint16_t* scale, int M, bool rt,
-                        hipStream_t st) {
+                        Prefetch pf, hipStream_t st) {
+    pf.rows = M;
+    const dim3 grid(prefetch_grid(M, pf, K4_THREADS));
     if (rt)
-        hipLaunchKernelGGL((k1_k4096<Src, true>), dim3((unsigned)M), dim3(K4_THREADS), 0, st, src, signs, packed,
-                           scale);
+        hipLaunchKernelGGL((k1_k4096<Src, true>), grid, dim3(K4_THREADS), 0, st, src, signs, packed, scale, pf);
     else
-        hipLaunchKernelGGL((k1_k4096<Src, false>), dim3((unsigned)M), dim3(K4_THREADS), 0, st, src, signs, packed,
-                           scale);
+        hipLaunchKernelGGL((k1_k4096<Src, false>), grid, dim3(K4_THREADS), 0, st, src, signs, packed, scale, pf);
     return hipGetLastError();
 }
 
 template <class Src>
 hipError_t launch_k12288(const Src& src, const int8_t* signs, int8_t* packed, uint16_t* scale, int M, bool rt,
-                         hipStream_t st) {
+                         Prefetch pf, hipStream_t st) {
+    pf.rows = M;
+    const dim3 grid(prefetch_grid(M, pf, K12_THREADS));
     if (rt)
-        hipLaunchKernelGGL((k1_k12288<Src, true>), dim3((unsigned)M), dim3(K12_THREADS), 0, st, src, signs, packed,
-                           scale);
+        hipLaunchKernelGGL((k1_k12288<Src, true>), grid, dim3(K12_THREADS), 0, st, src, signs, packed, scale, pf);
     else
-        hipLaunchKernelGGL((k1_k12288<Src, false>), dim3((unsigned)M), dim3(K12_THREADS), 0, st, src, signs, packed,
-                           scale);
+        hipLaunchKernelGGL((k1_k12288<Src, false>), grid, dim3(K12_THREADS), 0, st, src, signs, packed, scale, pf);
     return hipGetLastError();
 }
 
 template <bool RESID>
 hipError_t launch_rms4096(const RowRms<RESID>& src, const uint16_t* nw, const int8_t* signs, int8_t* packed,
-                          uint16_t* scale, int M, bool rt, hipStream_t st) {
+                          uint16_t* scale, int M, bool rt, Prefetch pf, hipStream_t st) {
+    pf.rows = M;
+    const dim3 grid(prefetch_grid(M, pf, K4_THREADS));
     if (rt)
-        hipLaunchKernelGGL((k1_k4096_rms<RESID, true>), dim3((unsigned)M), dim3(K4_THREADS), 0, st, src, nw, signs,
-                           packed, scale);
+        hipLaunchKernelGGL((k1_k4096_rms<RESID, true>), grid, dim3(K4_THREADS), 0, st, src, nw, signs, packed, scale,
+                           pf);
     else
-        hipLaunchKernelGGL((k1_k4096_rms<RESID, false>), dim3((unsigned)M), dim3(K4_THREADS), 0, st, src, nw, signs,
-                           packed, scale);
+        hipLaunchKernelGGL((k1_k4096_rms<RESID, false>), grid, dim3(K4_THREADS), 0, st, src, nw, signs, packed,
+                           scale, pf);
     return hipGetLastError();
 }
 
@@ -219,8 +260,18 @@ k1_block128(const uint16_t* __restrict__ x, const int8_t* __restrict__ signs,
 namespace nv4 {
 namespace {
 
+// Prefetch arguments: NULL / 0 for none; otherwise bytes a positive multiple
+// of 16 (at most 2^40) and the buffer 16-byte aligned.
+int check_prefetch(const void* p, int64_t bytes) {
+    if (bytes == 0) return NV4_OK;
+    if (!p) return NV4_E_NULL;
+    if (bytes < 16 || bytes % 16 || bytes > (1LL << 40)) return NV4_E_SHAPE;
+    if (reinterpret_cast<uintptr_t>(p) % 16) return NV4_E_ALIGN;
+    return NV4_OK;
+}
+
 int quant_pack_impl(const void* x, const int8_t* signs, int8_t* packed, void* scale, int64_t M, int64_t K,
-                    int layout, bool rt, void* stream) {
+                    int layout, bool rt, Prefetch pf, void* stream) {
     if (!x || !signs || !packed || !scale) return NV4_E_NULL;
     if (M < 1 || M > 0x7fffffffLL) return NV4_E_SHAPE;
     if (reinterpret_cast<uintptr_t>(x) % 16 || reinterpret_cast<uintptr_t>(packed) % 8 ||
@@ -230,8 +281,8 @@ int quant_pack_impl(const void* x, const int8_t* signs, int8_t* packed, void* sc
     if (layout == NV4_LAYOUT_REFERENCE) {
         const auto* xp = static_cast<const uint16_t*>(x);
         auto* sp = static_cast<uint16_t*>(scale);
-        if (K == 4096) return (int)launch_k4096(RowX{xp, 4096}, signs, packed, sp, (int)M, rt, st);
-        if (K == 12288) return (int)launch_k12288(RowX{xp, 12288}, signs, packed, sp, (int)M, rt, st);
+        if (K == 4096) return (int)launch_k4096(RowX{xp, 4096}, signs, packed, sp, (int)M, rt, pf, st);
+        if (K == 12288) return (int)launch_k12288(RowX{xp, 12288}, signs, packed, sp, (int)M, rt, pf, st);
         return NV4_E_SHAPE;
     }
     if (layout == NV4_LAYOUT_BLOCK128 && !rt) {
@@ -249,7 +300,7 @@ int quant_pack_impl(const void* x, const int8_t* signs, int8_t* packed, void* sc
 
 int rmsnorm_quant_impl(const void* x, const void* residual_in, void* residual_out, const void* norm_weight,
                        float eps, const int8_t* signs, int8_t* packed, void* scale, int64_t M, int64_t K, bool rt,
-                       void* stream) {
+                       Prefetch pf, void* stream) {
     if (!x || !norm_weight || !signs || !packed || !scale || (!residual_in) != (!residual_out)) return NV4_E_NULL;
     if (M < 1 || M > 0x7fffffffLL || K != 4096) return NV4_E_SHAPE;
     if (reinterpret_cast<uintptr_t>(x) % 16 || reinterpret_cast<uintptr_t>(residual_in) % 16 ||
@@ -264,14 +315,14 @@ int rmsnorm_quant_impl(const void* x, const void* residual_in, void* residual_ou
     if (residual_in) {
         RowRms<true> src{xp, static_cast<const uint16_t*>(residual_in), static_cast<uint16_t*>(residual_out), eps,
                          {}, {}, nullptr};
-        return (int)launch_rms4096(src, wp, signs, packed, sp, (int)M, rt, st);
+        return (int)launch_rms4096(src, wp, signs, packed, sp, (int)M, rt, pf, st);
     }
     RowRms<false> src{xp, nullptr, nullptr, eps, {}, {}, nullptr};
-    return (int)launch_rms4096(src, wp, signs, packed, sp, (int)M, rt, st);
+    return (int)launch_rms4096(src, wp, signs, packed, sp, (int)M, rt, pf, st);
 }
 
 int silu_quant_impl(const void* gate_up, const int8_t* signs, int8_t* packed, void* scale, int64_t M, int64_t K,
-                    bool rt, void* stream) {
+                    bool rt, Prefetch pf, void* stream) {
     if (!gate_up || !signs || !packed || !scale) return NV4_E_NULL;
     if (M < 1 || M > 0x7fffffffLL || (K != 4096 && K != 12288)) return NV4_E_SHAPE;
     if (reinterpret_cast<uintptr_t>(gate_up) % 16 || reinterpret_cast<uintptr_t>(packed) % 8 ||
@@ -280,8 +331,8 @@ int silu_quant_impl(const void* gate_up, const int8_t* signs, int8_t* packed, vo
     hipStream_t st = static_cast<hipStream_t>(stream);
     const auto* gp = static_cast<const uint16_t*>(gate_up);
     auto* sp = static_cast<uint16_t*>(scale);
-    if (K == 4096) return (int)launch_k4096(RowSilu{gp, 4096}, signs, packed, sp, (int)M, rt, st);
-    return (int)launch_k12288(RowSilu{gp, 12288}, signs, packed, sp, (int)M, rt, st);
+    if (K == 4096) return (int)launch_k4096(RowSilu{gp, 4096}, signs, packed, sp, (int)M, rt, pf, st);
+    return (int)launch_k12288(RowSilu{gp, 12288}, signs, packed, sp, (int)M, rt, pf, st);
 }
 
 }  // namespace
@@ -289,35 +340,46 @@ int silu_quant_impl(const void* gate_up, const int8_t* signs, int8_t* packed, vo
 
 extern "C" int nv4_rht_quant_pack(const void* x, const int8_t* signs, int8_t* packed, void* scale,
                                   int64_t M, int64_t K, int layout, void* stream) {
-    return nv4::quant_pack_impl(x, signs, packed, scale, M, K, layout, false, stream);
+    return nv4::quant_pack_impl(x, signs, packed, scale, M, K, layout, false, nv4::Prefetch{}, stream);
 }
 
 extern "C" int nv4_rht_quant_pack_rowtiled(const void* x, const int8_t* signs, int8_t* packed_rt, void* scale,
-                                           int64_t M, int64_t K, void* stream) {
-    return nv4::quant_pack_impl(x, signs, packed_rt, scale, M, K, NV4_LAYOUT_REFERENCE, true, stream);
+                                           int64_t M, int64_t K, const void* prefetch, int64_t prefetch_bytes,
+                                           void* stream) {
+    const int rc = nv4::check_prefetch(prefetch, prefetch_bytes);
+    if (rc != NV4_OK) return rc;
+    return nv4::quant_pack_impl(x, signs, packed_rt, scale, M, K, NV4_LAYOUT_REFERENCE, true,
+                                nv4::Prefetch{static_cast<const int8_t*>(prefetch), prefetch_bytes, 0}, stream);
 }
 
 extern "C" int nv4_rmsnorm_rht_quant_pack(const void* x, const void* residual_in, void* residual_out,
                                           const void* norm_weight, float eps, const int8_t* signs, int8_t* packed,
                                           void* scale, int64_t M, int64_t K, void* stream) {
     return nv4::rmsnorm_quant_impl(x, residual_in, residual_out, norm_weight, eps, signs, packed, scale, M, K, false,
-                                   stream);
+                                   nv4::Prefetch{}, stream);
 }
 
 extern "C" int nv4_rmsnorm_rht_quant_pack_rowtiled(const void* x, const void* residual_in, void* residual_out,
                                                    const void* norm_weight, float eps, const int8_t* signs,
                                                    int8_t* packed_rt, void* scale, int64_t M, int64_t K,
-                                                   void* stream) {
+                                                   const void* prefetch, int64_t prefetch_bytes, void* stream) {
+    const int rc = nv4::check_prefetch(prefetch, prefetch_bytes);
+    if (rc != NV4_OK) return rc;
     return nv4::rmsnorm_quant_impl(x, residual_in, residual_out, norm_weight, eps, signs, packed_rt, scale, M, K,
-                                   true, stream);
+                                   true, nv4::Prefetch{static_cast<const int8_t*>(prefetch), prefetch_bytes, 0},
+                                   stream);
 }
 
 extern "C" int nv4_silu_mul_rht_quant_pack(const void* gate_up, const int8_t* signs, int8_t* packed, void* scale,
                                            int64_t M, int64_t K, void* stream) {
-    return nv4::silu_quant_impl(gate_up, signs, packed, scale, M, K, false, stream);
+    return nv4::silu_quant_impl(gate_up, signs, packed, scale, M, K, false, nv4::Prefetch{}, stream);
 }
 
 extern "C" int nv4_silu_mul_rht_quant_pack_rowtiled(const void* gate_up, const int8_t* signs, int8_t* packed_rt,
-                                                    void* scale, int64_t M, int64_t K, void* stream) {
-    return nv4::silu_quant_impl(gate_up, signs, packed_rt, scale, M, K, true, stream);
+                                                    void* scale, int64_t M, int64_t K, const void* prefetch,
+                                                    int64_t prefetch_bytes, void* stream) {
+    const int rc = nv4::check_prefetch(prefetch, prefetch_bytes);
+    if (rc != NV4_OK) return rc;
+    return nv4::silu_quant_impl(gate_up, signs, packed_rt, scale, M, K, true,
+                                nv4::Prefetch{static_cast<const int8_t*>(prefetch), prefetch_bytes, 0}, stream);
 }

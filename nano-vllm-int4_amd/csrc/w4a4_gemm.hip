@@ -731,7 +731,11 @@ int linear_impl(const void* x, const int8_t* signs, const int8_t* w, const void*
     if (K != 4096 && K != 12288) return NV4_E_SHAPE;
     if (N < 1 || N % 8 || (tiled && N % 16)) return NV4_E_SHAPE;  // checked before K1 runs
     if (rowtiled && (M < 1 || M > 32)) return NV4_E_SHAPE;
-    const int rc = rowtiled ? nv4_rht_quant_pack_rowtiled(x, signs, a_packed, a_scale, M, K, stream)
+    // Decode-sized calls: K1's idle CUs read the head of the weights ahead of
+    // the GEMM (into the Infinity Cache; see the prefetch tail of K1).
+    const int64_t pf = nv4_w4a4_prefetch_bytes(N, K);
+    const int rc = rowtiled ? nv4_rht_quant_pack_rowtiled(x, signs, a_packed, a_scale, M, K, pf > 0 ? w : nullptr,
+                                                          pf, stream)
                             : nv4_rht_quant_pack(x, signs, a_packed, a_scale, M, K, NV4_LAYOUT_REFERENCE, stream);
     if (rc != NV4_OK) return rc;
     return gemm_impl(a_packed, w, a_scale, sw, 1, out, 0, tiled, rowtiled, M, N, K, stream);
@@ -754,6 +758,19 @@ int tile_impl(const int8_t* src, int8_t* dst, bool to_tiled, int64_t N, int64_t 
 
 }  // namespace
 }  // namespace nv4
+
+extern "C" int64_t nv4_w4a4_prefetch_bytes(int64_t N, int64_t K) {
+    // How much of a decode GEMM's packed weights the K1 before it reads
+    // ahead.  Measured on the Qwen3-8B projections at M = 32 (K1 + GEMM per
+    // call): K1 at K = 12288 runs long enough to bring in all of down's 25 MB
+    // (14.9 -> 13.6 us); at K = 4096 about 6 MB fits in K1's time (o 8.4 ->
+    // 8.1, qkv 10.7 -> 10.1-10.2, gate_up 19.0 -> 18.2 us), while reading
+    // gate_up's 50 MB whole made the pair 4.5 us slower.
+    if (N < 1 || K < 128 || K % 128 || N > (1LL << 31) || K > (1LL << 20)) return 0;
+    const int64_t bytes = N * K / 2;
+    const int64_t cap = K >= 12288 ? (32LL << 20) : (6LL << 20);
+    return bytes < cap ? bytes : cap;
+}
 
 extern "C" int nv4_w4a4_linear(const void* x, const int8_t* signs, const int8_t* w, const void* sw,
                                void* out, int8_t* a_packed, void* a_scale,

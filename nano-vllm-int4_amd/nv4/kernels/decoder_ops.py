@@ -22,6 +22,7 @@ import ctypes
 import torch
 
 from .. import _lib
+from .rht_a4 import prefetch_args
 
 
 def _ptr(t):
@@ -137,12 +138,14 @@ def _k1_outputs(M, K, dev, out_packed, out_scale, rowtiled=False):
     return out_packed, out_scale
 
 
-def rmsnorm_rht_quant_pack(x, weight, eps, signs, residual=None, out_packed=None, out_scale=None, rowtiled=False):
+def rmsnorm_rht_quant_pack(x, weight, eps, signs, residual=None, out_packed=None, out_scale=None, rowtiled=False,
+                           prefetch=None):
     """x bf16 [M, 4096] -> (packed, scale) of rht_quant_pack(rmsnorm(x)); with
     ``residual`` the norm input is x + residual, whose bf16 rounding is written
     into ``residual`` and returned as a third element.  ``rowtiled``: the codes
     in the row-tiled order of ``rht_quant_pack_rowtiled`` ([ceil(M/16)*16, K/2],
-    read by ``w4a4_gemm_rowtiled``)."""
+    read by ``w4a4_gemm_rowtiled``), with its ``prefetch`` (the consuming
+    GEMM's weights)."""
     if x.ndim != 2 or x.shape[1] != 4096 or x.dtype != torch.bfloat16 or not x.is_contiguous():
         raise ValueError("Expected contiguous BF16 x[M,4096]")
     if weight.dtype != torch.bfloat16 or tuple(weight.shape) != (4096,) or signs.dtype != torch.int8 \
@@ -157,15 +160,19 @@ def rmsnorm_rht_quant_pack(x, weight, eps, signs, residual=None, out_packed=None
     _check_dev((x, weight, signs, residual, out_packed, out_scale), dev)
     lib = _lib.load()
     stream = torch.cuda.current_stream(dev).cuda_stream
+    extra = prefetch_args(prefetch) if rowtiled else ()
+    if not rowtiled and prefetch is not None:
+        raise ValueError("prefetch goes with rowtiled=True")
     fn = lib.nv4_rmsnorm_rht_quant_pack_rowtiled if rowtiled else lib.nv4_rmsnorm_rht_quant_pack
     with torch.cuda.device(dev):
         rc = fn(_ptr(x), _ptr(residual), _ptr(residual), _ptr(weight),
-                ctypes.c_float(eps), _ptr(signs), _ptr(out_packed), _ptr(out_scale), M, K, ctypes.c_void_p(stream))
+                ctypes.c_float(eps), _ptr(signs), _ptr(out_packed), _ptr(out_scale), M, K, *extra,
+                ctypes.c_void_p(stream))
     _lib.check(rc, "rmsnorm_rht_quant_pack")
     return (out_packed, out_scale) if residual is None else (out_packed, out_scale, residual)
 
 
-def silu_mul_rht_quant_pack(gate_up, signs, out_packed=None, out_scale=None, rowtiled=False):
+def silu_mul_rht_quant_pack(gate_up, signs, out_packed=None, out_scale=None, rowtiled=False, prefetch=None):
     """gate_up bf16 [M, 2K] (K = 4096 or 12288) -> (packed, scale) of
     rht_quant_pack(silu_mul(gate_up)); ``rowtiled`` as in
     ``rmsnorm_rht_quant_pack``."""
@@ -180,8 +187,11 @@ def silu_mul_rht_quant_pack(gate_up, signs, out_packed=None, out_scale=None, row
     _check_dev((gate_up, signs, out_packed, out_scale), dev)
     lib = _lib.load()
     stream = torch.cuda.current_stream(dev).cuda_stream
+    extra = prefetch_args(prefetch) if rowtiled else ()
+    if not rowtiled and prefetch is not None:
+        raise ValueError("prefetch goes with rowtiled=True")
     fn = lib.nv4_silu_mul_rht_quant_pack_rowtiled if rowtiled else lib.nv4_silu_mul_rht_quant_pack
     with torch.cuda.device(dev):
-        rc = fn(_ptr(gate_up), _ptr(signs), _ptr(out_packed), _ptr(out_scale), M, K, ctypes.c_void_p(stream))
+        rc = fn(_ptr(gate_up), _ptr(signs), _ptr(out_packed), _ptr(out_scale), M, K, *extra, ctypes.c_void_p(stream))
     _lib.check(rc, "silu_mul_rht_quant_pack")
     return out_packed, out_scale

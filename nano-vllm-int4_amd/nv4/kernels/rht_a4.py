@@ -110,12 +110,27 @@ def rowtiled_rows(m):
     return (m + 15) // 16 * 16
 
 
-def rht_quant_pack_rowtiled(x, signs, *, out_packed=None, out_scale=None):
+def prefetch_args(prefetch):
+    """(pointer, bytes) of a buffer for the prefetch tail of the row-tiled K1
+    launches: a contiguous CUDA tensor whose size is a multiple of 16 bytes,
+    or None."""
+    if prefetch is None:
+        return None, 0
+    n = prefetch.numel() * prefetch.element_size()
+    if not prefetch.is_cuda or not prefetch.is_contiguous() or n % 16:
+        raise ValueError("prefetch must be a contiguous CUDA tensor of a multiple of 16 bytes")
+    return ctypes.c_void_p(prefetch.data_ptr()), n
+
+
+def rht_quant_pack_rowtiled(x, signs, *, out_packed=None, out_scale=None, prefetch=None):
     """``rht_quant_pack`` with the packed codes in the row-tiled order that the
     decode GEMM reads (``nv4_rht_quant_pack_rowtiled``): out_packed int8
     [ceil(M/16)*16, K/2] holds the same codes as the [M,K/2] form, in 1 KiB
     blocks of 16 rows x 128 k in matrix-core lane order; out_scale bf16
-    [M,K/128] as usual.  Returns (out_packed, out_scale)."""
+    [M,K/128] as usual.  ``prefetch``: a tensor (the weights of the GEMM that
+    consumes the codes) that spare workgroups of the launch read into the
+    Infinity Cache meanwhile; no result depends on it.  Returns
+    (out_packed, out_scale)."""
     if x.ndim != 2 or x.dtype != torch.bfloat16 or x.shape[1] not in (4096, 12288) or x.shape[0] < 1:
         raise ValueError('Expected BF16 X[M,K], M>0, K=4096/12288')
     m, k = x.shape
@@ -132,11 +147,15 @@ def rht_quant_pack_rowtiled(x, signs, *, out_packed=None, out_scale=None):
     if any(not t.is_cuda or not t.is_contiguous() or t.device != x.device
            for t in [x, signs, out_packed, out_scale]):
         raise ValueError('All tensors must be contiguous on one CUDA device')
+    if prefetch is not None and prefetch.device != x.device:
+        raise ValueError('prefetch must be on the input device')
+    pf, pf_bytes = prefetch_args(prefetch)
     lib = _lib.load()
     stream = torch.cuda.current_stream(x.device).cuda_stream
     with torch.cuda.device(x.device):
         rc = lib.nv4_rht_quant_pack_rowtiled(ctypes.c_void_p(x.data_ptr()), ctypes.c_void_p(signs.data_ptr()),
                                              ctypes.c_void_p(out_packed.data_ptr()),
-                                             ctypes.c_void_p(out_scale.data_ptr()), m, k, ctypes.c_void_p(stream))
+                                             ctypes.c_void_p(out_scale.data_ptr()), m, k, pf, pf_bytes,
+                                             ctypes.c_void_p(stream))
     _lib.check(rc, "rht_quant_pack_rowtiled")
     return out_packed, out_scale

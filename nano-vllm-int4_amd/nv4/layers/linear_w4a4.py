@@ -31,6 +31,7 @@ import torch
 from torch import nn
 import torch.distributed as dist
 
+from .. import _lib
 from ..kernels.w4a4_grouped import (ROWTILED_MAX_M, keep_weights_f6, tile_weights, untile_weights, w4a4_gemm_rowtiled,
                                    w4a4_grouped_gemm, weights_to_f6)
 from ..kernels.w4a4_linear import w4a4_linear
@@ -57,6 +58,9 @@ class W4A4Linear(nn.Module):
         self.register_buffer("weight_f6", None, persistent=False)
         self.weights_tiled = False
         self.keep_f6 = keep_weights_f6
+        # Decode-sized forwards: the K1 launch reads this layer's weights into
+        # the Infinity Cache while its one-workgroup-per-row transform runs.
+        self.prefetch_weights = True
 
     @torch.no_grad()
     def tile_weights_(self) -> "W4A4Linear":
@@ -139,6 +143,15 @@ class W4A4Linear(nn.Module):
         (tiled weights and M <= 32), so its producer should quantize with
         ``rowtiled=True``."""
         return self.weights_tiled and m <= ROWTILED_MAX_M
+
+    def prefetch_target(self, rowtiled: bool):
+        """What the K1 producing this layer's row-tiled codes should prefetch:
+        the head of its packed weights (``nv4_w4a4_prefetch_bytes``), or None
+        off the row-tiled path."""
+        if not (rowtiled and self.prefetch_weights):
+            return None
+        n = _lib.load().nv4_w4a4_prefetch_bytes(self.out_features, self.in_features)
+        return self.packed_weight.view(-1)[:n] if n > 0 else None
 
     def forward_quantized(self, packed: torch.Tensor, scale: torch.Tensor, rowtiled: bool = False) -> torch.Tensor:
         """The GEMM half of ``forward`` on activations already quantized by

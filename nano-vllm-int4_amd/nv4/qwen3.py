@@ -197,12 +197,15 @@ class Qwen3MLP(nn.Module):
     def forward_fused(self, x, residual, norm):
         """W4A4: post-attention add+RMSNorm inside gate_up's quantization,
         SiLU-mul inside down's; returns (output, residual)."""
+        # Decode-sized M: row-tiled codes, and each K1 reads the weights of
+        # the GEMM that follows it into the Infinity Cache.
         rt = self.gate_up_proj.uses_rowtiled(x.shape[0])
         packed, scale, residual = rmsnorm_rht_quant_pack(x, norm.weight, norm.eps, self.gate_up_proj.signs, residual,
-                                                         rowtiled=rt)
+                                                         rowtiled=rt, prefetch=self.gate_up_proj.prefetch_target(rt))
         gate_up = self.gate_up_proj.forward_quantized(packed, scale, rowtiled=rt)
         rt = self.down_proj.uses_rowtiled(x.shape[0])
-        packed, scale = silu_mul_rht_quant_pack(gate_up, self.down_proj.signs, rowtiled=rt)
+        packed, scale = silu_mul_rht_quant_pack(gate_up, self.down_proj.signs, rowtiled=rt,
+                                                prefetch=self.down_proj.prefetch_target(rt))
         return self.down_proj.forward_quantized(packed, scale, rowtiled=rt), residual
 
 
@@ -225,13 +228,15 @@ class Qwen3DecoderLayer(nn.Module):
             attn = self.self_attn
             norm = self.input_layernorm
             rt = attn.qkv_proj.uses_rowtiled(hidden_states.shape[0])
+            pf = attn.qkv_proj.prefetch_target(rt)
             if residual is None:
                 packed, scale = rmsnorm_rht_quant_pack(hidden_states, norm.weight, norm.eps, attn.qkv_proj.signs,
-                                                       rowtiled=rt)
+                                                       rowtiled=rt, prefetch=pf)
                 residual = hidden_states
             else:
                 packed, scale, residual = rmsnorm_rht_quant_pack(hidden_states, norm.weight, norm.eps,
-                                                                 attn.qkv_proj.signs, residual, rowtiled=rt)
+                                                                 attn.qkv_proj.signs, residual, rowtiled=rt,
+                                                                 prefetch=pf)
             hidden_states = attn(positions, qkv=attn.qkv_proj.forward_quantized(packed, scale, rowtiled=rt))
             return self.mlp.forward_fused(hidden_states, residual, self.post_attention_layernorm)
         if residual is None:

@@ -226,6 +226,15 @@ def test_paged_decode_attention_size_checks_do_not_wrap():
     assert g(*wrap, 32, 32, 8, 128, (1 << 31) + 1, 4352, 0.1, None) == _lib.NV4_E_SHAPE
 
 
+def test_prefetch_size_rule():
+    f = _lib.load().nv4_w4a4_prefetch_bytes
+    assert f(4096, 12288) == 4096 * 6144           # down: all of its weights
+    for n in (4096, 6144, 24576):                   # K = 4096: the first 6 MiB
+        assert f(n, 4096) == 6 << 20
+    assert f(16, 256) == 16 * 128
+    assert f(0, 4096) == 0 and f(64, 100) == 0
+
+
 def test_rowtiled_entry_point_rejections():
     lib = _lib.load()
     ok = [P(A16)] * 4
@@ -237,17 +246,24 @@ def test_rowtiled_entry_point_rejections():
     assert g(*ok, 1, P(A16), 0, 4, 64, 4000, None) == _lib.NV4_E_SHAPE     # K % 128
     assert g(P(A16 + 8), *ok[1:], 1, P(A16), 0, 4, 64, 4096, None) == _lib.NV4_E_ALIGN
     k = lib.nv4_rht_quant_pack_rowtiled
-    assert k(None, P(A16), P(A16), P(A16), 4, 4096, None) == _lib.NV4_E_NULL
-    assert k(P(A16), P(A16), P(A16), P(A16), 4, 2048, None) == _lib.NV4_E_SHAPE
-    assert k(P(A16), P(A16), P(A16), P(A16), 0, 4096, None) == _lib.NV4_E_SHAPE
+    assert k(None, P(A16), P(A16), P(A16), 4, 4096, None, 0, None) == _lib.NV4_E_NULL
+    assert k(P(A16), P(A16), P(A16), P(A16), 4, 2048, None, 0, None) == _lib.NV4_E_SHAPE
+    assert k(P(A16), P(A16), P(A16), P(A16), 0, 4096, None, 0, None) == _lib.NV4_E_SHAPE
+    # prefetch arguments: a buffer with a positive multiple of 16 bytes, 16-byte aligned
+    assert k(P(A16), P(A16), P(A16), P(A16), 4, 4096, None, 4096, None) == _lib.NV4_E_NULL
+    assert k(P(A16), P(A16), P(A16), P(A16), 4, 4096, P(A16), 100, None) == _lib.NV4_E_SHAPE
+    assert k(P(A16), P(A16), P(A16), P(A16), 4, 4096, P(A16), -16, None) == _lib.NV4_E_SHAPE
+    assert k(P(A16), P(A16), P(A16), P(A16), 4, 4096, P(A16 + 8), 4096, None) == _lib.NV4_E_ALIGN
     lin = lib.nv4_w4a4_linear_rowtiled
     assert lin(*([P(A16)] * 7), 33, 64, 4096, None) == _lib.NV4_E_SHAPE
     assert lin(*([P(A16)] * 7), 4, 72, 4096, None) == _lib.NV4_E_SHAPE
     assert lin(*([P(A16)] * 7), 4, 64, 2048, None) == _lib.NV4_E_SHAPE
     r = lib.nv4_rmsnorm_rht_quant_pack_rowtiled
-    assert r(P(A16), None, None, P(A16), 1e-6, P(A16), P(A16), P(A16), 4, 12288, None) == _lib.NV4_E_SHAPE
+    assert r(P(A16), None, None, P(A16), 1e-6, P(A16), P(A16), P(A16), 4, 12288, None, 0, None) == _lib.NV4_E_SHAPE
+    assert r(P(A16), None, None, P(A16), 1e-6, P(A16), P(A16), P(A16), 4, 4096, P(A16), 24, None) == _lib.NV4_E_SHAPE
     sm = lib.nv4_silu_mul_rht_quant_pack_rowtiled
-    assert sm(P(A16), P(A16), P(A16), P(A16), 4, 2048, None) == _lib.NV4_E_SHAPE
+    assert sm(P(A16), P(A16), P(A16), P(A16), 4, 2048, None, 0, None) == _lib.NV4_E_SHAPE
+    assert sm(P(A16), P(A16), P(A16), P(A16), 4, 4096, None, 32, None) == _lib.NV4_E_NULL
 
 
 def test_gumbel_split_rejections():

@@ -230,3 +230,32 @@ def test_linear_rowtiled_path_vs_oracle_chain(proj, M):
     p_ref, s_ref = oracle.rht_quant_pack(bf16_bits(case.x), case.signs.numpy())
     exp = oracle.w4a4_gemm(p_ref, case.w_packed.numpy(), s_ref, bf16_bits(case.w_scale))
     assert np.array_equal(bf16_bits(out), exp)
+
+
+@pytest.mark.parametrize("M", [1, 32])
+def test_k1_prefetch_tail_changes_nothing(M):
+    """The prefetch workgroups of the row-tiled K1 launches (reading the next
+    GEMM's weights into the Infinity Cache) write nothing: codes, scales and
+    the residual are the same bits with and without a 48 MiB prefetch, for
+    the plain, add+RMSNorm and SiLU-mul K1s."""
+    print(f"[k1-prefetch] M={M}", flush=True)
+    g = torch.Generator().manual_seed(31 + M)
+    buf = torch.randint(-128, 128, (48 << 20,), dtype=torch.int8).to(DEV)
+    x = torch.randn((M, 4096), generator=g).to(torch.bfloat16).to(DEV)
+    s4 = (torch.randint(0, 2, (4096,), generator=g) * 2 - 1).to(torch.int8).to(DEV)
+    a = rht_quant_pack_rowtiled(x, s4)
+    b = rht_quant_pack_rowtiled(x, s4, prefetch=buf)
+    w = (1 + 0.1 * torch.randn(4096, generator=g)).to(torch.bfloat16).to(DEV)
+    res = torch.randn((M, 4096), generator=g).to(torch.bfloat16).to(DEV)
+    r1, r2 = res.clone(), res.clone()
+    c = rmsnorm_rht_quant_pack(x, w, 1e-6, s4, r1, rowtiled=True)
+    d = rmsnorm_rht_quant_pack(x, w, 1e-6, s4, r2, rowtiled=True, prefetch=buf[: 12 << 20])
+    gu = torch.randn((M, 2 * 12288), generator=g).to(torch.bfloat16).to(DEV)
+    s12 = (torch.randint(0, 2, (12288,), generator=g) * 2 - 1).to(torch.int8).to(DEV)
+    e = silu_mul_rht_quant_pack(gu, s12, rowtiled=True)
+    f = silu_mul_rht_quant_pack(gu, s12, rowtiled=True, prefetch=buf)
+    torch.cuda.synchronize()
+    for u, v in ((a, b), (c[:2], d[:2]), (e, f)):  # rows past M of the block are never written: not compared
+        assert np.array_equal(untile(u[0].cpu().numpy(), M), untile(v[0].cpu().numpy(), M))
+        assert torch.equal(u[1].view(torch.int16), v[1].view(torch.int16))
+    assert torch.equal(r1.view(torch.int16), r2.view(torch.int16))
