@@ -265,10 +265,13 @@ int64_t nv4_w4a4_weights_f6_bytes(int64_t N, int64_t K);
  * Dequantization: bf16 activations use deq = bf16(bf16(q-z-1) * bf16(s)) as the
  * reference does; fp16 activations use deq = fp16((q-z-1) * s).  Products are
  * accumulated in fp32 over the whole K (deterministic; no split-K atomics).
- * For M <= 16 and K <= 4096 one launch applies the (bf16-rounded) scale per
- * group to exact sums of biased codes, sum x (q-z-1) s = s (S - (bias+z+1) X),
- * without rounding each dequantized weight: a difference far inside the
- * 1e-2 relative tolerance of the reference's own split-K product.
+ * Decode sizes -- M <= 16 (any K), or M <= 32 with K <= 4096 and
+ * ceil(N/32) <= the CU count; K*N/2 < 2^31; qweight 8-byte and scales 4-byte
+ * aligned -- run one launch (32 columns per workgroup over the whole K, no
+ * workspace) that applies the (bf16-rounded) scale per group to exact sums of
+ * biased codes, sum x (q-z-1) s = s (S - (bias+z+1) X), without rounding each
+ * dequantized weight: a difference far inside the 1e-2 relative tolerance of
+ * the reference's own split-K product.
  * group == 128; K % 128 == 0; N % 8 == 0; M >= 1.  x and out 16-byte aligned.
  */
 int nv4_w4a16_gemm(const void* x, int x_dtype, const int32_t* qweight, const int32_t* qzeros,

@@ -373,39 +373,47 @@ k3_reduce(const float* __restrict__ ws, void* __restrict__ out, int64_t MN, int 
 }
 
 // ----------------------------------------------------------------------------
-// Decode-sized kernel in one launch (M <= 16, K <= K3O_MAXK).  A workgroup
-// of 8 waves owns NB = 32 output columns over the whole K, so every output is
-// finished inside the workgroup: no workspace, no second launch.
+// Decode-sized kernel in one launch (M <= 16 any K, M <= 32 with K <= 4096).  A workgroup of 16 waves
+// owns 32 output columns over the whole K, so every output is finished inside
+// the workgroup: no workspace, no second launch.
+//  * Rounds: a round is one quantisation group (128 k = four 32-k steps) of
+//    one wave; wave w takes groups w, w + 16, w + 32, ...  A pass is two
+//    rounds per wave (4096 k for the workgroup); K beyond that runs further
+//    passes in the same launch.
+//  * Loads: every load of a pass is issued before any of its data is used,
+//    in the order it is needed -- the rounds' scale and zero words, round 0's
+//    activations and weights, then round 1's -- so the wave waits once per
+//    round on an in-order queue instead of once per load.
 //  * Weights: lane l (column slot c = l % 16, k-octet o = l / 16) loads the
-//    NB/16 words of columns n0 + (NB/16) c .. of one qweight row per 32-k
-//    step (16 lanes read NB * 4 contiguous bytes), all of a wave's steps up
-//    front.  Word j feeds the MFMA of column tile j, whose column i is
-//    n0 + (NB/16) i + j.
+//    two words of columns n0 + 2c, n0 + 2c + 1 of one qweight row per step
+//    (non-temporal: read once).  Word j feeds the MFMA of column tile j,
+//    whose column i is n0 + 2i + j.
+//  * Activations: a round's rows (M x 128 k) are read in whole lines -- 16
+//    lanes per row and round, 256 contiguous bytes -- into the wave's own
+//    LDS slot, each row's 16-byte octets XOR-swizzled by the row, and read
+//    back as MFMA A operands (rows past M repeat row M - 1; their results are
+//    dropped).  Up to 16 rows, both rounds go through VGPRs and are written
+//    octet-ordered (see below).  At 17..32 rows a round is 8 KiB per wave:
+//    round 0 goes straight from memory into the slot (buffer load to LDS),
+//    round 1 into VGPRs and into the slot once round 0 has been read.  No
+//    workgroup barrier before the epilogue: each wave reads only its slot.
 //  * Dequantisation by group: the MFMA B operand is the biased code
-//    128 + q (bf16 0x4300 | q) or 1024 + q (fp16 0x6400 | q), exact, built
-//    with one shift and one and-or per two codes; a further MFMA with an
-//    all-ones B gives the activation sums X over the same k.  For the wave's
-//    steps of one quantisation group the product is then
+//    128 + q (bf16 0x4300 | q) or 1024 + q (fp16 0x6400 | q), exact; a
+//    further MFMA with an all-ones B gives the activation sums X over the
+//    same k.  For the four steps of one group the product is then
 //        sum x (q - z - 1) s = s * (S - (bias + z + 1) X),
 //    two fmas per output and group instead of a rounded dequantised weight
 //    per code.  (The reference rounds each dequantised weight to the
 //    activation dtype; this form omits that rounding, a difference far
 //    inside the 1e-2 tolerance of a product the reference itself sums in a
-//    nondeterministic split-K order.)
-//  * Activations: codes of a k-octet are consumed in the order
-//    q0 q4 q1 q5 q2 q6 q3 q7, so activation octets are staged into LDS in
-//    that order.  Either all M rows over the whole K at once (M * K * 2 <=
-//    K3O_ONE_BYTES), or a two-slot ring of K3O_RING-byte chunks (ROWS x KC)
-//    loaded two chunks ahead, one barrier per chunk.  Rows at or beyond M are
-//    not read (A-operand rows alias row M - 1; their results are dropped).
-//  * Within a chunk wave w takes the SPW consecutive steps w*SPW ..; they lie
-//    in one quantisation group, so one scale and one zero word per lane and
-//    chunk.
-//  * At the end the 8 waves' fp32 tiles are added in wave order in LDS and
-//    rounded once (deterministic, no atomics).
+//    nondeterministic split-K order.)  Codes come out of a word in the
+//    order q0 q4 q1 q5 q2 q6 q3 q7, so activation octets are reordered the
+//    same way (octet_order) before they meet the codes.
+//  * Epilogue: each wave's fp32 tile goes to its own slot, then the 16 tiles
+//    are added in wave order and rounded once (deterministic, no atomics).
 // ----------------------------------------------------------------------------
-constexpr int K3O_MAXK = 4096;
-constexpr int K3O_ONE_BYTES = 65536;   // all activations staged at once when M * K * 2 fits
+constexpr int K3R_WAVES = 16;
+constexpr int K3R_NB = 32;  // columns per workgroup
 
 template <bool F16>
 struct BiasCode;
@@ -442,148 +450,181 @@ __device__ __forceinline__ v4u octet_order(v4u v) {
                __builtin_amdgcn_perm(v[3], v[1], 0x05040100u), __builtin_amdgcn_perm(v[3], v[1], 0x07060302u)};
 }
 
-template <int MB, int NB, int ST, int NWV, int RING, bool ONE, bool XF16, bool OF16>
-__global__ void __launch_bounds__(NWV * 64)
-k3_one(const uint16_t* __restrict__ x, const int32_t* __restrict__ qweight, const int32_t* __restrict__ qzeros,
-       const uint16_t* __restrict__ scales, void* __restrict__ out, int M, int N, int K) {
+// 16 bytes per lane from a buffer straight into LDS: lane l's bytes land at
+// lds + 16 l (the address is wave-uniform).
+__device__ __forceinline__ void load_lds16(__amdgpu_buffer_rsrc_t r, uint8_t* lds, uint32_t off) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16, off, 0, 0, 0);
+}
+
+// s_waitcnt immediate that waits until at most n vector-memory loads are
+// outstanding (expcnt and lgkmcnt left at their maxima).
+constexpr int vmcnt_imm(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
+
+template <int MR, bool MULTI, bool XF16, bool OF16>
+__global__ void __launch_bounds__(K3R_WAVES * 64)
+k3_rows(const uint16_t* __restrict__ x, const int32_t* __restrict__ qweight, const int32_t* __restrict__ qzeros,
+        const uint16_t* __restrict__ scales, void* __restrict__ out, int M, int N, int K) {
     using BC = BiasCode<XF16>;
     using vec = typename BC::vec;
-    constexpr int NT = NB / 16;                   // column tiles, words per lane and step
-    constexpr int ROWS = MB * 16;
-    constexpr int K3O_T = NWV * 64;
-    constexpr int KC = RING / (2 * ROWS);         // k per chunk (the group geometry of both modes)
-    constexpr int SPC = KC / 32;                  // 32-k steps per chunk
-    constexpr int SPW = SPC / NWV;                // steps per wave and chunk (4, 2 or 1)
-    constexpr int CPR = KC / 8;                   // octets per row and chunk
-    constexpr int PPT = RING / 16 / K3O_T;        // ring octets per thread and chunk (4)
-    constexpr int PPT1 = ONE ? K3O_ONE_BYTES / 16 / K3O_T : 1;
-    static_assert(SPW >= 1 && ST % SPW == 0, "chunk shape");
+    constexpr int NWV = K3R_WAVES, NT = 2, MB = MR > 16 ? 2 : 1;
+    constexpr bool DMA = MR > 16;                     // round 0 straight into LDS
+    constexpr int MRL = MR < 4 ? 4 : MR;              // rows laid out per slot (whole 1 KiB loads)
+    constexpr int LA = MRL / 4;                       // activation loads per lane and round
+    constexpr int SLOT = MRL * 256;                   // one round of activations
+    constexpr int PART = MB * NT * 1024;              // a wave's fp32 tiles
+    constexpr int REG = (DMA ? SLOT : 2 * SLOT) > PART ? (DMA ? SLOT : 2 * SLOT) : PART;
     extern __shared__ __align__(16) uint8_t smem[];
     const int t = threadIdx.x, lane = t & 63;
     const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
     const int c = lane & 15, o = lane >> 4;
-    const int n0 = blockIdx.x * NB;
+    const int n0 = blockIdx.x * K3R_NB;
     const int ncol = min(n0 + NT * c, N - NT);  // slots beyond N load the last valid columns (results dropped)
-    const int KS = K >> 5;
-    const int NCH = (KS + SPC - 1) / SPC;
-
+    const int G128 = K >> 7;
+    // Buffer resources: offsets with bit 31 set are out of range and read nothing.
     const __amdgpu_buffer_rsrc_t rx =
         __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(x), (short)0, (int)((uint32_t)M * K * 2u), K3_RSRC_WORD3);
-    auto load_chunk = [&](int ch, v4u (&xv)[PPT]) {
-        const int kbase = ch * KC, kvalid8 = min(KC, K - kbase) >> 3;
-#pragma unroll
-        for (int i = 0; i < PPT; ++i) {
-            const int p = t + i * K3O_T;
-            const int r = p / CPR, pc = min(p % CPR, kvalid8 - 1);
-            xv[i] = __builtin_bit_cast(v4u, __builtin_amdgcn_raw_buffer_load_b128(
-                                                rx, (int)(((uint32_t)r * K + kbase + pc * 8) * 2u), 0, 0));
-        }
-    };
-    auto store_chunk = [&](int ch, const v4u (&xv)[PPT]) {
-        uint8_t* base = smem + (ch & 1) * RING;
-#pragma unroll
-        for (int i = 0; i < PPT; ++i) {
-            const int p = t + i * K3O_T;
-            const int r = p / CPR, pc = p % CPR;
-            *reinterpret_cast<v4u*>(base + r * (KC * 2) + ((pc ^ (r & 7)) << 4)) = octet_order(xv[i]);
-        }
-    };
-    auto load_sz = [&](int ch, uint32_t& sw, uint32_t& zw) {
-        const int g = min((ch * SPC + wave * SPW) >> 2, (K >> 7) - 1);
-        if constexpr (NT == 2)
-            sw = *reinterpret_cast<const uint32_t*>(scales + (int64_t)g * N + ncol);
-        else
-            sw = (uint32_t)scales[(int64_t)g * N + ncol];
-        zw = (uint32_t)qzeros[(int64_t)g * (N >> 3) + (ncol >> 3)];
-    };
-
-    // ---- loads in the order their data is needed (vector loads complete in
-    // issue order): activations, the first scales, every weight step, and in
-    // ring mode the second chunk.
-    v4u x1[PPT1];
-    v4u xa[PPT], xb[PPT];
-    if constexpr (ONE) {
-        const int total = M * (K >> 3);
-#pragma unroll
-        for (int i = 0; i < PPT1; ++i) {
-            const int p = min(t + i * K3O_T, total - 1);
-            x1[i] = __builtin_bit_cast(v4u, __builtin_amdgcn_raw_buffer_load_b128(rx, (int)((uint32_t)p * 16u), 0, 0));
-        }
-    } else {
-        load_chunk(0, xa);
-    }
-    uint32_t sw, zw;
-    load_sz(0, sw, zw);
-    uint32_t wq[ST][NT];
-#pragma unroll
-    for (int i = 0; i < ST; ++i) {
-        const int ks = min((i / SPW) * SPC + wave * SPW + i % SPW, KS - 1);
-        const int32_t* src = qweight + (int64_t)(4 * ks + o) * N + ncol;
-        if constexpr (NT == 2) {
-            const uint2 v = *reinterpret_cast<const uint2*>(src);
-            wq[i][0] = v.x;
-            wq[i][NT - 1] = v.y;
-        } else {
-            wq[i][0] = (uint32_t)*src;
-        }
-    }
-    if constexpr (!ONE) load_chunk(min(1, NCH - 1), xb);
-
-    if constexpr (ONE) {
-        const int rowp = K >> 3, total = M * rowp;
-#pragma unroll
-        for (int i = 0; i < PPT1; ++i) {
-            const int p = min(t + i * K3O_T, total - 1);  // repeats of the last octet rewrite it unchanged
-            const int r = p / rowp, pc = p - r * rowp;
-            *reinterpret_cast<v4u*>(smem + r * (K * 2) + ((pc ^ (r & 7)) << 4)) = octet_order(x1[i]);
-        }
-        __syncthreads();
-    }
-
+    const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<int32_t*>(qweight), (short)0, (int)((uint32_t)(K >> 3) * N * 4u), K3_RSRC_WORD3);
+    uint8_t* reg = smem + wave * REG;
     const vec ones = __builtin_bit_cast(vec, v4u{BC::ONE, BC::ONE, BC::ONE, BC::ONE});
     const int zsh = 4 * (ncol & 7);
+    const int row_a = lane >> 4;  // activation load: row 4 i + row_a, octet (lane % 16) ^ row
     v4f total[MB][NT];
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
         for (int j = 0; j < NT; ++j) total[mb][j] = v4f{0.f, 0.f, 0.f, 0.f};
-    static_for<0, ST / SPW>([&](auto CH) {
-        constexpr int ch = CH;
-        if (ch >= NCH) return;  // uniform
-        if constexpr (!ONE) {
-            store_chunk(ch, (ch & 1) ? xb : xa);
-            if (ch + 2 < NCH) load_chunk(ch + 2, (ch & 1) ? xb : xa);  // uniform
-            __syncthreads();
+
+    // Two rounds per pass, all loads of both issued up front.  Several passes
+    // (K > 4096) only up to 16 rows: at 17..32 rows the pass loop's live state
+    // beside round 1's staging would spill.
+    static_assert(!(MULTI && DMA), "17..32 rows take K <= 4096 (one pass)");
+    constexpr int RPP = 2;
+    const int passes = MULTI ? (G128 + RPP * NWV - 1) / (RPP * NWV) : 1;  // MULTI false: K <= 4096
+    for (int p = 0; p < passes; ++p) {
+        int g[RPP];
+        uint32_t dead[RPP], aoff[RPP][LA], woff[RPP][4];
+#pragma unroll
+        for (int r = 0; r < RPP; ++r) {
+            const int gr = (RPP * p + r) * NWV + wave;
+            dead[r] = (uint32_t)(gr >= G128) << 31;  // rounds past K read nothing and add nothing
+            g[r] = min(gr, G128 - 1);
+            if constexpr (!DMA) {
+#pragma unroll
+                for (int i = 0; i < LA; ++i) {
+                    const int row = 4 * i + row_a, oc = (lane & 15) ^ (row & 15);
+                    aoff[r][i] = (((uint32_t)row * K + g[r] * 128 + oc * 8) * 2u) | dead[r] |
+                                 ((uint32_t)(row >= M) << 31);
+                }
+                const uint32_t w0 = (uint32_t)((g[r] * 16 + o) * N + ncol) * 4u;
+#pragma unroll
+                for (int s2 = 0; s2 < 4; ++s2) woff[r][s2] = (w0 + (uint32_t)s2 * 16u * (uint32_t)N) | dead[r];
+            }
         }
-        float sj[NT], cj[NT];
+        // ---- loads, issued before any of their data is used; offsets are
+        // computed ahead of them (no address arithmetic between the loads)
+        uint32_t sw[RPP], zw[RPP];
+        v4u xa[RPP][LA];
+        uint32_t wq[RPP][4][NT];
+        auto load_sz = [&]() {
 #pragma unroll
-        for (int j = 0; j < NT; ++j) {
-            sj[j] = BC::scale_of((uint16_t)(sw >> (16 * j)));
-            cj[j] = BC::BIAS + (float)((zw >> (zsh + 4 * j)) & 15u) + 1.0f;
+            for (int r = 0; r < RPP; ++r) {
+                sw[r] = *reinterpret_cast<const uint32_t*>(scales + (int64_t)g[r] * N + ncol);
+                zw[r] = (uint32_t)qzeros[(int64_t)g[r] * (N >> 3) + (ncol >> 3)];
+            }
+        };
+        auto load_w = [&](int r) {
+#pragma unroll
+            for (int s2 = 0; s2 < 4; ++s2) {
+                const auto v = __builtin_amdgcn_raw_buffer_load_b64(rw, (int)woff[r][s2], 0, 2);
+                wq[r][s2][0] = v[0];
+                wq[r][s2][1] = v[1];
+            }
+        };
+        if constexpr (!DMA) {
+            // up to 16 rows: the activations of both rounds (hot in L2, shared by every
+            // workgroup), the scale/zero words, then the weights
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int r = 0; r < RPP; ++r)
+#pragma unroll
+                for (int i = 0; i < LA; ++i)
+                    xa[r][i] = __builtin_bit_cast(v4u, __builtin_amdgcn_raw_buffer_load_b128(rx, (int)aoff[r][i], 0, 0));
+            load_sz();
+#pragma unroll
+            for (int r = 0; r < RPP; ++r) load_w(r);
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int r = 0; r < RPP; ++r)
+#pragma unroll
+                for (int i = 0; i < LA; ++i)
+                    *reinterpret_cast<v4u*>(reg + r * SLOT + (4 * i + row_a) * 256 + ((lane & 15) << 4)) =
+                        octet_order(xa[r][i]);
+        } else {
+            // 17..32 rows: scale/zero words, then per round its activations and
+            // weights (offsets of a round computed just before its loads)
+            load_sz();
+#pragma unroll
+            for (int r = 0; r < RPP; ++r) {
+#pragma unroll
+                for (int i = 0; i < LA; ++i) {
+                    const int row = 4 * i + row_a, oc = (lane & 15) ^ (row & 15);
+                    aoff[r][i] = (((uint32_t)row * K + g[r] * 128 + oc * 8) * 2u) | dead[r] |
+                                 ((uint32_t)(row >= M) << 31);
+                }
+                const uint32_t w0 = (uint32_t)((g[r] * 16 + o) * N + ncol) * 4u;
+#pragma unroll
+                for (int s2 = 0; s2 < 4; ++s2) woff[r][s2] = (w0 + (uint32_t)s2 * 16u * (uint32_t)N) | dead[r];
+                __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                for (int i = 0; i < LA; ++i) {
+                    if (r == 0)
+                        load_lds16(rx, reg + i * 1024, aoff[r][i]);
+                    else
+                        xa[r][i] = __builtin_bit_cast(v4u, __builtin_amdgcn_raw_buffer_load_b128(rx, (int)aoff[r][i], 0, 0));
+                }
+                load_w(r);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+            // round 0 in (the load to LDS included): round 1's loads may still be out
+            __builtin_amdgcn_s_waitcnt(vmcnt_imm(LA + 4));
         }
-        load_sz(min(ch + 1, NCH - 1), sw, zw);
-        const uint8_t* base = ONE ? smem : smem + (ch & 1) * RING;
-        const int rstride = ONE ? K * 2 : KC * 2;
-        v4f S[MB][NT], X[MB];
 #pragma unroll
-        for (int mb = 0; mb < MB; ++mb) {
-            X[mb] = v4f{0.f, 0.f, 0.f, 0.f};
+        for (int r = 0; r < RPP; ++r) {
+            uint8_t* slot = reg + (DMA ? 0 : r * SLOT);
+            const bool raw = DMA && r == 0;  // written by the load itself: octets still in memory order
+            if (DMA && r == 1) {
+                // round 1 through VGPRs: octet-ordered into the slot after round 0's reads
+                // (a wave's LDS operations complete in order)
 #pragma unroll
-            for (int j = 0; j < NT; ++j) S[mb][j] = v4f{0.f, 0.f, 0.f, 0.f};
-        }
+                for (int i = 0; i < LA; ++i)
+                    *reinterpret_cast<v4u*>(slot + (4 * i + row_a) * 256 + ((lane & 15) << 4)) = octet_order(xa[r][i]);
+            }
+            float sj[NT], cj[NT];
 #pragma unroll
-        for (int s = 0; s < SPW; ++s) {
-            const int cs = wave * SPW + s;  // step within the chunk
-            if (ch * SPC + cs < KS) {       // uniform
+            for (int j = 0; j < NT; ++j) {
+                sj[j] = BC::scale_of((uint16_t)(sw[r] >> (16 * j)));
+                cj[j] = BC::BIAS + (float)((zw[r] >> (zsh + 4 * j)) & 15u) + 1.0f;
+            }
+            v4f S[MB][NT], X[MB];
+#pragma unroll
+            for (int mb = 0; mb < MB; ++mb) {
+                X[mb] = v4f{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int j = 0; j < NT; ++j) S[mb][j] = v4f{0.f, 0.f, 0.f, 0.f};
+            }
+#pragma unroll
+            for (int s2 = 0; s2 < 4; ++s2) {
+                const int oc = 4 * s2 + o;
                 vec b[NT];
 #pragma unroll
-                for (int j = 0; j < NT; ++j) b[j] = biased8<XF16>(wq[ch * SPW + s][j]);
-                const int pc = (ONE ? ch * SPC : 0) * 4 + cs * 4 + o;  // octet in the staged row
+                for (int j = 0; j < NT; ++j) b[j] = biased8<XF16>(wq[r][s2][j]);
 #pragma unroll
                 for (int mb = 0; mb < MB; ++mb) {
-                    const int r = min(mb * 16 + c, M - 1);
-                    const vec a = __builtin_bit_cast(
-                        vec, *reinterpret_cast<const v4u*>(base + r * rstride + ((pc ^ (r & 7)) << 4)));
+                    const int mr = min(mb * 16 + c, M - 1);
+                    v4u av = *reinterpret_cast<const v4u*>(slot + mr * 256 + ((oc ^ (mr & 15)) << 4));
+                    if (raw) av = octet_order(av);
+                    const vec a = __builtin_bit_cast(vec, av);
 #pragma unroll
                     for (int j = 0; j < NT; ++j) {
                         if constexpr (XF16)
@@ -597,37 +638,41 @@ k3_one(const uint16_t* __restrict__ x, const int32_t* __restrict__ qweight, cons
                         X[mb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, ones, X[mb], 0, 0, 0);
                 }
             }
+            // total += s * (S - (bias + z + 1) X) over the round's group (rounds past K add nothing)
+#pragma unroll
+            for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+                for (int j = 0; j < NT; ++j)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const float v = __builtin_fmaf(sj[j], __builtin_fmaf(-cj[j], X[mb][e], S[mb][j][e]),
+                                                       total[mb][j][e]);
+                        total[mb][j][e] = dead[r] ? total[mb][j][e] : v;
+                    }
         }
-        // total += s * (S - (bias + z + 1) X) over this wave's steps of one group.
-#pragma unroll
-        for (int mb = 0; mb < MB; ++mb)
-#pragma unroll
-            for (int j = 0; j < NT; ++j)
-#pragma unroll
-                for (int e = 0; e < 4; ++e)
-                    total[mb][j][e] = __builtin_fmaf(sj[j], __builtin_fmaf(-cj[j], X[mb][e], S[mb][j][e]),
-                                                     total[mb][j][e]);
-    });
-    __syncthreads();  // the staged activations are dead; their LDS takes the wave partials [wave][mb][j][256]
-    float* part = reinterpret_cast<float*>(smem);
+        // the next pass writes the slots again (a load to LDS does not wait for this wave's reads)
+        __builtin_amdgcn_s_waitcnt(vmcnt_imm(63) & ~(15 << 8));
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    // ---- epilogue: the wave's tiles into its own region, then the 16 tiles in wave order
+    float* part = reinterpret_cast<float*>(reg);
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
-        for (int j = 0; j < NT; ++j)
-            *reinterpret_cast<v4f*>(&part[((wave * MB + mb) * NT + j) * 256 + lane * 4]) = total[mb][j];
+        for (int j = 0; j < NT; ++j) *reinterpret_cast<v4f*>(&part[(mb * NT + j) * 256 + lane * 4]) = total[mb][j];
     __syncthreads();
-    // Entry e of tile (mb, j): MFMA lane e/4, result e%4 -> row 4 (lane/16) + e%4,
-    // column n0 + NT (lane%16) + j; summed over the waves in order.
-    constexpr int ENT = MB * NT * 256;
+    // Entry e of tile (mb, j): MFMA lane e/4, result e%4 -> row 16 mb + 4 (lane/16) + e%4,
+    // column n0 + 2 (lane%16) + j.
+    constexpr int ENT = MB * NT * 256, T = NWV * 64;
 #pragma unroll
-    for (int e0 = 0; e0 < ENT; e0 += K3O_T) {
+    for (int e0 = 0; e0 < ENT; e0 += T) {
         const int e = e0 + t;
         if (e < ENT) {
             const int tile = e >> 8, el = (e & 255) >> 2, ei = e & 3;
             const int mb = tile / NT, j = tile % NT;
-            float v = part[e];
+            float v = reinterpret_cast<const float*>(smem)[e];
 #pragma unroll
-            for (int w = 1; w < NWV; ++w) v = v + part[w * ENT + e];
+            for (int w = 1; w < NWV; ++w) v = v + reinterpret_cast<const float*>(smem + w * REG)[e];
             const int m = mb * 16 + 4 * (el >> 4) + ei, n = n0 + NT * (el & 15) + j;
             if (m < M && n < N) {
                 const uint16_t h = OF16 ? __builtin_bit_cast(uint16_t, (_Float16)v) : (uint16_t)f32_to_bf16_rne(v);
@@ -637,41 +682,43 @@ k3_one(const uint16_t* __restrict__ x, const int32_t* __restrict__ qweight, cons
     }
 }
 
-template <int MB, int NB, int ST, int NWV, int RING, bool XF, bool OF>
-hipError_t launch_one_k(const void* x, const int32_t* qw, const int32_t* qz, const void* sc, void* out, int M, int N,
-                        int K, hipStream_t st) {
-    const dim3 grid((unsigned)((N + NB - 1) / NB));
-    const auto* xp = static_cast<const uint16_t*>(x);
-    const auto* sp = static_cast<const uint16_t*>(sc);
-    const int parts = NWV * MB * (NB / 16) * 256 * 4;
-    if (MB == 1 && (int64_t)M * K * 2 <= K3O_ONE_BYTES) {
-        const int lds = max(((M * K * 2) + 15) & ~15, parts);
-        hipLaunchKernelGGL((k3_one<MB, NB, ST, NWV, RING, true, XF, OF>), grid, dim3(NWV * 64), lds, st, xp, qw, qz,
-                           sp, out, M, N, K);
+template <int MR, bool XF, bool OF>
+hipError_t launch_rows(const void* x, const int32_t* qw, const int32_t* qz, const void* sc, void* out, int M, int N,
+                       int K, hipStream_t st) {
+    constexpr int MB = MR > 16 ? 2 : 1, MRL = MR < 4 ? 4 : MR, SLOT = MRL * 256, PART = MB * 2 * 1024;
+    constexpr int REG = (MR > 16 ? SLOT : 2 * SLOT) > PART ? (MR > 16 ? SLOT : 2 * SLOT) : PART;
+    const dim3 grid((unsigned)((N + K3R_NB - 1) / K3R_NB)), block(K3R_WAVES * 64);
+    if (K <= 2 * K3R_WAVES * 128) {
+        hipLaunchKernelGGL((k3_rows<MR, false, XF, OF>), grid, block, K3R_WAVES * REG, st,
+                           static_cast<const uint16_t*>(x), qw, qz, static_cast<const uint16_t*>(sc), out, M, N, K);
     } else {
-        const int lds = max(2 * RING, parts);
-        hipLaunchKernelGGL((k3_one<MB, NB, ST, NWV, RING, false, XF, OF>), grid, dim3(NWV * 64), lds, st, xp, qw, qz,
-                           sp, out, M, N, K);
+        if constexpr (MR > 16) return hipErrorInvalidValue;  // one_launch_fits keeps 17..32 rows at K <= 4096
+        else
+            hipLaunchKernelGGL((k3_rows<MR, true, XF, OF>), grid, block, K3R_WAVES * REG, st,
+                               static_cast<const uint16_t*>(x), qw, qz, static_cast<const uint16_t*>(sc), out, M, N, K);
     }
     return hipGetLastError();
 }
 
-// Whether the one-launch kernel serves this shape: K <= 4096 and M <= 16
-// (8 waves, 32 KiB activation chunks), or M <= 32 when the 32-column
-// workgroups fill more than half the CUs and at most all of them (16 waves,
-// two row blocks, 64 KiB chunks: one workgroup per CU; fused QKV at M = 32,
-// 10.9 us against 11.8 for split-K).  Other shapes run the split-K form,
-// which measured faster there (o at M = 32: 9.2 us against 10.6).
-bool one_launch_fits(int M, int N, int K) {
-    const int wg = (N + 31) / 32, cus = device_cu_count();
-    return K <= K3O_MAXK && (M <= 16 || (M <= 32 && 2 * wg > cus && wg <= cus));
+// Whether the one-launch kernel serves this shape: the weight under 2 GiB (so
+// every 32-bit buffer offset, with its out-of-range bit, is exact) and M <= 16,
+// or M <= 32 with K <= 4096 and at most one workgroup per CU.  Every workgroup
+// reads all M x K activations, so at 17..32 rows a longer K (down: 12288) or
+// several workgroups per CU (gate/up: 768) read more per CU than the split-K
+// form, which measured faster there (down at M = 32: 17.6 us against 21.4).
+bool one_launch_fits(int64_t M, int64_t N, int64_t K) {
+    if (M > 32 || K * N / 2 >= (1LL << 31)) return false;
+    return M <= 16 || (K <= 2 * K3R_WAVES * 128 && (N + K3R_NB - 1) / K3R_NB <= device_cu_count());
 }
 
 template <bool XF, bool OF>
-hipError_t dispatch_one(const void* x, const int32_t* qw, const int32_t* qz, const void* sc, void* out, int M, int N,
-                        int K, hipStream_t st) {
-    if (M <= 16) return launch_one_k<1, 32, 16, 8, 32768, XF, OF>(x, qw, qz, sc, out, M, N, K, st);
-    return launch_one_k<2, 32, 8, 16, 65536, XF, OF>(x, qw, qz, sc, out, M, N, K, st);
+hipError_t dispatch_rows(const void* x, const int32_t* qw, const int32_t* qz, const void* sc, void* out, int M, int N,
+                         int K, hipStream_t st) {
+    if (M <= 2) return launch_rows<2, XF, OF>(x, qw, qz, sc, out, M, N, K, st);
+    if (M <= 4) return launch_rows<4, XF, OF>(x, qw, qz, sc, out, M, N, K, st);
+    if (M <= 8) return launch_rows<8, XF, OF>(x, qw, qz, sc, out, M, N, K, st);
+    if (M <= 16) return launch_rows<16, XF, OF>(x, qw, qz, sc, out, M, N, K, st);
+    return launch_rows<32, XF, OF>(x, qw, qz, sc, out, M, N, K, st);
 }
 
 template <int MB, bool XF, bool OF>
@@ -794,15 +841,15 @@ extern "C" int nv4_w4a16_gemm(const void* x, int x_dtype, const int32_t* qweight
     hipStream_t st = static_cast<hipStream_t>(stream);
     const int m = (int)M, n = (int)N, k = (int)K;
     hipError_t e;
-    // Small decode batches: the one-launch kernel (8-byte weight and 4-byte scale loads).
-    if (one_launch_fits(m, n, k) && reinterpret_cast<uintptr_t>(qweight) % 8 == 0 &&
+    // Decode batches: the one-launch kernel (8-byte weight and 4-byte scale loads).
+    if (one_launch_fits(M, N, K) && reinterpret_cast<uintptr_t>(qweight) % 8 == 0 &&
         reinterpret_cast<uintptr_t>(scales) % 4 == 0) {
         if (x_dtype == NV4_FP16)
-            e = out_dtype == NV4_FP16 ? dispatch_one<true, true>(x, qweight, qzeros, scales, out, m, n, k, st)
-                                      : dispatch_one<true, false>(x, qweight, qzeros, scales, out, m, n, k, st);
+            e = out_dtype == NV4_FP16 ? dispatch_rows<true, true>(x, qweight, qzeros, scales, out, m, n, k, st)
+                                      : dispatch_rows<true, false>(x, qweight, qzeros, scales, out, m, n, k, st);
         else
-            e = out_dtype == NV4_FP16 ? dispatch_one<false, true>(x, qweight, qzeros, scales, out, m, n, k, st)
-                                      : dispatch_one<false, false>(x, qweight, qzeros, scales, out, m, n, k, st);
+            e = out_dtype == NV4_FP16 ? dispatch_rows<false, true>(x, qweight, qzeros, scales, out, m, n, k, st)
+                                      : dispatch_rows<false, false>(x, qweight, qzeros, scales, out, m, n, k, st);
         return (int)e;
     }
     if (x_dtype == NV4_FP16)

@@ -9,15 +9,17 @@ reference (split-K 8 with bf16 atomics onto a zeroed output) the HIP kernel
 sums all of K in fp32 and writes each output once, so results do not depend
 on scheduling.  FP16 activations are accepted as well (output fp16).
 
-Decode sizes: for K <= 4096 and M <= 16 (or M <= 32 when its 32-column
-workgroups fill between half and all of the CUs, as the fused QKV does)
-``nv4_w4a16_gemm`` runs one launch whose workgroups own 32 columns over the
-whole K (the K split over their waves and added in a fixed order in LDS);
-other M <= 64 take the split-K
-form (``nv4_w4a16_gemm_ws``): 64-column workgroups per 1024-deep K slice
-writing fp32 partials into a workspace from torch's caching allocator, added
-in slice order by a second launch.  Both are deterministic and
-graph-capturable.  At prefill sizes (M > 64) the weight is dequantized once
+Decode sizes: for M <= 16 (any K), and for M <= 32 when K <= 4096 and the
+32-column workgroups are at most one per CU (the fused QKV and o_proj of an
+8B model), ``nv4_w4a16_gemm`` runs one launch whose 16-wave workgroups own 32
+columns over the whole K (each wave takes whole quantisation groups; the
+waves' fp32 tiles are added in a fixed order in LDS); no workspace.  Other
+M <= 64 (every workgroup of the one-launch form reads all M x K activations,
+which at 17..32 rows costs more than splitting K when K is long or the
+workgroups are several per CU) take the split-K form
+(``nv4_w4a16_gemm_ws``): 64-column workgroups per 1024-deep K slice writing
+fp32 partials into a workspace from torch's caching allocator, added in slice
+order by a second launch.  Both are deterministic and graph-capturable.  At prefill sizes (M > 64) the weight is dequantized once
 into a dense [K, N] tensor (``nv4_w4a16_dequant``, the same per-element
 rounding) and the product runs as a library GEMM (torch.mm on hipBLASLt,
 fp32 accumulation).
@@ -32,7 +34,7 @@ from .. import _lib
 
 _DT = {torch.bfloat16: _lib.BF16, torch.float16: _lib.FP16}
 SLICE_K = 1024  # K per partial of the decode-size split
-ONE_LAUNCH_MAX_K = 4096  # nv4_w4a16_gemm runs one launch up to this K (see one_launch)
+ONE_LAUNCH_MAX_M = 32  # nv4_w4a16_gemm runs one launch up to this M (see one_launch)
 
 
 def dequant_w4a16(qweight, qzeros, scales, dtype=torch.bfloat16, group_size=128):
@@ -63,19 +65,19 @@ def dequant_w4a16(qweight, qzeros, scales, dtype=torch.bfloat16, group_size=128)
 _CUS = {}
 
 
-def one_launch(M, N, K, device):
+def one_launch(M, N, K, device=None):
     """Whether ``nv4_w4a16_gemm`` runs these sizes in its one-launch kernel
-    (the rule it applies itself): K <= 4096 and M <= 16, or M <= 32 with
-    between half and all of the CUs filled by 32-column workgroups."""
-    if K > ONE_LAUNCH_MAX_K or M > 32:
+    (the rule it applies itself): the packed weight (K * N / 2 bytes) under
+    2 GiB and M <= 16, or M <= 32 with K <= 4096 and ceil(N / 32) workgroups
+    at most one per CU."""
+    if M > ONE_LAUNCH_MAX_M or K * N // 2 >= (1 << 31):
         return False
     if M <= 16:
         return True
-    idx = torch.device(device).index or 0
+    idx = (torch.device(device).index or 0) if device is not None else torch.cuda.current_device()
     if idx not in _CUS:
         _CUS[idx] = torch.cuda.get_device_properties(idx).multi_processor_count
-    wg = (N + 31) // 32
-    return 2 * wg > _CUS[idx] and wg <= _CUS[idx]
+    return K <= 4096 and (N + 31) // 32 <= _CUS[idx]
 
 
 def dequant_matmul_w4a16(x, qweight, qzeros, scales, group_size=128, out=None):

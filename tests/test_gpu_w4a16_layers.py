@@ -79,12 +79,18 @@ def test_k3_shapes(N, K, M):
     check_close(out, ref)
 
 
-@pytest.mark.parametrize("M,N,K", [(20, 4104, 2048), (32, 8192, 4096), (17, 6144, 640), (32, 4104, 3968)])
-def test_k3_one_launch_two_row_blocks(M, N, K):
-    """Shapes the one-launch kernel takes with two row blocks (17 <= M <= 32,
-    K <= 4096, between half and all of the CUs filled by 32-column
-    workgroups): a column tail, a partial activation chunk (K = 640, 3968),
-    fp16 and bf16 activations; deterministic across calls."""
+@pytest.mark.parametrize("M,N,K", [(20, 4104, 2048), (32, 8192, 4096), (17, 6144, 640), (32, 4104, 3968),
+                                   (32, 6144, 4096), (3, 264, 8320), (16, 4096, 12288), (9, 24576, 4096),
+                                   (1, 8, 128), (16, 136, 4224)])
+def test_k3_one_launch_shapes(M, N, K):
+    """Shapes the one-launch decode kernel takes: one and two row blocks
+    (rows past M repeat row M - 1), a column tail (N = 4104, 136, 264, 8),
+    fewer groups than waves (K = 640, 128), several passes over K (K = 8320,
+    12288, 4224: a last pass with a single live round), the widest N of the
+    model (gate/up); fp16 and bf16 activations; deterministic across calls and
+    taken without a workspace."""
+    from nv4.kernels.w4a16 import one_launch
+    assert one_launch(M, N, K, DEV)
     for dtype in (torch.bfloat16, torch.float16):
         case = W.w4a16_case(M, N=N, K=K, dtype=dtype)
         xd = oracle.X_FP16 if dtype == torch.float16 else oracle.X_BF16
