@@ -23,7 +23,9 @@
 // lines; the results are the same bits.
 //
 // Three kernels, no split-K, no atomics:
-//  * k2_dec (M <= 64): one workgroup per 16 output columns and all M rows.
+//  * k2_dec (M <= 64): one workgroup per 16 output columns (two 16-column
+//    blocks when one each would put two workgroups, each reading all of the
+//    activations, on some CUs) and all M rows.
 //    Its 8 or 16 waves each take one K group per round, compute the exact
 //    int32 group dots with v_mfma_i32_16x16x64_i8 and hand them through LDS
 //    to the whole workgroup, which runs the fp32 epilogue in group order.
@@ -95,13 +97,13 @@ constexpr int DC_RSRC_WORD3 = 0x00020000;  // buffer resource word 3 (CDNA): 32-
 // down, while k2_wide measured 9 % slower with it and keeps the default.
 constexpr int DC_NT = 2;
 
-template <int MB, int NW, int D, bool TW, bool RT, bool SW_GROUPED, bool OUT_F32>
+template <int MB, int NW, int D, bool TW, bool RT, bool SW_GROUPED, bool OUT_F32, int CB = 1>
 __global__ void __launch_bounds__(NW * 64, 16 / NW)
 k2_dec(const int8_t* __restrict__ a, const int8_t* __restrict__ w,
        const uint16_t* __restrict__ sa, const uint16_t* __restrict__ sw,
        void* __restrict__ out, int M, int N, int K) {
     constexpr int DC_T = NW * 64;
-    constexpr int ROWS = MB * 16, NOUT = ROWS * 16;
+    constexpr int ROWS = MB * 16, TOUT = ROWS * 16, NOUT = TOUT * CB;  // CB column blocks of 16
     constexpr int GR = NW;                                              // groups per round
     constexpr int SLB = GR * 64;                                        // slice bytes per row and round
     constexpr int CPR = SLB / 16;                                       // 16-byte chunks per row and round
@@ -109,21 +111,22 @@ k2_dec(const int8_t* __restrict__ a, const int8_t* __restrict__ w,
     constexpr int APT = ROWS * CPR / DC_T;                              // activation chunks per thread
     constexpr int NA = RT ? MB : APT;                                   // activation loads per thread and round
     constexpr int N_SA = ROWS * GR;                                     // scale entries per round
-    constexpr int N_SW = SW_GROUPED ? 16 * GR : 0;
+    constexpr int N_SW = SW_GROUPED ? 16 * CB * GR : 0;
     constexpr int SPT = (N_SA + N_SW + DC_T - 1) / DC_T;
     static_assert(RT || APT * DC_T == ROWS * CPR, "activation slice must split evenly");
     static_assert(!RT || TW, "row-tiled activations go with tiled weights");
+    static_assert(CB == 1 || TW, "several column blocks per workgroup read tiled weights");
     static_assert(N_SA % 64 == 0 && N_SW % 64 == 0, "scale classes must be wave-uniform");
     __shared__ __align__(16) uint8_t a_l[2][RT ? 16 : ROWS * SLB];
     __shared__ __align__(16) int16_t dots[2][GR][NOUT];
     __shared__ __align__(16) float sal[2][ROWS][GR];  // a row's scales of the round together
-    __shared__ __align__(16) float swl[2][16][GR];
+    __shared__ __align__(16) float swl[2][16 * CB][GR];
     __shared__ float ssink[1];
 
     const int t = threadIdx.x;
     const int lane = t & 63;
     const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
-    const int n0 = blockIdx.x * 16;
+    const int n0 = blockIdx.x * 16 * CB;
     const int G = K >> 7;
     const int R = (G + GR - 1) / GR;  // rounds
     const int KB = K >> 1;
@@ -134,9 +137,12 @@ k2_dec(const int8_t* __restrict__ a, const int8_t* __restrict__ w,
     // address work is scalar.  All offsets are clamped into range.
     // Weights: the column block's K/128 tiled 1 KiB groups (lane l's 16 bytes
     // at l*16), or its rows of the reference layout [N][K/2].
-    const int8_t* wblk = TW ? w + (int64_t)blockIdx.x * G * 1024 : w + (int64_t)n0 * KB;
+    // With CB column blocks per workgroup their tiled groups are consecutive
+    // (block b at b * G KiB); a block past N reads the last one (results dropped).
+    const int8_t* wblk = TW ? w + (int64_t)blockIdx.x * CB * G * 1024 : w + (int64_t)n0 * KB;
+    const int ncb = TW ? min(CB, (N - n0 + 15) / 16) : 1;  // column blocks of this workgroup inside N
     const __amdgpu_buffer_rsrc_t rsw_w = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<int8_t*>(wblk), (short)0, TW ? G * 1024 : min(16, N - n0) * KB, DC_RSRC_WORD3);
+        const_cast<int8_t*>(wblk), (short)0, TW ? ncb * G * 1024 : min(16, N - n0) * KB, DC_RSRC_WORD3);
     const int w_voff = TW ? lane * 16 : (min(n0 + rc, N - 1) - n0) * KB + part * 16;
     const int wstep = TW ? 1024 : 64;
     // Activations: thread t moves chunks q = t + DC_T i (row q / CPR, chunk
@@ -181,7 +187,7 @@ k2_dec(const int8_t* __restrict__ a, const int8_t* __restrict__ w,
             const int col = (e - N_SA) / GR;
             s_voff[q] = min(n0 + col, N - 1) * G * 2;
             sdst[q] = &swl[0][col][sgl[q]];
-            sstride[q] = GR * 16;
+            sstride[q] = GR * 16 * CB;
         } else {  // nothing to stage: load a valid scale, store to the sink
             s_voff[q] = 0;
             sgl[q] = 0;
@@ -190,11 +196,14 @@ k2_dec(const int8_t* __restrict__ a, const int8_t* __restrict__ w,
         }
     }
 
-    v4u rw[D], ra[D][NA];
+    v4u rw[D][CB], ra[D][NA];
     uint16_t rs[D][SPT];
-    auto issue = [&](int r, v4u& w_out, v4u (&a_out)[NA], uint16_t (&s_out)[SPT]) {
+    auto issue = [&](int r, v4u (&w_out)[CB], v4u (&a_out)[NA], uint16_t (&s_out)[SPT]) {
         const int gw = min(r * GR + wave, G - 1);  // the wave's group of round r
-        w_out = __builtin_bit_cast(v4u, __builtin_amdgcn_raw_buffer_load_b128(rsw_w, w_voff, gw * wstep, DC_NT));
+#pragma unroll
+        for (int cb = 0; cb < CB; ++cb)
+            w_out[cb] = __builtin_bit_cast(v4u, __builtin_amdgcn_raw_buffer_load_b128(
+                                                    rsw_w, w_voff, (min(cb, ncb - 1) * G + gw) * wstep, DC_NT));
         const int rr = min(r, R - 1);        // rounds past the end reload the last one (unused)
         if constexpr (RT) {
 #pragma unroll
@@ -232,7 +241,7 @@ k2_dec(const int8_t* __restrict__ a, const int8_t* __restrict__ w,
     // 128 (j >> 1) + x[j & 1] with x precomputed per lane.
     const int ax0 = rc * SLB + (((part ^ rc) & 7) << 4);
     const int ax1 = rc * SLB + ((((4 + part) ^ rc) & 7) << 4);
-    auto mma = [&](int r, const v4u& w_in, const v4u (&a_in)[NA], const uint16_t (&s_in)[SPT]) {
+    auto mma = [&](int r, const v4u (&w_in)[CB], const v4u (&a_in)[NA], const uint16_t (&s_in)[SPT]) {
         const int buf = r & 1;
         if (r * GR + wave < G) {  // uniform over the wave
             v4u av[MB];  // every operand read issued before the first use
@@ -247,20 +256,27 @@ k2_dec(const int8_t* __restrict__ a, const int8_t* __restrict__ w,
                     av[mb] = *reinterpret_cast<const v4u*>(&a_l[0][aoff + mb * 16 * SLB]);
                 __builtin_amdgcn_sched_barrier(0);
             }
-            const v4i w0 = unpack8_x16(w_in[0], w_in[1]);
-            const v4i w1 = unpack8_x16(w_in[2], w_in[3]);
+            v4i w0[CB], w1[CB];
+#pragma unroll
+            for (int cb = 0; cb < CB; ++cb) {
+                w0[cb] = unpack8_x16(w_in[cb][0], w_in[cb][1]);
+                w1[cb] = unpack8_x16(w_in[cb][2], w_in[cb][3]);
+            }
 #pragma unroll
             for (int mb = 0; mb < MB; ++mb) {
                 const v4i a0 = unpack8_x16(av[mb][0], av[mb][1]);
                 const v4i a1 = unpack8_x16(av[mb][2], av[mb][3]);
-                v4i acc = {0, 0, 0, 0};
-                acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, w0, acc, 0, 0, 0);
-                acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, w1, acc, 0, 0, 0);
-                // 256 * dot -> dot: |dot| <= 8192, so bytes 1..2 of 256 * dot
-                // are the int16 dot; one byte permute packs two of them.
-                const uint32_t lo = __builtin_amdgcn_perm((uint32_t)acc[1], (uint32_t)acc[0], 0x06050201u);
-                const uint32_t hi = __builtin_amdgcn_perm((uint32_t)acc[3], (uint32_t)acc[2], 0x06050201u);
-                *reinterpret_cast<uint2*>(&dots[buf][wave][mb * 256 + lane * 4]) = make_uint2(lo, hi);
+#pragma unroll
+                for (int cb = 0; cb < CB; ++cb) {
+                    v4i acc = {0, 0, 0, 0};
+                    acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, w0[cb], acc, 0, 0, 0);
+                    acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, w1[cb], acc, 0, 0, 0);
+                    // 256 * dot -> dot: |dot| <= 8192, so bytes 1..2 of 256 * dot
+                    // are the int16 dot; one byte permute packs two of them.
+                    const uint32_t lo = __builtin_amdgcn_perm((uint32_t)acc[1], (uint32_t)acc[0], 0x06050201u);
+                    const uint32_t hi = __builtin_amdgcn_perm((uint32_t)acc[3], (uint32_t)acc[2], 0x06050201u);
+                    *reinterpret_cast<uint2*>(&dots[buf][wave][cb * TOUT + mb * 256 + lane * 4]) = make_uint2(lo, hi);
+                }
             }
         }
 #pragma unroll
@@ -277,8 +293,8 @@ k2_dec(const int8_t* __restrict__ a, const int8_t* __restrict__ w,
         for (int oi = 0; oi < OPT; ++oi) {
             const int o = t + oi * DC_T;
             if (o < NOUT) {
-                const int l = (o >> 2) & 63;
-                const int row = (o >> 8) * 16 + 4 * (l >> 4) + (o & 3), col = l & 15;
+                const int l = (o >> 2) & 63, ot = o % TOUT;
+                const int row = (ot >> 8) * 16 + 4 * (l >> 4) + (o & 3), col = (o / TOUT) * 16 + (l & 15);
                 if (ng == GR) {
                     // All LDS reads first (one wait), then the in-order chain.
                     int dr[GR];
@@ -341,8 +357,8 @@ k2_dec(const int8_t* __restrict__ a, const int8_t* __restrict__ w,
 #pragma unroll
     for (int oi = 0; oi < OPT; ++oi) {
         const int o = t + oi * DC_T;
-        const int l = (o >> 2) & 63;
-        const int row = (o >> 8) * 16 + 4 * (l >> 4) + (o & 3), n = n0 + (l & 15);
+        const int l = (o >> 2) & 63, ot = o % TOUT;
+        const int row = (ot >> 8) * 16 + 4 * (l >> 4) + (o & 3), n = n0 + (o / TOUT) * 16 + (l & 15);
         if (o < NOUT && row < M && n < N) {
             float v = total[oi];
             if constexpr (!SW_GROUPED) v = v * bf16_to_f32(sw[n]);
@@ -595,11 +611,22 @@ hipError_t launch_dec(const int8_t* a, const int8_t* w, const void* sa, const vo
     // When one workgroup per CU covers every column block, 16 waves with a
     // two-round ring (16 groups per round) hide more latency than 8 waves;
     // with more column blocks than CUs, two 8-wave workgroups share a CU.
+    // With more 16-column blocks than CUs (some CUs would run two workgroups,
+    // each reading all M x K activations) and tiled weights, a workgroup takes
+    // two column blocks instead: the activations are read once per CU.
     if constexpr (MB <= 2) {
-        if (K >= 2048 && blocks <= device_cu_count()) {
+        const int cus = device_cu_count();
+        if (K >= 2048 && blocks <= cus) {
             hipLaunchKernelGGL((k2_dec<MB, 16, 2, TW, RT, SG, OF>), grid, dim3(16 * 64), 0, st, a, w, sap, swp, out, M,
                                N, K);
             return hipGetLastError();
+        }
+        if constexpr (TW) {
+            if (K >= 2048 && (blocks + 1) / 2 <= cus) {
+                hipLaunchKernelGGL((k2_dec<MB, 16, 2, TW, RT, SG, OF, 2>), dim3((unsigned)((blocks + 1) / 2)),
+                                   dim3(16 * 64), 0, st, a, w, sap, swp, out, M, N, K);
+                return hipGetLastError();
+            }
         }
     }
     constexpr int D = 4;  // rounds in flight: all of them for K <= 4096

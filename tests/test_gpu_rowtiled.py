@@ -162,6 +162,7 @@ def run_rowtiled(ap, wp, sa, sw, what, seed=0):
     (1, 4096, 4096), (5, 6144, 4096), (16, 4096, 12288), (17, 4096, 4096), (32, 4096, 4096),
     (32, 6144, 4096), (32, 4096, 12288),                 # o / qkv / down shapes: 16- and 8-wave kernels
     (9, 272, 2176), (32, 144, 640), (24, 4112, 2048),     # partial last rounds, column tails
+    (32, 4112, 4096), (1, 6160, 4096),                    # two column blocks per workgroup, odd last block
     (32, 24576, 4096), (3, 24576, 4096), (32, 16384, 2048),  # wide-N kernel
 ])
 def test_gemm_rowtiled_vs_oracle(M, N, K):

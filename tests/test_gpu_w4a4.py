@@ -140,12 +140,15 @@ def test_k2_m_sweep(M):
 
 
 @pytest.mark.parametrize("M,N,K", [(1, 4104, 4096), (16, 4104, 4096), (17, 4104, 4096), (32, 4104, 4096),
-                                   (33, 4104, 4096), (48, 264, 4096), (8, 520, 12288), (16, 264, 8192)])
+                                   (33, 4104, 4096), (48, 264, 4096), (8, 520, 12288), (16, 264, 8192),
+                                   (32, 4112, 4096), (7, 6160, 2048)])
 def test_k2_decode_activations_in_lds(M, N, K):
     """Shapes served by the decode kernel (one workgroup per 16 columns, the
     K groups split over its waves, activation slices staged in LDS): every
     M block, a column tail, more 16-column blocks than compute units, K =
-    8192 and 12288 (rounds beyond the load ring)."""
+    8192 and 12288 (rounds beyond the load ring).  With tiled weights and
+    more 16-column blocks than CUs (N = 4112, 6160: 257 and 385 blocks) a
+    workgroup takes two column blocks, the last one a single block."""
     run_case(M, N, K, 3000 + M + K)
     if M in (17, 48):
         run_case(M, N, K, 4000 + M + K, grouped=False)
