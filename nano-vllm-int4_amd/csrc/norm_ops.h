@@ -17,9 +17,24 @@
 namespace nv4 {
 namespace {
 
+// Lane value rotated within its row of 16 lanes (DPP row_ror:n, n = CTRL - 0x120).
+template <int CTRL>
+__device__ __forceinline__ float row_ror(float x) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), CTRL, 0xF, 0xF, false));
+}
+
+// Sum over the wave by xor-butterflies 32, 16, 8, 4, 2, 1 (v + partner at each
+// step).  After the 32 and 16 steps the partial sums repeat every 16 lanes,
+// after the 8 step every 8 and so on, so rotating by 8, 4, 2, 1 inside a row of
+// 16 lanes hands each lane the same partner value as xor 8, 4, 2, 1: the same
+// additions in the same order, on the VALU instead of the LDS crossbar.
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off);
+    v += __shfl_xor(v, 32);
+    v += __shfl_xor(v, 16);
+    v += row_ror<0x128>(v);
+    v += row_ror<0x124>(v);
+    v += row_ror<0x122>(v);
+    v += row_ror<0x121>(v);
     return v;
 }
 

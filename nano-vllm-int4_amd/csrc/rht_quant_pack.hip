@@ -95,12 +95,16 @@ template <int T>
 __device__ __forceinline__ bool prefetch_tail(const Prefetch& pf) {
     if ((int)blockIdx.x < pf.rows) return false;
     const int64_t base = (int64_t)(blockIdx.x - pf.rows) * (T * 16 * PF_LOADS);
-    v4u acc = {0u, 0u, 0u, 0u};
+    v4u v[PF_LOADS];
 #pragma unroll
     for (int i = 0; i < PF_LOADS; ++i) {
         const int64_t off = min(base + (int64_t)(i * T + threadIdx.x) * 16, pf.bytes - 16);
-        acc ^= *reinterpret_cast<const v4u*>(pf.p + off);
+        v[i] = *reinterpret_cast<const v4u*>(pf.p + off);
     }
+    __builtin_amdgcn_sched_barrier(0);  // all loads in flight before the first use
+    v4u acc = v[0];
+#pragma unroll
+    for (int i = 1; i < PF_LOADS; ++i) acc ^= v[i];
     asm volatile("" ::"v"(acc[0] ^ acc[1] ^ acc[2] ^ acc[3]));  // keep the loads
     return true;
 }
