@@ -65,6 +65,10 @@
  *                          packed activations in a row-tiled order (no
  *                          counterpart in the reference, whose kernels pass
  *                          [M,K/2] from rht_quant_pack to w4a4_grouped_gemm)
+ *   nv4_w4a4_gemm_rowtiled_silu <- the gate_up W4A4Linear followed by
+ *                          SiluAndMul (nanovllm/models/qwen3.py:125-129,
+ *                          nanovllm/layers/activation.py:8-11) in one launch, for
+ *                          decode-sized M (no counterpart call in the reference)
  */
 #ifndef NV4_H
 #define NV4_H
@@ -200,6 +204,27 @@ int nv4_rht_quant_pack_rowtiled(const void* x, const int8_t* signs, int8_t* pack
 int nv4_w4a4_gemm_rowtiled(const int8_t* a_rt, const int8_t* w_tiled, const void* sa, const void* sw,
                            int sw_grouped, void* out, int out_fp32,
                            int64_t M, int64_t N, int64_t K, void* stream);
+
+/*
+ * SiLU-and-mul of a fused gate/up projection on row-tiled activations, in
+ * one launch.  w_tiled is the MFMA-tiled weight of N = 2I rows, the gate
+ * projection's I rows first, then the up projection's (the reference's
+ * merged layout, nanovllm/layers/linear.py:87-93, shard 0 = gate), sw its
+ * [N] or [N, K/128] scales.
+ * out bf16 [M, I] = bf16(bf16(g / (1 + expf(-g))) * u), g and u the bf16
+ * results nv4_w4a4_gemm_rowtiled would store for the paired columns n and
+ * I + n: the bits of that GEMM followed by SiLU-and-mul
+ * (nanovllm/layers/activation.py:8-11), without the [M, N] round trip.
+ * Serves the wide decode kernel's sizes only: 1 <= M <= 32, N % 32 == 0,
+ * K % 256 == 0, 4..8 column blocks of 16 per CU, M x K activations and the
+ * scales within the kernel's LDS; other sizes return NV4_E_SHAPE (run
+ * nv4_w4a4_gemm_rowtiled and nv4_silu_mul_rht_quant_pack_rowtiled instead).
+ * No counterpart call in the reference (which runs the GEMM and the
+ * activation as two ops); it replaces that pair for decode-sized batches.
+ */
+int nv4_w4a4_gemm_rowtiled_silu(const int8_t* a_rt, const int8_t* w_tiled, const void* a_scale,
+                                const void* w_scale, int w_scale_grouped, void* out, int64_t M, int64_t N,
+                                int64_t K, void* stream);
 int nv4_w4a4_linear_rowtiled(const void* x, const int8_t* signs, const int8_t* w_tiled, const void* sw,
                              void* out, int8_t* a_packed_rt, void* a_scale,
                              int64_t M, int64_t N, int64_t K, void* stream);

@@ -34,6 +34,7 @@
 //    activations widened once per CU into LDS.
 //  * k2_prefill (M > 64, w4a4_prefill.hip): LDS-staged 128x128 tiles.
 #include "k2_launch.h"
+#include "norm_ops.h"
 #include "nv4_common.h"
 
 namespace nv4 {
@@ -394,12 +395,13 @@ constexpr int WIDE_A_BYTES = 128 * 1024;  // widened activation block limit (M x
 constexpr int WIDE_SCALES = 1024;         // G * ROWS limit
 constexpr int WIDE_WSCALES = 3072;        // G * CBW * 16 limit
 
-template <int MB, int CBW, int D, bool TW, bool RT, bool SW_GROUPED, bool OUT_F32>
+template <int MB, int CBW, int D, bool TW, bool RT, bool SW_GROUPED, bool OUT_F32, bool PAIR = false>
 __global__ void __launch_bounds__(CBW * MB * 64)
 k2_wide(const int8_t* __restrict__ a, const int8_t* __restrict__ w,
         const uint16_t* __restrict__ sa, const uint16_t* __restrict__ sw,
         void* __restrict__ out, int M, int N, int K) {
     constexpr int T = CBW * MB * 64, ROWS = MB * 16, COLS = CBW * 16;
+    static_assert(!PAIR || (CBW % 2 == 0 && !OUT_F32), "gate/up pairs: an even block count, bf16 output");
     constexpr int AC = (WIDE_A_BYTES / 32 + T - 1) / T;  // packed 16-byte chunks per thread (upper bound)
     constexpr int SC = (WIDE_SCALES + T - 1) / T;
     constexpr int WC = SW_GROUPED ? (WIDE_WSCALES + T - 1) / T : 0;
@@ -407,6 +409,7 @@ k2_wide(const int8_t* __restrict__ a, const int8_t* __restrict__ w,
     __shared__ __align__(16) float sa_l[WIDE_SCALES + 4];     // [g][row] + sink
     __shared__ float sw_l[WIDE_WSCALES + 1];                  // [g][col] + sink
     __shared__ uint32_t wave_bad[CBW * MB];                   // scale-range flags, one per wave
+    __shared__ float up_l[PAIR ? CBW / 2 * MB * 256 : 1];    // PAIR: the up halves' bf16 results
 
     const int t = threadIdx.x;
     const int lane = t & 63, wave = t >> 6;
@@ -416,10 +419,20 @@ k2_wide(const int8_t* __restrict__ a, const int8_t* __restrict__ w,
     const int chunks_row = KB >> 4;             // packed 16-byte chunks per row
     const int a_chunks = ROWS * chunks_row;
     const int rc = lane & 15, part = lane >> 4;
-    const int col0 = blockIdx.x * COLS;
-    const int col = col0 + cbl * 16 + rc;
+    // Column block of local block lb: consecutive blocks, or (PAIR) the gate
+    // blocks of the workgroup's CBW/2 output blocks followed by the matching
+    // up blocks N/32 blocks further (the fused gate/up weight, up rows after
+    // gate rows).
+    const int HB = N >> 5;  // PAIR: 16-column blocks per half
+    auto block_of = [&](int lb) {
+        if constexpr (PAIR)
+            return lb < CBW / 2 ? blockIdx.x * (CBW / 2) + lb : HB + blockIdx.x * (CBW / 2) + lb - CBW / 2;
+        else
+            return (int)blockIdx.x * CBW + lb;
+    };
+    const int col = block_of(cbl) * 16 + rc;
     // Weights: tiled layout [N/16][G][64 lanes][16 bytes] (TW) or [N][K/2].
-    const int8_t* wp = TW ? w + (int64_t)min(blockIdx.x * CBW + cbl, (N >> 4) - 1) * G * 1024 + lane * 16
+    const int8_t* wp = TW ? w + (int64_t)min(block_of(cbl), (N >> 4) - 1) * G * 1024 + lane * 16
                           : w + (int64_t)min(col, N - 1) * KB + part * 16;
     constexpr int WSTEP = TW ? 1024 : 64;
 
@@ -457,8 +470,9 @@ k2_wide(const int8_t* __restrict__ a, const int8_t* __restrict__ w,
     }
 #pragma unroll
     for (int i = 0; i < WC; ++i) {
-        const int e = min(t + i * T, G * COLS - 1);  // e = col * G + g
-        rsw[i] = sw[(int64_t)min(col0 + e / G, N - 1) * G + e % G];
+        const int e = min(t + i * T, G * COLS - 1);  // e = local col * G + g
+        const int lc = e / G;
+        rsw[i] = sw[(int64_t)min(block_of(lc >> 4) * 16 + (lc & 15), N - 1) * G + e % G];
     }
     v4u rw[D];
     auto issue = [&](int g, v4u& w_out) {
@@ -586,7 +600,27 @@ k2_wide(const int8_t* __restrict__ a, const int8_t* __restrict__ w,
         main_loop(std::false_type{});
     }
 
-    if (col < N) {
+    if constexpr (PAIR) {
+        // y = silu(g) * u on the bf16 results of the paired gate and up
+        // columns, as the separate SiLU-and-mul would compute it from the
+        // stored [M, N] output; y is [M, N/2].
+        float swn = 1.0f;
+        if constexpr (!SW_GROUPED) swn = bf16_to_f32(sw[min(col, N - 1)]);
+        float vb[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) vb[i] = round_bf16(SW_GROUPED ? total[i] : total[i] * swn);
+        if (cbl >= CBW / 2)
+            *reinterpret_cast<v4f*>(&up_l[((cbl - CBW / 2) * MB + mb) * 256 + lane * 4]) = v4f{vb[0], vb[1], vb[2], vb[3]};
+        __syncthreads();
+        if (cbl < CBW / 2 && col < N / 2) {
+            const v4f u = *reinterpret_cast<const v4f*>(&up_l[(cbl * MB + mb) * 256 + lane * 4]);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int row = mb * 16 + 4 * part + i;
+                if (row < M) store_out<false>(out, (int64_t)row * (N / 2) + col, silu_mul1(vb[i], u[i]));
+            }
+        }
+    } else if (col < N) {
         float swn = 1.0f;
         if constexpr (!SW_GROUPED) swn = bf16_to_f32(sw[col]);
 #pragma unroll
@@ -645,24 +679,26 @@ bool wide_fits(int M, int N, int K) {
            (int64_t)(K / 128) * 16 * (per_cu <= 4 ? 4 : per_cu <= 6 ? 6 : 8) <= WIDE_WSCALES;
 }
 
-template <int MB, int CBW, bool TW, bool RT, bool SG, bool OF>
+template <int MB, int CBW, bool TW, bool RT, bool SG, bool OF, bool PAIR = false>
 hipError_t launch_wide_cbw(const int8_t* a, const int8_t* w, const void* sa, const void* sw, void* out,
                            int M, int N, int K, hipStream_t st) {
     constexpr int D = 8;  // groups in flight per wave
-    const int ncb = (N + 15) / 16;
-    hipLaunchKernelGGL((k2_wide<MB, CBW, D, TW, RT, SG, OF>), dim3((unsigned)((ncb + CBW - 1) / CBW)), dim3(CBW * MB * 64),
-                       0, st, a, w, static_cast<const uint16_t*>(sa), static_cast<const uint16_t*>(sw), out, M, N, K);
+    // PAIR: CBW/2 output blocks of 16 (gate and up block each) per workgroup.
+    const int nb = PAIR ? N / 32 : (N + 15) / 16, per = PAIR ? CBW / 2 : CBW;
+    hipLaunchKernelGGL((k2_wide<MB, CBW, D, TW, RT, SG, OF, PAIR>), dim3((unsigned)((nb + per - 1) / per)),
+                       dim3(CBW * MB * 64), 0, st, a, w, static_cast<const uint16_t*>(sa),
+                       static_cast<const uint16_t*>(sw), out, M, N, K);
     return hipGetLastError();
 }
 
-template <int MB, bool TW, bool RT, bool SG, bool OF>
+template <int MB, bool TW, bool RT, bool SG, bool OF, bool PAIR = false>
 hipError_t launch_wide(const int8_t* a, const int8_t* w, const void* sa, const void* sw, void* out,
                        int M, int N, int K, hipStream_t st) {
     // Column blocks per workgroup: enough that one workgroup per CU covers N.
     const int per_cu = ((N + 15) / 16 + device_cu_count() - 1) / device_cu_count();
-    if (per_cu <= 4) return launch_wide_cbw<MB, 4, TW, RT, SG, OF>(a, w, sa, sw, out, M, N, K, st);
-    if (per_cu <= 6) return launch_wide_cbw<MB, 6, TW, RT, SG, OF>(a, w, sa, sw, out, M, N, K, st);
-    return launch_wide_cbw<MB, 8, TW, RT, SG, OF>(a, w, sa, sw, out, M, N, K, st);
+    if (per_cu <= 4) return launch_wide_cbw<MB, 4, TW, RT, SG, OF, PAIR>(a, w, sa, sw, out, M, N, K, st);
+    if (per_cu <= 6) return launch_wide_cbw<MB, 6, TW, RT, SG, OF, PAIR>(a, w, sa, sw, out, M, N, K, st);
+    return launch_wide_cbw<MB, 8, TW, RT, SG, OF, PAIR>(a, w, sa, sw, out, M, N, K, st);
 }
 
 template <bool TW, bool SG, bool OF>
@@ -833,6 +869,30 @@ extern "C" int nv4_w4a4_gemm_rowtiled(const int8_t* a_rt, const int8_t* w_tiled,
                                       int sw_grouped, void* out, int out_fp32,
                                       int64_t M, int64_t N, int64_t K, void* stream) {
     return nv4::gemm_impl(a_rt, w_tiled, sa, sw, sw_grouped, out, out_fp32, true, true, M, N, K, stream);
+}
+
+extern "C" int nv4_w4a4_gemm_rowtiled_silu(const int8_t* a_rt, const int8_t* w_tiled, const void* sa, const void* sw,
+                                           int sw_grouped, void* out, int64_t M, int64_t N, int64_t K,
+                                           void* stream) {
+    using namespace nv4;
+    if (!a_rt || !w_tiled || !sa || !sw || !out) return NV4_E_NULL;
+    if (M < 1 || M > 32 || N < 32 || N % 32 || K < 128 || K % 128 || N > 0x7fffffffLL || K > (1LL << 20))
+        return NV4_E_SHAPE;
+    if (N * (K / 128) > 0x7fffffffLL || !wide_fits((int)M, (int)N, (int)K)) return NV4_E_SHAPE;
+    if (reinterpret_cast<uintptr_t>(a_rt) % 16 || reinterpret_cast<uintptr_t>(w_tiled) % 16 ||
+        reinterpret_cast<uintptr_t>(sa) % 2 || reinterpret_cast<uintptr_t>(sw) % 2 ||
+        reinterpret_cast<uintptr_t>(out) % 2)
+        return NV4_E_ALIGN;
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    const int m = (int)M, n = (int)N, k = (int)K;
+    hipError_t e;
+    if (sw_grouped)
+        e = m <= 16 ? launch_wide<1, true, true, true, false, true>(a_rt, w_tiled, sa, sw, out, m, n, k, st)
+                    : launch_wide<2, true, true, true, false, true>(a_rt, w_tiled, sa, sw, out, m, n, k, st);
+    else
+        e = m <= 16 ? launch_wide<1, true, true, false, false, true>(a_rt, w_tiled, sa, sw, out, m, n, k, st)
+                    : launch_wide<2, true, true, false, false, true>(a_rt, w_tiled, sa, sw, out, m, n, k, st);
+    return (int)e;
 }
 
 extern "C" int nv4_w4a4_tile_weights(const int8_t* w, int8_t* w_tiled, int64_t N, int64_t K, void* stream) {

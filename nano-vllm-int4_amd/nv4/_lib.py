@@ -44,6 +44,7 @@ SIGNATURES = {
     "nv4_w4a4_linear_tiled": ([_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _P], _I),
     "nv4_rht_quant_pack_rowtiled": ([_P, _P, _P, _P, _I64, _I64, _P, _I64, _P], _I),
     "nv4_w4a4_gemm_rowtiled": ([_P, _P, _P, _P, _I, _P, _I, _I64, _I64, _I64, _P], _I),
+    "nv4_w4a4_gemm_rowtiled_silu": ([_P, _P, _P, _P, _I, _P, _I64, _I64, _I64, _P], _I),
     "nv4_w4a4_linear_rowtiled": ([_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _P], _I),
     "nv4_w4a4_prefetch_bytes": ([_I64, _I64], _I64),
     "nv4_rmsnorm_rht_quant_pack_rowtiled": ([_P, _P, _P, _P, ctypes.c_float, _P, _P, _P, _I64, _I64, _P, _I64, _P],

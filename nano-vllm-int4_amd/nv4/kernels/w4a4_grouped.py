@@ -295,3 +295,64 @@ def w4a4_gemm_rowtiled(a_rt, w_tiled, a_scale, w_scale, out=None, *, output_fp32
                                         1 if output_fp32 else 0, M, N, K, ctypes.c_void_p(stream))
     _lib.check(rc, "w4a4_gemm_rowtiled")
     return out
+
+
+# Limits of the wide decode kernel (its LDS holds the widened activation block
+# and the scales): the same rule the library applies.
+_WIDE_A_BYTES, _WIDE_SCALES, _WIDE_WSCALES = 128 * 1024, 1024, 3072
+_CUS = {}
+
+
+def rowtiled_silu_fits(M, N, K, device=None):
+    """Whether ``w4a4_gemm_rowtiled_silu`` serves a fused gate/up weight of N
+    rows (gate rows, then up rows) at these sizes: the wide decode kernel's
+    limits (4 to 8 column blocks of 16 per CU, activations and scales in LDS)
+    and N a multiple of 32."""
+    if not 1 <= M <= ROWTILED_MAX_M or N % 32 or K % 256:
+        return False
+    idx = (torch.device(device).index or 0) if device is not None else torch.cuda.current_device()
+    if idx not in _CUS:
+        _CUS[idx] = torch.cuda.get_device_properties(idx).multi_processor_count
+    mb = (M + 15) // 16
+    per_cu = (N // 16 + _CUS[idx] - 1) // _CUS[idx]
+    cbw = 4 if per_cu <= 4 else 6 if per_cu <= 6 else 8
+    return (mb * 16 * K <= _WIDE_A_BYTES and (K // 128) * mb * 16 <= _WIDE_SCALES and 4 <= per_cu <= 8
+            and (K // 128) * 16 * cbw <= _WIDE_WSCALES)
+
+
+def w4a4_gemm_rowtiled_silu(a_rt, w_tiled, a_scale, w_scale, out=None):
+    """SiLU-and-mul of a fused gate/up projection in one launch: with the
+    tiled weight's first N/2 rows the gate and the last N/2 the up projection,
+    out bf16 [M, N/2] = bf16(bf16(silu(g)) * u) for g, u the bf16 results
+    ``w4a4_gemm_rowtiled`` would store -- the same bits as that GEMM followed
+    by ``silu_mul``.  Sizes as ``rowtiled_silu_fits``."""
+    if a_scale.ndim != 2 or w_tiled.ndim != 2 or a_rt.ndim != 2:
+        raise ValueError("Expected Sa[M,K/128], tiled weights [N,K/2] and row-tiled activations")
+    M, N, K = a_scale.shape[0], w_tiled.shape[0], w_tiled.shape[1] * 2
+    if a_rt.dtype != torch.int8 or w_tiled.dtype != torch.int8:
+        raise TypeError("Packed inputs must use int8 storage")
+    if a_scale.dtype != torch.bfloat16 or w_scale.dtype != torch.bfloat16:
+        raise TypeError("Both scale tensors must be BF16")
+    if not rowtiled_silu_fits(M, N, K, a_rt.device):
+        raise ValueError("Sizes outside the paired gate/up kernel (see rowtiled_silu_fits)")
+    if tuple(a_rt.shape) != ((M + 15) // 16 * 16, K // 2) or tuple(a_scale.shape) != (M, K // GROUP_SIZE):
+        raise ValueError("Require row-tiled activations [ceil(M/16)*16,K/2] and Sa[M,K/128]")
+    weight_grouped = w_scale.ndim == 2
+    if tuple(w_scale.shape) != ((N, K // GROUP_SIZE) if weight_grouped else (N,)):
+        raise ValueError("Require Sw[N] or Sw[N,K/128]")
+    if out is None:
+        out = torch.empty((M, N // 2), device=a_rt.device, dtype=torch.bfloat16)
+    if tuple(out.shape) != (M, N // 2) or out.dtype != torch.bfloat16:
+        raise ValueError("Output must be bf16 [M,N/2]")
+    if any(not t.is_cuda or not t.is_contiguous() or t.device != a_rt.device
+           for t in (a_rt, w_tiled, a_scale, w_scale, out)):
+        raise ValueError("All tensors must be contiguous CUDA tensors on one device")
+    lib = _lib.load()
+    stream = torch.cuda.current_stream(a_rt.device).cuda_stream
+    with torch.cuda.device(a_rt.device):
+        rc = lib.nv4_w4a4_gemm_rowtiled_silu(ctypes.c_void_p(a_rt.data_ptr()), ctypes.c_void_p(w_tiled.data_ptr()),
+                                             ctypes.c_void_p(a_scale.data_ptr()), ctypes.c_void_p(w_scale.data_ptr()),
+                                             1 if weight_grouped else 0, ctypes.c_void_p(out.data_ptr()), M, N, K,
+                                             ctypes.c_void_p(stream))
+    _lib.check(rc, "w4a4_gemm_rowtiled_silu")
+    return out

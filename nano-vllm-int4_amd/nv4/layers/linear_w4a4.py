@@ -32,8 +32,8 @@ from torch import nn
 import torch.distributed as dist
 
 from .. import _lib
-from ..kernels.w4a4_grouped import (ROWTILED_MAX_M, keep_weights_f6, tile_weights, untile_weights, w4a4_gemm_rowtiled,
-                                   w4a4_grouped_gemm, weights_to_f6)
+from ..kernels.w4a4_grouped import (ROWTILED_MAX_M, keep_weights_f6, rowtiled_silu_fits, tile_weights, untile_weights,
+                                   w4a4_gemm_rowtiled, w4a4_gemm_rowtiled_silu, w4a4_grouped_gemm, weights_to_f6)
 from ..kernels.w4a4_linear import w4a4_linear
 
 
@@ -164,3 +164,16 @@ class W4A4Linear(nn.Module):
             return w4a4_gemm_rowtiled(packed, self.packed_weight, scale, self.weight_scale)
         return w4a4_grouped_gemm(packed, self.packed_weight, scale, self.weight_scale,
                                  weights_tiled=self.weights_tiled, weights_f6=self._f6())
+
+    def uses_rowtiled_silu(self, m: int) -> bool:
+        """For a fused gate/up projection (gate rows, then up rows): whether
+        ``forward_quantized_silu`` serves M rows (row-tiled path and the paired
+        decode kernel's sizes)."""
+        return self.uses_rowtiled(m) and rowtiled_silu_fits(m, self.out_features, self.in_features,
+                                                             self.packed_weight.device)
+
+    def forward_quantized_silu(self, packed: torch.Tensor, scale: torch.Tensor) -> torch.Tensor:
+        """SiLU-and-mul of this fused gate/up projection on row-tiled codes:
+        bf16 [M, out/2], the same bits as ``silu_mul(forward_quantized(packed,
+        scale, rowtiled=True))`` in one launch (needs ``uses_rowtiled_silu(M)``)."""
+        return w4a4_gemm_rowtiled_silu(packed, self.packed_weight, scale, self.weight_scale)

@@ -23,7 +23,10 @@ loader address the same names:
 * W4A4 layers fuse the input and post-attention add+RMSNorm into the qkv
   and gate_up activation quantization, and SiLU-mul into down's
   (``rmsnorm_rht_quant_pack``, ``silu_mul_rht_quant_pack``): same bits,
-  one launch and one activation round trip less per fused pair.
+  one launch and one activation round trip less per fused pair.  At decode
+  sizes SiLU-mul runs in the gate/up GEMM's epilogue instead
+  (``W4A4Linear.forward_quantized_silu``), spread over every CU, and down
+  takes the plain row-tiled K1: same bits again.
 * Embedding and LM head, the head reading only each sequence's last
   position in prefill (nanovllm/layers/embed_head.py:56-66).
 * Attention through ``nv4.attention.Attention`` (paged KV cache).
@@ -43,6 +46,7 @@ from torch import nn
 from .attention import Attention
 from .kernels.decoder_ops import (qk_norm_rope_store, rmsnorm, rmsnorm_rht_quant_pack, silu_mul,
                                   silu_mul_rht_quant_pack)
+from .kernels.rht_a4 import rht_quant_pack_rowtiled
 from .layers.linear_w4a4 import W4A4Linear
 from .layers.linear_w4a16 import W4A16Linear, fuse_w4a16
 from .utils.context import get_context
@@ -199,11 +203,19 @@ class Qwen3MLP(nn.Module):
         SiLU-mul inside down's; returns (output, residual)."""
         # Decode-sized M: row-tiled codes, and each K1 reads the weights of
         # the GEMM that follows it into the Infinity Cache.
-        rt = self.gate_up_proj.uses_rowtiled(x.shape[0])
+        m = x.shape[0]
+        rt = self.gate_up_proj.uses_rowtiled(m)
         packed, scale, residual = rmsnorm_rht_quant_pack(x, norm.weight, norm.eps, self.gate_up_proj.signs, residual,
                                                          rowtiled=rt, prefetch=self.gate_up_proj.prefetch_target(rt))
+        if self.gate_up_proj.uses_rowtiled_silu(m) and self.down_proj.uses_rowtiled(m):
+            # Decode: SiLU-and-mul in the gate/up GEMM's epilogue (spread over
+            # every CU), then down's plain row-tiled K1.
+            act = self.gate_up_proj.forward_quantized_silu(packed, scale)
+            packed, scale = rht_quant_pack_rowtiled(act, self.down_proj.signs,
+                                                    prefetch=self.down_proj.prefetch_target(True))
+            return self.down_proj.forward_quantized(packed, scale, rowtiled=True), residual
         gate_up = self.gate_up_proj.forward_quantized(packed, scale, rowtiled=rt)
-        rt = self.down_proj.uses_rowtiled(x.shape[0])
+        rt = self.down_proj.uses_rowtiled(m)
         packed, scale = silu_mul_rht_quant_pack(gate_up, self.down_proj.signs, rowtiled=rt,
                                                 prefetch=self.down_proj.prefetch_target(rt))
         return self.down_proj.forward_quantized(packed, scale, rowtiled=rt), residual

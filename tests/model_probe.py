@@ -4,12 +4,16 @@ forward, and checks each one against the oracle (test helper, GPU).
 In the W4A4 decoder every projection's activations are quantized by a fused
 producer + K1 launch (add+RMSNorm before qkv and gate_up, SiLU-mul before
 down) and multiplied by the grouped INT4 GEMM on the MFMA-tiled weights
-(``W4A4Linear.forward_quantized``).  ``ProjectionProbe`` wraps both for the
+(``W4A4Linear.forward_quantized``).  At decode sizes SiLU-mul may run in the
+gate/up GEMM's epilogue instead (``forward_quantized_silu``), followed by
+down's plain row-tiled K1 (``rht_quant_pack_rowtiled``).  ``ProjectionProbe`` wraps both for the
 layers it is given and keeps copies of what went in and came out; the
 ``check_*`` functions then compare:
 
 * every GEMM output with the oracle's grouped GEMM on the recorded codes and
-  scales and the weights in the reference layout (bit for bit);
+  scales and the weights in the reference layout (bit for bit); a gate/up
+  GEMM with SiLU-mul in its epilogue with the separate SiLU-mul kernel on the
+  oracle's GEMM output;
 * every whole ``W4A4Linear.forward`` (o_proj, whose input is the attention
   output in bf16) with the oracle's K1 + GEMM chain on the same input;
 * every fused K1 output with the oracle's K1 on the producer's bf16 output
@@ -58,8 +62,8 @@ class ProjectionProbe:
                 self._by_signs[m.signs.data_ptr()] = (f"layer{i}.{name}", m)
 
     def __enter__(self):
-        self._saved = (qwen3.rmsnorm_rht_quant_pack, qwen3.silu_mul_rht_quant_pack)
-        rms_k1, silu_k1 = self._saved
+        self._saved = (qwen3.rmsnorm_rht_quant_pack, qwen3.silu_mul_rht_quant_pack, qwen3.rht_quant_pack_rowtiled)
+        rms_k1, silu_k1, plain_k1 = self._saved
         probe = self
 
         def rms_wrap(x, weight, eps, signs, residual=None, **kw):
@@ -83,27 +87,43 @@ class ProjectionProbe:
                                   packed, out[1].clone()))
             return out
 
+        def plain_wrap(x, signs, **kw):
+            hit = probe._by_signs.get(signs.data_ptr())
+            out = plain_k1(x, signs, **kw)
+            if hit is not None:
+                probe.k1s.append((hit[0], "plain", {"x": x.clone(), "signs": signs},
+                                  rowtiled_to_reference(out[0], x.shape[0]), out[1].clone()))
+            return out
+
         qwen3.rmsnorm_rht_quant_pack, qwen3.silu_mul_rht_quant_pack = rms_wrap, silu_wrap
+        qwen3.rht_quant_pack_rowtiled = plain_wrap
         self._patched = []
         for name, m in self._by_signs.values():
             def fq(packed, scale, rowtiled=False, _m=m, _name=name, _orig=m.forward_quantized):
                 out = _orig(packed, scale, rowtiled=rowtiled)
                 ref_packed = rowtiled_to_reference(packed, scale.shape[0]) if rowtiled else packed.clone()
-                probe.gemms.append((_name, _m, ref_packed, scale.clone(), out.clone()))
+                probe.gemms.append((_name, _m, ref_packed, scale.clone(), out.clone(), False))
+                return out
+            def fqs(packed, scale, _m=m, _name=name, _orig=m.forward_quantized_silu):
+                out = _orig(packed, scale)
+                ref_packed = rowtiled_to_reference(packed, scale.shape[0])
+                probe.gemms.append((_name, _m, ref_packed, scale.clone(), out.clone(), True))
                 return out
             def fw(x, _m=m, _name=name, _orig=m.forward):
                 out = _orig(x)
                 probe.linears.append((_name, _m, x.clone(), out.clone()))
                 return out
             m.forward_quantized = fq
+            m.forward_quantized_silu = fqs
             m.forward = fw
             self._patched.append(m)
         return self
 
     def __exit__(self, *exc):
-        qwen3.rmsnorm_rht_quant_pack, qwen3.silu_mul_rht_quant_pack = self._saved
+        qwen3.rmsnorm_rht_quant_pack, qwen3.silu_mul_rht_quant_pack, qwen3.rht_quant_pack_rowtiled = self._saved
         for m in self._patched:
             del m.forward_quantized
+            del m.forward_quantized_silu
             del m.forward
         return False
 
@@ -124,13 +144,15 @@ def check_gemms(probe: ProjectionProbe, rows=None, weights=None):
     of the module's own (e.g. tensors read from a checkpoint file)."""
     assert probe.gemms, "no W4A4 GEMM was recorded"
     cache = {}
-    for name, m, packed, scale, out in probe.gemms:
+    for name, m, packed, scale, out, silu in probe.gemms:
         if name not in cache:
             cache[name] = weights[name] if weights and name in weights else reference_weights(m)
         wp, sw = cache[name]
         a = _rows(packed, rows).cpu().numpy()
         sa = bf16_bits(_rows(scale, rows))
         ref = oracle.w4a4_gemm(a, wp, sa, sw)
+        if silu:  # SiLU-mul in the epilogue: the separate kernel on the oracle's gate/up output
+            ref = bf16_bits(silu_mul(torch.from_numpy(ref.view(np.int16)).view(torch.bfloat16).to(out.device)))
         got = bf16_bits(_rows(out, rows))
         assert np.array_equal(got, ref), f"{name}: GEMM output differs from the oracle " \
                                          f"({int((got != ref).sum())} of {ref.size} elements)"
@@ -165,6 +187,8 @@ def check_k1s(probe: ProjectionProbe, rows=None):
                 y, _ = rmsnorm(x, inp["weight"], inp["eps"], residual=res.clone())
             else:
                 y = rmsnorm(x, inp["weight"], inp["eps"])
+        elif kind == "plain":
+            y = _rows(inp["x"], rows).contiguous()
         else:
             y = silu_mul(_rows(inp["gate_up"], rows).contiguous())
         p_ref, s_ref = oracle.rht_quant_pack(bf16_bits(y), inp["signs"].cpu().numpy())

@@ -264,6 +264,12 @@ def test_rowtiled_entry_point_rejections():
     sm = lib.nv4_silu_mul_rht_quant_pack_rowtiled
     assert sm(P(A16), P(A16), P(A16), P(A16), 4, 2048, None, 0, None) == _lib.NV4_E_SHAPE
     assert sm(P(A16), P(A16), P(A16), P(A16), 4, 4096, None, 32, None) == _lib.NV4_E_NULL
+    gs = lib.nv4_w4a4_gemm_rowtiled_silu
+    assert gs(None, *ok[1:], 1, P(A16), 4, 24576, 4096, None) == _lib.NV4_E_NULL
+    assert gs(*ok, 1, P(A16), 33, 24576, 4096, None) == _lib.NV4_E_SHAPE      # M > 32
+    assert gs(*ok, 1, P(A16), 4, 24592, 4096, None) == _lib.NV4_E_SHAPE      # N % 32
+    assert gs(*ok, 1, P(A16), 4, 24576, 4224, None) == _lib.NV4_E_SHAPE      # K % 256
+    assert gs(*ok, 1, P(A16), 4, 4096, 4096, None) == _lib.NV4_E_SHAPE       # fewer than 4 blocks per CU
 
 
 def test_gumbel_split_rejections():

@@ -29,7 +29,8 @@ from nv4 import W4A4Linear, rht_quant_pack, tile_weights, w4a4_grouped_gemm
 from nv4 import workloads as W
 from nv4.kernels.decoder_ops import rmsnorm_rht_quant_pack, silu_mul_rht_quant_pack
 from nv4.kernels.rht_a4 import rht_quant_pack_rowtiled, rowtiled_rows
-from nv4.kernels.w4a4_grouped import w4a4_gemm_rowtiled
+from nv4.kernels.decoder_ops import silu_mul
+from nv4.kernels.w4a4_grouped import rowtiled_silu_fits, w4a4_gemm_rowtiled, w4a4_gemm_rowtiled_silu
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda:0"
@@ -260,3 +261,31 @@ def test_k1_prefetch_tail_changes_nothing(M):
         assert np.array_equal(untile(u[0].cpu().numpy(), M), untile(v[0].cpu().numpy(), M))
         assert torch.equal(u[1].view(torch.int16), v[1].view(torch.int16))
     assert torch.equal(r1.view(torch.int16), r2.view(torch.int16))
+
+
+@pytest.mark.parametrize("M,N,K", [(1, 24576, 4096), (7, 24576, 4096), (16, 24576, 4096), (17, 24576, 4096),
+                                   (32, 24576, 4096), (32, 24544, 4096), (9, 16384, 2048)])
+def test_gemm_rowtiled_silu_equals_gemm_then_silu(M, N, K):
+    """The gate/up GEMM with SiLU-and-mul in its epilogue gives exactly the
+    bits of the row-tiled GEMM (itself bit-exact with the oracle) followed by
+    silu_mul: gate columns n < N/2 paired with up columns N/2 + n; M blocks 1
+    and 2, a partial last workgroup (N = 24544: 767 output blocks, 3 per
+    workgroup), 4 column blocks per workgroup (N = 16384, K = 2048), grouped and
+    per-channel weight scales."""
+    print(f"[k2-silu] M={M} N={N} K={K}", flush=True)
+    assert rowtiled_silu_fits(M, N, K, DEV)
+    ap, wp, sa, sw = gemm_inputs(M, N, K, 11 * M + N + K)
+    a_rt = torch.from_numpy(rowtile(ap)).to(DEV)
+    wt = tile_weights(torch.from_numpy(wp).to(DEV))
+    s_a = bits_to_bf16(sa).to(DEV)
+    for grouped in (True, False):
+        s_w = bits_to_bf16(sw if grouped else sw[:, 0].copy()).to(DEV)
+        two = silu_mul(w4a4_gemm_rowtiled(a_rt, wt, s_a, s_w))
+        out = torch.full((M, N // 2), float("nan"), dtype=torch.bfloat16, device=DEV)
+        got = w4a4_gemm_rowtiled_silu(a_rt, wt, s_a, s_w, out=out)
+        torch.cuda.synchronize()
+        assert got.data_ptr() == out.data_ptr()
+        assert np.array_equal(bf16_bits(out), bf16_bits(two)), f"grouped={grouped}"
+    if M == 32 and N == 24576:
+        exp = oracle.w4a4_gemm(ap, wp, sa, sw)   # the GEMM half against the oracle once more
+        assert np.array_equal(bf16_bits(w4a4_gemm_rowtiled(a_rt, wt, s_a, bits_to_bf16(sw).to(DEV))), exp)
