@@ -204,7 +204,8 @@ def pmc_pass(torch, linear, R):
     print(f"pmc pass done: {3 * R * len(PROJECTIONS)} linear launches, 3 copies of {COPY_BYTES} bytes", flush=True)
 
 
-DECODE_GEMM_SOURCES = ("nano-vllm-int4_amd/csrc/w4a4_gemm.hip", "nano-vllm-int4_amd/csrc/nv4_common.h")
+DECODE_GEMM_SOURCES = ("nano-vllm-int4_amd/csrc/w4a4_gemm.hip", "nano-vllm-int4_amd/csrc/nv4_common.h",
+                       "nano-vllm-int4_amd/csrc/norm_ops.h", "nano-vllm-int4_amd/csrc/k2_launch.h")
 
 
 def decode_gemm_source_sha():
