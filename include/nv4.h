@@ -69,6 +69,11 @@
  *                          SiluAndMul (nanovllm/models/qwen3.py:125-129,
  *                          nanovllm/layers/activation.py:8-11) in one launch, for
  *                          decode-sized M (no counterpart call in the reference)
+ *   nv4_paged_decode_attention_qkv <- the decode step's q_norm/k_norm +
+ *                          rotary_emb + store_kvcache + flash_attn_with_kvcache
+ *                          (nanovllm/models/qwen3.py:78-94,
+ *                          nanovllm/layers/attention.py:10-40, 72-74) in one call
+ *                          (no counterpart call in the reference)
  */
 #ifndef NV4_H
 #define NV4_H
@@ -388,6 +393,30 @@ int nv4_paged_decode_attention_noalloc(const void* q, int64_t q_row_stride, cons
                                        const int32_t* context_lens, void* out, int64_t B, int64_t Hq, int64_t Hkv,
                                        int64_t D, int64_t block_size, int64_t max_context, float scale,
                                        void* stream);
+
+/*
+ * The decode step's nv4_qk_norm_rope_store (one token per sequence, T = B)
+ * fused into nv4_paged_decode_attention: one launch less per layer, the same
+ * bits in out, k_cache and v_cache as the two calls in sequence (the second
+ * with q = the first's q_out).  Replaces, in the decode branch, q_norm/k_norm +
+ * rotary_emb (nanovllm/models/qwen3.py:78-94, layers/rotary_embedding.py:6-48),
+ * store_kvcache (layers/attention.py:10-40) and flash_attn_with_kvcache
+ * (layers/attention.py:72-74).
+ *   qkv, qkv_row_stride, q/k_norm_w, cos_sin, max_position, positions,
+ *   slot_mapping, num_slots: as nv4_qk_norm_rope_store, with T = B
+ *   k/v_cache, block_tables, context_lens, out, workspace, max_context, scale:
+ *   as nv4_paged_decode_attention (q = the query heads of qkv)
+ * The workgroup that reads a sequence's last context token stores the step's
+ * key and value and uses them from registers for that token.  Precondition
+ * (the engine's): a step's slots are not in any other sequence's context.
+ */
+int nv4_paged_decode_attention_qkv(const void* qkv, int64_t qkv_row_stride, const void* q_norm_w,
+                                   const void* k_norm_w, const float* cos_sin, int64_t max_position,
+                                   const int64_t* positions, const int32_t* slot_mapping, int64_t num_slots,
+                                   void* k_cache, void* v_cache, const int32_t* block_tables, int64_t max_blocks,
+                                   const int32_t* context_lens, void* out, float* workspace, int64_t workspace_bytes,
+                                   int64_t B, int64_t Hq, int64_t Hkv, int64_t D, int64_t block_size,
+                                   int64_t max_context, float eps, float scale, void* stream);
 
 /*
  * RMSNorm over rows of H bf16 values (nanovllm/layers/layernorm.py:16-50):

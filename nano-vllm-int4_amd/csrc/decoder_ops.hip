@@ -21,6 +21,7 @@
 //  * nv4_silu_mul (nanovllm/layers/activation.py:8-11): bf16(bf16(silu(g)) * u)
 //    with silu(g) = g / (1 + exp(-g)) in fp32.
 #include "norm_ops.h"
+#include "qk_ops.h"
 
 namespace nv4 {
 namespace {
@@ -110,41 +111,8 @@ qk_norm_rope_store(const uint16_t* __restrict__ qkv, int64_t qkv_row, int T, int
         }
         return;
     }
-    float x1[4], x2[4], w1[4], w2[4];
-    const uint32_t xs[4] = {xa.x, xa.y, xb.x, xb.y}, ws[4] = {wa.x, wa.y, wb.x, wb.y};
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-        x1[2 * i] = bf16_to_f32(xs[i] & 0xffffu);
-        x1[2 * i + 1] = bf16_to_f32(xs[i] >> 16);
-        x2[2 * i] = bf16_to_f32(xs[2 + i] & 0xffffu);
-        x2[2 * i + 1] = bf16_to_f32(xs[2 + i] >> 16);
-        w1[2 * i] = bf16_to_f32(ws[i] & 0xffffu);
-        w1[2 * i + 1] = bf16_to_f32(ws[i] >> 16);
-        w2[2 * i] = bf16_to_f32(ws[2 + i] & 0xffffu);
-        w2[2 * i + 1] = bf16_to_f32(ws[2 + i] >> 16);
-    }
-    float ss = 0.0f;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) ss += x1[i] * x1[i] + x2[i] * x2[i];
-#pragma unroll
-    for (int off = 8; off >= 1; off >>= 1) ss += __shfl_xor(ss, off);
-    const float r = rsqrtf(ss / 128.0f + eps);
-    uint32_t y1p[2], y2p[2];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const float a1 = round_bf16(round_bf16(x1[i] * r) * w1[i]);
-        const float a2 = round_bf16(round_bf16(x2[i] * r) * w2[i]);
-        const uint32_t y1 = f32_to_bf16_rne(a1 * c[i] - a2 * s[i]);
-        const uint32_t y2 = f32_to_bf16_rne(a2 * c[i] + a1 * s[i]);
-        if (i & 1) {
-            y1p[i >> 1] |= y1 << 16;
-            y2p[i >> 1] |= y2 << 16;
-        } else {
-            y1p[i >> 1] = y1;
-            y2p[i >> 1] = y2;
-        }
-    }
-    const uint2 o1 = make_uint2(y1p[0], y1p[1]), o2 = make_uint2(y2p[0], y2p[1]);
+    uint2 o1, o2;
+    qk_head16(xa, xb, wa, wb, c, s, eps, o1, o2);
     if (is_q) {
         uint16_t* dst = q_out + (tok * Hq + h) * 128;
         *reinterpret_cast<uint2*>(dst + j4) = o1;

@@ -30,7 +30,8 @@
 //    reads split s's (m, l), M = max m_s, w_s = 2^(m_s - M) (broadcast with
 //    lane reads), o = sum w_s o_s / sum w_s l_s with lane i owning dims 2i,
 //    2i+1 and every split's loads issued before the sums.
-#include "nv4_common.h"
+#include "norm_ops.h"
+#include "qk_ops.h"
 
 #include <mutex>
 
@@ -44,17 +45,100 @@ constexpr int PA_THREADS = 256;  // 4 waves x 64 tokens
 typedef __bf16 v2bf __attribute__((ext_vector_type(2)));
 typedef float v2f __attribute__((ext_vector_type(2)));
 
-template <int G, bool BLK16>
+// The step's q/k RMSNorm, rotary embedding and KV store, fused into the
+// decode attention (FUSED): q is then the raw fused qkv row of the step's
+// token, [Hq q heads | Hkv k heads | Hkv v heads] x 128.
+struct QkvStep {
+    const uint16_t* qw;        // q_norm weight [128]
+    const uint16_t* kw;        // k_norm weight [128]
+    const float* cos_sin;      // [max_position, 128]: cos of dims 0..63, then sin
+    const int64_t* positions;  // [B]
+    const int32_t* slots;      // [B] cache slot of the step's token (-1: none)
+    uint16_t* k_cache;         // the caches kc / vc, written at the slots
+    uint16_t* v_cache;
+    int64_t max_position, num_slots;
+    float eps;
+};
+
+// FUSED prologue.  Every wave normalises and rotates the group's G q heads
+// itself, sixteen lanes per head as qk_norm_rope_store does (qk_head16: lane
+// j of a head holds dims 4j .. 4j+3 and 64 + 4j .. 64 + 4j+3), into LDS rows
+// of its own, so no workgroup barrier couples the four waves.  Loads of one
+// head's values and norm weights for lane offset j4 = 4j:
+struct Head16 {
+    uint2 xa, xb, wa, wb;
+};
+__device__ __forceinline__ Head16 head16_loads(const uint16_t* src, const uint16_t* w, int j4) {
+    return Head16{*reinterpret_cast<const uint2*>(src + j4), *reinterpret_cast<const uint2*>(src + 64 + j4),
+                  *reinterpret_cast<const uint2*>(w + j4), *reinterpret_cast<const uint2*>(w + 64 + j4)};
+}
+// cos and sin of dims j4 .. j4+3 at position pos (row 0 outside the table).
+__device__ __forceinline__ void rope_cs(const QkvStep& qs, int64_t pos, int j4, v4f& c, v4f& sn) {
+    if (pos < 0 || pos >= qs.max_position) pos = 0;
+    c = *reinterpret_cast<const v4f*>(qs.cos_sin + pos * PA_D + j4);
+    sn = *reinterpret_cast<const v4f*>(qs.cos_sin + pos * PA_D + 64 + j4);
+}
+// Orders one wave's LDS accesses (the LDS unit runs them in order) without a
+// workgroup barrier.
+__device__ __forceinline__ void wave_lds_order() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+// The step's key (norm + rotary, by all four sixteen-lane groups alike) into
+// ko1 / ko2, and the value pair loaded by the caller: stored at the slot by
+// wave 3 (key) and wave 2 (value: lane (kq, rc) holds dims 8 rc .. 8 rc + 7)
+// when the slot is in [0, num_slots).
+__device__ __forceinline__ void kv_store(const QkvStep& qs, const Head16& kh, v4u vch, const v4f& c, const v4f& sn,
+                                         int64_t slot, bool slot_ok, int Hkv, int kvh, int wave, int lane,
+                                         uint2& ko1, uint2& ko2) {
+    const int j4 = (lane & 15) * 4;
+    qk_head16(kh.xa, kh.xb, kh.wa, kh.wb, c, sn, qs.eps, ko1, ko2);
+    if (slot_ok && wave == 3 && lane < 16) {
+        uint16_t* dst = qs.k_cache + (slot * Hkv + kvh) * PA_D;
+        *reinterpret_cast<uint2*>(dst + j4) = ko1;
+        *reinterpret_cast<uint2*>(dst + 64 + j4) = ko2;
+    }
+    if (slot_ok && wave == 2 && lane < 16)
+        *reinterpret_cast<v4u*>(qs.v_cache + (slot * Hkv + kvh) * PA_D + 8 * lane) = vch;
+}
+
+template <int G, bool BLK16, bool FUSED>
 __global__ void __launch_bounds__(PA_THREADS)
-pa_split(const uint16_t* __restrict__ q, int64_t q_row, const uint16_t* __restrict__ kc,
-         const uint16_t* __restrict__ vc, const int32_t* __restrict__ block_tables, int max_blocks,
-         const int32_t* __restrict__ context_lens, uint16_t* __restrict__ out, float* __restrict__ part_o,
-         float* __restrict__ part_ml, int Hkv, int bs, int S, int max_ctx, float qscale) {
+pa_split(const uint16_t* __restrict__ q, int64_t q_row, const uint16_t* kc, const uint16_t* vc,
+         const int32_t* __restrict__ block_tables, int max_blocks, const int32_t* __restrict__ context_lens,
+         uint16_t* __restrict__ out, float* __restrict__ part_o, float* __restrict__ part_ml, int Hkv, int bs,
+         int S, int max_ctx, float qscale, QkvStep qs) {
     const int s = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
     const int Hq = Hkv * G;
-    const int ctx = min(context_lens[b], max_ctx);  // never past the block table's row
+    const int clen = context_lens[b];
+    const int ctx = min(clen, max_ctx);  // never past the block table's row
     const int start = s * PA_SPLIT;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint16_t* qrow = q + (int64_t)b * q_row;
+    int64_t slot = -1, pos = 0;
+    bool kv_wg = false, slot_ok = false;
+    if constexpr (FUSED) {
+        // Read with the context length, in one round trip.
+        pos = qs.positions[b];
+        slot = qs.slots[b];
+        slot_ok = slot >= 0 && slot < qs.num_slots;
+        kv_wg = s == (ctx > 0 ? (ctx - 1) / PA_SPLIT : 0);
+    }
     if (start >= ctx) {
+        if constexpr (FUSED) {
+            if (kv_wg) {  // an empty context: only the store
+                const int j4 = (lane & 15) * 4;
+                v4f c, sn;
+                rope_cs(qs, pos, j4, c, sn);
+                const Head16 kh = head16_loads(qrow + (int64_t)(Hq + kvh) * PA_D, qs.kw, j4);
+                const v4u vch =
+                    *reinterpret_cast<const v4u*>(qrow + (int64_t)(Hq + Hkv + kvh) * PA_D + 8 * (lane & 15));
+                uint2 ko1, ko2;
+                kv_store(qs, kh, vch, c, sn, slot, slot_ok, Hkv, kvh, wave, lane, ko1, ko2);
+            }
+        }
         // Nothing of this sequence here; pass 2 skips the split.  An empty
         // context (ctx <= 0) with a single split has no pass 2: its output
         // is defined as zeros.
@@ -64,12 +148,12 @@ pa_split(const uint16_t* __restrict__ q, int64_t q_row, const uint16_t* __restri
         return;
     }
     const int end = min(start + PA_SPLIT, ctx);
-    const int lane = threadIdx.x & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int kq = lane >> 4, rc = lane & 15;  // MFMA k-octet and row/column of the lane
 
     __shared__ float sm_m[4][G], sm_l[4][G];
     __shared__ float sm_o[4][G][PA_D];
+    // FUSED: per wave, the G normalised, rotated q heads, then the step's key.
+    __shared__ __align__(16) uint16_t s_qk[FUSED ? 4 : 1][G + 1][PA_D];
 
     const int32_t* bt = block_tables + (int64_t)b * max_blocks;
     const uint32_t row = (uint32_t)Hkv * PA_D;  // elements between consecutive slots
@@ -123,12 +207,32 @@ pa_split(const uint16_t* __restrict__ q, int64_t q_row, const uint16_t* __restri
     // first and unconditionally (a clamped head, then zeroed), so that the
     // first half's waits leave the second half's loads in flight.
     v8bf qb[4];
+    // FUSED: the q head of this lane's sixteen-lane group (clamped to the
+    // group's G), rotary factors, norm weights; in the storing workgroup also
+    // the step's key head and the value chunk of the V operand's layout.
+    const int j4 = (lane & 15) * 4;
+    Head16 qh{}, kh;
+    v4u vch;
+    v4f c{}, sn{};
+    const int tl = ctx - 1;  // the last context token
+    bool subst = false;      // FUSED: see below
+    if constexpr (FUSED) {
+        // Ahead of the K and V loads, like q in the plain form: they arrive
+        // first, and the q products below overlap the K and V loads.
+        qh = head16_loads(qrow + (int64_t)(kvh * G + min(lane >> 4, G - 1)) * PA_D, qs.qw, j4);
+        rope_cs(qs, pos, j4, c, sn);
+        if (kv_wg) {
+            kh = head16_loads(qrow + (int64_t)(Hq + kvh) * PA_D, qs.kw, j4);
+            vch = *reinterpret_cast<const v4u*>(qrow + (int64_t)(Hq + Hkv + kvh) * PA_D + 8 * rc);
+        }
+    } else {
 #pragma unroll
-    for (int st = 0; st < 4; ++st) {
-        v4u w = *reinterpret_cast<const v4u*>(q + (int64_t)b * q_row + (int64_t)(kvh * G + min(rc, G - 1)) * PA_D +
-                                              8 * (kq + 4 * st));
-        if (rc >= G) w = v4u{0u, 0u, 0u, 0u};
-        qb[st] = __builtin_bit_cast(v8bf, w);
+        for (int st = 0; st < 4; ++st) {
+            v4u w = *reinterpret_cast<const v4u*>(qrow + (int64_t)(kvh * G + min(rc, G - 1)) * PA_D +
+                                                  8 * (kq + 4 * st));
+            if (rc >= G) w = v4u{0u, 0u, 0u, 0u};
+            qb[st] = __builtin_bit_cast(v8bf, w);
+        }
     }
     __builtin_amdgcn_sched_barrier(0);
     v4u ka[8], va[8], kb[8], vb[8];
@@ -140,6 +244,61 @@ pa_split(const uint16_t* __restrict__ q, int64_t q_row, const uint16_t* __restri
         issue(kb, vb, b0, b1);
         __builtin_amdgcn_sched_barrier(0);
     }
+    if constexpr (FUSED) {
+        // (Read after the K and V loads are issued, its wait overlaps them.)
+        subst = kv_wg && slot_ok && clen == ctx &&
+                (int64_t)(block_tables[(int64_t)b * max_blocks + tl / bs] * bs + tl % bs) == slot;
+        uint16_t (*sq)[PA_D] = s_qk[wave];
+        {
+            uint2 o1, o2;
+            qk_head16(qh.xa, qh.xb, qh.wa, qh.wb, c, sn, qs.eps, o1, o2);
+            if ((lane >> 4) < G) {
+                *reinterpret_cast<uint2*>(&sq[lane >> 4][j4]) = o1;
+                *reinterpret_cast<uint2*>(&sq[lane >> 4][64 + j4]) = o2;
+            }
+        }
+        if (kv_wg) {
+            uint2 ko1, ko2;
+            kv_store(qs, kh, vch, c, sn, slot, slot_ok, Hkv, kvh, wave, lane, ko1, ko2);
+            if (lane < 16) {
+                *reinterpret_cast<uint2*>(&sq[G][j4]) = ko1;
+                *reinterpret_cast<uint2*>(&sq[G][64 + j4]) = ko2;
+            }
+        }
+        wave_lds_order();
+#pragma unroll
+        for (int st = 0; st < 4; ++st) {
+            v4u w = *reinterpret_cast<const v4u*>(&sq[min(rc, G - 1)][8 * (kq + 4 * st)]);
+            if (rc >= G) w = v4u{0u, 0u, 0u, 0u};
+            qb[st] = __builtin_bit_cast(v8bf, w);
+        }
+    }
+    // FUSED: the cache slot of the last context token was loaded before this
+    // step's key and value reached it: every operand lane that holds that
+    // token (the clamped lanes past the end too) takes them instead, right
+    // before the half's products (which wait for its loads anyway).  Only
+    // when the token is the step's own (context not cut by max_ctx) and its
+    // block-table slot is the one just stored.
+    v4u knew[4];
+    if constexpr (FUSED) {
+        if (subst) {
+#pragma unroll
+            for (int st = 0; st < 4; ++st)
+                knew[st] = *reinterpret_cast<const v4u*>(&s_qk[wave][G][8 * (kq + 4 * st)]);
+        }
+    }
+    auto take = [&](v4u (&kx)[8], v4u (&vx)[8], int h0) {
+#pragma unroll
+        for (int cc = 0; cc < 2; ++cc) {
+            const int t0 = h0 + 16 * cc;
+            if (t0 + rc >= tl)
+#pragma unroll
+                for (int st = 0; st < 4; ++st) kx[4 * cc + st] = knew[st];
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                if (t0 + 4 * kq + i >= tl) vx[4 * cc + i] = vch;
+        }
+    };
 
     // Softmax state of head rc (the same in the four k-octet rows): running
     // max m (raw score units), partial sum l over this lane's tokens.  Output
@@ -219,7 +378,9 @@ pa_split(const uint16_t* __restrict__ q, int64_t q_row, const uint16_t* __restri
         }
     };
 
+    if (subst) take(ka, va, half0(0));
     compute(ka, va, half0(0));
+    if (subst) take(kb, vb, half0(1));
     compute(kb, vb, half0(1));
 
     // Merge the four wave states of the workgroup.
@@ -357,21 +518,23 @@ pa_merge(const int32_t* __restrict__ context_lens, const float* __restrict__ par
     *reinterpret_cast<uint32_t*>(o) = n > 0 ? f32_to_bf16_rne(O0 / L) | (f32_to_bf16_rne(O1 / L) << 16) : 0u;
 }
 
-template <int G>
+template <int G, bool FUSED>
 hipError_t pa_launch(const void* q, int64_t q_row, const void* kc, const void* vc, const int32_t* bt, int max_blocks,
                      const int32_t* cl, void* out, float* ws, int B, int Hkv, int bs, int S, int max_ctx,
-                     float qscale, hipStream_t st) {
+                     float qscale, const QkvStep& qs, hipStream_t st) {
     float* part_o = ws;
     float* part_ml = ws + (int64_t)B * Hkv * G * S * PA_D;
     const dim3 grid((unsigned)S, (unsigned)Hkv, (unsigned)B);
     if (bs % 16 == 0)
-        hipLaunchKernelGGL((pa_split<G, true>), grid, dim3(PA_THREADS), 0, st, static_cast<const uint16_t*>(q), q_row,
-                           static_cast<const uint16_t*>(kc), static_cast<const uint16_t*>(vc), bt, max_blocks, cl,
-                           static_cast<uint16_t*>(out), part_o, part_ml, Hkv, bs, S, max_ctx, qscale);
+        hipLaunchKernelGGL((pa_split<G, true, FUSED>), grid, dim3(PA_THREADS), 0, st,
+                           static_cast<const uint16_t*>(q), q_row, static_cast<const uint16_t*>(kc),
+                           static_cast<const uint16_t*>(vc), bt, max_blocks, cl, static_cast<uint16_t*>(out), part_o,
+                           part_ml, Hkv, bs, S, max_ctx, qscale, qs);
     else
-        hipLaunchKernelGGL((pa_split<G, false>), grid, dim3(PA_THREADS), 0, st, static_cast<const uint16_t*>(q),
-                           q_row, static_cast<const uint16_t*>(kc), static_cast<const uint16_t*>(vc), bt, max_blocks,
-                           cl, static_cast<uint16_t*>(out), part_o, part_ml, Hkv, bs, S, max_ctx, qscale);
+        hipLaunchKernelGGL((pa_split<G, false, FUSED>), grid, dim3(PA_THREADS), 0, st,
+                           static_cast<const uint16_t*>(q), q_row, static_cast<const uint16_t*>(kc),
+                           static_cast<const uint16_t*>(vc), bt, max_blocks, cl, static_cast<uint16_t*>(out), part_o,
+                           part_ml, Hkv, bs, S, max_ctx, qscale, qs);
     if (S > 1) {
         const dim3 mg((unsigned)(Hkv * G), (unsigned)B);
         auto* o16 = static_cast<uint16_t*>(out);
@@ -439,17 +602,24 @@ int64_t pa_partials_bytes(int64_t B, int64_t Hq, int64_t S, int64_t D) {
 int pa_run(const void* q, int64_t q_row_stride, const void* k_cache, const void* v_cache,
            const int32_t* block_tables, int64_t max_blocks, const int32_t* context_lens, void* out, float* ws,
            int64_t B, int64_t Hq, int64_t Hkv, int64_t block_size, int64_t max_context, int64_t S, float scale,
-           void* stream) {
+           const QkvStep* fused, void* stream) {
     const float qscale = scale * 1.4426950408889634f;  // log2(e): softmax in base 2
     hipStream_t st = static_cast<hipStream_t>(stream);
     const int b = (int)B, hkv = (int)Hkv, bs = (int)block_size, s = (int)S, mb = (int)max_blocks;
+    const QkvStep none{};
+    auto run = [&](auto g, auto f) {
+        constexpr int G = decltype(g)::value;
+        constexpr bool F = decltype(f)::value;
+        return (int)pa_launch<G, F>(q, q_row_stride, k_cache, v_cache, block_tables, mb, context_lens, out, ws, b,
+                                    hkv, bs, s, (int)max_context, qscale, F ? *fused : none, st);
+    };
+    using T = std::true_type;
+    using F = std::false_type;
     switch (Hq / Hkv) {
-        case 1: return (int)pa_launch<1>(q, q_row_stride, k_cache, v_cache, block_tables, mb, context_lens, out, ws,
-                                         b, hkv, bs, s, (int)max_context, qscale, st);
-        case 2: return (int)pa_launch<2>(q, q_row_stride, k_cache, v_cache, block_tables, mb, context_lens, out, ws,
-                                         b, hkv, bs, s, (int)max_context, qscale, st);
-        default: return (int)pa_launch<4>(q, q_row_stride, k_cache, v_cache, block_tables, mb, context_lens, out,
-                                          ws, b, hkv, bs, s, (int)max_context, qscale, st);
+        case 1: return fused ? run(std::integral_constant<int, 1>{}, T{}) : run(std::integral_constant<int, 1>{}, F{});
+        case 2: return fused ? run(std::integral_constant<int, 2>{}, T{}) : run(std::integral_constant<int, 2>{}, F{});
+        default:
+            return fused ? run(std::integral_constant<int, 4>{}, T{}) : run(std::integral_constant<int, 4>{}, F{});
     }
 }
 
@@ -494,7 +664,7 @@ extern "C" int nv4_paged_decode_attention(const void* q, int64_t q_row_stride, c
     if (need < 0 || workspace_bytes < need) return NV4_E_SHAPE;
     if (reinterpret_cast<uintptr_t>(workspace) % 8) return NV4_E_ALIGN;
     return pa_run(q, q_row_stride, k_cache, v_cache, block_tables, max_blocks, context_lens, out, workspace, B, Hq,
-                  Hkv, block_size, max_context, S, scale, stream);
+                  Hkv, block_size, max_context, S, scale, nullptr, stream);
 }
 
 extern "C" int nv4_paged_decode_attention_noalloc(const void* q, int64_t q_row_stride, const void* k_cache,
@@ -517,5 +687,36 @@ extern "C" int nv4_paged_decode_attention_noalloc(const void* q, int64_t q_row_s
     rc = scratch_on_current_device(&ws);
     if (rc != NV4_OK) return rc;
     return pa_run(q, q_row_stride, k_cache, v_cache, block_tables, max_blocks, context_lens, out, ws, B, Hq, Hkv,
-                  block_size, max_context, S, scale, stream);
+                  block_size, max_context, S, scale, nullptr, stream);
+}
+
+extern "C" int nv4_paged_decode_attention_qkv(const void* qkv, int64_t qkv_row_stride, const void* q_norm_w,
+                                              const void* k_norm_w, const float* cos_sin, int64_t max_position,
+                                              const int64_t* positions, const int32_t* slot_mapping,
+                                              int64_t num_slots, void* k_cache, void* v_cache,
+                                              const int32_t* block_tables, int64_t max_blocks,
+                                              const int32_t* context_lens, void* out, float* workspace,
+                                              int64_t workspace_bytes, int64_t B, int64_t Hq, int64_t Hkv, int64_t D,
+                                              int64_t block_size, int64_t max_context, float eps, float scale,
+                                              void* stream) {
+    using namespace nv4;
+    int64_t S = 0;
+    const int rc = pa_check(qkv, qkv_row_stride, k_cache, v_cache, block_tables, max_blocks, context_lens, out, B,
+                            Hq, Hkv, D, block_size, max_context, &S);
+    if (rc != NV4_OK) return rc;
+    if (!q_norm_w || !k_norm_w || !cos_sin || !positions || !slot_mapping || !workspace) return NV4_E_NULL;
+    if (qkv_row_stride < (Hq + 2 * Hkv) * D || max_position < 1 || max_position > ((int64_t)1 << 40) ||
+        num_slots < 0)
+        return NV4_E_SHAPE;
+    const int64_t need = pa_partials_bytes(B, Hq, S, D);
+    if (need < 0 || workspace_bytes < need) return NV4_E_SHAPE;
+    if (reinterpret_cast<uintptr_t>(workspace) % 8 || reinterpret_cast<uintptr_t>(q_norm_w) % 2 ||
+        reinterpret_cast<uintptr_t>(k_norm_w) % 2 || reinterpret_cast<uintptr_t>(cos_sin) % 4 ||
+        reinterpret_cast<uintptr_t>(positions) % 8 || reinterpret_cast<uintptr_t>(slot_mapping) % 4)
+        return NV4_E_ALIGN;
+    const QkvStep qs{static_cast<const uint16_t*>(q_norm_w), static_cast<const uint16_t*>(k_norm_w), cos_sin,
+                     positions, slot_mapping, static_cast<uint16_t*>(k_cache), static_cast<uint16_t*>(v_cache),
+                     max_position, num_slots, eps};
+    return pa_run(qkv, qkv_row_stride, k_cache, v_cache, block_tables, max_blocks, context_lens, out, workspace, B,
+                  Hq, Hkv, block_size, max_context, S, scale, &qs, stream);
 }

@@ -57,6 +57,9 @@ SIGNATURES = {
     "nv4_w4a16_dequant": ([_P, _P, _P, _P, _I, _I64, _I64, _I, _P], _I),
     "nv4_paged_decode_attention": ([_P, _I64, _P, _P, _P, _I64, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64,
                                     _I64, ctypes.c_float, _P], _I),
+    "nv4_paged_decode_attention_qkv": ([_P, _I64, _P, _P, _P, _I64, _P, _P, _I64, _P, _P, _P, _I64, _P, _P, _P,
+                                        _I64, _I64, _I64, _I64, _I64, _I64, _I64, ctypes.c_float, ctypes.c_float,
+                                        _P], _I),
     "nv4_paged_decode_attention_noalloc": ([_P, _I64, _P, _P, _P, _I64, _P, _P, _I64, _I64, _I64, _I64, _I64,
                                             _I64, ctypes.c_float, _P], _I),
     "nv4_rmsnorm": ([_P, _P, _P, _P, _P, _I64, _I64, ctypes.c_float, _P], _I),

@@ -16,7 +16,11 @@ of which this build uses:
   :64-70).
 * Decode: ``paged_decode_attention``, the HIP kernel ``nv4_paged_decode_attention``
   (split over the context, one workgroup per (sequence, KV head, split);
-  online softmax in fp32; a second pass merges the splits).
+  online softmax in fp32; a second pass merges the splits).  The decoder
+  calls ``paged_decode_attention_qkv`` (``Attention.decode_qkv``) instead:
+  the same kernel also takes the step's raw qkv rows, normalises and rotates
+  q and k itself and stores the step's key and value, so no separate
+  ``qk_norm_rope_store`` launch precedes it.
 """
 from __future__ import annotations
 
@@ -68,6 +72,63 @@ def paged_decode_attention(q, k_cache, v_cache, block_tables, context_lens, scal
             ctypes.c_void_p(workspace.data_ptr()), workspace.numel() * 4, B, Hq, Hkv, D, bs, max_context,
             ctypes.c_float(scale), ctypes.c_void_p(stream))
     _lib.check(rc, "paged_decode_attention")
+    return out
+
+
+def paged_decode_attention_qkv(qkv, num_heads, num_kv_heads, q_norm_w, k_norm_w, cos_sin, positions, slot_mapping,
+                               eps, k_cache, v_cache, block_tables, context_lens, scale, out=None, workspace=None,
+                               max_context=None):
+    """The decode step's q/k RMSNorm + rotary + KV store and the paged decode
+    attention in one launch (``nv4_paged_decode_attention_qkv``): the same
+    bits as ``qk_norm_rope_store`` followed by ``paged_decode_attention`` on
+    its q.  qkv bf16 [B, (Hq + 2 Hkv) * 128] (one token per sequence, rows may
+    be strided), positions int64 [B], slot_mapping int32 [B] -> [B, Hq, 128];
+    the step's keys and values are stored in the caches."""
+    B = qkv.shape[0]
+    D = 128
+    if qkv.dtype != torch.bfloat16 or qkv.ndim != 2 or qkv.stride(1) != 1:
+        raise TypeError("qkv must be BF16 [B, heads*128] with unit column stride")
+    if qkv.shape[1] != (num_heads + 2 * num_kv_heads) * D:
+        raise ValueError("qkv width does not match the head counts (head_dim 128)")
+    if cos_sin.dtype != torch.float32 or cos_sin.shape[-1] != D or not cos_sin.is_contiguous():
+        raise TypeError("cos_sin must be a contiguous FP32 [max_position, 128] table")
+    if positions.dtype != torch.int64 or tuple(positions.shape) != (B,):
+        raise TypeError("positions must be int64 [B]")
+    if slot_mapping.dtype != torch.int32 or tuple(slot_mapping.shape) != (B,):
+        raise TypeError("slot_mapping must be int32 [B]")
+    for w in (q_norm_w, k_norm_w):
+        if w.dtype != torch.bfloat16 or tuple(w.shape) != (D,) or not w.is_contiguous():
+            raise TypeError("q/k norm weights must be contiguous BF16 [128]")
+    nb, bs, Hkv, Dk = k_cache.shape
+    if k_cache.dtype != torch.bfloat16 or v_cache.dtype != torch.bfloat16:
+        raise TypeError("the caches must be BF16")
+    if (Dk != D or Hkv != num_kv_heads or v_cache.shape != k_cache.shape or not k_cache.is_contiguous()
+            or not v_cache.is_contiguous() or block_tables.dtype != torch.int32
+            or context_lens.dtype != torch.int32 or tuple(context_lens.shape) != (B,)
+            or block_tables.shape[0] != B):
+        raise ValueError("Inconsistent paged attention arguments")
+    dev = qkv.device
+    for t in (q_norm_w, k_norm_w, cos_sin, positions, slot_mapping, k_cache, v_cache, block_tables, context_lens):
+        if t.device != dev:
+            raise ValueError("all tensors must be on the device of qkv")
+    if max_context is None:
+        max_context = block_tables.shape[1] * bs
+    if out is None:
+        out = torch.empty((B, num_heads, D), dtype=torch.bfloat16, device=dev)
+    if workspace is None:
+        workspace = decode_workspace(B, num_heads, max_context, D, dev)
+    lib = _lib.load()
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    P = ctypes.c_void_p
+    with torch.cuda.device(dev):
+        rc = lib.nv4_paged_decode_attention_qkv(
+            P(qkv.data_ptr()), qkv.stride(0), P(q_norm_w.data_ptr()), P(k_norm_w.data_ptr()),
+            P(cos_sin.data_ptr()), cos_sin.numel() // D, P(positions.data_ptr()), P(slot_mapping.data_ptr()),
+            nb * bs, P(k_cache.data_ptr()), P(v_cache.data_ptr()), P(block_tables.data_ptr()),
+            block_tables.shape[1], P(context_lens.data_ptr()), P(out.data_ptr()), P(workspace.data_ptr()),
+            workspace.numel() * 4, B, num_heads, num_kv_heads, D, bs, max_context, ctypes.c_float(eps),
+            ctypes.c_float(scale), P(stream))
+    _lib.check(rc, "paged_decode_attention_qkv")
     return out
 
 
@@ -127,3 +188,12 @@ class Attention(nn.Module):
             return prefill_attention(q, k, v, ctx.seqlens_q, self.scale)
         return paged_decode_attention(q, self.k_cache, self.v_cache, ctx.block_tables, ctx.context_lens,
                                       self.scale, workspace=self.workspace, max_context=self.max_context)
+
+    def decode_qkv(self, qkv, q_norm_w, k_norm_w, cos_sin, positions, eps):
+        """Decode from the raw fused qkv rows: q/k norm, rotary, KV store and
+        attention in one launch (``paged_decode_attention_qkv``)."""
+        ctx = get_context()
+        return paged_decode_attention_qkv(qkv, self.num_heads, self.num_kv_heads, q_norm_w, k_norm_w, cos_sin,
+                                          positions, ctx.slot_mapping, eps, self.k_cache, self.v_cache,
+                                          ctx.block_tables, ctx.context_lens, self.scale, workspace=self.workspace,
+                                          max_context=self.max_context)

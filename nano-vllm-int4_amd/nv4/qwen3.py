@@ -158,6 +158,11 @@ class Qwen3Attention(nn.Module):
         elif qkv is None:
             qkv = self.qkv_proj(hidden_states)
         ctx = get_context()
+        if not ctx.is_prefill and self.attn.k_cache.numel() > 0:
+            # Decode: q/k RMSNorm + rotary + KV store inside the attention launch.
+            o = self.attn.decode_qkv(qkv, self.q_norm.weight, self.k_norm.weight, self.rotary_emb.cos_sin_cache,
+                                     positions, self.q_norm.eps)
+            return self.o_proj(o.flatten(1, -1))
         # q/k RMSNorm + rotary + KV-cache store in one launch; prefill also
         # needs the rotated keys and the values as tensors.
         out = qk_norm_rope_store(qkv, self.num_heads, self.num_kv_heads, self.q_norm.weight, self.k_norm.weight,

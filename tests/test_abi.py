@@ -208,6 +208,30 @@ def test_paged_decode_attention_rejections():
     assert call(q=P(A16 + 4)) == _lib.NV4_E_ALIGN
 
 
+def test_paged_decode_attention_qkv_rejections():
+    f = _lib.load().nv4_paged_decode_attention_qkv
+    # qkv, row, qw, kw, cos_sin, max_pos, positions, slots, num_slots, k, v, block_tables, max_blocks,
+    # context_lens, out, ws, ws_bytes, B, Hq, Hkv, D, bs, max_ctx, eps, scale, stream
+    def call(row=6144, qw=P(A16), cs=P(A16), pos=P(A16), slots=P(A16), ws=P(A16), max_pos=4096, num_slots=1 << 20,
+             ws_bytes=1 << 30, Hq=32, Hkv=8, max_ctx=4352, max_blocks=17):
+        return f(P(A16), row, qw, P(A16), cs, max_pos, pos, slots, num_slots, P(A16), P(A16), P(A16), max_blocks,
+                 P(A16), P(A16), ws, ws_bytes, 32, Hq, Hkv, 128, 256, max_ctx, 1e-6, 0.1, None)
+    assert call(qw=None) == _lib.NV4_E_NULL
+    assert call(cs=None) == _lib.NV4_E_NULL
+    assert call(pos=None) == _lib.NV4_E_NULL
+    assert call(slots=None) == _lib.NV4_E_NULL
+    assert call(ws=None) == _lib.NV4_E_NULL
+    assert call(row=4096 + 2048 - 8) == _lib.NV4_E_SHAPE      # row narrower than Hq + 2 Hkv heads
+    assert call(max_pos=0) == _lib.NV4_E_SHAPE
+    assert call(num_slots=-1) == _lib.NV4_E_SHAPE
+    assert call(ws_bytes=1000) == _lib.NV4_E_SHAPE
+    assert call(max_blocks=16) == _lib.NV4_E_SHAPE
+    assert call(Hq=64, row=(64 + 16) * 128) == _lib.NV4_E_SHAPE  # GQA group 8
+    assert call(cs=P(A16 + 2)) == _lib.NV4_E_ALIGN
+    assert call(pos=P(A16 + 4)) == _lib.NV4_E_ALIGN
+    assert call(qw=P(A16 + 1)) == _lib.NV4_E_ALIGN
+
+
 def test_paged_decode_attention_size_checks_do_not_wrap():
     """Sizes at the accepted maxima whose workspace size does not fit in int64
     (B * Hq * splits * 130 * 4 ~ 2^65) are rejected -- NV4_E_SHAPE for the
