@@ -86,21 +86,20 @@ __device__ __forceinline__ void wave_lds_order() {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 // The step's key (norm + rotary, by all four sixteen-lane groups alike) into
-// ko1 / ko2, and the value pair loaded by the caller: stored at the slot by
-// wave 3 (key) and wave 2 (value: lane (kq, rc) holds dims 8 rc .. 8 rc + 7)
-// when the slot is in [0, num_slots).
-__device__ __forceinline__ void kv_store(const QkvStep& qs, const Head16& kh, v4u vch, const v4f& c, const v4f& sn,
-                                         int64_t slot, bool slot_ok, int Hkv, int kvh, int wave, int lane,
-                                         uint2& ko1, uint2& ko2) {
+// ko1 / ko2, and the value chunk loaded by the caller (lane (kq, rc): dims
+// 8 rc .. 8 rc + 7); lanes 0-15 store the key (store_k) and the value
+// (store_v) at the slot.
+__device__ __forceinline__ void kv_step(const QkvStep& qs, const Head16& kh, v4u vch, const v4f& c, const v4f& sn,
+                                        int64_t slot, bool store_k, bool store_v, int Hkv, int kvh, int lane,
+                                        uint2& ko1, uint2& ko2) {
     const int j4 = (lane & 15) * 4;
     qk_head16(kh.xa, kh.xb, kh.wa, kh.wb, c, sn, qs.eps, ko1, ko2);
-    if (slot_ok && wave == 3 && lane < 16) {
+    if (store_k && lane < 16) {
         uint16_t* dst = qs.k_cache + (slot * Hkv + kvh) * PA_D;
         *reinterpret_cast<uint2*>(dst + j4) = ko1;
         *reinterpret_cast<uint2*>(dst + 64 + j4) = ko2;
     }
-    if (slot_ok && wave == 2 && lane < 16)
-        *reinterpret_cast<v4u*>(qs.v_cache + (slot * Hkv + kvh) * PA_D + 8 * lane) = vch;
+    if (store_v && lane < 16) *reinterpret_cast<v4u*>(qs.v_cache + (slot * Hkv + kvh) * PA_D + 8 * lane) = vch;
 }
 
 template <int G, bool BLK16, bool FUSED>
@@ -136,7 +135,8 @@ pa_split(const uint16_t* __restrict__ q, int64_t q_row, const uint16_t* kc, cons
                 const v4u vch =
                     *reinterpret_cast<const v4u*>(qrow + (int64_t)(Hq + Hkv + kvh) * PA_D + 8 * (lane & 15));
                 uint2 ko1, ko2;
-                kv_store(qs, kh, vch, c, sn, slot, slot_ok, Hkv, kvh, wave, lane, ko1, ko2);
+                kv_step(qs, kh, vch, c, sn, slot, slot_ok && wave == 3, slot_ok && wave == 2, Hkv, kvh, lane, ko1,
+                        ko2);
             }
         }
         // Nothing of this sequence here; pass 2 skips the split.  An empty
@@ -214,7 +214,8 @@ pa_split(const uint16_t* __restrict__ q, int64_t q_row, const uint16_t* kc, cons
     Head16 qh{}, kh;
     v4u vch;
     v4f c{}, sn{};
-    const int tl = ctx - 1;  // the last context token
+    const int tl = ctx - 1;                       // the last context token
+    const int w_last = (tl - start) >> 6;         // the wave holding it (kv_wg)
     bool subst = false;      // FUSED: see below
     if constexpr (FUSED) {
         // Ahead of the K and V loads, like q in the plain form: they arrive
@@ -257,9 +258,12 @@ pa_split(const uint16_t* __restrict__ q, int64_t q_row, const uint16_t* kc, cons
                 *reinterpret_cast<uint2*>(&sq[lane >> 4][64 + j4]) = o2;
             }
         }
-        if (kv_wg) {
+        // The wave holding the last context token computes and stores the
+        // step's key and value; only it needs the key (past the token every
+        // lane is masked out of the scores).
+        if (kv_wg && wave == w_last) {
             uint2 ko1, ko2;
-            kv_store(qs, kh, vch, c, sn, slot, slot_ok, Hkv, kvh, wave, lane, ko1, ko2);
+            kv_step(qs, kh, vch, c, sn, slot, slot_ok, slot_ok, Hkv, kvh, lane, ko1, ko2);
             if (lane < 16) {
                 *reinterpret_cast<uint2*>(&sq[G][j4]) = ko1;
                 *reinterpret_cast<uint2*>(&sq[G][64 + j4]) = ko2;
@@ -281,17 +285,19 @@ pa_split(const uint16_t* __restrict__ q, int64_t q_row, const uint16_t* kc, cons
     // block-table slot is the one just stored.
     v4u knew[4];
     if constexpr (FUSED) {
-        if (subst) {
+        if (subst && wave == w_last) {
 #pragma unroll
             for (int st = 0; st < 4; ++st)
                 knew[st] = *reinterpret_cast<const v4u*>(&s_qk[wave][G][8 * (kq + 4 * st)]);
         }
     }
+    // Waves past w_last take only the value (a finite one for the masked
+    // lanes, as the two-launch form reads there).
     auto take = [&](v4u (&kx)[8], v4u (&vx)[8], int h0) {
 #pragma unroll
         for (int cc = 0; cc < 2; ++cc) {
             const int t0 = h0 + 16 * cc;
-            if (t0 + rc >= tl)
+            if (wave == w_last && t0 + rc >= tl)
 #pragma unroll
                 for (int st = 0; st < 4; ++st) kx[4 * cc + st] = knew[st];
 #pragma unroll
@@ -378,9 +384,9 @@ pa_split(const uint16_t* __restrict__ q, int64_t q_row, const uint16_t* kc, cons
         }
     };
 
-    if (subst) take(ka, va, half0(0));
+    if (subst && wave >= w_last) take(ka, va, half0(0));
     compute(ka, va, half0(0));
-    if (subst) take(kb, vb, half0(1));
+    if (subst && wave >= w_last) take(kb, vb, half0(1));
     compute(kb, vb, half0(1));
 
     // Merge the four wave states of the workgroup.

@@ -41,8 +41,12 @@ __device__ __forceinline__ void qk_head16(uint2 xa, uint2 xb, uint2 wa, uint2 wb
     float ss = 0.0f;
 #pragma unroll
     for (int i = 0; i < 4; ++i) ss += x1[i] * x1[i] + x2[i] * x2[i];
-#pragma unroll
-    for (int off = 8; off >= 1; off >>= 1) ss += __shfl_xor(ss, off);
+    // xor steps 8, 4, 2, 1 as rotations inside the row of sixteen lanes (the
+    // same partners: see wave_sum).
+    ss += row_ror<0x128>(ss);
+    ss += row_ror<0x124>(ss);
+    ss += row_ror<0x122>(ss);
+    ss += row_ror<0x121>(ss);
     const float r = rsqrtf(ss / 128.0f + eps);
     uint32_t y1p[2], y2p[2];
 #pragma unroll
