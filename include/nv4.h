@@ -533,6 +533,14 @@ void nv4_philox4x32_10(const uint32_t* counter, const uint32_t* key, uint32_t* o
  */
 int nv4_probe_mfma(int kind, int64_t iters, int64_t workgroups, int* sink, void* stream);
 int nv4_probe_read(const void* buf, int64_t bytes, int* sink, void* stream);
+/*
+ * nv4_probe_bf16_rne: adds to *mismatches (a device counter the caller
+ * zeroes) the number of non-NaN fp32 inputs, out of all 2^32, whose bf16
+ * conversion by the kernels (the hardware instruction) differs from integer
+ * round-to-nearest-even.  No counterpart in the reference; it pins the
+ * rounding every bf16 output and intermediate of this library relies on.
+ */
+int nv4_probe_bf16_rne(unsigned long long* mismatches, void* stream);
 
 const char* nv4_version(void);
 

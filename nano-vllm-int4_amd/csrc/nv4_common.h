@@ -50,12 +50,21 @@ __device__ __forceinline__ void static_for(F&& f) {
 
 __device__ __forceinline__ float bf16_to_f32(uint32_t h) { return __uint_as_float(h << 16); }
 
-// fp32 -> bf16 bits, round to nearest even (NaN kept as a quiet NaN).
-__device__ __forceinline__ uint32_t f32_to_bf16_rne(float f) {
+// fp32 -> bf16 bits, round to nearest even, in integer arithmetic (NaN kept
+// as a quiet NaN).
+__device__ __forceinline__ uint32_t f32_to_bf16_rne_int(float f) {
     uint32_t u = __float_as_uint(f);
     if ((u & 0x7fffffffu) > 0x7f800000u) return (u >> 16) | 0x40u;
     u += 0x7fffu + ((u >> 16) & 1u);
     return u >> 16;
+}
+
+// fp32 -> bf16 bits, round to nearest even, by the hardware conversion
+// (v_cvt_pk_bf16_f32, one instruction): the bits of f32_to_bf16_rne_int for
+// every non-NaN input, denormals included (nv4_probe_bf16_rne checks all 2^32
+// inputs on the device); a NaN gives a quiet NaN.
+__device__ __forceinline__ uint32_t f32_to_bf16_rne(float f) {
+    return __builtin_bit_cast(uint16_t, (__bf16)f);
 }
 
 // Two packed signed nibbles per byte, even k in the low nibble.  Returns the

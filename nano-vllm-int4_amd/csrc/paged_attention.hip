@@ -449,6 +449,10 @@ pa_merge(const int32_t* __restrict__ context_lens, const float* __restrict__ par
 #pragma unroll
         for (int u = 0; u < SMAX; ++u)
             v[u] = *reinterpret_cast<const float2*>(part_o + (base + min(u, S - 1)) * PA_D + 2 * lane);
+        // Every row is used only under u < n below; without these pins the
+        // compiler may move each load into its branch, one round trip per row.
+#pragma unroll
+        for (int u = 0; u < SMAX; ++u) asm volatile("" : "+v"(v[u].x), "+v"(v[u].y));
         const int n = min(S, (min(clen, max_ctx) + PA_SPLIT - 1) / PA_SPLIT);
         const float ms = lane < n ? ml.x : -__builtin_inff(), ls = lane < n ? ml.y : 0.0f;
         float M = ms;

@@ -74,8 +74,33 @@ probe_read(const v4u* __restrict__ p, int* __restrict__ sink) {
     if (v == 0x89abcdefu) sink[blockIdx.x & 1023] = (int)v;
 }
 
+// Every fp32 bit pattern (two per thread and step, grid-stride): the
+// library's hardware bf16 conversion against the integer round-to-nearest-
+// even, NaN inputs skipped; mismatches are counted into *bad.
+__global__ void __launch_bounds__(256)
+probe_bf16_rne(unsigned long long* __restrict__ bad) {
+    const uint64_t n = (uint64_t)gridDim.x * 256;
+    unsigned long long nbad = 0;
+    for (uint64_t i = ((uint64_t)blockIdx.x * 256 + threadIdx.x) * 2; i < (1ull << 32); i += 2 * n) {
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+            const uint32_t u = (uint32_t)(i + k);
+            const float f = __uint_as_float(u);
+            if ((u & 0x7fffffffu) <= 0x7f800000u && f32_to_bf16_rne(f) != f32_to_bf16_rne_int(f)) ++nbad;
+        }
+    }
+    if (nbad) atomicAdd(bad, nbad);
+}
+
 }  // namespace
 }  // namespace nv4
+
+extern "C" int nv4_probe_bf16_rne(unsigned long long* mismatches, void* stream) {
+    using namespace nv4;
+    if (!mismatches) return NV4_E_NULL;
+    hipLaunchKernelGGL(probe_bf16_rne, dim3(8192), dim3(256), 0, static_cast<hipStream_t>(stream), mismatches);
+    return (int)hipGetLastError();
+}
 
 extern "C" int nv4_probe_mfma(int kind, int64_t iters, int64_t workgroups, int* sink, void* stream) {
     using namespace nv4;

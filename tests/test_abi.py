@@ -351,6 +351,7 @@ def test_probe_rejections():
     lib = _lib.load()
     sink = P(A16)
     assert lib.nv4_probe_mfma(0, 10, 8, None, None) == _lib.NV4_E_NULL
+    assert lib.nv4_probe_bf16_rne(None, None) == _lib.NV4_E_NULL
     assert lib.nv4_probe_mfma(3, 10, 8, sink, None) == _lib.NV4_E_SHAPE        # unknown kind
     assert lib.nv4_probe_mfma(-1, 10, 8, sink, None) == _lib.NV4_E_SHAPE
     assert lib.nv4_probe_mfma(1, 0, 8, sink, None) == _lib.NV4_E_SHAPE         # no rounds
