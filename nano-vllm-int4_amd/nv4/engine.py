@@ -23,6 +23,7 @@ from __future__ import annotations
 import math
 import time
 
+import numpy as np
 import torch
 
 from .attention import decode_workspace
@@ -128,6 +129,7 @@ class Engine:
             max_num_seqs, self.blocks_per_seq)
         self.graphs: dict[int, torch.cuda.CUDAGraph] = {}
         self.graph_vars: dict[str, torch.Tensor] = {}
+        self._stage: dict[int, dict] = {}
         self.sampler = Sampler()
 
     def model_bytes(self) -> int:
@@ -174,28 +176,53 @@ class Engine:
         reset_context()
         return token
 
+    def _staging(self, bs: int) -> dict:
+        """The decode inputs of batch size ``bs`` in one pinned host buffer and
+        its device twin, so a step moves them in one copy: int64 input_ids
+        [bs] and positions [bs], then int32 context_lens [bs] and slot_mapping
+        [bs].  The device views are the captured graph's static inputs; the
+        block tables stay in place until the step's sequence slots change."""
+        st = self._stage.get(bs)
+        if st is None:
+            host = torch.empty(3 * bs, dtype=torch.int64, pin_memory=True)
+            dev = torch.zeros(3 * bs, dtype=torch.int64, device=self.device)
+            i32 = dev[2 * bs:].view(torch.int32)
+            i32[:bs].fill_(1)  # a valid context for the capture's warm-up forward
+            st = {"host": host, "np": host.numpy(), "dev": dev, "input_ids": dev[:bs], "positions": dev[bs:2 * bs],
+                  "context_lens": i32[:bs], "slot_mapping": i32[bs:], "block_tables": self.block_tables[:bs].clone(),
+                  "slots": tuple(range(bs)), "copied": torch.cuda.Event()}
+            st["copied"].record(torch.cuda.current_stream(self.device))
+            self._stage[bs] = st
+        return st
+
     def _set_decode_inputs(self, seq_slots, last_tokens, lengths):
         bs = len(seq_slots)
         if len(last_tokens) != bs or len(lengths) != bs or bs < 1:
             raise ValueError("decode needs one last token and one length per sequence slot")
         self._check_fits(seq_slots, lengths)
-        input_ids = self._to_dev(last_tokens, torch.int64)
-        positions = self._to_dev([n - 1 for n in lengths], torch.int64)
-        context_lens = self._to_dev(lengths, torch.int32)
-        slot_mapping = self._to_dev([self._slots(s, n - 1, n)[0] for s, n in zip(seq_slots, lengths)], torch.int32)
-        block_tables = self.block_tables[torch.tensor(seq_slots, device=self.device)] if list(seq_slots) != list(
-            range(bs)) else self.block_tables[:bs]
-        return input_ids, positions, context_lens, slot_mapping, block_tables
+        st = self._staging(bs)
+        st["copied"].synchronize()  # the previous step's copy has read the host buffer
+        h = st["np"]
+        n = np.asarray(lengths, dtype=np.int64)
+        h[:bs] = last_tokens
+        h[bs:2 * bs] = n - 1
+        h32 = h[2 * bs:].view(np.int32)
+        h32[:bs] = n
+        h32[bs:] = np.asarray(seq_slots, dtype=np.int64) * (self.blocks_per_seq * self.block_size) + n - 1
+        st["dev"].copy_(st["host"], non_blocking=True)
+        st["copied"].record(torch.cuda.current_stream(self.device))
+        slots = tuple(int(s) for s in seq_slots)
+        if slots != st["slots"]:
+            st["block_tables"].copy_(self.block_tables[torch.tensor(slots, device=self.device)])
+            st["slots"] = slots
+        return st["input_ids"], st["positions"], st["context_lens"], st["slot_mapping"], st["block_tables"]
 
     @torch.inference_mode()
     def capture(self, bs: int) -> None:
         """Capture the decode forward (model only, as the reference does) for
         batch size ``bs`` with static input buffers."""
-        gv = {"input_ids": torch.zeros(bs, dtype=torch.int64, device=self.device),
-              "positions": torch.zeros(bs, dtype=torch.int64, device=self.device),
-              "slot_mapping": torch.zeros(bs, dtype=torch.int32, device=self.device),
-              "context_lens": torch.ones(bs, dtype=torch.int32, device=self.device),
-              "block_tables": self.block_tables[:bs].clone()}
+        st = self._staging(bs)
+        gv = {k: st[k] for k in ("input_ids", "positions", "slot_mapping", "context_lens", "block_tables")}
         set_context(False, slot_mapping=gv["slot_mapping"], context_lens=gv["context_lens"],
                     block_tables=gv["block_tables"])
         side = torch.cuda.Stream(self.device)
@@ -221,13 +248,8 @@ class Engine:
         if eager or bs not in self.graphs:
             set_context(False, slot_mapping=slot_mapping, context_lens=context_lens, block_tables=block_tables)
             hidden = self.model(input_ids, positions)
-        else:
+        else:  # the inputs already sit in the graph's static buffers
             gv = self.graph_vars[bs]
-            gv["input_ids"].copy_(input_ids)
-            gv["positions"].copy_(positions)
-            gv["slot_mapping"].copy_(slot_mapping)
-            gv["context_lens"].copy_(context_lens)
-            gv["block_tables"].copy_(block_tables)
             self.graphs[bs].replay()
             hidden = gv["outputs"]
             set_context(False)
