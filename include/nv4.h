@@ -69,6 +69,9 @@
  *                          SiluAndMul (nanovllm/models/qwen3.py:125-129,
  *                          nanovllm/layers/activation.py:8-11) in one launch, for
  *                          decode-sized M (no counterpart call in the reference)
+ *   nv4_lm_head         <- F.linear of ParallelLMHead.forward,
+ *                          nanovllm/layers/embed_head.py:56-61 (decode-sized M; caller of
+ *                          the hot path)
  *   nv4_paged_decode_attention_qkv <- the decode step's q_norm/k_norm +
  *                          rotary_emb + store_kvcache + flash_attn_with_kvcache
  *                          (nanovllm/models/qwen3.py:78-94,
@@ -452,6 +455,18 @@ int nv4_qk_norm_rope_store(const void* qkv, int64_t qkv_row_stride, int64_t T, i
                            const void* q_norm_w, const void* k_norm_w, const float* cos_sin, int64_t max_position,
                            const int64_t* positions, const int32_t* slot_mapping, int64_t num_slots, void* q_out,
                            void* k_cache, void* v_cache, void* k_out, void* v_out, float eps, void* stream);
+
+/*
+ * LM head for decode-sized batches: out[M, N] = bf16(h[M, K] . w[N, K]^T), fp32
+ * sums (replaces ParallelLMHead.forward's F.linear, nanovllm/layers/embed_head.py:56-61,
+ * for M <= 32 rows).  h bf16 rows h_row_stride elements apart (a multiple of 8),
+ * w bf16 [N, K] contiguous, out bf16 rows out_row_stride apart; h and w 16-byte
+ * aligned.  1 <= M <= 32, K in {2048, 4096, 5120}, 1 <= N <= 2^30.  The sum
+ * order is fixed (four K-quarters added in order), so results repeat bit for
+ * bit; they may differ from another library's GEMM in the last bits.
+ */
+int nv4_lm_head(const void* h, int64_t h_row_stride, const void* w, void* out, int64_t out_row_stride, int64_t M,
+                int64_t N, int64_t K, void* stream);
 
 /*
  * SiLU-and-mul (nanovllm/layers/activation.py:8-11): gate_up bf16 [rows, 2*I]

@@ -75,6 +75,7 @@ SIGNATURES = {
     "nv4_probe_mfma": ([_I, _I64, _I64, _P, _P], _I),
     "nv4_probe_read": ([_P, _I64, _P, _P], _I),
     "nv4_probe_bf16_rne": ([_P, _P], _I),
+    "nv4_lm_head": ([_P, _I64, _P, _P, _I64, _I64, _I64, _I64, _P], _I),
     "nv4_version": ([], ctypes.c_char_p),
     "nv4_strerror": ([_I], ctypes.c_char_p),
 }

@@ -108,6 +108,41 @@ def qk_norm_rope_store(qkv, num_heads, num_kv_heads, q_norm_w, k_norm_w, cos_sin
     return (q, k, v) if return_kv else q
 
 
+LM_HEAD_MAX_ROWS = 32
+LM_HEAD_K = (2048, 4096, 5120)
+
+
+def lm_head_fits(h, weight) -> bool:
+    """Whether ``lm_head`` takes this call (decode-sized rows, a supported
+    hidden size, bf16, 16-byte aligned rows); otherwise use F.linear."""
+    return (h.ndim == 2 and weight.ndim == 2 and 1 <= h.shape[0] <= LM_HEAD_MAX_ROWS and h.shape[1] in LM_HEAD_K
+            and weight.shape[1] == h.shape[1] and h.dtype == torch.bfloat16 and weight.dtype == torch.bfloat16
+            and h.stride(1) == 1 and h.stride(0) % 8 == 0 and weight.is_contiguous()
+            and h.data_ptr() % 16 == 0 and weight.data_ptr() % 16 == 0 and h.is_cuda and h.device == weight.device)
+
+
+def lm_head(h, weight, out=None):
+    """logits = h @ weight^T (ParallelLMHead's F.linear,
+    nanovllm/layers/embed_head.py:56-61) for M <= 32 rows: h bf16 [M, K],
+    weight bf16 [N, K] -> bf16 [M, N], fp32 sums (``nv4_lm_head``)."""
+    if not lm_head_fits(h, weight):
+        raise ValueError("lm_head takes bf16 h [M <= 32, K in (2048, 4096, 5120)] and a contiguous weight [N, K]")
+    M, K = h.shape
+    N = weight.shape[0]
+    if out is None:
+        out = torch.empty((M, N), dtype=torch.bfloat16, device=h.device)
+    elif (out.dtype != torch.bfloat16 or tuple(out.shape) != (M, N) or out.stride(1) != 1
+          or out.device != h.device):
+        raise ValueError("out must be bf16 [M, N] with unit column stride on the device of h")
+    lib = _lib.load()
+    stream = torch.cuda.current_stream(h.device).cuda_stream
+    with torch.cuda.device(h.device):
+        rc = lib.nv4_lm_head(_ptr(h), h.stride(0), _ptr(weight), _ptr(out), out.stride(0), M, N, K,
+                             ctypes.c_void_p(stream))
+    _lib.check(rc, "lm_head")
+    return out
+
+
 def silu_mul(gate_up, out=None):
     """gate_up bf16 [..., 2I] -> bf16 [..., I] = silu(gate) * up."""
     I2 = gate_up.shape[-1]

@@ -44,8 +44,8 @@ import torch.nn.functional as F
 from torch import nn
 
 from .attention import Attention
-from .kernels.decoder_ops import (qk_norm_rope_store, rmsnorm, rmsnorm_rht_quant_pack, silu_mul,
-                                  silu_mul_rht_quant_pack)
+from .kernels.decoder_ops import (lm_head, lm_head_fits, qk_norm_rope_store, rmsnorm, rmsnorm_rht_quant_pack,
+                                  silu_mul, silu_mul_rht_quant_pack)
 from .kernels.rht_a4 import rht_quant_pack_rowtiled
 from .layers.linear_w4a4 import W4A4Linear
 from .layers.linear_w4a16 import W4A16Linear, fuse_w4a16
@@ -303,6 +303,8 @@ class Qwen3ForCausalLM(nn.Module):
         ctx = get_context()
         if ctx.is_prefill and ctx.cu_seqlens_q is not None:
             hidden_states = hidden_states[ctx.cu_seqlens_q[1:] - 1].contiguous()
+        if lm_head_fits(hidden_states, self.lm_head.weight):  # decode-sized: one HIP launch
+            return lm_head(hidden_states, self.lm_head.weight)
         return F.linear(hidden_states, self.lm_head.weight)
 
 

@@ -208,6 +208,24 @@ def test_paged_decode_attention_rejections():
     assert call(q=P(A16 + 4)) == _lib.NV4_E_ALIGN
 
 
+def test_lm_head_rejections():
+    f = _lib.load().nv4_lm_head
+    def call(h=P(A16), w=P(A16), out=P(A16), h_row=4096, out_row=151936, M=32, N=151936, K=4096):
+        return f(h, h_row, w, out, out_row, M, N, K, None)
+    assert call(h=None) == _lib.NV4_E_NULL
+    assert call(w=None) == _lib.NV4_E_NULL
+    assert call(out=None) == _lib.NV4_E_NULL
+    assert call(M=0) == _lib.NV4_E_SHAPE
+    assert call(M=33) == _lib.NV4_E_SHAPE
+    assert call(K=3072, h_row=3072) == _lib.NV4_E_SHAPE     # unsupported hidden size
+    assert call(h_row=4000) == _lib.NV4_E_SHAPE             # rows narrower than K
+    assert call(out_row=100) == _lib.NV4_E_SHAPE
+    assert call(N=0) == _lib.NV4_E_SHAPE
+    assert call(h=P(A16 + 8)) == _lib.NV4_E_ALIGN
+    assert call(w=P(A16 + 2)) == _lib.NV4_E_ALIGN
+    assert call(h_row=4100) == _lib.NV4_E_ALIGN
+
+
 def test_paged_decode_attention_qkv_rejections():
     f = _lib.load().nv4_paged_decode_attention_qkv
     # qkv, row, qw, kw, cos_sin, max_pos, positions, slots, num_slots, k, v, block_tables, max_blocks,
