@@ -41,6 +41,7 @@ namespace {
 constexpr int PA_D = 128;        // head dim
 constexpr int PA_SPLIT = 256;    // context tokens per pass-1 workgroup
 constexpr int PA_THREADS = 256;  // 4 waves x 64 tokens
+constexpr int PA_KT_ROW = 272;   // bytes per K row in the transposing LDS buffer
 
 typedef __bf16 v2bf __attribute__((ext_vector_type(2)));
 typedef float v2f __attribute__((ext_vector_type(2)));
@@ -152,12 +153,15 @@ pa_split(const uint16_t* __restrict__ q, int64_t q_row, const uint16_t* kc, cons
 
     __shared__ float sm_m[4][G], sm_l[4][G];
     __shared__ float sm_o[4][G][PA_D];
+    // Per wave: one half's K rows (2 runs x 16 tokens) on their way to the
+    // operand layout.
+    __shared__ __align__(16) uint8_t s_kt[4][2 * 16 * PA_KT_ROW];
     // FUSED: per wave, the G normalised, rotated q heads, then the step's key.
     __shared__ __align__(16) uint16_t s_qk[FUSED ? 4 : 1][G + 1][PA_D];
 
     const int32_t* bt = block_tables + (int64_t)b * max_blocks;
     const uint32_t row = (uint32_t)Hkv * PA_D;  // elements between consecutive slots
-    const uint16_t* kbase = kc + kvh * PA_D + 8 * kq;
+    const uint16_t* kbase = kc + kvh * PA_D + 8 * rc;
     const uint16_t* vbase = vc + kvh * PA_D + 8 * rc;
     // First token of half hh (32 tokens) of this wave; a half is two 16-token
     // runs, 16-aligned.
@@ -183,18 +187,21 @@ pa_split(const uint16_t* __restrict__ q, int64_t q_row, const uint16_t* kc, cons
             return (uint32_t)(bt[c / bs] * bs + c % bs);
     };
     // Loads of one half (non-temporal: each K/V byte is read once per step;
-    // 2 % faster than plain loads at bs32 x 4.1k tokens).  K, as the A
-    // operand of the score MFMA: lane (kq, rc)
-    // holds 16-byte chunks kq, kq+4, kq+8, kq+12 of token h0 + 16c + rc.  V,
-    // as rows: lane (kq, rc) holds chunk rc of tokens h0 + 16c + 4kq + r.
+    // 2 % faster than plain loads at bs32 x 4.1k tokens).  K and V alike, as
+    // rows: lane (kq, rc) holds chunk rc (16 bytes) of tokens h0 + 16c + 4kq
+    // + r, so every instruction reads four whole 256-byte rows (K read as
+    // 16 tokens x 64 bytes per instruction, in the operand order, streamed
+    // at 5.2 against 7.0 TB/s for whole rows).  k_operand then turns K into
+    // the A operand of the score MFMA through LDS: lane (kq, rc) holds chunks
+    // kq, kq+4, kq+8, kq+12 of token h0 + 16c + rc.
     auto issue = [&](v4u (&kx)[8], v4u (&vx)[8], const Run& r0, const Run& r1) {
 #pragma unroll
         for (int c = 0; c < 2; ++c) {
             const Run& r = c ? r1 : r0;
-            const uint16_t* pk = kbase + (uint64_t)slot_of(r, rc) * row;
 #pragma unroll
-            for (int st = 0; st < 4; ++st)
-                kx[4 * c + st] = __builtin_nontemporal_load(reinterpret_cast<const v4u*>(pk + 32 * st));
+            for (int i = 0; i < 4; ++i)
+                kx[4 * c + i] =
+                    __builtin_nontemporal_load(reinterpret_cast<const v4u*>(kbase + (uint64_t)slot_of(r, 4 * kq + i) * row));
         }
 #pragma unroll
         for (int c = 0; c < 2; ++c) {
@@ -204,6 +211,24 @@ pa_split(const uint16_t* __restrict__ q, int64_t q_row, const uint16_t* kc, cons
                 vx[4 * c + i] =
                     __builtin_nontemporal_load(reinterpret_cast<const v4u*>(vbase + (uint64_t)slot_of(r, 4 * kq + i) * row));
         }
+    };
+    // Row-layout K of one half -> A-operand layout, through this wave's LDS
+    // rows (272-byte stride: the transposed reads spread over the banks).
+    // LDS accesses of one wave run in order, so the next half may reuse them.
+    uint8_t* kt = reinterpret_cast<uint8_t*>(s_kt[wave]);
+    auto k_operand = [&](v4u (&kx)[8]) {
+        wave_lds_order();
+#pragma unroll
+        for (int c = 0; c < 2; ++c)
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                *reinterpret_cast<v4u*>(kt + c * 16 * PA_KT_ROW + (4 * kq + i) * PA_KT_ROW + 16 * rc) = kx[4 * c + i];
+        wave_lds_order();
+#pragma unroll
+        for (int c = 0; c < 2; ++c)
+#pragma unroll
+            for (int st = 0; st < 4; ++st)
+                kx[4 * c + st] = *reinterpret_cast<const v4u*>(kt + c * 16 * PA_KT_ROW + rc * PA_KT_ROW + 16 * (kq + 4 * st));
     };
 
     // B operand of the score MFMA: q of head rc (zero past the group's G
@@ -388,8 +413,10 @@ pa_split(const uint16_t* __restrict__ q, int64_t q_row, const uint16_t* kc, cons
         }
     };
 
+    k_operand(ka);
     if (subst && wave >= w_last) take(ka, va, half0(0));
     compute(ka, va, half0(0));
+    k_operand(kb);
     if (subst && wave >= w_last) take(kb, vb, half0(1));
     compute(kb, vb, half0(1));
 
