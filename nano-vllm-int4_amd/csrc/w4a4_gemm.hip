@@ -402,7 +402,7 @@ constexpr int WIDE_A_BYTES = 128 * 1024;  // widened activation block limit (M x
 constexpr int WIDE_SCALES = 1024;         // G * ROWS limit
 constexpr int WIDE_WSCALES = 3072;        // G * CBW * 16 limit
 
-template <int MB, int CBW, int D, bool TW, bool RT, bool SW_GROUPED, bool OUT_F32, bool PAIR = false>
+template <int MB, int CBW, int D, bool TW, bool RT, bool SW_GROUPED, bool OUT_F32, bool PAIR = false, int GC = 0>
 __global__ void __launch_bounds__(CBW * MB * 64)
 k2_wide(const int8_t* __restrict__ a, const int8_t* __restrict__ w,
         const uint16_t* __restrict__ sa, const uint16_t* __restrict__ sw,
@@ -421,8 +421,10 @@ k2_wide(const int8_t* __restrict__ a, const int8_t* __restrict__ w,
     const int t = threadIdx.x;
     const int lane = t & 63, wave = t >> 6;
     const int cbl = wave / MB, mb = wave % MB;  // local column block, row block
-    const int G = K >> 7;
-    const int KB = K >> 1;
+    // GC > 0: K = 128 GC known at compile time, so the prologue's divisions
+    // by G (chunk and scale indices) become shifts and multiplies.
+    const int G = GC > 0 ? GC : K >> 7;
+    const int KB = G * 64;
     const int chunks_row = KB >> 4;             // packed 16-byte chunks per row
     const int a_chunks = ROWS * chunks_row;
     const int rc = lane & 15, part = lane >> 4;
@@ -692,9 +694,15 @@ hipError_t launch_wide_cbw(const int8_t* a, const int8_t* w, const void* sa, con
     constexpr int D = 8;  // groups in flight per wave
     // PAIR: CBW/2 output blocks of 16 (gate and up block each) per workgroup.
     const int nb = PAIR ? N / 32 : (N + 15) / 16, per = PAIR ? CBW / 2 : CBW;
-    hipLaunchKernelGGL((k2_wide<MB, CBW, D, TW, RT, SG, OF, PAIR>), dim3((unsigned)((nb + per - 1) / per)),
-                       dim3(CBW * MB * 64), 0, st, a, w, static_cast<const uint16_t*>(sa),
-                       static_cast<const uint16_t*>(sw), out, M, N, K);
+    const dim3 grid((unsigned)((nb + per - 1) / per)), block(CBW * MB * 64);
+    const auto* sap = static_cast<const uint16_t*>(sa);
+    const auto* swp = static_cast<const uint16_t*>(sw);
+    if (K == 4096)  // the decoder's hidden size: group count known at compile time
+        hipLaunchKernelGGL((k2_wide<MB, CBW, D, TW, RT, SG, OF, PAIR, 32>), grid, block, 0, st, a, w, sap, swp, out,
+                           M, N, K);
+    else
+        hipLaunchKernelGGL((k2_wide<MB, CBW, D, TW, RT, SG, OF, PAIR>), grid, block, 0, st, a, w, sap, swp, out, M,
+                           N, K);
     return hipGetLastError();
 }
 
