@@ -85,21 +85,21 @@ struct RowRms {
 struct Prefetch {
     const int8_t* p = nullptr;
     int64_t bytes = 0;  // a multiple of 16
-    int rows = 0;       // workgroups 0..rows-1 run K1, the others prefetch
 };
 constexpr int PF_LOADS = 8;  // 16-byte loads per thread of a prefetch workgroup
 
-// True for a prefetch workgroup (which has then issued its loads).  The loads
-// are unconditional (offsets clamped into the buffer), so none waits alone.
+// True for a prefetch workgroup, one past the `rows` K1 workgroups (which has
+// then issued its loads).  The loads are unconditional (offsets clamped into
+// the buffer), so none waits alone.
 template <int T>
-__device__ __forceinline__ bool prefetch_tail(const Prefetch& pf) {
-    if ((int)blockIdx.x < pf.rows) return false;
-    const int64_t base = (int64_t)(blockIdx.x - pf.rows) * (T * 16 * PF_LOADS);
+__device__ __forceinline__ bool prefetch_tail(int rows, const int8_t* __restrict__ p, int64_t bytes) {
+    if ((int)blockIdx.x < rows) return false;
+    const int64_t base = (int64_t)(blockIdx.x - rows) * (T * 16 * PF_LOADS);
     v4u v[PF_LOADS];
 #pragma unroll
     for (int i = 0; i < PF_LOADS; ++i) {
-        const int64_t off = min(base + (int64_t)(i * T + threadIdx.x) * 16, pf.bytes - 16);
-        v[i] = *reinterpret_cast<const v4u*>(pf.p + off);
+        const int64_t off = min(base + (int64_t)(i * T + threadIdx.x) * 16, bytes - 16);
+        v[i] = *reinterpret_cast<const v4u*>(p + off);
     }
     __builtin_amdgcn_sched_barrier(0);  // all loads in flight before the first use
     v4u acc = v[0];
@@ -129,26 +129,32 @@ __device__ __forceinline__ void k1_k4096_body(const Src& src, const int8_t* __re
                packed_dst<RT>(packed, row, threadIdx.x, 4096), scale + row * 32, buf);
 }
 
+// The K1 kernels take plain scalars and pointers, the row count and the
+// row's inputs first: the first 14 argument dwords are preloaded into SGPRs
+// when the waves launch (a struct argument would end the preload there), so
+// a row's loads issue without a round trip to the kernel-argument buffer.
+// The prefetch workgroups' arguments come last and are loaded as usual.
 template <class Src, bool RT>
 __global__ void __launch_bounds__(K4_THREADS)
-k1_k4096(Src src, const int8_t* __restrict__ signs, int8_t* __restrict__ packed, uint16_t* __restrict__ scale,
-         Prefetch pf) {
+k1_k4096(int rows, const uint16_t* __restrict__ src_p, const int8_t* __restrict__ signs,
+         int8_t* __restrict__ packed, uint16_t* __restrict__ scale, const int8_t* __restrict__ pf_p,
+         int64_t pf_bytes) {
     __shared__ float buf[K4_LDS];
-    if (prefetch_tail<K4_THREADS>(pf)) return;
-    k1_k4096_body<RT>(src, signs, packed, scale, buf);
+    if (prefetch_tail<K4_THREADS>(rows, pf_p, pf_bytes)) return;
+    k1_k4096_body<RT>(Src{src_p, 4096}, signs, packed, scale, buf);
 }
 
 // add + RMSNorm in front: the norm weights are loaded ahead of the row.
 template <bool RESID, bool RT>
 __global__ void __launch_bounds__(K4_THREADS)
-k1_k4096_rms(RowRms<RESID> src, const uint16_t* __restrict__ nw, const int8_t* __restrict__ signs,
-             int8_t* __restrict__ packed, uint16_t* __restrict__ scale, Prefetch pf) {
+k1_k4096_rms(int rows, float eps, const uint16_t* x, const uint16_t* res_in, uint16_t* res_out,
+             const uint16_t* __restrict__ nw, const int8_t* __restrict__ signs, int8_t* __restrict__ packed,
+             uint16_t* __restrict__ scale, const int8_t* __restrict__ pf_p, int64_t pf_bytes) {
     __shared__ float buf[K4_LDS];
     __shared__ float red[4];
-    if (prefetch_tail<K4_THREADS>(pf)) return;
-    src.w0 = *reinterpret_cast<const v4u*>(nw + 16 * threadIdx.x);
-    src.w1 = *reinterpret_cast<const v4u*>(nw + 16 * threadIdx.x + 8);
-    src.red = red;
+    if (prefetch_tail<K4_THREADS>(rows, pf_p, pf_bytes)) return;
+    const RowRms<RESID> src{x, res_in, res_out, eps, *reinterpret_cast<const v4u*>(nw + 16 * threadIdx.x),
+                            *reinterpret_cast<const v4u*>(nw + 16 * threadIdx.x + 8), red};
     k1_k4096_body<RT>(src, signs, packed, scale, buf);
 }
 
@@ -157,10 +163,12 @@ k1_k4096_rms(RowRms<RESID> src, const uint16_t* __restrict__ nw, const int8_t* _
 // repeat the row's last 16 columns, so that every load is unconditional.
 template <class Src, bool RT>
 __global__ void __launch_bounds__(K12_THREADS)
-k1_k12288(Src src, const int8_t* __restrict__ signs, int8_t* __restrict__ packed, uint16_t* __restrict__ scale,
-          Prefetch pf) {
+k1_k12288(int rows, const uint16_t* __restrict__ src_p, const int8_t* __restrict__ signs,
+          int8_t* __restrict__ packed, uint16_t* __restrict__ scale, const int8_t* __restrict__ pf_p,
+          int64_t pf_bytes) {
     __shared__ float buf[K12_LDS];
-    if (prefetch_tail<K12_THREADS>(pf)) return;
+    if (prefetch_tail<K12_THREADS>(rows, pf_p, pf_bytes)) return;
+    const Src src{src_p, 12288};
     const v4u sv = k1_signs12288(signs);
     const int64_t row = blockIdx.x;
     const int c0 = 16 * min((int)threadIdx.x, 767);
@@ -171,40 +179,42 @@ k1_k12288(Src src, const int8_t* __restrict__ signs, int8_t* __restrict__ packed
 }
 
 template <class Src>
-hipError_t launch_k4096(const Src& src, const int8_t* signs, int8_t* packed, uint16_t* scale, int M, bool rt,
+hipError_t launch_k4096(const uint16_t* src_p, const int8_t* signs, int8_t* packed, uint16_t* scale, int M, bool rt,
                         Prefetch pf, hipStream_t st) {
-    pf.rows = M;
     const dim3 grid(prefetch_grid(M, pf, K4_THREADS));
     if (rt)
-        hipLaunchKernelGGL((k1_k4096<Src, true>), grid, dim3(K4_THREADS), 0, st, src, signs, packed, scale, pf);
+        hipLaunchKernelGGL((k1_k4096<Src, true>), grid, dim3(K4_THREADS), 0, st, M, src_p, signs, packed, scale,
+                           pf.p, pf.bytes);
     else
-        hipLaunchKernelGGL((k1_k4096<Src, false>), grid, dim3(K4_THREADS), 0, st, src, signs, packed, scale, pf);
+        hipLaunchKernelGGL((k1_k4096<Src, false>), grid, dim3(K4_THREADS), 0, st, M, src_p, signs, packed, scale,
+                           pf.p, pf.bytes);
     return hipGetLastError();
 }
 
 template <class Src>
-hipError_t launch_k12288(const Src& src, const int8_t* signs, int8_t* packed, uint16_t* scale, int M, bool rt,
-                         Prefetch pf, hipStream_t st) {
-    pf.rows = M;
+hipError_t launch_k12288(const uint16_t* src_p, const int8_t* signs, int8_t* packed, uint16_t* scale, int M,
+                         bool rt, Prefetch pf, hipStream_t st) {
     const dim3 grid(prefetch_grid(M, pf, K12_THREADS));
     if (rt)
-        hipLaunchKernelGGL((k1_k12288<Src, true>), grid, dim3(K12_THREADS), 0, st, src, signs, packed, scale, pf);
+        hipLaunchKernelGGL((k1_k12288<Src, true>), grid, dim3(K12_THREADS), 0, st, M, src_p, signs, packed, scale,
+                           pf.p, pf.bytes);
     else
-        hipLaunchKernelGGL((k1_k12288<Src, false>), grid, dim3(K12_THREADS), 0, st, src, signs, packed, scale, pf);
+        hipLaunchKernelGGL((k1_k12288<Src, false>), grid, dim3(K12_THREADS), 0, st, M, src_p, signs, packed, scale,
+                           pf.p, pf.bytes);
     return hipGetLastError();
 }
 
 template <bool RESID>
-hipError_t launch_rms4096(const RowRms<RESID>& src, const uint16_t* nw, const int8_t* signs, int8_t* packed,
-                          uint16_t* scale, int M, bool rt, Prefetch pf, hipStream_t st) {
-    pf.rows = M;
+hipError_t launch_rms4096(const uint16_t* x, const uint16_t* res_in, uint16_t* res_out, float eps,
+                          const uint16_t* nw, const int8_t* signs, int8_t* packed, uint16_t* scale, int M, bool rt,
+                          Prefetch pf, hipStream_t st) {
     const dim3 grid(prefetch_grid(M, pf, K4_THREADS));
     if (rt)
-        hipLaunchKernelGGL((k1_k4096_rms<RESID, true>), grid, dim3(K4_THREADS), 0, st, src, nw, signs, packed, scale,
-                           pf);
+        hipLaunchKernelGGL((k1_k4096_rms<RESID, true>), grid, dim3(K4_THREADS), 0, st, M, eps, x, res_in, res_out,
+                           nw, signs, packed, scale, pf.p, pf.bytes);
     else
-        hipLaunchKernelGGL((k1_k4096_rms<RESID, false>), grid, dim3(K4_THREADS), 0, st, src, nw, signs, packed,
-                           scale, pf);
+        hipLaunchKernelGGL((k1_k4096_rms<RESID, false>), grid, dim3(K4_THREADS), 0, st, M, eps, x, res_in, res_out,
+                           nw, signs, packed, scale, pf.p, pf.bytes);
     return hipGetLastError();
 }
 
@@ -285,8 +295,8 @@ int quant_pack_impl(const void* x, const int8_t* signs, int8_t* packed, void* sc
     if (layout == NV4_LAYOUT_REFERENCE) {
         const auto* xp = static_cast<const uint16_t*>(x);
         auto* sp = static_cast<uint16_t*>(scale);
-        if (K == 4096) return (int)launch_k4096(RowX{xp, 4096}, signs, packed, sp, (int)M, rt, pf, st);
-        if (K == 12288) return (int)launch_k12288(RowX{xp, 12288}, signs, packed, sp, (int)M, rt, pf, st);
+        if (K == 4096) return (int)launch_k4096<RowX>(xp, signs, packed, sp, (int)M, rt, pf, st);
+        if (K == 12288) return (int)launch_k12288<RowX>(xp, signs, packed, sp, (int)M, rt, pf, st);
         return NV4_E_SHAPE;
     }
     if (layout == NV4_LAYOUT_BLOCK128 && !rt) {
@@ -316,13 +326,11 @@ int rmsnorm_quant_impl(const void* x, const void* residual_in, void* residual_ou
     const auto* xp = static_cast<const uint16_t*>(x);
     const auto* wp = static_cast<const uint16_t*>(norm_weight);
     auto* sp = static_cast<uint16_t*>(scale);
-    if (residual_in) {
-        RowRms<true> src{xp, static_cast<const uint16_t*>(residual_in), static_cast<uint16_t*>(residual_out), eps,
-                         {}, {}, nullptr};
-        return (int)launch_rms4096(src, wp, signs, packed, sp, (int)M, rt, pf, st);
-    }
-    RowRms<false> src{xp, nullptr, nullptr, eps, {}, {}, nullptr};
-    return (int)launch_rms4096(src, wp, signs, packed, sp, (int)M, rt, pf, st);
+    if (residual_in)
+        return (int)launch_rms4096<true>(xp, static_cast<const uint16_t*>(residual_in),
+                                         static_cast<uint16_t*>(residual_out), eps, wp, signs, packed, sp, (int)M, rt,
+                                         pf, st);
+    return (int)launch_rms4096<false>(xp, nullptr, nullptr, eps, wp, signs, packed, sp, (int)M, rt, pf, st);
 }
 
 int silu_quant_impl(const void* gate_up, const int8_t* signs, int8_t* packed, void* scale, int64_t M, int64_t K,
@@ -335,8 +343,8 @@ int silu_quant_impl(const void* gate_up, const int8_t* signs, int8_t* packed, vo
     hipStream_t st = static_cast<hipStream_t>(stream);
     const auto* gp = static_cast<const uint16_t*>(gate_up);
     auto* sp = static_cast<uint16_t*>(scale);
-    if (K == 4096) return (int)launch_k4096(RowSilu{gp, 4096}, signs, packed, sp, (int)M, rt, pf, st);
-    return (int)launch_k12288(RowSilu{gp, 12288}, signs, packed, sp, (int)M, rt, pf, st);
+    if (K == 4096) return (int)launch_k4096<RowSilu>(gp, signs, packed, sp, (int)M, rt, pf, st);
+    return (int)launch_k12288<RowSilu>(gp, signs, packed, sp, (int)M, rt, pf, st);
 }
 
 }  // namespace
@@ -353,7 +361,7 @@ extern "C" int nv4_rht_quant_pack_rowtiled(const void* x, const int8_t* signs, i
     const int rc = nv4::check_prefetch(prefetch, prefetch_bytes);
     if (rc != NV4_OK) return rc;
     return nv4::quant_pack_impl(x, signs, packed_rt, scale, M, K, NV4_LAYOUT_REFERENCE, true,
-                                nv4::Prefetch{static_cast<const int8_t*>(prefetch), prefetch_bytes, 0}, stream);
+                                nv4::Prefetch{static_cast<const int8_t*>(prefetch), prefetch_bytes}, stream);
 }
 
 extern "C" int nv4_rmsnorm_rht_quant_pack(const void* x, const void* residual_in, void* residual_out,
@@ -370,7 +378,7 @@ extern "C" int nv4_rmsnorm_rht_quant_pack_rowtiled(const void* x, const void* re
     const int rc = nv4::check_prefetch(prefetch, prefetch_bytes);
     if (rc != NV4_OK) return rc;
     return nv4::rmsnorm_quant_impl(x, residual_in, residual_out, norm_weight, eps, signs, packed_rt, scale, M, K,
-                                   true, nv4::Prefetch{static_cast<const int8_t*>(prefetch), prefetch_bytes, 0},
+                                   true, nv4::Prefetch{static_cast<const int8_t*>(prefetch), prefetch_bytes},
                                    stream);
 }
 
@@ -385,5 +393,5 @@ extern "C" int nv4_silu_mul_rht_quant_pack_rowtiled(const void* gate_up, const i
     const int rc = nv4::check_prefetch(prefetch, prefetch_bytes);
     if (rc != NV4_OK) return rc;
     return nv4::silu_quant_impl(gate_up, signs, packed_rt, scale, M, K, true,
-                                nv4::Prefetch{static_cast<const int8_t*>(prefetch), prefetch_bytes, 0}, stream);
+                                nv4::Prefetch{static_cast<const int8_t*>(prefetch), prefetch_bytes}, stream);
 }
