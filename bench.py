@@ -205,7 +205,8 @@ def pmc_pass(torch, linear, R):
 
 
 DECODE_GEMM_SOURCES = ("nano-vllm-int4_amd/csrc/w4a4_gemm.hip", "nano-vllm-int4_amd/csrc/nv4_common.h",
-                       "nano-vllm-int4_amd/csrc/norm_ops.h", "nano-vllm-int4_amd/csrc/k2_launch.h")
+                       "nano-vllm-int4_amd/csrc/norm_ops.h", "nano-vllm-int4_amd/csrc/k2_launch.h",
+                       "nano-vllm-int4_amd/Makefile")
 
 
 def decode_gemm_source_sha():

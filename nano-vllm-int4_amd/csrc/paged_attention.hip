@@ -103,19 +103,38 @@ __device__ __forceinline__ void kv_step(const QkvStep& qs, const Head16& kh, v4u
     if (store_v && lane < 16) *reinterpret_cast<v4u*>(qs.v_cache + (slot * Hkv + kvh) * PA_D + 8 * lane) = vch;
 }
 
-template <int G, bool BLK16, bool FUSED>
+// The arguments the first loads need (q, the caches, the block table, the
+// context lengths, max_blocks, bs, Hkv, max_ctx) come first: they fill the 14
+// argument dwords preloaded into SGPRs at wave launch, so the context length
+// and block-table loads issue before any wait.  BLK: 0 for any block size, 16 for block
+// sizes that are multiples of 16, PA_SPLIT for blocks of exactly PA_SPLIT.
+template <int G, int BLK, bool FUSED>
 __global__ void __launch_bounds__(PA_THREADS)
-pa_split(const uint16_t* __restrict__ q, int64_t q_row, const uint16_t* kc, const uint16_t* vc,
-         const int32_t* __restrict__ block_tables, int max_blocks, const int32_t* __restrict__ context_lens,
-         uint16_t* __restrict__ out, float* __restrict__ part_o, float* __restrict__ part_ml, int Hkv, int bs,
-         int S, int max_ctx, float qscale, QkvStep qs) {
+pa_split(const uint16_t* __restrict__ q, const uint16_t* kc, const uint16_t* vc,
+         const int32_t* __restrict__ block_tables, const int32_t* __restrict__ context_lens, int max_blocks, int bs,
+         int Hkv, int max_ctx, int64_t q_row, uint16_t* __restrict__ out, float* __restrict__ part_o,
+         float* __restrict__ part_ml, int S, float qscale, QkvStep qs) {
+    constexpr bool BLK16 = BLK != 0;
     const int s = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
     const int Hq = Hkv * G;
-    const int clen = context_lens[b];
-    const int ctx = min(clen, max_ctx);  // never past the block table's row
     const int start = s * PA_SPLIT;
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int32_t* bt = block_tables + (int64_t)b * max_blocks;
+    const int clen = context_lens[b];
+    // Blocks of PA_SPLIT tokens (BLK == PA_SPLIT): the split is block s, whose
+    // entry goes out with the context length, in one round trip (clamped
+    // into the row; for a split that runs, start < ctx <= max_blocks * bs, so
+    // s < max_blocks and every token of the split, clamped runs included,
+    // lies in block s).
+    int bt_split = 0;
+    if constexpr (BLK == PA_SPLIT) {
+        bt_split = bt[min(s, max_blocks - 1)];
+        // Issued with the context length, ahead of the wait on the other
+        // (non-preloaded) arguments.
+        asm volatile("" ::"s"(bt_split), "s"(clen));
+    }
+    const int ctx = min(clen, max_ctx);  // never past the block table's row
     const uint16_t* qrow = q + (int64_t)b * q_row;
     int64_t slot = -1, pos = 0;
     bool kv_wg = false, slot_ok = false;
@@ -159,7 +178,6 @@ pa_split(const uint16_t* __restrict__ q, int64_t q_row, const uint16_t* kc, cons
     // FUSED: per wave, the G normalised, rotated q heads, then the step's key.
     __shared__ __align__(16) uint16_t s_qk[FUSED ? 4 : 1][G + 1][PA_D];
 
-    const int32_t* bt = block_tables + (int64_t)b * max_blocks;
     const uint32_t row = (uint32_t)Hkv * PA_D;  // elements between consecutive slots
     const uint16_t* kbase = kc + kvh * PA_D + 8 * rc;
     const uint16_t* vbase = vc + kvh * PA_D + 8 * rc;
@@ -169,14 +187,17 @@ pa_split(const uint16_t* __restrict__ q, int64_t q_row, const uint16_t* kc, cons
     // A run of 16 tokens starting at t0 (wave-uniform), clamped into the
     // sequence: token t0 + d is token t0c + min(d, ctx - 1 - t0c).  With
     // block_size % 16 == 0 the run lies in one block, whose block-table entry
-    // run_of reads ahead of its use.
+    // run_of reads ahead of its use (read at entry for BLK == PA_SPLIT).
     struct Run {
         int t0c, blk;
     };
     auto run_of = [&](int t0) {
         Run r;
         r.t0c = min(t0, ctx - 1);
-        r.blk = BLK16 ? bt[r.t0c / bs] : 0;
+        if constexpr (BLK == PA_SPLIT)
+            r.blk = bt_split;
+        else
+            r.blk = BLK16 ? bt[r.t0c / bs] : 0;
         return r;
     };
     auto slot_of = [&](const Run& r, int d) -> uint32_t {
@@ -566,16 +587,21 @@ hipError_t pa_launch(const void* q, int64_t q_row, const void* kc, const void* v
     float* part_o = ws;
     float* part_ml = ws + (int64_t)B * Hkv * G * S * PA_D;
     const dim3 grid((unsigned)S, (unsigned)Hkv, (unsigned)B);
-    if (bs % 16 == 0)
-        hipLaunchKernelGGL((pa_split<G, true, FUSED>), grid, dim3(PA_THREADS), 0, st,
-                           static_cast<const uint16_t*>(q), q_row, static_cast<const uint16_t*>(kc),
-                           static_cast<const uint16_t*>(vc), bt, max_blocks, cl, static_cast<uint16_t*>(out), part_o,
-                           part_ml, Hkv, bs, S, max_ctx, qscale, qs);
+    if (bs == PA_SPLIT)
+        hipLaunchKernelGGL((pa_split<G, PA_SPLIT, FUSED>), grid, dim3(PA_THREADS), 0, st,
+                           static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(kc),
+                           static_cast<const uint16_t*>(vc), bt, cl, max_blocks, bs, Hkv, max_ctx, q_row,
+                           static_cast<uint16_t*>(out), part_o, part_ml, S, qscale, qs);
+    else if (bs % 16 == 0)
+        hipLaunchKernelGGL((pa_split<G, 16, FUSED>), grid, dim3(PA_THREADS), 0, st,
+                           static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(kc),
+                           static_cast<const uint16_t*>(vc), bt, cl, max_blocks, bs, Hkv, max_ctx, q_row,
+                           static_cast<uint16_t*>(out), part_o, part_ml, S, qscale, qs);
     else
-        hipLaunchKernelGGL((pa_split<G, false, FUSED>), grid, dim3(PA_THREADS), 0, st,
-                           static_cast<const uint16_t*>(q), q_row, static_cast<const uint16_t*>(kc),
-                           static_cast<const uint16_t*>(vc), bt, max_blocks, cl, static_cast<uint16_t*>(out), part_o,
-                           part_ml, Hkv, bs, S, max_ctx, qscale, qs);
+        hipLaunchKernelGGL((pa_split<G, 0, FUSED>), grid, dim3(PA_THREADS), 0, st,
+                           static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(kc),
+                           static_cast<const uint16_t*>(vc), bt, cl, max_blocks, bs, Hkv, max_ctx, q_row,
+                           static_cast<uint16_t*>(out), part_o, part_ml, S, qscale, qs);
     if (S > 1) {
         const dim3 mg((unsigned)(Hkv * G), (unsigned)B);
         auto* o16 = static_cast<uint16_t*>(out);
