@@ -176,19 +176,23 @@ lm_head_p(const uint16_t* __restrict__ h, int64_t h_row, const uint16_t* __restr
     constexpr int KS = 32 * KSTEPS;
     v4f carry[3][2];  // pass-0 sums this wave reduces: [tile / 16][half of h]
     for (int pass = 0; pass < 2; ++pass) {
-        const int k0 = pass * (K >> 1) + wave * KS + q * 8 * KSTEPS;
+        // MFMA step j takes k = 32 j + 8 q .. + 7 of the wave's slice for lane
+        // group q (any assignment of k to steps gives the same dot product),
+        // so the four lanes of a row read 64 contiguous bytes per load: one
+        // cache line per row and instruction instead of two.
+        const int k0 = pass * (K >> 1) + wave * KS + q * 8;
         v4u b[2][KSTEPS];
 #pragma unroll
         for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
             for (int j = 0; j < KSTEPS; ++j)
-                b[mt][j] = *reinterpret_cast<const v4u*>(h + (int64_t)min(16 * mt + r, M - 1) * h_row + k0 + 8 * j);
+                b[mt][j] = *reinterpret_cast<const v4u*>(h + (int64_t)min(16 * mt + r, M - 1) * h_row + k0 + 32 * j);
         auto wrow = [&](int t) { return w + (int64_t)min(16 * (t0 + t) + r, N - 1) * K + k0; };
         v4u a[LMP_RING][KSTEPS];
         auto issue = [&](int slot, int t) {
             const uint16_t* p = wrow(min(t, nt - 1));
 #pragma unroll
-            for (int j = 0; j < KSTEPS; ++j) a[slot][j] = *reinterpret_cast<const v4u*>(p + 8 * j);
+            for (int j = 0; j < KSTEPS; ++j) a[slot][j] = *reinterpret_cast<const v4u*>(p + 32 * j);
         };
         // The ring always holds LMP_RING tiles (past the last tile it reloads
         // the last one), so the loop body has one fixed form.
