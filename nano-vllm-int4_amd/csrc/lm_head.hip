@@ -34,21 +34,23 @@ lm_head_k(const uint16_t* __restrict__ h, int64_t h_row, const uint16_t* __restr
     const int n0 = blockIdx.x * LM_ROWS;
     const int kq = STEPS * LM_STEP;  // the wave's K-quarter (K = 4 kq)
     // Rows past the matrix edge repeat its last row (never stored).
-    const uint16_t* pw = w + (int64_t)min(n0 + r, N - 1) * K + wave * kq + 32 * q;
+    // Product j of a step takes k = 32 j + 8 q .. + 7 (lane group q): a row's
+    // four lanes read 64 contiguous bytes per load.
+    const uint16_t* pw = w + (int64_t)min(n0 + r, N - 1) * K + wave * kq + 8 * q;
     const uint16_t* ph[MT];
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt) ph[mt] = h + (int64_t)min(16 * mt + r, M - 1) * h_row + wave * kq + 32 * q;
+    for (int mt = 0; mt < MT; ++mt) ph[mt] = h + (int64_t)min(16 * mt + r, M - 1) * h_row + wave * kq + 8 * q;
 
     // A fixed step count: every load and wait is placed at compile time, the
     // wait before step s leaves the loads of the next steps in flight.
     v4u a[LM_RING][4], b[LM_RING][MT][4];
     auto issue = [&](int slot, int s) {
 #pragma unroll
-        for (int j = 0; j < 4; ++j) a[slot][j] = *reinterpret_cast<const v4u*>(pw + s * LM_STEP + 8 * j);
+        for (int j = 0; j < 4; ++j) a[slot][j] = *reinterpret_cast<const v4u*>(pw + s * LM_STEP + 32 * j);
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-            for (int j = 0; j < 4; ++j) b[slot][mt][j] = *reinterpret_cast<const v4u*>(ph[mt] + s * LM_STEP + 8 * j);
+            for (int j = 0; j < 4; ++j) b[slot][mt][j] = *reinterpret_cast<const v4u*>(ph[mt] + s * LM_STEP + 32 * j);
     };
     v4f acc[MT];
 #pragma unroll
@@ -106,14 +108,16 @@ lm_head_k32(const uint16_t* __restrict__ h, int64_t h_row, const uint16_t* __res
     const int r = lane & 31, hh = lane >> 5;
     const int n0 = blockIdx.x * 32;
     const int kq = STEPS * STEP;  // the wave's K-quarter
-    const uint16_t* pw = w + (int64_t)min(n0 + r, N - 1) * K + wave * kq + 32 * hh;
-    const uint16_t* ph = h + (int64_t)min(r, M - 1) * h_row + wave * kq + 32 * hh;
+    // Product j of a step takes k = 16 j + 8 hh .. + 7: a row's two lanes read
+    // 32 contiguous bytes per load.
+    const uint16_t* pw = w + (int64_t)min(n0 + r, N - 1) * K + wave * kq + 8 * hh;
+    const uint16_t* ph = h + (int64_t)min(r, M - 1) * h_row + wave * kq + 8 * hh;
     v4u a[LM_RING][4], b[LM_RING][4];
     auto issue = [&](int slot, int s) {
 #pragma unroll
-        for (int j = 0; j < 4; ++j) a[slot][j] = *reinterpret_cast<const v4u*>(pw + s * STEP + 8 * j);
+        for (int j = 0; j < 4; ++j) a[slot][j] = *reinterpret_cast<const v4u*>(pw + s * STEP + 16 * j);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) b[slot][j] = *reinterpret_cast<const v4u*>(ph + s * STEP + 8 * j);
+        for (int j = 0; j < 4; ++j) b[slot][j] = *reinterpret_cast<const v4u*>(ph + s * STEP + 16 * j);
     };
     v16f acc = {};
     static_for<0, (LM_RING < STEPS ? LM_RING : STEPS)>([&](auto s) { issue(s.value, s.value); });
@@ -153,9 +157,9 @@ lm_head_k32(const uint16_t* __restrict__ h, int64_t h_row, const uint16_t* __res
 // halves of h (pass 0 kept in registers, pass 1 added to it, then rounded and
 // stored).  All waves take the same tiles, so
 // the one barrier per tile is reached by every wave the same number of times.
-// Lane (r, q) = (l % 16, l / 16) of a slice of KS = 32 KSTEPS values loads the
-// 8 KSTEPS contiguous values at q 8 KSTEPS of its row and feeds them to
-// KSTEPS products, 8 each; the h operand is read the same way.
+// Lane (r, q) = (l % 16, l / 16) of a slice of KS = 32 KSTEPS values feeds
+// product j the 8 values at 32 j + 8 q of its row, so the four lanes of a row
+// read 64 contiguous bytes per load; the h operand is read the same way.
 constexpr int LMP_WAVES = 16;
 constexpr int LMP_RING = 2;      // tiles of W loads in flight per wave
 constexpr int LMP_MAX_TILES = 48;  // tiles per workgroup (3 per wave to reduce)
