@@ -840,13 +840,17 @@ int tile_impl(const int8_t* src, int8_t* dst, bool to_tiled, int64_t N, int64_t 
 extern "C" int64_t nv4_w4a4_prefetch_bytes(int64_t N, int64_t K) {
     // How much of a decode GEMM's packed weights the K1 before it reads
     // ahead.  Measured on the Qwen3-8B projections at M = 32 (K1 + GEMM per
-    // call): K1 at K = 12288 runs long enough to bring in all of down's 25 MB
-    // (14.9 -> 13.6 us); at K = 4096 about 6 MB fits in K1's time (o 8.4 ->
-    // 8.1, qkv 10.7 -> 10.1-10.2, gate_up 19.0 -> 18.2 us), while reading
-    // gate_up's 50 MB whole made the pair 4.5 us slower.
+    // call, graph replays over weight sets larger than the Infinity Cache):
+    // a weight read whole beats a head of it (the GEMM then waits on no HBM
+    // tail): down's 25 MB after K1 at K = 12288 (15.1 -> 13.3 us), o's 8.4 MB
+    // (7.6-7.7 with 6 MB -> 7.2 us); gate_up's 50 MB is best at 9 MB (16.2
+    // without, 15.4-16.0 with 6 MB, 15.3 with 9 MB, and 4.5 us slower whole);
+    // qkv's 12.6 MB stays within 0.1 us from none to 6 MB (9 MB: +0.4 us).
     if (N < 1 || K < 128 || K % 128 || N > (1LL << 31) || K > (1LL << 20)) return 0;
     const int64_t bytes = N * K / 2;
-    const int64_t cap = K >= 12288 ? (32LL << 20) : (6LL << 20);
+    const int64_t cap = K >= 12288 || bytes <= (9LL << 20) ? (32LL << 20)
+                        : bytes > (24LL << 20)             ? (9LL << 20)
+                                                           : (6LL << 20);
     return bytes < cap ? bytes : cap;
 }
 

@@ -271,8 +271,9 @@ def test_paged_decode_attention_size_checks_do_not_wrap():
 def test_prefetch_size_rule():
     f = _lib.load().nv4_w4a4_prefetch_bytes
     assert f(4096, 12288) == 4096 * 6144           # down: all of its weights
-    for n in (4096, 6144, 24576):                   # K = 4096: the first 6 MiB
-        assert f(n, 4096) == 6 << 20
+    assert f(4096, 4096) == 4096 * 2048             # o (8 MiB): all of it
+    assert f(6144, 4096) == 6 << 20                 # qkv (12 MiB): the first 6 MiB
+    assert f(24576, 4096) == 9 << 20                # gate_up (48 MiB): the first 9 MiB
     assert f(16, 256) == 16 * 128
     assert f(0, 4096) == 0 and f(64, 100) == 0
 
